@@ -1,0 +1,599 @@
+// api.hip -- the C ABI declared in include/gonn_hip.h.
+//
+// Argument checks run on the host before anything is queued, so every
+// GONN_E_* path is testable without a GPU. Device work goes to the caller's
+// stream; the f64 compatibility shims are synchronous like the reference's
+// (backend/cuda/gonn_cuda.cu:466-560) but check every runtime call.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <vector>
+
+#include "../../include/gonn_hip.h"
+#include "common.h"
+#include "kernels.h"
+
+#define GONN_HIP_VERSION "gonn-hip 0.1.0 (gfx950)"
+
+namespace {
+
+std::atomic<int> g_mode{-1};
+
+int env_mode() {
+    const char* e = std::getenv("GONN_HIP_ATTN_MODE");
+    if (e && (std::strcmp(e, "bf16") == 0 || std::strcmp(e, "1") == 0)) return GONN_ATTN_BF16_MFMA;
+    return GONN_ATTN_FP32_MFMA;
+}
+
+int current_mode() {
+    int m = g_mode.load();
+    if (m < 0) {
+        int expected = -1;
+        g_mode.compare_exchange_strong(expected, env_mode());
+        m = g_mode.load();
+    }
+    return m;
+}
+
+bool fail_alloc_injected() {
+    const char* e = std::getenv("GONN_HIP_FAIL_ALLOC");
+    return e && e[0] == '1';
+}
+
+size_t dtype_size(int dt) {
+    switch (dt) {
+        case GONN_F32: return 4;
+        case GONN_BF16: return 2;
+        case GONN_F64: return 8;
+        case GONN_I32: return 4;
+        default: return 0;
+    }
+}
+
+bool buf_ok(const gonn_buf& b, size_t elems, int dt0, int dt1 = -1) {
+    if (!b.ptr) return false;
+    if (b.dtype != dt0 && b.dtype != dt1) return false;
+    return b.bytes >= elems * dtype_size(b.dtype);
+}
+
+int herr(hipError_t e) { return e == hipSuccess ? GONN_OK : (int)e; }
+
+bool head_dim_ok(int D) { return D == 64 || D == 128; }
+
+size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
+
+// ---- forward -----------------------------------------------------------
+
+int check_fwd(const gonn_attn_fwd_args* a) {
+    if (!a) return GONN_E_INVALID;
+    if (a->B <= 0 || a->H <= 0 || a->Sq <= 0 || a->Sk <= 0 || a->D <= 0) return GONN_E_INVALID;
+    if (a->mode != GONN_ATTN_FP32_MFMA && a->mode != GONN_ATTN_BF16_MFMA) return GONN_E_INVALID;
+    if (!std::isfinite(a->scale)) return GONN_E_INVALID;
+    if (!head_dim_ok(a->D)) return GONN_E_UNSUPPORTED;
+    const size_t BH = (size_t)a->B * a->H;
+    if ((double)BH * a->Sq * a->D >= 2147483647.0 * 8 || (double)BH * a->Sk * a->D >= 2147483647.0 * 8)
+        return GONN_E_UNSUPPORTED;
+    const size_t nq = BH * a->Sq * a->D, nk = BH * a->Sk * a->D;
+    if (a->mode == GONN_ATTN_FP32_MFMA) {
+        if (!buf_ok(a->q, nq, GONN_F32) || !buf_ok(a->k, nk, GONN_F32) || !buf_ok(a->v, nk, GONN_F32))
+            return GONN_E_INVALID;
+    } else {
+        if (!buf_ok(a->q, nq, GONN_F32, GONN_BF16) || !buf_ok(a->k, nk, GONN_F32, GONN_BF16) ||
+            !buf_ok(a->v, nk, GONN_F32, GONN_BF16) || a->k.dtype != a->v.dtype)
+            return GONN_E_INVALID;
+    }
+    if (!buf_ok(a->o, nq, GONN_F32)) return GONN_E_INVALID;
+    if (a->lse.ptr && !buf_ok(a->lse, BH * a->Sq, GONN_F32)) return GONN_E_INVALID;
+    return GONN_OK;
+}
+
+size_t fwd_ws(const gonn_attn_fwd_args* a) {
+    if (a->mode != GONN_ATTN_BF16_MFMA) return 0;
+    const size_t BH = (size_t)a->B * a->H;
+    const size_t Skp = round_up((size_t)a->Sk, 64);
+    return 2 * BH * Skp * a->D * sizeof(uint16_t) + 256;
+}
+
+// ---- decode ------------------------------------------------------------
+
+int decode_split(const gonn_attn_decode_args* a) {
+    if (a->split_keys > 0) return a->split_keys;
+    return 512;
+}
+
+int check_decode(const gonn_attn_decode_args* a) {
+    if (!a) return GONN_E_INVALID;
+    if (a->B <= 0 || a->H <= 0 || a->Lmax <= 0 || a->D <= 0) return GONN_E_INVALID;
+    if (!std::isfinite(a->scale)) return GONN_E_INVALID;
+    if (a->split_keys < 0 || (a->split_keys % 64) != 0) return GONN_E_INVALID;
+    if (!head_dim_ok(a->D)) return GONN_E_UNSUPPORTED;
+    const size_t BH = (size_t)a->B * a->H;
+    if (!buf_ok(a->q, BH * a->D, GONN_F32, GONN_BF16)) return GONN_E_INVALID;
+    const size_t nc = BH * (size_t)a->Lmax * a->D;
+    if (!buf_ok(a->kcache, nc, GONN_BF16) || !buf_ok(a->vcache, nc, GONN_BF16)) return GONN_E_INVALID;
+    if (!buf_ok(a->kv_len, (size_t)a->B, GONN_I32)) return GONN_E_INVALID;
+    if (!buf_ok(a->o, BH * a->D, GONN_F32)) return GONN_E_INVALID;
+    return GONN_OK;
+}
+
+size_t decode_ws(const gonn_attn_decode_args* a) {
+    const size_t BH = (size_t)a->B * a->H;
+    const int sk = decode_split(a);
+    const size_t ns = ((size_t)a->Lmax + sk - 1) / sk;
+    return BH * ns * ((size_t)a->D + 2) * sizeof(float) + 1024;
+}
+
+// ---- backward ----------------------------------------------------------
+
+int check_bwd(const gonn_attn_bwd_args* a) {
+    if (!a) return GONN_E_INVALID;
+    if (a->B <= 0 || a->H <= 0 || a->S <= 0 || a->D <= 0) return GONN_E_INVALID;
+    if (a->mode != GONN_ATTN_FP32_MFMA && a->mode != GONN_ATTN_BF16_MFMA) return GONN_E_INVALID;
+    if (!std::isfinite(a->scale)) return GONN_E_INVALID;
+    if (!head_dim_ok(a->D)) return GONN_E_UNSUPPORTED;
+    const size_t BH = (size_t)a->B * a->H, n = BH * a->S * a->D;
+    if ((double)n >= 2147483647.0 * 8) return GONN_E_UNSUPPORTED;
+    const gonn_buf* in[] = {&a->q, &a->k, &a->v, &a->o, &a->dO, &a->dq, &a->dk, &a->dv};
+    for (const gonn_buf* b : in)
+        if (!buf_ok(*b, n, GONN_F32)) return GONN_E_INVALID;
+    if (!buf_ok(a->lse, BH * a->S, GONN_F32)) return GONN_E_INVALID;
+    return GONN_OK;
+}
+
+// ---- helpers for the host shims ----------------------------------------
+
+struct DevMem {
+    std::vector<void*> ptrs;
+    ~DevMem() {
+        for (void* p : ptrs) (void)hipFree(p);
+    }
+    int alloc(void** p, size_t bytes) {
+        if (fail_alloc_injected()) return GONN_E_INJECTED;
+        if (bytes == 0) bytes = 16;
+        if (hipMalloc(p, bytes) != hipSuccess) {
+            *p = nullptr;
+            return GONN_E_NOMEM;
+        }
+        ptrs.push_back(*p);
+        return GONN_OK;
+    }
+};
+
+int pad_dim(int d) { return d <= 64 ? 64 : 128; }
+
+#define TRY(x)                      \
+    do {                            \
+        const int _rc = (x);        \
+        if (_rc != GONN_OK) return _rc; \
+    } while (0)
+#define TRYH(x) TRY(herr(x))
+
+// Upload n rows of d doubles and convert to f32 rows of dp (zero-padded).
+int upload_padded(DevMem& mem, const double* host, size_t rows, int d, int dp, float** out) {
+    void* stage = nullptr;
+    void* dst = nullptr;
+    TRY(mem.alloc(&stage, rows * d * sizeof(double)));
+    TRY(mem.alloc(&dst, rows * dp * sizeof(float)));
+    TRYH(hipMemcpy(stage, host, rows * d * sizeof(double), hipMemcpyHostToDevice));
+    TRYH(gonn::launch_convert_from_f64((const double*)stage, dst, 0, rows, d, dp, nullptr));
+    *out = (float*)dst;
+    return GONN_OK;
+}
+
+int download_padded(DevMem& mem, const float* dev, size_t rows, int d, int dp, double* host) {
+    void* stage = nullptr;
+    TRY(mem.alloc(&stage, rows * d * sizeof(double)));
+    TRYH(gonn::launch_convert_to_f64(dev, 0, (double*)stage, rows, d, dp, nullptr));
+    TRYH(hipMemcpy(host, stage, rows * d * sizeof(double), hipMemcpyDeviceToHost));
+    return GONN_OK;
+}
+
+int run_fwd_f32(DevMem& mem, const float* q, const float* k, const float* v, float* o, float* lse,
+                int BH, int S, int dp, double scale, int causal) {
+    gonn_attn_fwd_args a{};
+    const size_t n = (size_t)BH * S * dp;
+    a.q = {(void*)q, n * 4, GONN_F32};
+    a.k = {(void*)k, n * 4, GONN_F32};
+    a.v = {(void*)v, n * 4, GONN_F32};
+    a.o = {(void*)o, n * 4, GONN_F32};
+    a.lse = {(void*)lse, lse ? (size_t)BH * S * 4 : 0, GONN_F32};
+    a.B = BH;
+    a.H = 1;
+    a.Sq = a.Sk = S;
+    a.D = dp;
+    a.scale = scale;
+    a.causal = causal;
+    a.mode = current_mode();
+    const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_FWD, &a);
+    void* ws = nullptr;
+    if (wsb) TRY(mem.alloc(&ws, wsb));
+    return gonn_hip_attn_fwd(&a, ws, wsb, nullptr);
+}
+
+bool shim_args_ok(int BH, int S, int d) { return BH > 0 && S > 0 && d > 0 && d <= 128; }
+
+}  // namespace
+
+extern "C" {
+
+const char* gonn_hip_version(void) { return GONN_HIP_VERSION; }
+
+const char* gonn_hip_strerror(int code) {
+    switch (code) {
+        case GONN_OK: return "success";
+        case GONN_E_INVALID: return "invalid argument (shape, null pointer, dtype or short buffer)";
+        case GONN_E_UNSUPPORTED: return "unsupported configuration (head dim must be 64 or 128)";
+        case GONN_E_WORKSPACE: return "workspace missing or too small";
+        case GONN_E_NOMEM: return "device allocation failed";
+        case GONN_E_NODEVICE: return "no usable gfx950 device";
+        case GONN_E_INJECTED: return "failure injected by GONN_HIP_FAIL_ALLOC";
+        default: break;
+    }
+    if (code > 0) return hipGetErrorString((hipError_t)code);
+    return "unknown error";
+}
+
+int gonn_hip_available(void) {
+    static int cached = -1;
+    static std::mutex mu;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached >= 0) return cached;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        cached = 0;
+        return 0;
+    }
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) != hipSuccess || hipGetDeviceProperties(&prop, dev) != hipSuccess) {
+        cached = 0;
+        return 0;
+    }
+    cached = std::strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 0;
+    return cached;
+}
+
+int gonn_hip_attn_supports(int D, int Sq, int Sk) {
+    return head_dim_ok(D) && Sq > 0 && Sk > 0 ? 1 : 0;
+}
+
+int gonn_hip_set_attn_mode(int mode) {
+    if (mode != GONN_ATTN_FP32_MFMA && mode != GONN_ATTN_BF16_MFMA) return GONN_E_INVALID;
+    g_mode.store(mode);
+    return GONN_OK;
+}
+
+int gonn_hip_get_attn_mode(void) { return current_mode(); }
+
+size_t gonn_hip_attn_workspace_bytes(int op, const void* args) {
+    if (!args) return 0;
+    switch (op) {
+        case GONN_OP_FWD: {
+            const auto* a = (const gonn_attn_fwd_args*)args;
+            if (a->B <= 0 || a->H <= 0 || a->Sk <= 0 || a->D <= 0) return 0;
+            return fwd_ws(a);
+        }
+        case GONN_OP_BWD: {
+            const auto* a = (const gonn_attn_bwd_args*)args;
+            if (a->B <= 0 || a->H <= 0 || a->S <= 0 || !head_dim_ok(a->D)) return 0;
+            return gonn::bwd_workspace_bytes(a->mode, a->B * a->H, a->S, a->D) + 256;
+        }
+        case GONN_OP_DECODE: {
+            const auto* a = (const gonn_attn_decode_args*)args;
+            if (a->B <= 0 || a->H <= 0 || a->Lmax <= 0 || a->D <= 0) return 0;
+            return decode_ws(a);
+        }
+        default: return 0;
+    }
+}
+
+int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, void* stream) {
+    TRY(check_fwd(a));
+    const size_t need = fwd_ws(a);
+    if (need && (!ws || ws_bytes < need)) return GONN_E_WORKSPACE;
+    hipStream_t s = (hipStream_t)stream;
+    const int BH = a->B * a->H;
+    gonn::FwdParams p{};
+    p.o = (float*)a->o.ptr;
+    p.lse = a->lse.ptr ? (float*)a->lse.ptr : nullptr;
+    p.BH = BH;
+    p.Sq = a->Sq;
+    p.Sk = a->Sk;
+    p.nqb = (a->Sq + 127) / 128;
+    if (a->scale == 0.0) {  // all scores 0: uniform weights; Q is zeroed
+        p.qsign = 0.f;
+        p.scale_abs = 1.f;
+    } else {
+        p.qsign = a->scale < 0 ? -1.f : 1.f;
+        p.scale_abs = (float)std::fabs(a->scale);
+    }
+    p.scale_log2 = p.scale_abs * gonn::kLog2e;
+    p.q = a->q.ptr;
+    if (a->mode == GONN_ATTN_BF16_MFMA) {
+        const int Skp = (int)round_up((size_t)a->Sk, 64);
+        uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
+        const size_t half = (size_t)BH * Skp * a->D * sizeof(uint16_t);
+        void* Kb = w;
+        void* Vt = w + half;
+        TRYH(gonn::launch_pack_kv(a->k.ptr, a->v.ptr, a->k.dtype == GONN_BF16, Kb, Vt, BH, a->Sk,
+                                  Skp, a->D, s));
+        p.k = Kb;
+        p.v = Vt;
+        p.Skp = Skp;
+    } else {
+        p.k = a->k.ptr;
+        p.v = a->v.ptr;
+        p.Skp = a->Sk;
+    }
+    return herr(gonn::launch_fwd(p, a->mode, a->D, a->causal, a->q.dtype == GONN_BF16, s));
+}
+
+int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, void* stream) {
+    TRY(check_bwd(a));
+    const size_t need = gonn_hip_attn_workspace_bytes(GONN_OP_BWD, a);
+    if (need && (!ws || ws_bytes < need)) return GONN_E_WORKSPACE;
+    gonn::BwdParams p{};
+    p.q = a->q.ptr;
+    p.k = a->k.ptr;
+    p.v = a->v.ptr;
+    p.dO = a->dO.ptr;
+    p.lse = (const float*)a->lse.ptr;
+    p.dq = (float*)a->dq.ptr;
+    p.dk = (float*)a->dk.ptr;
+    p.dv = (float*)a->dv.ptr;
+    p.BH = a->B * a->H;
+    p.S = a->S;
+    p.Sp = (int)round_up((size_t)a->S, 64);
+    p.scale = (float)a->scale;
+    p.scale_log2 = (float)a->scale * gonn::kLog2e;
+    void* w = (void*)round_up((size_t)ws, 256);
+    return herr(gonn::launch_bwd(p, a->mode, a->D, a->causal, (const float*)a->o.ptr, w,
+                                 (hipStream_t)stream));
+}
+
+int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
+    TRY(check_decode(a));
+    const size_t need = decode_ws(a);
+    if (!ws || ws_bytes < need) return GONN_E_WORKSPACE;
+    gonn::DecodeParams p{};
+    const int sk = decode_split(a);
+    p.q = a->q.ptr;
+    p.kc = a->kcache.ptr;
+    p.vc = a->vcache.ptr;
+    p.kv_len = (const int*)a->kv_len.ptr;
+    p.o = (float*)a->o.ptr;
+    p.B = a->B;
+    p.H = a->H;
+    p.Lmax = a->Lmax;
+    p.split_keys = sk;
+    p.nsplit = (a->Lmax + sk - 1) / sk;
+    float* w = (float*)round_up((size_t)ws, 256);
+    p.part_ml = w;
+    p.part_o = w + round_up((size_t)a->B * a->H * p.nsplit * 2, 64);
+    p.scale_log2 = (float)a->scale * gonn::kLog2e;
+    return herr(gonn::launch_decode(p, a->D, a->q.dtype == GONN_BF16, (hipStream_t)stream));
+}
+
+int gonn_hip_alloc(gonn_buf* b, size_t n_elems, int dtype) {
+    if (!b || dtype_size(dtype) == 0) return GONN_E_INVALID;
+    b->ptr = nullptr;
+    b->bytes = 0;
+    b->dtype = dtype;
+    if (fail_alloc_injected()) return GONN_E_INJECTED;
+    const size_t bytes = n_elems * dtype_size(dtype);
+    void* p = nullptr;
+    if (hipMalloc(&p, bytes ? bytes : 16) != hipSuccess) {
+        (void)hipGetLastError();
+        return GONN_E_NOMEM;
+    }
+    b->ptr = p;
+    b->bytes = bytes;
+    return GONN_OK;
+}
+
+int gonn_hip_free(gonn_buf* b) {
+    if (!b) return GONN_E_INVALID;
+    if (b->ptr) {
+        const hipError_t e = hipFree(b->ptr);
+        b->ptr = nullptr;
+        b->bytes = 0;
+        return herr(e);
+    }
+    return GONN_OK;
+}
+
+int gonn_hip_upload_from_f64(gonn_buf* dst, const double* src, size_t n, void* stream) {
+    if (!dst || !dst->ptr || (!src && n)) return GONN_E_INVALID;
+    if (dst->dtype != GONN_F32 && dst->dtype != GONN_BF16 && dst->dtype != GONN_F64)
+        return GONN_E_INVALID;
+    if (dst->bytes < n * dtype_size(dst->dtype)) return GONN_E_INVALID;
+    if (n == 0) return GONN_OK;
+    hipStream_t s = (hipStream_t)stream;
+    if (dst->dtype == GONN_F64) {
+        TRYH(hipMemcpyAsync(dst->ptr, src, n * 8, hipMemcpyHostToDevice, s));
+        return herr(hipStreamSynchronize(s));
+    }
+    DevMem mem;
+    void* stage = nullptr;
+    TRY(mem.alloc(&stage, n * 8));
+    TRYH(hipMemcpyAsync(stage, src, n * 8, hipMemcpyHostToDevice, s));
+    TRYH(gonn::launch_convert_from_f64((const double*)stage, dst->ptr, dst->dtype == GONN_BF16, n,
+                                       1, 1, s));
+    return herr(hipStreamSynchronize(s));
+}
+
+int gonn_hip_download_to_f64(double* dst, const gonn_buf* src, size_t n, void* stream) {
+    if (!src || !src->ptr || (!dst && n)) return GONN_E_INVALID;
+    if (src->dtype != GONN_F32 && src->dtype != GONN_BF16 && src->dtype != GONN_F64)
+        return GONN_E_INVALID;
+    if (src->bytes < n * dtype_size(src->dtype)) return GONN_E_INVALID;
+    if (n == 0) return GONN_OK;
+    hipStream_t s = (hipStream_t)stream;
+    if (src->dtype == GONN_F64) {
+        TRYH(hipMemcpyAsync(dst, src->ptr, n * 8, hipMemcpyDeviceToHost, s));
+        return herr(hipStreamSynchronize(s));
+    }
+    DevMem mem;
+    void* stage = nullptr;
+    TRY(mem.alloc(&stage, n * 8));
+    TRYH(gonn::launch_convert_to_f64(src->ptr, src->dtype == GONN_BF16, (double*)stage, n, 1, 1, s));
+    TRYH(hipMemcpyAsync(dst, stage, n * 8, hipMemcpyDeviceToHost, s));
+    return herr(hipStreamSynchronize(s));
+}
+
+int gonn_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
+    if ((!dst || !src) && bytes) return GONN_E_INVALID;
+    hipStream_t s = (hipStream_t)stream;
+    TRYH(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, s));
+    return herr(hipStreamSynchronize(s));
+}
+
+int gonn_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) {
+    if ((!dst || !src) && bytes) return GONN_E_INVALID;
+    hipStream_t s = (hipStream_t)stream;
+    TRYH(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s));
+    return herr(hipStreamSynchronize(s));
+}
+
+int gonn_hip_stream_sync(void* stream) { return herr(hipStreamSynchronize((hipStream_t)stream)); }
+
+int gonn_hip_flash_attn_f64(const double* Q, const double* K, const double* V, double* O, int BH,
+                            int S, int d, double scale, int causal) {
+    if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O) return GONN_E_INVALID;
+    if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    DevMem mem;
+    const int dp = pad_dim(d);
+    const size_t rows = (size_t)BH * S;
+    float *q, *k, *v, *o;
+    TRY(upload_padded(mem, Q, rows, d, dp, &q));
+    TRY(upload_padded(mem, K, rows, d, dp, &k));
+    TRY(upload_padded(mem, V, rows, d, dp, &v));
+    TRY(mem.alloc((void**)&o, rows * dp * 4));
+    TRY(run_fwd_f32(mem, q, k, v, o, nullptr, BH, S, dp, scale, causal));
+    TRY(download_padded(mem, o, rows, d, dp, O));
+    return herr(hipDeviceSynchronize());
+}
+
+int gonn_hip_flash_attn_f64_fwd(const double* Q, const double* K, const double* V, double* O,
+                                double* L, int BH, int S, int d, double scale, int causal) {
+    if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O || !L) return GONN_E_INVALID;
+    if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    DevMem mem;
+    const int dp = pad_dim(d);
+    const size_t rows = (size_t)BH * S;
+    float *q, *k, *v, *o, *l;
+    TRY(upload_padded(mem, Q, rows, d, dp, &q));
+    TRY(upload_padded(mem, K, rows, d, dp, &k));
+    TRY(upload_padded(mem, V, rows, d, dp, &v));
+    TRY(mem.alloc((void**)&o, rows * dp * 4));
+    TRY(mem.alloc((void**)&l, rows * 4));
+    TRY(run_fwd_f32(mem, q, k, v, o, l, BH, S, dp, scale, causal));
+    TRY(download_padded(mem, o, rows, d, dp, O));
+    TRY(download_padded(mem, l, rows, 1, 1, L));
+    return herr(hipDeviceSynchronize());
+}
+
+int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* V, const double* O,
+                                const double* L, const double* dO, double* dQ, double* dK,
+                                double* dV, int BH, int S, int d, double scale, int causal) {
+    if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O || !L || !dO || !dQ || !dK || !dV)
+        return GONN_E_INVALID;
+    if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    DevMem mem;
+    const int dp = pad_dim(d);
+    const size_t rows = (size_t)BH * S, n = rows * dp;
+    float *q, *k, *v, *o, *l, *g, *dq, *dk, *dv;
+    TRY(upload_padded(mem, Q, rows, d, dp, &q));
+    TRY(upload_padded(mem, K, rows, d, dp, &k));
+    TRY(upload_padded(mem, V, rows, d, dp, &v));
+    TRY(upload_padded(mem, O, rows, d, dp, &o));
+    TRY(upload_padded(mem, L, rows, 1, 1, &l));
+    TRY(upload_padded(mem, dO, rows, d, dp, &g));
+    TRY(mem.alloc((void**)&dq, n * 4));
+    TRY(mem.alloc((void**)&dk, n * 4));
+    TRY(mem.alloc((void**)&dv, n * 4));
+    gonn_attn_bwd_args a{};
+    a.q = {q, n * 4, GONN_F32};
+    a.k = {k, n * 4, GONN_F32};
+    a.v = {v, n * 4, GONN_F32};
+    a.o = {o, n * 4, GONN_F32};
+    a.lse = {l, rows * 4, GONN_F32};
+    a.dO = {g, n * 4, GONN_F32};
+    a.dq = {dq, n * 4, GONN_F32};
+    a.dk = {dk, n * 4, GONN_F32};
+    a.dv = {dv, n * 4, GONN_F32};
+    a.B = BH;
+    a.H = 1;
+    a.S = S;
+    a.D = dp;
+    a.scale = scale;
+    a.causal = causal;
+    a.mode = current_mode();
+    a.deterministic = 1;
+    const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_BWD, &a);
+    void* ws = nullptr;
+    if (wsb) TRY(mem.alloc(&ws, wsb));
+    TRY(gonn_hip_attn_bwd(&a, ws, wsb, nullptr));
+    TRY(download_padded(mem, dq, rows, d, dp, dQ));
+    TRY(download_padded(mem, dk, rows, d, dp, dK));
+    TRY(download_padded(mem, dv, rows, d, dp, dV));
+    return herr(hipDeviceSynchronize());
+}
+
+double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal) {
+    if (!shim_args_ok(BH, S, d) || iters <= 0) return (double)GONN_E_INVALID;
+    if (!gonn_hip_available()) return (double)GONN_E_NODEVICE;
+    DevMem mem;
+    const int dp = pad_dim(d);
+    const size_t n = (size_t)BH * S * dp;
+    float *q, *k, *v, *o;
+    if (mem.alloc((void**)&q, n * 4) || mem.alloc((void**)&k, n * 4) ||
+        mem.alloc((void**)&v, n * 4) || mem.alloc((void**)&o, n * 4))
+        return (double)GONN_E_NOMEM;
+    if (gonn::launch_fill_zero(q, n * 4, nullptr) || gonn::launch_fill_zero(k, n * 4, nullptr) ||
+        gonn::launch_fill_zero(v, n * 4, nullptr))
+        return -1.0;
+    const double scale = 1.0 / std::sqrt((double)d);
+    gonn_attn_fwd_args a{};
+    a.q = {q, n * 4, GONN_F32};
+    a.k = {k, n * 4, GONN_F32};
+    a.v = {v, n * 4, GONN_F32};
+    a.o = {o, n * 4, GONN_F32};
+    a.B = BH;
+    a.H = 1;
+    a.Sq = a.Sk = S;
+    a.D = dp;
+    a.scale = scale;
+    a.causal = causal;
+    a.mode = current_mode();
+    const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_FWD, &a);
+    void* ws = nullptr;
+    if (wsb && mem.alloc(&ws, wsb)) return (double)GONN_E_NOMEM;
+    for (int i = 0; i < 5; i++)
+        if (gonn_hip_attn_fwd(&a, ws, wsb, nullptr)) return -1.0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1.0;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
+    (void)hipEventRecord(e0, nullptr);
+    for (int i = 0; i < iters; i++) (void)gonn_hip_attn_fwd(&a, ws, wsb, nullptr);
+    (void)hipEventRecord(e1, nullptr);
+    (void)hipEventSynchronize(e1);
+    float ms = 0.f;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return (double)ms / iters;
+}
+
+int gonn_hip_selftest_mfma(void) {
+    if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    return gonn::selftest_mfma();
+}
+
+}  // extern "C"

@@ -1,0 +1,161 @@
+// attn_decode.hip -- split-KV decode over a bf16 KV cache, plus the combine.
+//
+// New relative to the reference (GoNN has no KV cache); the result is pinned
+// to MultiHeadAttention.ForwardMasked with a key-padding mask
+// (nn/attention.go:305-341, :261-272): query 1 x D per (b,h), keys
+// 0..kv_len[b]-1 of the cache, no causal mask. A padded key gets weight
+// exactly 0 in the reference, so it is never read here.
+//
+// One query row per (b,h) makes this a pair of GEMVs; the bound is HBM
+// bandwidth over the valid K/V rows, so the kernel is built for streaming:
+//  * split kernel: grid (nsplit, B*H); workgroup s of (b,h) owns keys
+//    [s*split_keys, min((s+1)*split_keys, len)) and exits at once when that
+//    range is empty, so only valid rows are ever fetched;
+//  * a row of 16 lanes covers one key (D=128: 8 bf16 = 16 bytes per lane), so
+//    one wave instruction reads 4 whole consecutive rows (1 KB contiguous);
+//    each lane keeps 8 keys' K and V loads in flight per iteration;
+//  * q.k is reduced across the 16 lanes of a row with DPP row_ror adds;
+//  * each lane row runs its own online softmax in log2 units (scale*log2e is
+//    folded into q); the 16 lane rows of a workgroup merge through LDS and
+//    write one partial (m, l, o[D]) per split;
+//  * combine kernel: per (b,h), O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s.
+#include "common.h"
+#include "kernels.h"
+
+namespace gonn {
+
+template <int D, typename QT>
+__global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
+    constexpr int EPL = D / 16;  // elements per lane
+    constexpr int U = 8;         // keys per lane row per iteration
+    constexpr int NROWS = 16;    // lane rows per workgroup
+    __shared__ float pm[NROWS], pl[NROWS];
+    __shared__ float po[NROWS][D];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rr = lane >> 4, dc = lane & 15, d0 = dc * EPL;
+    const int s = blockIdx.x, bh = blockIdx.y, b = bh / p.H;
+    int len = p.kv_len[b];
+    len = len < 0 ? 0 : (len > p.Lmax ? p.Lmax : len);
+    const int k0 = s * p.split_keys;
+    if (k0 >= len) return;  // uniform for the workgroup
+    const int k1 = (k0 + p.split_keys < len) ? k0 + p.split_keys : len;
+
+    float q[EPL];
+    {
+        const QT* qp = (const QT*)p.q + (size_t)bh * D + d0;
+        for (int e = 0; e < EPL; e++) {
+            float v;
+            if constexpr (sizeof(QT) == 4) v = qp[e];
+            else v = bf16_to_f32(*(const uint16_t*)(qp + e));
+            q[e] = v * p.scale_log2;
+        }
+    }
+    const bf16* Kb = (const bf16*)p.kc + (size_t)bh * p.Lmax * D + d0;
+    const bf16* Vb = (const bf16*)p.vc + (size_t)bh * p.Lmax * D + d0;
+
+    float m = -INFINITY, l = 0.f, o[EPL];
+    for (int e = 0; e < EPL; e++) o[e] = 0.f;
+
+    typedef uint16_t ld_t __attribute__((ext_vector_type(EPL)));
+    for (int base = k0 + wave * (4 * U); base < k1; base += 4 * 4 * U) {
+        ld_t kr[U], vr[U];
+        for (int u = 0; u < U; u++) {
+            const int key = base + u * 4 + rr;
+            if (key < k1) {
+                kr[u] = *(const ld_t*)(Kb + (size_t)key * D);
+                vr[u] = *(const ld_t*)(Vb + (size_t)key * D);
+            } else {
+                for (int e = 0; e < EPL; e++) { kr[u][e] = 0; vr[u][e] = 0; }
+            }
+        }
+        float sc[U];
+        float mb = -INFINITY;
+        for (int u = 0; u < U; u++) {
+            float a = 0.f;
+            for (int e = 0; e < EPL; e++) a = __builtin_fmaf(q[e], bf16_to_f32(kr[u][e]), a);
+            a = row_sum16(a);
+            const int key = base + u * 4 + rr;
+            sc[u] = key < k1 ? a : -INFINITY;
+            mb = fmaxf(mb, sc[u]);
+        }
+        const float mnew = fmaxf(m, mb);
+        if (mnew != -INFINITY) {
+            const float alpha = fast_exp2(m - mnew);  // 0 when m == -inf
+            float rs = 0.f;
+            for (int e = 0; e < EPL; e++) o[e] *= alpha;
+            for (int u = 0; u < U; u++) {
+                const float pu = fast_exp2(sc[u] - mnew);
+                rs += pu;
+                for (int e = 0; e < EPL; e++) o[e] = __builtin_fmaf(pu, bf16_to_f32(vr[u][e]), o[e]);
+            }
+            l = l * alpha + rs;
+            m = mnew;
+        }
+    }
+
+    const int row = wave * 4 + rr;
+    if (dc == 0) {
+        pm[row] = m;
+        pl[row] = l;
+    }
+    for (int e = 0; e < EPL; e++) po[row][d0 + e] = o[e];
+    __syncthreads();
+    if (tid < D) {
+        float M = -INFINITY;
+        for (int i = 0; i < NROWS; i++) M = fmaxf(M, pm[i]);
+        float L = 0.f, O = 0.f;
+        for (int i = 0; i < NROWS; i++) {
+            const float w = (pm[i] == -INFINITY) ? 0.f : fast_exp2(pm[i] - M);
+            L = __builtin_fmaf(w, pl[i], L);
+            O = __builtin_fmaf(w, po[i][tid], O);
+        }
+        const size_t part = (size_t)bh * p.nsplit + s;
+        p.part_o[part * D + tid] = O;
+        if (tid == 0) {
+            p.part_ml[part * 2 + 0] = M;
+            p.part_ml[part * 2 + 1] = L;
+        }
+    }
+}
+
+template <int D>
+__global__ __launch_bounds__(D) void decode_combine_kernel(DecodeParams p) {
+    const int bh = blockIdx.x, b = bh / p.H, tid = threadIdx.x;
+    int len = p.kv_len[b];
+    len = len < 0 ? 0 : (len > p.Lmax ? p.Lmax : len);
+    const int ns = (len + p.split_keys - 1) / p.split_keys;
+    const float* ml = p.part_ml + (size_t)bh * p.nsplit * 2;
+    const float* po = p.part_o + (size_t)bh * p.nsplit * D;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; s++) M = fmaxf(M, ml[2 * s]);
+    float L = 0.f, O = 0.f;
+    for (int s = 0; s < ns; s++) {
+        const float w = fast_exp2(ml[2 * s] - M);
+        L = __builtin_fmaf(w, ml[2 * s + 1], L);
+        O = __builtin_fmaf(w, po[(size_t)s * D + tid], O);
+    }
+    p.o[(size_t)bh * D + tid] = ns > 0 ? O / L : 0.f;
+}
+
+template <int D>
+static void launch_decode_d(const DecodeParams& p, int q_bf16, hipStream_t s) {
+    dim3 grid(p.nsplit, p.B * p.H);
+    if (q_bf16)
+        decode_split_kernel<D, bf16><<<grid, 256, 0, s>>>(p);
+    else
+        decode_split_kernel<D, float><<<grid, 256, 0, s>>>(p);
+    decode_combine_kernel<D><<<p.B * p.H, D, 0, s>>>(p);
+}
+
+hipError_t launch_decode(const DecodeParams& p, int D, int q_bf16, hipStream_t s) {
+    if (D == 128)
+        launch_decode_d<128>(p, q_bf16, s);
+    else if (D == 64)
+        launch_decode_d<64>(p, q_bf16, s);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+}  // namespace gonn

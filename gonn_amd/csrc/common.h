@@ -1,0 +1,94 @@
+// common.h -- shared device helpers for the gfx950 attention kernels.
+//
+// MFMA operand/result layouts used throughout (wave64, lane l, g = l / 32,
+// n = l % 32), for both v_mfma_f32_32x32x16_bf16 and v_mfma_f32_32x32x2_f32:
+//   A (32 x K):  lane l holds row m = n, k-slots of lane-group g
+//   B (K x 32):  lane l holds column n, the same k-slots of group g
+//   C (32 x 32): lane l holds column n; register r holds row
+//                8*(r/4) + 4*g + (r%4)
+// Only the C layout is relied upon; the assignment of k to (g, item) merely
+// has to be the same for A and B, which it is by construction.
+// gonn_hip_selftest_mfma() checks this layout on the device.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+#define GONN_DEV __device__ __forceinline__
+
+namespace gonn {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+GONN_DEV f32x16 mfma_bf16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+GONN_DEV f32x16 mfma_f32(float a, float b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (v_cvt_pk_bf16_f32 on gfx950).
+GONN_DEV bf16 to_bf16(float x) { return (bf16)x; }
+
+GONN_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+GONN_DEV bf16x8 pack8(float a0, float a1, float a2, float a3, float a4, float a5, float a6,
+                      float a7) {
+    bf16x8 r;
+    r[0] = to_bf16(a0); r[1] = to_bf16(a1); r[2] = to_bf16(a2); r[3] = to_bf16(a3);
+    r[4] = to_bf16(a4); r[5] = to_bf16(a5); r[6] = to_bf16(a6); r[7] = to_bf16(a7);
+    return r;
+}
+
+// 2^x on the transcendental unit (v_exp_f32).
+GONN_DEV float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// log2(x) (v_log_f32).
+GONN_DEV float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// Combine a value with the one held by the lane 32 positions away
+// (v_permlane32_swap). Both results of the swap are used, so the operation
+// is symmetric in the two halves of the wave.
+GONN_DEV float pair_max32(float x) {
+    const uint32_t u = __float_as_uint(x);
+    auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+GONN_DEV float pair_sum32(float x) {
+    const uint32_t u = __float_as_uint(x);
+    auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Rotate within each row of 16 lanes (DPP row_ror:n). n in 1..15.
+template <int N>
+GONN_DEV float row_ror(float x) {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x120 | N, 0xf, 0xf, false));
+}
+// Sum over each row of 16 lanes; every lane of the row receives the total.
+GONN_DEV float row_sum16(float x) {
+    x += row_ror<8>(x);
+    x += row_ror<4>(x);
+    x += row_ror<2>(x);
+    x += row_ror<1>(x);
+    return x;
+}
+
+// Key position inside a 16-key group of the transposed-V (Vt) layout. The
+// bf16 PV product reads, for lane-group g, keys {4g..4g+3, 8+4g..8+4g+3} as 8
+// consecutive elements, which is how the S^T accumulator holds P. The map is
+// its own inverse: it swaps the middle two quads.
+GONN_DEV int vt_pos(int o) {
+    return (o >= 4 && o < 8) ? o + 4 : ((o >= 8 && o < 12) ? o - 4 : o);
+}
+
+}  // namespace gonn

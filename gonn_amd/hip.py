@@ -1,0 +1,259 @@
+"""gonn_amd.hip -- host side of the HIP attention backend.
+
+Two layers, both over the C ABI (include/gonn_hip.h):
+
+1. The reference's backend/cuda attention entry points under their own names
+   and meaning (backend/cuda/cuda.go:125-194), on host fp64 arrays:
+       FlashAttnF64(Q, K, V, O, BH, S, d, scale, causal)            cuda.go:128-140
+       FlashAttnF64Fwd(Q, K, V, BH, S, d, scale, causal) -> (O, L)  cuda.go:144-160
+       FlashAttnF64Bwd(Q, K, V, O, L, dO, BH, S, d, scale, causal)  cuda.go:162-184
+       BenchFlashAttnF64(BH, S, d, iters, causal) -> ms             cuda.go:188-194
+   The reference returns nothing and ignores device errors; these raise
+   GonnHipError on any non-zero status.
+
+2. The device-resident API on torch device tensors (torch only supplies
+   device memory and the current HIP stream):
+       attn_fwd, attn_bwd, attn_decode
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import threading
+
+import numpy as np
+
+from . import _lib
+from ._lib import (GONN_ATTN_BF16_MFMA, GONN_ATTN_FP32_MFMA, GONN_BF16, GONN_F32, GONN_I32,
+                   GONN_OP_BWD, GONN_OP_DECODE, GONN_OP_FWD, Buf, BwdArgs, DecodeArgs, FwdArgs,
+                   GonnHipError, check)
+
+MODES = {"fp32": GONN_ATTN_FP32_MFMA, "bf16": GONN_ATTN_BF16_MFMA,
+         GONN_ATTN_FP32_MFMA: GONN_ATTN_FP32_MFMA, GONN_ATTN_BF16_MFMA: GONN_ATTN_BF16_MFMA}
+
+_dp = ctypes.POINTER(ctypes.c_double)
+
+
+# ---------------------------------------------------------------------------
+# library queries
+# ---------------------------------------------------------------------------
+def Available() -> bool:
+    """fusedAttnAvailable (nn/flashattn_cuda.go:13) as a runtime query."""
+    return bool(_lib.load().gonn_hip_available())
+
+
+def Supports(D: int, Sq: int, Sk: int) -> bool:
+    """Replaces the D == 64 && Tq == Tk gate of nn/attention.go:129."""
+    return bool(_lib.load().gonn_hip_attn_supports(int(D), int(Sq), int(Sk)))
+
+
+def SetAttnMode(mode) -> None:
+    check(_lib.load().gonn_hip_set_attn_mode(MODES[mode]), "SetAttnMode")
+
+
+def AttnMode() -> str:
+    return "bf16" if _lib.load().gonn_hip_get_attn_mode() == GONN_ATTN_BF16_MFMA else "fp32"
+
+
+def Version() -> str:
+    return _lib.load().gonn_hip_version().decode()
+
+
+def SelftestMFMA() -> int:
+    return int(_lib.load().gonn_hip_selftest_mfma())
+
+
+# ---------------------------------------------------------------------------
+# reference-named f64 entry points
+# ---------------------------------------------------------------------------
+def _f64(a, n, name):
+    a = np.ascontiguousarray(a, dtype=np.float64)
+    if a.size != n:
+        raise ValueError(f"{name}: expected {n} elements, got {a.size}")
+    return a
+
+
+def _p(a):
+    return a.ctypes.data_as(_dp)
+
+
+def FlashAttnF64(Q, K, V, O, BH: int, S: int, d: int, scale: float, causal: bool) -> None:
+    """Fused forward on host fp64 (BH,S,d) arrays; writes O in place."""
+    n = BH * S * d
+    Q, K, V = (_f64(x, n, "FlashAttnF64") for x in (Q, K, V))
+    if not (isinstance(O, np.ndarray) and O.dtype == np.float64 and O.flags.c_contiguous
+            and O.size == n):
+        raise ValueError("FlashAttnF64: O must be a contiguous float64 array of BH*S*d")
+    check(_lib.load().gonn_hip_flash_attn_f64(_p(Q), _p(K), _p(V), _p(O), BH, S, d,
+                                              float(scale), int(bool(causal))), "FlashAttnF64")
+
+
+def FlashAttnF64Fwd(Q, K, V, BH: int, S: int, d: int, scale: float, causal: bool):
+    """Training forward: returns (O, L) with L the per-row logsumexp (BH*S)."""
+    n = BH * S * d
+    Q, K, V = (_f64(x, n, "FlashAttnF64Fwd") for x in (Q, K, V))
+    O = np.zeros(n)
+    L = np.zeros(BH * S)
+    check(_lib.load().gonn_hip_flash_attn_f64_fwd(_p(Q), _p(K), _p(V), _p(O), _p(L), BH, S, d,
+                                                  float(scale), int(bool(causal))),
+          "FlashAttnF64Fwd")
+    return O, L
+
+
+def FlashAttnF64Bwd(Q, K, V, O, L, dO, BH: int, S: int, d: int, scale: float, causal: bool):
+    """Backward from the saved forward tensors: returns (dQ, dK, dV)."""
+    n = BH * S * d
+    Q, K, V, O, dO = (_f64(x, n, "FlashAttnF64Bwd") for x in (Q, K, V, O, dO))
+    L = _f64(L, BH * S, "FlashAttnF64Bwd")
+    dQ, dK, dV = np.zeros(n), np.zeros(n), np.zeros(n)
+    check(_lib.load().gonn_hip_flash_attn_f64_bwd(_p(Q), _p(K), _p(V), _p(O), _p(L), _p(dO),
+                                                  _p(dQ), _p(dK), _p(dV), BH, S, d,
+                                                  float(scale), int(bool(causal))),
+          "FlashAttnF64Bwd")
+    return dQ, dK, dV
+
+
+def BenchFlashAttnF64(BH: int, S: int, d: int, iters: int, causal: bool) -> float:
+    """Device-resident, event-timed forward; mean ms per launch."""
+    ms = float(_lib.load().gonn_hip_bench_flash_attn_f64(BH, S, d, iters, int(bool(causal))))
+    if ms < 0:
+        raise GonnHipError(int(ms), "BenchFlashAttnF64")
+    return ms
+
+
+# ---------------------------------------------------------------------------
+# device-resident API on torch tensors
+# ---------------------------------------------------------------------------
+def _torch():
+    import torch  # imported lazily: the f64 API above does not need torch
+    return torch
+
+
+def _dtype_code(t):
+    torch = _torch()
+    if t.dtype == torch.float32:
+        return GONN_F32
+    if t.dtype == torch.bfloat16:
+        return GONN_BF16
+    if t.dtype == torch.int32:
+        return GONN_I32
+    raise TypeError(f"unsupported tensor dtype {t.dtype}")
+
+
+def buf(t) -> Buf:
+    if t is None:
+        return Buf(None, 0, GONN_F32)
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError("device API needs contiguous device tensors")
+    return Buf(t.data_ptr(), t.numel() * t.element_size(), _dtype_code(t))
+
+
+def _stream(stream):
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return ctypes.c_void_p(stream.cuda_stream)
+
+
+class _Workspace:
+    """Grow-only device workspace per (device, stream). Each call uses it in
+    stream order, so reuse across calls on one stream is safe."""
+
+    def __init__(self):
+        self._bufs = {}
+        self._mu = threading.Lock()
+
+    def get(self, nbytes: int, device, stream):
+        if nbytes == 0:
+            return None
+        torch = _torch()
+        key = (str(device), stream.value)
+        with self._mu:
+            t = self._bufs.get(key)
+            if t is None or t.numel() < nbytes:
+                t = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+                self._bufs[key] = t
+            return t
+
+
+_WS = _Workspace()
+
+
+def _shape4(t, name):
+    if t.dim() == 4:
+        return t.shape[0], t.shape[1], t.shape[2], t.shape[3]
+    if t.dim() == 3:
+        return t.shape[0], 1, t.shape[1], t.shape[2]
+    raise ValueError(f"{name}: expected (B,H,S,D) or (BH,S,D), got {tuple(t.shape)}")
+
+
+def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None,
+             lse=True, stream=None):
+    """O = softmax(scale QK^T + mask) V on device tensors.
+
+    q (B,H,Sq,D) or (BH,Sq,D); k, v (.., Sk, D). fp32 mode needs float32
+    inputs; bf16 mode takes float32 or bfloat16 inputs. Returns (O, LSE) with O
+    float32 like q and LSE float32 (B*H, Sq) in natural-log units (or None).
+    """
+    torch = _torch()
+    B, H, Sq, D = _shape4(q, "q")
+    Sk = k.shape[-2]
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    l = torch.empty((B * H, Sq), dtype=torch.float32, device=q.device) if lse else None
+    a = FwdArgs(buf(q), buf(k), buf(v), buf(out), buf(l), B, H, Sq, Sk, D, float(scale),
+                int(bool(causal)), MODES[mode])
+    lib = _lib.load()
+    st = _stream(stream)
+    nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_FWD, ctypes.byref(a))
+    ws = _WS.get(nb, q.device, st)
+    check(lib.gonn_hip_attn_fwd(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
+                                nb, st), "attn_fwd")
+    return out, l
+
+
+def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp32",
+             stream=None):
+    """dQ, dK, dV (float32) from the saved forward tensors (all float32)."""
+    torch = _torch()
+    B, H, S, D = _shape4(q, "q")
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    dq, dk, dv = (torch.empty(q.shape, dtype=torch.float32, device=q.device) for _ in range(3))
+    a = BwdArgs(buf(q), buf(k), buf(v), buf(o), buf(lse), buf(dO), buf(dq), buf(dk), buf(dv),
+                B, H, S, D, float(scale), int(bool(causal)), MODES[mode], 1)
+    lib = _lib.load()
+    st = _stream(stream)
+    nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
+    ws = _WS.get(nb, q.device, st)
+    check(lib.gonn_hip_attn_bwd(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
+                                nb, st), "attn_bwd")
+    return dq, dk, dv
+
+
+def attn_decode(q, kcache, vcache, kv_len, *, scale=None, split_keys: int = 0, out=None,
+                stream=None):
+    """Split-KV decode: q (B,H,D) float32/bfloat16, caches (B,H,Lmax,D) bfloat16,
+    kv_len int32 (B,) on the device. Returns o (B,H,D) float32."""
+    torch = _torch()
+    B, H, Lmax, D = kcache.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    if out is None:
+        out = torch.empty((B, H, D), dtype=torch.float32, device=q.device)
+    a = DecodeArgs(buf(q), buf(kcache), buf(vcache), buf(kv_len), buf(out), B, H, Lmax, D,
+                   float(scale), int(split_keys))
+    lib = _lib.load()
+    st = _stream(stream)
+    nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_DECODE, ctypes.byref(a))
+    ws = _WS.get(nb, q.device, st)
+    check(lib.gonn_hip_attn_decode(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
+                                   nb, st), "attn_decode")
+    return out
+
+
+__all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
+           "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "BenchFlashAttnF64",
+           "attn_fwd", "attn_bwd", "attn_decode", "buf", "GonnHipError"]

@@ -1,0 +1,142 @@
+"""gonn_amd.nn -- the nn-level attention seam on the HIP backend.
+
+Mirrors GoNN's build-tagged seam nn/flashattn_cuda.go (what a Go maintainer
+adds as nn/flashattn_hip.go) and the fused branch of
+MultiHeadAttention.Forward / ForwardFused (nn/attention.go:107-180):
+
+    fused_attn_available()                         nn/flashattn_cuda.go:13
+    fused_attn_supports(D, Tq, Tk)                 gate of nn/attention.go:129
+    fused_attn_f64(Q, K, V, BH, S, D, scale, c)    nn/flashattn_cuda.go:17-21
+    fused_attn_diff(qp, kp, vp, BH, S, D, scale, c)nn/flashattn_cuda.go:26-38
+    MultiHeadAttention.forward / forward_fused     nn/attention.go:107-148, :159-180
+
+Tensors are host float64 arrays as in GoNN (tensor/tensor.go:22-23); the
+projections and the output projection run on the host in fp64 exactly like
+the reference's fused path (nn/attention.go:115-117, :132), and the core runs
+in the HIP kernels. There is no CPU fallback for the core: when the HIP
+library or device is missing, these functions raise, like the reference's
+non-cuda stubs panic (nn/flashattn_nocuda.go:12-20).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import hip
+
+
+def fused_attn_available() -> bool:
+    return hip.Available()
+
+
+def fused_attn_supports(D: int, Tq: int, Tk: int) -> bool:
+    return hip.Supports(D, Tq, Tk)
+
+
+def fused_attn_f64(Q, K, V, BH: int, S: int, D: int, scale: float, causal: bool) -> np.ndarray:
+    """Inference forward of the core on flat (BH,S,D) float64 data."""
+    O = np.zeros(BH * S * D)
+    hip.FlashAttnF64(Q, K, V, O, BH, S, D, scale, causal)
+    return O
+
+
+class FusedAttnNode:
+    """The autograd node fusedAttnDiff attaches (MakeNode "FlashAttn",
+    nn/flashattn_cuda.go:29-37): holds what the backward needs and runs the
+    device backward when called with the upstream gradient."""
+
+    def __init__(self, Q, K, V, O, L, BH, S, D, scale, causal):
+        self.saved = (Q, K, V, O, L)
+        self.shape = (BH, S, D)
+        self.scale = scale
+        self.causal = causal
+
+    def __call__(self, grad):
+        Q, K, V, O, L = self.saved
+        BH, S, D = self.shape
+        return hip.FlashAttnF64Bwd(Q, K, V, O, L, grad, BH, S, D, self.scale, self.causal)
+
+
+def fused_attn_diff(qp, kp, vp, BH: int, S: int, D: int, scale: float, causal: bool):
+    """Differentiable core: returns (O, node) where node(dO) -> (dQ, dK, dV)."""
+    O, L = hip.FlashAttnF64Fwd(qp, kp, vp, BH, S, D, scale, causal)
+    return O, FusedAttnNode(np.ascontiguousarray(qp, dtype=np.float64).ravel(),
+                            np.ascontiguousarray(kp, dtype=np.float64).ravel(),
+                            np.ascontiguousarray(vp, dtype=np.float64).ravel(), O, L, BH, S, D,
+                            scale, causal)
+
+
+class Linear:
+    """y = x @ W^T + b (nn/linear.go:40-59); W is (out, in)."""
+
+    def __init__(self, W, b=None):
+        self.W = np.asarray(W, dtype=np.float64)
+        self.b = None if b is None else np.asarray(b, dtype=np.float64)
+
+    def forward(self, x):
+        y = x.reshape(-1, x.shape[-1]) @ self.W.T
+        if self.b is not None:
+            y = y + self.b
+        return y.reshape(*x.shape[:-1], self.W.shape[0])
+
+
+class MultiHeadAttention:
+    """Forward-path mirror of nn.MultiHeadAttention with the fused core.
+
+    Weights are given explicitly (GoNN draws them from its global math/rand
+    stream, nn/linear.go:20-36, which only Go can reproduce).
+    """
+
+    def __init__(self, embed_dim: int, num_heads: int, Wq, bq, Wk, bk, Wv, bv, Wo, bo):
+        if embed_dim % num_heads != 0:
+            raise ValueError("MultiHeadAttention: embedDim must be divisible by numHeads")
+        self.EmbedDim = embed_dim
+        self.NumHeads = num_heads
+        self.HeadDim = embed_dim // num_heads
+        self.QProj, self.KProj = Linear(Wq, bq), Linear(Wk, bk)
+        self.VProj, self.OutProj = Linear(Wv, bv), Linear(Wo, bo)
+
+    def _check(self, q, k, v):
+        # checkQKVDims, nn/attention.go:83-103
+        E = self.EmbedDim
+        if q.ndim != 3 or q.shape[2] != E:
+            raise ValueError(f"MultiHeadAttention: q shape {q.shape}, want (B, Tq, {E})")
+        if k.ndim != 3 or k.shape[2] != self.KProj.W.shape[1]:
+            raise ValueError(f"MultiHeadAttention: k shape {k.shape}")
+        if v.ndim != 3 or v.shape[2] != self.VProj.W.shape[1]:
+            raise ValueError(f"MultiHeadAttention: v shape {v.shape}")
+        if k.shape[1] != v.shape[1]:
+            raise ValueError("MultiHeadAttention: k and v sequence lengths differ")
+
+    def _split(self, x):
+        B, T, _ = x.shape
+        H, D = self.NumHeads, self.HeadDim
+        return np.ascontiguousarray(x.reshape(B, T, H, D).transpose(0, 2, 1, 3))
+
+    def forward_fused(self, q, k, v, causal: bool):
+        """ForwardFused: projections, fused core, output projection."""
+        q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+        self._check(q, k, v)
+        B, Tq, _ = q.shape
+        Tk = k.shape[1]
+        H, D = self.NumHeads, self.HeadDim
+        if not fused_attn_available():
+            raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
+        if Tq != Tk:
+            raise ValueError("nn: the fused core needs Tq == Tk (flash-attention seam contract)")
+        qp = self._split(self.QProj.forward(q))
+        kp = self._split(self.KProj.forward(k))
+        vp = self._split(self.VProj.forward(v))
+        scale = 1.0 / math.sqrt(D)
+        O = fused_attn_f64(qp, kp, vp, B * H, Tq, D, scale, causal)
+        ctx = O.reshape(B, H, Tq, D).transpose(0, 2, 1, 3).reshape(B, Tq, self.EmbedDim)
+        return self.OutProj.forward(ctx)
+
+    forward = forward_fused
+
+
+def attn_decode(q, kcache, vcache, kv_len, scale=None, split_keys: int = 0):
+    """KV-cache decode on device tensors: ForwardMasked with a key-padding mask
+    pad[b][t] = (t >= kv_len[b]) on the post-projection core."""
+    return hip.attn_decode(q, kcache, vcache, kv_len, scale=scale, split_keys=split_keys)

@@ -1,0 +1,209 @@
+/*
+ * gonn_hip.h -- C ABI of the MI355X (gfx950) attention core for GoNN.
+ *
+ * This library replaces the fused flash-attention seam of GoNN
+ * (nn/flashattn_cuda.go -> backend/cuda/cuda.go -> backend/cuda/gonn_cuda.cu).
+ * Every entry point is plain C: scalar arguments, raw pointers and sizes.
+ * Nothing here needs HIP or PyTorch headers; a hipStream_t is passed as an
+ * opaque pointer (NULL = the legacy default stream).
+ *
+ * Layouts (all dense row-major, exactly the reference's layout after the head
+ * split at nn/attention.go:120-122 and nn/attention.go:170-176):
+ *   Q        (B*H, Sq, D)          K, V   (B*H, Sk, D)
+ *   O        (B*H, Sq, D) fp32     LSE    (B*H, Sq) fp32, natural-log units:
+ *            LSE[i] = max_j s_ij + ln(sum_j exp(s_ij - max_j s_ij)) with
+ *            s_ij = scale * q_i . k_j over the unmasked keys, the quantity
+ *            the reference kernel stores as L = m + log(l)
+ *            (backend/cuda/gonn_cuda.cu:330 and :448).
+ *   decode   q (B, H, D), cache (B, H, Lmax, D) bf16, o (B, H, D) fp32.
+ *
+ * Masking semantics follow the reference CPU path bit-for-bit in which keys
+ * carry weight:
+ *   causal   key j is masked for query i when j > i, top-left aligned even
+ *            when Sq != Sk (causalMaskAdd, nn/attention.go:185-196);
+ *   kv_len   keys t >= kv_len[b] are masked for every head and query
+ *            (keyPaddingMaskAdd, nn/attention.go:261-272). A -1e30 additive
+ *            mask gives an exactly-zero weight in fp64, so skipping the key
+ *            is the same result. The kernels never read a key >= kv_len[b].
+ *
+ * Return values: 0 on success; a negative GONN_E_* code for argument and
+ * library errors (checked on the host before any GPU work is queued); a
+ * positive value is a hipError_t from the runtime.
+ *
+ * Threading: every call is reentrant. Entry points that take a workspace keep
+ * no hidden global state; calls on the same stream are ordered, calls on
+ * different streams may run concurrently as long as their buffers do not
+ * alias. The f64 compatibility shims allocate per call, like the reference.
+ */
+#ifndef GONN_HIP_H
+#define GONN_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- error codes ------------------------------------------------------- */
+enum {
+    GONN_OK = 0,
+    GONN_E_INVALID = -1,     /* bad shape, null pointer, short buffer, bad enum  */
+    GONN_E_UNSUPPORTED = -2, /* valid request the kernels do not cover (e.g. D) */
+    GONN_E_WORKSPACE = -3,   /* workspace missing or smaller than required      */
+    GONN_E_NOMEM = -4,       /* device allocation failed                        */
+    GONN_E_NODEVICE = -5,    /* no usable gfx950 device                         */
+    GONN_E_INJECTED = -6     /* failure forced by GONN_HIP_FAIL_ALLOC=1         */
+};
+
+/* ---- element types and arithmetic modes --------------------------------- */
+typedef enum { GONN_F32 = 0, GONN_BF16 = 1, GONN_F64 = 2, GONN_I32 = 3 } gonn_dtype;
+
+/* The two dense contractions (QK^T and PV, and the five backward products)
+ * run on MFMA in one of two modes. Accumulation is fp32 in both.           */
+typedef enum {
+    GONN_ATTN_FP32_MFMA = 0, /* fp32 operands (v_mfma_f32_32x32x2_f32)        */
+    GONN_ATTN_BF16_MFMA = 1  /* bf16 operands (v_mfma_f32_32x32x16_bf16)      */
+} gonn_attn_mode;
+
+/* A device buffer handle: a device pointer, its size in bytes and the type
+ * of its elements. The library checks `bytes` against the shape it needs.  */
+typedef struct {
+    void* ptr;
+    size_t bytes;
+    int dtype; /* gonn_dtype */
+} gonn_buf;
+
+/* Forward: O = softmax(scale * Q K^T + mask) V, plus LSE.
+ * q, k, v: GONN_F32 or GONN_BF16. o: GONN_F32. lse: GONN_F32 or ptr NULL. */
+typedef struct {
+    gonn_buf q, k, v, o, lse;
+    int B, H, Sq, Sk, D;
+    double scale;
+    int causal;
+    int mode; /* gonn_attn_mode */
+} gonn_attn_fwd_args;
+
+/* Backward from the saved forward tensors: dQ, dK, dV (all GONN_F32).
+ * q, k, v, o, dO: GONN_F32; lse: GONN_F32 from gonn_hip_attn_fwd.
+ * Sq == Sk is required (the reference backward's contract).
+ * deterministic: accepted for API completeness; every mode of this library
+ * is deterministic (no floating-point atomics), so 0 and 1 give
+ * bit-identical results.                                                   */
+typedef struct {
+    gonn_buf q, k, v, o, lse, dO, dq, dk, dv;
+    int B, H, S, D;
+    double scale;
+    int causal;
+    int mode;
+    int deterministic;
+} gonn_attn_bwd_args;
+
+/* KV-cache decode, one query per (b, h): o[b,h] = attention of q[b,h] over
+ * the first kv_len[b] rows of kcache[b,h] / vcache[b,h], non-causal.
+ * q: GONN_F32 or GONN_BF16 (B,H,D); kcache, vcache: GONN_BF16 (B,H,Lmax,D);
+ * kv_len: GONN_I32 device array [B], values clamped to [0, Lmax];
+ * o: GONN_F32 (B,H,D). A sequence with kv_len 0 gets o = 0.
+ * split_keys: keys per split-KV work item (multiple of 64, 0 = automatic). */
+typedef struct {
+    gonn_buf q, kcache, vcache, kv_len, o;
+    int B, H, Lmax, D;
+    double scale;
+    int split_keys;
+} gonn_attn_decode_args;
+
+enum { GONN_OP_FWD = 0, GONN_OP_BWD = 1, GONN_OP_DECODE = 2 };
+
+/* ---- library ----------------------------------------------------------- */
+
+/* Version string of the library build. */
+const char* gonn_hip_version(void);
+
+/* Human-readable text for a return code (GONN_E_* or hipError_t). */
+const char* gonn_hip_strerror(int code);
+
+/* 1 when a gfx950 device is present and usable, else 0. Replaces
+ * fusedAttnAvailable (nn/flashattn_cuda.go:13) as a runtime query.        */
+int gonn_hip_available(void);
+
+/* 1 when the fused kernels cover head dim D with Sq x Sk, else 0. The
+ * reference hard-codes D == 64 && Tq == Tk at nn/attention.go:129 and :165;
+ * this predicate replaces that gate.                                       */
+int gonn_hip_attn_supports(int D, int Sq, int Sk);
+
+/* Default arithmetic mode used by the f64 compatibility shims. Initialised
+ * from the environment variable GONN_HIP_ATTN_MODE ("fp32" or "bf16"),
+ * default fp32-MFMA. Returns GONN_E_INVALID for an unknown mode.          */
+int gonn_hip_set_attn_mode(int mode);
+int gonn_hip_get_attn_mode(void);
+
+/* ---- device-resident API ---------------------------------------------- */
+
+/* Workspace bytes a call with these arguments needs (0 if none).
+ * op: GONN_OP_FWD / GONN_OP_BWD / GONN_OP_DECODE with the matching struct. */
+size_t gonn_hip_attn_workspace_bytes(int op, const void* args);
+
+/* Flash forward. Replaces gonn_flash_attn_f64_fwd
+ * (backend/cuda/gonn_cuda.h:67-69, gonn_cuda.cu:483-498) for device buffers.
+ * ws: device workspace of gonn_hip_attn_workspace_bytes(GONN_OP_FWD) bytes. */
+int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, void* stream);
+
+/* Flash backward. Replaces gonn_flash_attn_f64_bwd
+ * (backend/cuda/gonn_cuda.h:71-74, gonn_cuda.cu:501-529) for device buffers. */
+int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, void* stream);
+
+/* Split-KV decode plus combine. New: the reference has no KV cache; the
+ * semantics are ForwardMasked with WithKeyPaddingMask (nn/attention.go:305-341,
+ * :261-272) on the post-projection core with pad[b][t] = (t >= kv_len[b]).  */
+int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_bytes, void* stream);
+
+/* ---- device buffers ------------------------------------------------------
+ * Replace gonn_dev_alloc / gonn_dev_free / gonn_dev_upload / gonn_dev_download
+ * (backend/cuda/gonn_cuda.h:77-80) for the attention path. The f64 transfer
+ * helpers convert on the device (f64 <-> f32 or bf16, round to nearest even). */
+int gonn_hip_alloc(gonn_buf* b, size_t n_elems, int dtype);
+int gonn_hip_free(gonn_buf* b);
+int gonn_hip_upload_from_f64(gonn_buf* dst, const double* src, size_t n_elems, void* stream);
+int gonn_hip_download_to_f64(double* dst, const gonn_buf* src, size_t n_elems, void* stream);
+int gonn_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
+int gonn_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
+int gonn_hip_stream_sync(void* stream);
+
+/* ---- f64 host compatibility shims (reference signatures, synchronous) ----
+ * Same arguments and meaning as the reference entry points; they upload the
+ * host fp64 arrays, convert on the device, run the kernels in the current
+ * mode and download fp64 results. Any 1 <= d <= 128 is accepted: head dims
+ * other than 64/128 are zero-padded on the device, which leaves every score
+ * and every kept output column unchanged. Unlike the reference, which
+ * returns void and ignores CUDA errors, they return a status code.        */
+
+/* backend/cuda/gonn_cuda.h:60-61, gonn_cuda.cu:466-480 */
+int gonn_hip_flash_attn_f64(const double* Q, const double* K, const double* V,
+                            double* O, int BH, int S, int d, double scale, int causal);
+/* backend/cuda/gonn_cuda.h:67-69, gonn_cuda.cu:483-498 */
+int gonn_hip_flash_attn_f64_fwd(const double* Q, const double* K, const double* V,
+                                double* O, double* L, int BH, int S, int d,
+                                double scale, int causal);
+/* backend/cuda/gonn_cuda.h:71-74, gonn_cuda.cu:501-529 */
+int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* V,
+                                const double* O, const double* L, const double* dO,
+                                double* dQ, double* dK, double* dV,
+                                int BH, int S, int d, double scale, int causal);
+/* backend/cuda/gonn_cuda.h:63, gonn_cuda.cu:532-560: device-resident,
+ * event-timed forward; returns mean ms per launch, or a negative value on
+ * error. Inputs are zero-filled like the reference's benchmark.           */
+double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal);
+
+/* ---- diagnostics ---------------------------------------------------------- */
+
+/* Runs one v_mfma_f32_32x32x16_bf16 and one v_mfma_f32_32x32x2_f32 on known
+ * inputs and compares every output element with a host matrix product; the
+ * kernels rely on that operand/result lane layout. Returns the number of
+ * mismatching elements (0 = layout as assumed) or a negative error.       */
+int gonn_hip_selftest_mfma(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GONN_HIP_H */
