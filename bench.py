@@ -1,0 +1,243 @@
+#!/usr/bin/env python3
+"""bench.py -- headline benchmark of the gfx950 attention core on one MI355X.
+
+Metric: "attn TFLOP/s (causal fwd S=4096 D=128) + decode HBM
+GB/s, 1 MI355X".
+
+  value      causal prefill forward, config C3: B=4 H=32 S=4096 D=128, fp32
+             Q/K/V in HBM, fp32 O and LSE out, bf16 MFMA with fp32 accumulate.
+             A step is one gonn_hip_attn_fwd call (pack kernel + attention
+             kernel). FLOP per step = 4*B*H*S^2*D*0.5 (the reference's
+             convention, benchmark/flashattn/main.go:138-142).
+  decode     config C4: B=64 H=32 D=128, bf16 cache of 8192 positions,
+             lengths ~ U[512, 8192]; bytes per step = valid K+V rows + q + o.
+  roofline   the dominant kernel of each workload, timed live with HIP events
+             recorded by the library on the stream the kernel runs on.
+  cpu_baseline  the fp64 oracle (a C restatement of GoNN's CPU attention op
+             sequence; GoNN's Go path cannot run here) on a bounded sample of
+             the same workload: whole (b,h) slices, scaled to TFLOP/s with
+             the same FLOP convention.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "attn TFLOP/s (causal fwd S=4096 D=128) + decode HBM GB/s, 1 MI355X"
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE and
+    WRITE_SIZE runs, scaled by a copy-kernel calibration); None if absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            t = json.load(f)
+        return t.get(kernel, {}).get("bytes_per_launch")
+    except (OSError, ValueError):
+        return None
+
+
+def bench_prefill(torch, hip, steps, warmup):
+    B, H, S, D = 4, 32, 4096, 128
+    flop = 4.0 * B * H * S * S * D * 0.5
+    g = torch.Generator(device="cuda")
+    g.manual_seed(3)
+    q = torch.randn((B * H, S, D), generator=g, device="cuda")
+    k = torch.randn((B * H, S, D), generator=g, device="cuda")
+    v = torch.randn((B * H, S, D), generator=g, device="cuda")
+    o = torch.empty_like(q)
+    run = lambda: hip.attn_fwd(q, k, v, causal=True, mode="bf16", out=o)  # noqa: E731
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_time(e1) / steps
+    # per-kernel pass (events recorded by the library around each stage)
+    hip.profile_reset()
+    hip.profile_enable(True)
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    hip.profile_enable(False)
+    kt, kn = hip.profile_read("fwd_bf16")
+    pt, pn = hip.profile_read("pack_kv")
+    hip.profile_reset()
+    return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, wall_s=wall,
+                kernel_ms=kt / max(kn, 1), pack_ms=pt / max(pn, 1), q=q, k=k, v=v)
+
+
+def bench_decode(torch, hip, steps, warmup):
+    import numpy as np
+    B, H, Lmax, D = 64, 32, 8192, 128
+    lens = np.random.default_rng(4).integers(512, Lmax + 1, B).astype(np.int32)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(44)
+    q = torch.randn((B, H, D), generator=g, device="cuda").to(torch.bfloat16)
+    kc = torch.randn((B, H, Lmax, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    vc = torch.randn((B, H, Lmax, D), generator=g, device="cuda", dtype=torch.bfloat16)
+    kl = torch.from_numpy(lens).cuda()
+    o = torch.empty((B, H, D), dtype=torch.float32, device="cuda")
+    nbytes = int(2 * H * D * 2 * int(lens.sum()) + B * H * D * 2 + B * H * D * 4)
+    run = lambda: hip.attn_decode(q, kc, vc, kl, out=o)  # noqa: E731
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    hip.profile_reset()
+    hip.profile_enable(True)
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    hip.profile_enable(False)
+    st, sn = hip.profile_read("decode_split")
+    ct, cn = hip.profile_read("decode_combine")
+    hip.profile_reset()
+    del kc, vc
+    return dict(B=B, H=H, Lmax=Lmax, D=D, mean_len=float(lens.mean()), bytes=nbytes, ms=ms,
+                split_ms=st / max(sn, 1), combine_ms=ct / max(cn, 1))
+
+
+def cpu_baseline(pre, seconds):
+    """Time the fp64 oracle on whole (b,h) slices of the prefill workload."""
+    import numpy as np
+    import oracle
+    S, D = pre["S"], pre["D"]
+    threads = oracle.get_threads()
+    q = pre["q"][:1].double().cpu().numpy()
+    k = pre["k"][:1].double().cpu().numpy()
+    v = pre["v"][:1].double().cpu().numpy()
+    t0 = time.perf_counter()
+    oracle.attn_fwd(q, k, v, causal=True)
+    t1 = time.perf_counter() - t0
+    n = max(1, min(int(seconds / max(t1, 1e-3)), pre["B"] * pre["H"]))
+    qs = pre["q"][:n].double().cpu().numpy()
+    ks = pre["k"][:n].double().cpu().numpy()
+    vs = pre["v"][:n].double().cpu().numpy()
+    t0 = time.perf_counter()
+    oracle.attn_fwd(qs, ks, vs, causal=True)
+    dt = time.perf_counter() - t0
+    flop = 4.0 * n * S * S * D * 0.5
+    return {"value": flop / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"{n} of {pre['B'] * pre['H']} (b,h) slices of C3 (S={S}, D={D}, causal), "
+                      f"fp64, materialised scores as in GoNN's CPU path; {dt:.1f} s on "
+                      f"{threads} threads of {cpu_model()} (nproc {os.cpu_count()}); "
+                      f"same FLOP convention as value",
+            "seconds": dt}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[1])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this attention core is measured on one GPU; --gpus {args.gpus} "
+              f"(WORLD_SIZE {world}) is not run. The (b,h) slices shard with no exchange; "
+              "see the sharding paragraph of the design notes.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from gonn_amd import hip
+    if not hip.Available():
+        print("bench.py: no gfx950 device visible to libgonn_hip.so", file=sys.stderr)
+        sys.exit(1)
+
+    log("[bench] prefill C3")
+    pre = bench_prefill(torch, hip, args.steps, args.warmup)
+    tflops = pre["flop"] / (pre["ms"] * 1e-3) / 1e12
+    ach = pre["flop"] / (pre["kernel_ms"] * 1e-3) / 1e12
+    line = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(pre["ms"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: seeded N(0,1) fp32 Q/K/V (torch cuda generator)",
+        "config": {"workload": "C3 causal prefill forward, fp32 in/out, bf16 MFMA",
+                   "B": pre["B"], "H": pre["H"], "S": pre["S"], "D": pre["D"], "causal": True,
+                   "flop_per_step": pre["flop"], "wall_s": round(pre["wall_s"], 4)},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
+                     "traffic": load_traffic("fwd_bf16"), "kernel": "fwd_bf16_kernel",
+                     "kernel_ms": round(pre["kernel_ms"], 5),
+                     "pack_kv_ms": round(pre["pack_ms"], 5)},
+    }
+    if not args.no_decode:
+        log("[bench] decode C4")
+        dec = bench_decode(torch, hip, args.steps, args.warmup)
+        gbs = dec["bytes"] / (dec["ms"] * 1e-3) / 1e9
+        kgbs = dec["bytes"] / (dec["split_ms"] * 1e-3) / 1e9
+        line["decode"] = {
+            "metric": "decode HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
+            "ms_per_step": round(dec["ms"], 5), "bytes_per_step": dec["bytes"],
+            "config": {"workload": "C4 split-KV decode, bf16 cache", "B": dec["B"],
+                       "H": dec["H"], "Lmax": dec["Lmax"], "D": dec["D"],
+                       "mean_len": dec["mean_len"]},
+            "roofline": {"bound": "hbm", "achieved": round(kgbs, 2), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(kgbs / PEAK_HBM_GBS, 4),
+                         "traffic": load_traffic("decode_split"),
+                         "kernel": "decode_split_kernel",
+                         "kernel_ms": round(dec["split_ms"], 5),
+                         "combine_ms": round(dec["combine_ms"], 5)},
+        }
+    if not args.no_cpu_baseline:
+        log("[bench] cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(pre, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -24,6 +24,37 @@ namespace {
 
 std::atomic<int> g_mode{-1};
 
+// ---- per-kernel event profiler (diagnostics) -----------------------------
+// When enabled, every kernel stage launched through this ABI is bracketed by
+// two HIP events recorded on the stream it runs on.
+struct ProfRec {
+    const char* name;
+    hipEvent_t a, b;
+};
+std::mutex g_prof_mu;
+std::atomic<bool> g_prof_on{false};
+std::vector<ProfRec> g_prof;
+
+struct ProfScope {
+    hipEvent_t a = nullptr, b = nullptr;
+    const char* name;
+    hipStream_t s;
+    ProfScope(const char* n, hipStream_t st) : name(n), s(st) {
+        if (!g_prof_on.load()) return;
+        if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
+            a = b = nullptr;
+            return;
+        }
+        (void)hipEventRecord(a, s);
+    }
+    ~ProfScope() {
+        if (!a) return;
+        (void)hipEventRecord(b, s);
+        std::lock_guard<std::mutex> lock(g_prof_mu);
+        g_prof.push_back({name, a, b});
+    }
+};
+
 int env_mode() {
     const char* e = std::getenv("GONN_HIP_ATTN_MODE");
     if (e && (std::strcmp(e, "bf16") == 0 || std::strcmp(e, "1") == 0)) return GONN_ATTN_BF16_MFMA;
@@ -321,8 +352,11 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
         const size_t half = (size_t)BH * Skp * a->D * sizeof(uint16_t);
         void* Kb = w;
         void* Vt = w + half;
-        TRYH(gonn::launch_pack_kv(a->k.ptr, a->v.ptr, a->k.dtype == GONN_BF16, Kb, Vt, BH, a->Sk,
-                                  Skp, a->D, s));
+        {
+            ProfScope ps("pack_kv", s);
+            TRYH(gonn::launch_pack_kv(a->k.ptr, a->v.ptr, a->k.dtype == GONN_BF16, Kb, Vt, BH,
+                                      a->Sk, Skp, a->D, s));
+        }
         p.k = Kb;
         p.v = Vt;
         p.Skp = Skp;
@@ -331,6 +365,7 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
         p.v = a->v.ptr;
         p.Skp = a->Sk;
     }
+    ProfScope ps(a->mode == GONN_ATTN_BF16_MFMA ? "fwd_bf16" : "fwd_f32", s);
     return herr(gonn::launch_fwd(p, a->mode, a->D, a->causal, a->q.dtype == GONN_BF16, s));
 }
 
@@ -377,7 +412,13 @@ int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_byt
     p.part_ml = w;
     p.part_o = w + round_up((size_t)a->B * a->H * p.nsplit * 2, 64);
     p.scale_log2 = (float)a->scale * gonn::kLog2e;
-    return herr(gonn::launch_decode(p, a->D, a->q.dtype == GONN_BF16, (hipStream_t)stream));
+    hipStream_t s = (hipStream_t)stream;
+    {
+        ProfScope ps("decode_split", s);
+        TRYH(gonn::launch_decode_split(p, a->D, a->q.dtype == GONN_BF16, s));
+    }
+    ProfScope ps("decode_combine", s);
+    return herr(gonn::launch_decode_combine(p, a->D, s));
 }
 
 int gonn_hip_alloc(gonn_buf* b, size_t n_elems, int dtype) {
@@ -589,6 +630,39 @@ double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return (double)ms / iters;
+}
+
+int gonn_hip_profile_enable(int on) {
+    g_prof_on.store(on != 0);
+    return GONN_OK;
+}
+
+int gonn_hip_profile_reset(void) {
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    for (auto& r : g_prof) {
+        (void)hipEventDestroy(r.a);
+        (void)hipEventDestroy(r.b);
+    }
+    g_prof.clear();
+    return GONN_OK;
+}
+
+int gonn_hip_profile_read(const char* kernel, double* total_ms, int* count) {
+    if (!kernel || !total_ms || !count) return GONN_E_INVALID;
+    std::lock_guard<std::mutex> lock(g_prof_mu);
+    double tot = 0.0;
+    int n = 0;
+    for (auto& r : g_prof) {
+        if (std::strcmp(r.name, kernel) != 0) continue;
+        TRYH(hipEventSynchronize(r.b));
+        float ms = 0.f;
+        TRYH(hipEventElapsedTime(&ms, r.a, r.b));
+        tot += ms;
+        n++;
+    }
+    *total_ms = tot;
+    *count = n;
+    return GONN_OK;
 }
 
 int gonn_hip_selftest_mfma(void) {

@@ -44,6 +44,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
     float q[EPL];
     {
         const QT* qp = (const QT*)p.q + (size_t)bh * D + d0;
+#pragma unroll
         for (int e = 0; e < EPL; e++) {
             float v;
             if constexpr (sizeof(QT) == 4) v = qp[e];
@@ -55,43 +56,48 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
     const bf16* Vb = (const bf16*)p.vc + (size_t)bh * p.Lmax * D + d0;
 
     float m = -INFINITY, l = 0.f, o[EPL];
+#pragma unroll
     for (int e = 0; e < EPL; e++) o[e] = 0.f;
 
     typedef uint16_t ld_t __attribute__((ext_vector_type(EPL)));
     for (int base = k0 + wave * (4 * U); base < k1; base += 4 * 4 * U) {
+        // Keys past k1 are clamped to k1-1 (a valid row) and masked below, so
+        // every load is in bounds and the loop body has no branches.
         ld_t kr[U], vr[U];
+#pragma unroll
         for (int u = 0; u < U; u++) {
-            const int key = base + u * 4 + rr;
-            if (key < k1) {
-                kr[u] = *(const ld_t*)(Kb + (size_t)key * D);
-                vr[u] = *(const ld_t*)(Vb + (size_t)key * D);
-            } else {
-                for (int e = 0; e < EPL; e++) { kr[u][e] = 0; vr[u][e] = 0; }
-            }
+            int key = base + u * 4 + rr;
+            key = key < k1 ? key : k1 - 1;
+            kr[u] = *(const ld_t*)(Kb + (size_t)key * D);
+            vr[u] = *(const ld_t*)(Vb + (size_t)key * D);
         }
         float sc[U];
         float mb = -INFINITY;
+#pragma unroll
         for (int u = 0; u < U; u++) {
             float a = 0.f;
+#pragma unroll
             for (int e = 0; e < EPL; e++) a = __builtin_fmaf(q[e], bf16_to_f32(kr[u][e]), a);
             a = row_sum16(a);
-            const int key = base + u * 4 + rr;
-            sc[u] = key < k1 ? a : -INFINITY;
+            sc[u] = (base + u * 4 + rr < k1) ? a : -INFINITY;
             mb = fmaxf(mb, sc[u]);
         }
         const float mnew = fmaxf(m, mb);
-        if (mnew != -INFINITY) {
-            const float alpha = fast_exp2(m - mnew);  // 0 when m == -inf
-            float rs = 0.f;
-            for (int e = 0; e < EPL; e++) o[e] *= alpha;
-            for (int u = 0; u < U; u++) {
-                const float pu = fast_exp2(sc[u] - mnew);
-                rs += pu;
-                for (int e = 0; e < EPL; e++) o[e] = __builtin_fmaf(pu, bf16_to_f32(vr[u][e]), o[e]);
-            }
-            l = l * alpha + rs;
-            m = mnew;
+        // A lane row that has seen no valid key keeps m = -inf and l = o = 0.
+        const float mref = (mnew == -INFINITY) ? 0.f : mnew;
+        const float alpha = fast_exp2(m - mref);
+        float rs = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[e] *= alpha;
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const float pu = fast_exp2(sc[u] - mref);
+            rs += pu;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[e] = __builtin_fmaf(pu, bf16_to_f32(vr[u][e]), o[e]);
         }
+        l = l * alpha + rs;
+        m = mnew;
     }
 
     const int row = wave * 4 + rr;
@@ -99,6 +105,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
         pm[row] = m;
         pl[row] = l;
     }
+#pragma unroll
     for (int e = 0; e < EPL; e++) po[row][d0 + e] = o[e];
     __syncthreads();
     if (tid < D) {
@@ -138,23 +145,24 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeParams p) {
     p.o[(size_t)bh * D + tid] = ns > 0 ? O / L : 0.f;
 }
 
-template <int D>
-static void launch_decode_d(const DecodeParams& p, int q_bf16, hipStream_t s) {
+hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStream_t s) {
     dim3 grid(p.nsplit, p.B * p.H);
-    if (q_bf16)
-        decode_split_kernel<D, bf16><<<grid, 256, 0, s>>>(p);
-    else
-        decode_split_kernel<D, float><<<grid, 256, 0, s>>>(p);
-    decode_combine_kernel<D><<<p.B * p.H, D, 0, s>>>(p);
+    if (D == 128) {
+        if (q_bf16) decode_split_kernel<128, bf16><<<grid, 256, 0, s>>>(p);
+        else decode_split_kernel<128, float><<<grid, 256, 0, s>>>(p);
+    } else if (D == 64) {
+        if (q_bf16) decode_split_kernel<64, bf16><<<grid, 256, 0, s>>>(p);
+        else decode_split_kernel<64, float><<<grid, 256, 0, s>>>(p);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
-hipError_t launch_decode(const DecodeParams& p, int D, int q_bf16, hipStream_t s) {
-    if (D == 128)
-        launch_decode_d<128>(p, q_bf16, s);
-    else if (D == 64)
-        launch_decode_d<64>(p, q_bf16, s);
-    else
-        return hipErrorInvalidValue;
+hipError_t launch_decode_combine(const DecodeParams& p, int D, hipStream_t s) {
+    if (D == 128) decode_combine_kernel<128><<<p.B * p.H, 128, 0, s>>>(p);
+    else if (D == 64) decode_combine_kernel<64><<<p.B * p.H, 64, 0, s>>>(p);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -54,7 +54,8 @@ hipError_t launch_pack_kv(const void* K, const void* V, int in_bf16, void* Kb, v
                           int Sk, int Skp, int D, hipStream_t s);
 hipError_t launch_fwd(const FwdParams& p, int mode, int D, int causal, int q_bf16,
                       hipStream_t s);
-hipError_t launch_decode(const DecodeParams& p, int D, int q_bf16, hipStream_t s);
+hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStream_t s);
+hipError_t launch_decode_combine(const DecodeParams& p, int D, hipStream_t s);
 hipError_t launch_bwd(const BwdParams& p, int mode, int D, int causal, const float* O,
                       void* ws, hipStream_t s);
 size_t bwd_workspace_bytes(int mode, int BH, int S, int D);

@@ -63,6 +63,23 @@ def SelftestMFMA() -> int:
     return int(_lib.load().gonn_hip_selftest_mfma())
 
 
+def profile_enable(on: bool) -> None:
+    check(_lib.load().gonn_hip_profile_enable(int(bool(on))), "profile_enable")
+
+
+def profile_reset() -> None:
+    check(_lib.load().gonn_hip_profile_reset(), "profile_reset")
+
+
+def profile_read(kernel: str):
+    """(total_ms, count) of one kernel stage recorded while profiling was on."""
+    tot = ctypes.c_double(0.0)
+    n = ctypes.c_int(0)
+    check(_lib.load().gonn_hip_profile_read(kernel.encode(), ctypes.byref(tot), ctypes.byref(n)),
+          "profile_read")
+    return tot.value, n.value
+
+
 # ---------------------------------------------------------------------------
 # reference-named f64 entry points
 # ---------------------------------------------------------------------------

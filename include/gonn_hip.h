@@ -196,6 +196,17 @@ double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal
 
 /* ---- diagnostics ---------------------------------------------------------- */
 
+/* Per-kernel event profiler. While enabled, every kernel stage this library
+ * launches ("pack_kv", "fwd_bf16", "fwd_f32", "decode_split",
+ * "decode_combine", "bwd_prep", "bwd_dkdv", "bwd_dq") is bracketed by two HIP
+ * events on its own stream. profile_read synchronises on the recorded events
+ * and returns the summed milliseconds and launch count of one stage. No
+ * reference counterpart: the reference times whole launches with CUDA events
+ * (backend/cuda/gonn_cuda.cu:548-559).                                    */
+int gonn_hip_profile_enable(int on);
+int gonn_hip_profile_reset(void);
+int gonn_hip_profile_read(const char* kernel, double* total_ms, int* count);
+
 /* Runs one v_mfma_f32_32x32x16_bf16 and one v_mfma_f32_32x32x2_f32 on known
  * inputs and compares every output element with a host matrix product; the
  * kernels rely on that operand/result lane layout. Returns the number of
