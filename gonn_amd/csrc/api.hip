@@ -176,6 +176,35 @@ int check_bwd(const gonn_attn_bwd_args* a) {
     return GONN_OK;
 }
 
+// Backward workspace: lse2 and delta (BH,Sp) f32, then in bf16 mode the
+// packed operands Qb, dOb, Kb, Vb (BH,Sp,D) and Qt, dOt, Kt (BH,D,Sp) bf16,
+// each region 256-byte aligned.
+struct BwdLayout {
+    size_t lse2, delta, packed[7], total;
+};
+
+BwdLayout bwd_layout(int mode, size_t BH, int S, int D) {
+    BwdLayout L{};
+    const size_t Sp = round_up((size_t)S, gonn::kBwdPad);
+    size_t off = 0;
+    L.lse2 = off;
+    off = round_up(off + BH * Sp * 4, 256);
+    L.delta = off;
+    off = round_up(off + BH * Sp * 4, 256);
+    if (mode == GONN_ATTN_BF16_MFMA) {
+        for (int i = 0; i < 7; i++) {
+            L.packed[i] = off;
+            off = round_up(off + BH * Sp * D * 2, 256);
+        }
+    }
+    L.total = off;
+    return L;
+}
+
+size_t bwd_ws(const gonn_attn_bwd_args* a) {
+    return bwd_layout(a->mode, (size_t)a->B * a->H, a->S, a->D).total + 256;
+}
+
 // ---- helpers for the host shims ----------------------------------------
 
 struct DevMem {
@@ -313,7 +342,7 @@ size_t gonn_hip_attn_workspace_bytes(int op, const void* args) {
         case GONN_OP_BWD: {
             const auto* a = (const gonn_attn_bwd_args*)args;
             if (a->B <= 0 || a->H <= 0 || a->S <= 0 || !head_dim_ok(a->D)) return 0;
-            return gonn::bwd_workspace_bytes(a->mode, a->B * a->H, a->S, a->D) + 256;
+            return bwd_ws(a);
         }
         case GONN_OP_DECODE: {
             const auto* a = (const gonn_attn_decode_args*)args;
@@ -354,8 +383,14 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
         void* Vt = w + half;
         {
             ProfScope ps("pack_kv", s);
-            TRYH(gonn::launch_pack_kv(a->k.ptr, a->v.ptr, a->k.dtype == GONN_BF16, Kb, Vt, BH,
-                                      a->Sk, Skp, a->D, s));
+            gonn::PackParams pp{};
+            pp.src[0] = a->k.ptr;
+            pp.row[0] = Kb;
+            pp.src[1] = a->v.ptr;
+            pp.tr[1] = Vt;
+            pp.S = a->Sk;
+            pp.Sp = Skp;
+            TRYH(gonn::launch_pack(pp, 2, a->k.dtype == GONN_BF16, BH, a->D, s));
         }
         p.k = Kb;
         p.v = Vt;
@@ -371,25 +406,77 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
 
 int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, void* stream) {
     TRY(check_bwd(a));
-    const size_t need = gonn_hip_attn_workspace_bytes(GONN_OP_BWD, a);
-    if (need && (!ws || ws_bytes < need)) return GONN_E_WORKSPACE;
+    const size_t need = bwd_ws(a);
+    if (!ws || ws_bytes < need) return GONN_E_WORKSPACE;
+    hipStream_t s = (hipStream_t)stream;
+    const int BH = a->B * a->H, S = a->S, D = a->D;
+    const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
+    const BwdLayout L = bwd_layout(a->mode, (size_t)BH, S, D);
+    uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
     gonn::BwdParams p{};
-    p.q = a->q.ptr;
-    p.k = a->k.ptr;
-    p.v = a->v.ptr;
-    p.dO = a->dO.ptr;
-    p.lse = (const float*)a->lse.ptr;
+    p.lse2 = (const float*)(w + L.lse2);
+    p.delta = (const float*)(w + L.delta);
     p.dq = (float*)a->dq.ptr;
     p.dk = (float*)a->dk.ptr;
     p.dv = (float*)a->dv.ptr;
-    p.BH = a->B * a->H;
-    p.S = a->S;
-    p.Sp = (int)round_up((size_t)a->S, 64);
+    p.BH = BH;
+    p.S = S;
+    p.Sp = Sp;
     p.scale = (float)a->scale;
-    p.scale_log2 = (float)a->scale * gonn::kLog2e;
-    void* w = (void*)round_up((size_t)ws, 256);
-    return herr(gonn::launch_bwd(p, a->mode, a->D, a->causal, (const float*)a->o.ptr, w,
-                                 (hipStream_t)stream));
+    p.scale_log2 = (float)(a->scale * (double)gonn::kLog2e);
+    {
+        ProfScope ps("bwd_prep", s);
+        TRYH(gonn::launch_bwd_prep((const float*)a->o.ptr, (const float*)a->dO.ptr,
+                                   (const float*)a->lse.ptr, (float*)(w + L.lse2),
+                                   (float*)(w + L.delta), BH, S, Sp, D, s));
+    }
+    if (a->mode == GONN_ATTN_BF16_MFMA) {
+        void* Qb = w + L.packed[0];
+        void* dOb = w + L.packed[1];
+        void* Kb = w + L.packed[2];
+        void* Vb = w + L.packed[3];
+        void* Qt = w + L.packed[4];
+        void* dOt = w + L.packed[5];
+        void* Kt = w + L.packed[6];
+        ProfScope ps("bwd_pack", s);
+        gonn::PackParams p1{};
+        p1.src[0] = a->q.ptr;
+        p1.row[0] = Qb;
+        p1.tr[0] = Qt;
+        p1.src[1] = a->dO.ptr;
+        p1.row[1] = dOb;
+        p1.tr[1] = dOt;
+        p1.S = S;
+        p1.Sp = Sp;
+        TRYH(gonn::launch_pack(p1, 2, 0, BH, D, s));
+        gonn::PackParams p2{};
+        p2.src[0] = a->k.ptr;
+        p2.row[0] = Kb;
+        p2.tr[0] = Kt;
+        p2.src[1] = a->v.ptr;
+        p2.row[1] = Vb;
+        p2.S = S;
+        p2.Sp = Sp;
+        TRYH(gonn::launch_pack(p2, 2, 0, BH, D, s));
+        p.q = Qb;
+        p.dO = dOb;
+        p.k = Kb;
+        p.v = Vb;
+        p.qt = Qt;
+        p.dot = dOt;
+        p.kt = Kt;
+    } else {
+        p.q = a->q.ptr;
+        p.dO = a->dO.ptr;
+        p.k = a->k.ptr;
+        p.v = a->v.ptr;
+    }
+    {
+        ProfScope ps("bwd_dkdv", s);
+        TRYH(gonn::launch_bwd_dkdv(p, a->mode, D, a->causal, s));
+    }
+    ProfScope ps("bwd_dq", s);
+    return herr(gonn::launch_bwd_dq(p, a->mode, D, a->causal, s));
 }
 
 int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_bytes, void* stream) {

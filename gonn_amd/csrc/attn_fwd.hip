@@ -21,90 +21,16 @@
 //    q-blocks sharing one head's K/V run on the same XCD's L2.
 //
 // Two arithmetic modes:
-//  bf16: v_mfma_f32_32x32x16_bf16. A pack kernel converts K to bf16 (BH,Skp,D)
-//        and V to a transposed bf16 layout Vt (BH,D,Skp) whose 16-key groups
-//        are permuted (vt_pos) so each lane's PV operand is one 16-byte read.
-//        Skp = Sk rounded up to 64; the pad is zero-filled and masked.
+//  bf16: v_mfma_f32_32x32x16_bf16. The pack kernel (attn_pack.hip) converts K
+//        to bf16 (BH,Skp,D) and V to a transposed bf16 layout Vt (BH,D,Skp)
+//        whose 16-key groups are permuted (vt_pos) so each lane's PV operand
+//        is one 16-byte read. Skp = Sk rounded up to 64; the pad is zero and
+//        masked.
 //  fp32: v_mfma_f32_32x32x2_f32 straight from the fp32 K/V (no pack).
 #include "common.h"
 #include "kernels.h"
 
 namespace gonn {
-
-// ---------------------------------------------------------------------------
-// Workgroup -> (bh, q-block) map.
-// ---------------------------------------------------------------------------
-GONN_DEV void map_block(int L, int nqb, int BH, bool causal, int& bh, int& qb) {
-    const int N = nqb * BH;
-    int idx = L;
-    if ((N & 7) == 0) {
-        const int per = N >> 3;
-        idx = (L & 7) * per + (L >> 3);
-    }
-    bh = idx / nqb;
-    const int r = idx - bh * nqb;
-    qb = causal ? (nqb - 1 - r) : r;
-}
-
-// ---------------------------------------------------------------------------
-// Pack: K -> Kb bf16 (BH,Skp,D); V -> Vt bf16 (BH,D,Skp), key-permuted.
-// grid (Skp/64, BH), 256 threads.
-// ---------------------------------------------------------------------------
-template <typename T, int D>
-__global__ __launch_bounds__(256) void pack_kv_kernel(const T* __restrict__ K,
-                                                      const T* __restrict__ V,
-                                                      bf16* __restrict__ Kb,
-                                                      bf16* __restrict__ Vt, int Sk, int Skp) {
-    constexpr int BN = 64;
-    constexpr int VS = D + 2;
-    __shared__ bf16 tile[BN * VS];
-    const int tid = threadIdx.x;
-    const int kt = blockIdx.x, bh = blockIdx.y;
-    const size_t src0 = ((size_t)bh * Sk) * D;
-    // K rows and the V tile: chunks of 8 elements along D.
-    constexpr int CH = BN * D / 8;
-    for (int c = tid; c < CH; c += 256) {
-        const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-        const int key = kt * BN + row;
-        float kv[8], vv[8];
-        if (key < Sk) {
-            const T* kp = K + src0 + (size_t)key * D + col;
-            const T* vp = V + src0 + (size_t)key * D + col;
-            if constexpr (sizeof(T) == 4) {
-                const f32x4 k0 = *(const f32x4*)kp, k1 = *(const f32x4*)(kp + 4);
-                const f32x4 v0 = *(const f32x4*)vp, v1 = *(const f32x4*)(vp + 4);
-                for (int i = 0; i < 4; i++) {
-                    kv[i] = k0[i]; kv[4 + i] = k1[i];
-                    vv[i] = v0[i]; vv[4 + i] = v1[i];
-                }
-            } else {
-                const u16x8 k8 = *(const u16x8*)kp, v8 = *(const u16x8*)vp;
-                for (int i = 0; i < 8; i++) {
-                    kv[i] = bf16_to_f32(k8[i]);
-                    vv[i] = bf16_to_f32(v8[i]);
-                }
-            }
-        } else {
-            for (int i = 0; i < 8; i++) kv[i] = vv[i] = 0.f;
-        }
-        *(bf16x8*)(Kb + ((size_t)bh * Skp + key) * D + col) =
-            pack8(kv[0], kv[1], kv[2], kv[3], kv[4], kv[5], kv[6], kv[7]);
-        for (int i = 0; i < 8; i++) tile[row * VS + col + i] = to_bf16(vv[i]);
-    }
-    __syncthreads();
-    // Vt rows: chunk c -> (d, 8 positions); positions map to keys by vt_pos.
-    constexpr int VC = D * BN / 8;
-    for (int c = tid; c < VC; c += 256) {
-        const int d = c / (BN / 8), j = c % (BN / 8);
-        const int grp = (j >> 1) * 16;
-        bf16x8 r;
-        for (int i = 0; i < 8; i++) {
-            const int pos = (j & 1) * 8 + i;
-            r[i] = tile[(grp + vt_pos(pos)) * VS + d];
-        }
-        *(bf16x8*)(Vt + ((size_t)bh * D + d) * Skp + kt * BN + j * 8) = r;
-    }
-}
 
 // ---------------------------------------------------------------------------
 // bf16-MFMA forward.
@@ -399,28 +325,6 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(FwdParams p) {
 // ---------------------------------------------------------------------------
 // Launchers.
 // ---------------------------------------------------------------------------
-template <typename T>
-static hipError_t launch_pack_t(const T* K, const T* V, bf16* Kb, bf16* Vt, int BH, int Sk,
-                                int Skp, int D, hipStream_t s) {
-    dim3 grid(Skp / 64, BH);
-    if (D == 64)
-        pack_kv_kernel<T, 64><<<grid, 256, 0, s>>>(K, V, Kb, Vt, Sk, Skp);
-    else if (D == 128)
-        pack_kv_kernel<T, 128><<<grid, 256, 0, s>>>(K, V, Kb, Vt, Sk, Skp);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
-}
-
-hipError_t launch_pack_kv(const void* K, const void* V, int in_bf16, void* Kb, void* Vt, int BH,
-                          int Sk, int Skp, int D, hipStream_t s) {
-    if (in_bf16)
-        return launch_pack_t<bf16>((const bf16*)K, (const bf16*)V, (bf16*)Kb, (bf16*)Vt, BH, Sk,
-                                   Skp, D, s);
-    return launch_pack_t<float>((const float*)K, (const float*)V, (bf16*)Kb, (bf16*)Vt, BH, Sk,
-                                Skp, D, s);
-}
-
 template <int D, bool C>
 static void launch_bf16_d(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t s) {
     if (q_bf16)

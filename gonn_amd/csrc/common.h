@@ -83,6 +83,24 @@ GONN_DEV float row_sum16(float x) {
     return x;
 }
 
+// Workgroup -> (bh, block) map for a grid of nblk blocks per (b,h) slice.
+// Workgroups are dealt round-robin to the 8 XCDs (L & 7), so XCD x receives a
+// contiguous range of slices in dispatch order: the blocks that share one
+// slice's K/V (or Q/dO) run on the same XCD and share its L2. Within a slice
+// the block order is reversed when `reverse` is set, which puts the longest
+// causal blocks first.
+GONN_DEV void map_block(int L, int nblk, int BH, bool reverse, int& bh, int& blk) {
+    const int N = nblk * BH;
+    int idx = L;
+    if ((N & 7) == 0) {
+        const int per = N >> 3;
+        idx = (L & 7) * per + (L >> 3);
+    }
+    bh = idx / nblk;
+    const int r = idx - bh * nblk;
+    blk = reverse ? (nblk - 1 - r) : r;
+}
+
 // Key position inside a 16-key group of the transposed-V (Vt) layout. The
 // bf16 PV product reads, for lane-group g, keys {4g..4g+3, 8+4g..8+4g+3} as 8
 // consecutive elements, which is how the S^T accumulator holds P. The map is

@@ -30,19 +30,30 @@ struct DecodeParams {
     float scale_log2;  // scale * log2(e) (any sign)
 };
 
+// Up to two sources packed by one launch (attn_pack.hip): src[i] (BH,S,D)
+// f32 or bf16 -> row[i] (BH,Sp,D) bf16 and/or tr[i] (BH,D,Sp) bf16
+// (transposed, 16-groups permuted by vt_pos). Null outputs are skipped.
+struct PackParams {
+    const void* src[2];
+    void* row[2];
+    void* tr[2];
+    int S, Sp;
+};
+
 struct BwdParams {
-    // bf16 mode operands live in the workspace (see api.hip); fp32 mode uses
-    // the caller's buffers directly.
-    const void* q;    // Q   (BH,S,D)
-    const void* k;    // K   (BH,S,D)
-    const void* v;    // V   (BH,S,D)
-    const void* qt;   // Q^T (BH,D,Sp) key-permuted, bf16 mode only
-    const void* kt;   // K^T (BH,D,Sp) key-permuted, bf16 mode only
-    const void* dot;  // dO^T (BH,D,Sp) key-permuted, bf16 mode only
-    const void* dO;   // dO  (BH,S,D)
-    const float* lse; // (BH,S) natural log
-    const float* delta; // (BH,S) rowsum(dO * O)
-    float* dq;        // (BH,S,D)
+    // bf16 mode: packed operands in the workspace (row-major (BH,Sp,D) and
+    // transposed (BH,D,Sp)); fp32 mode: the caller's (BH,S,D) f32 buffers in
+    // q, k, v, dO and null transposes.
+    const void* q;
+    const void* k;
+    const void* v;
+    const void* dO;
+    const void* qt;   // Q^T  bf16 mode only
+    const void* kt;   // K^T  bf16 mode only
+    const void* dot;  // dO^T bf16 mode only
+    const float* lse2;   // (BH,Sp) LSE * log2(e); +inf on pad rows
+    const float* delta;  // (BH,Sp) rowsum(dO * O); 0 on pad rows
+    float* dq;           // (BH,S,D)
     float* dk;
     float* dv;
     int BH, S, Sp;
@@ -50,15 +61,19 @@ struct BwdParams {
     float scale_log2;  // scale * log2(e)
 };
 
-hipError_t launch_pack_kv(const void* K, const void* V, int in_bf16, void* Kb, void* Vt, int BH,
-                          int Sk, int Skp, int D, hipStream_t s);
+hipError_t launch_pack(const PackParams& p, int nsrc, int in_bf16, int BH, int D, hipStream_t s);
 hipError_t launch_fwd(const FwdParams& p, int mode, int D, int causal, int q_bf16,
                       hipStream_t s);
 hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStream_t s);
 hipError_t launch_decode_combine(const DecodeParams& p, int D, hipStream_t s);
-hipError_t launch_bwd(const BwdParams& p, int mode, int D, int causal, const float* O,
-                      void* ws, hipStream_t s);
-size_t bwd_workspace_bytes(int mode, int BH, int S, int D);
+// Backward stages: prep (lse2, delta), then dK/dV (one workgroup per key
+// block) and dQ (one workgroup per query block), both deterministic.
+hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, float* lse2,
+                           float* delta, int BH, int S, int Sp, int D, hipStream_t s);
+hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipStream_t s);
+hipError_t launch_bwd_dq(const BwdParams& p, int mode, int D, int causal, hipStream_t s);
+// Sequence padding of the backward's workspace layouts.
+constexpr int kBwdPad = 128;
 
 // f64 <-> f32/bf16 conversion with optional head-dim padding:
 // dst (rows, dpad) <- src (rows, d); pad columns are zero.

@@ -178,6 +178,25 @@ def test_bwd_argument_errors():
     assert lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, None) == 0
 
 
+def test_bwd_workspace_contract():
+    """fp32 mode needs LSE*log2(e) and D_i rows (BH, Sp) in f32; bf16 mode adds
+    seven packed bf16 operands (BH, Sp, D), with Sp = S rounded up to 128."""
+    lib = _lib.load()
+    B, H, S, D = 1, 2, 200, 128
+    n = B * H * S * D * 4
+    f = lambda: Buf(P, n, GONN_F32)  # noqa: E731
+    a = BwdArgs(f(), f(), f(), f(), Buf(P, B * H * S * 4, GONN_F32), f(), f(), f(), f(), B, H,
+                S, D, 0.125, 1, 0, 1)
+    Sp = 256
+    nb32 = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
+    assert nb32 >= 2 * B * H * Sp * 4
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), P, nb32 - 1, None) == GONN_E_WORKSPACE
+    a.mode = 1
+    nb16 = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
+    assert nb16 >= nb32 + 7 * B * H * Sp * D * 2
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), P, nb32, None) == GONN_E_WORKSPACE
+
+
 def test_no_device_fails_loudly():
     """Without a gfx950 device the reference-named entry points raise; there is
     no CPU fallback (like the reference's non-cuda stubs,
