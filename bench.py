@@ -36,6 +36,7 @@ if ROOT not in sys.path:
 
 METRIC = "attn TFLOP/s (causal fwd S=4096 D=128) + decode HBM GB/s, 1 MI355X"
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3   # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
@@ -139,6 +140,68 @@ def bench_decode(torch, hip, steps, warmup):
                 split_ms=st / max(sn, 1), combine_ms=ct / max(cn, 1))
 
 
+def _timed(torch, hip, run, steps, warmup, stages):
+    """Mean ms per step over `steps` launches bracketed by events on the current
+    stream, then a second pass with the library's per-stage event profiler;
+    returns (ms_per_step, {stage: mean ms per launch})."""
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    hip.profile_reset()
+    hip.profile_enable(True)
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    hip.profile_enable(False)
+    per = {}
+    for st in stages:
+        t, n = hip.profile_read(st)
+        per[st] = t / max(n, 1)
+    hip.profile_reset()
+    return ms, per
+
+
+def bench_fwd_bwd(torch, hip, steps, warmup):
+    """C5: causal flash forward + backward, B=2 H=16 S=8192 D=128, bf16 MFMA."""
+    B, H, S, D = 2, 16, 8192, 128
+    fwd_flop = 4.0 * B * H * S * S * D * 0.5
+    bwd_flop = 2.5 * fwd_flop
+    g = torch.Generator(device="cuda")
+    g.manual_seed(5)
+    q, k, v, do = (torch.randn((B * H, S, D), generator=g, device="cuda") for _ in range(4))
+    o, lse = hip.attn_fwd(q, k, v, causal=True, mode="bf16")
+    grads = tuple(torch.empty_like(q) for _ in range(3))
+
+    def run():
+        hip.attn_fwd(q, k, v, causal=True, mode="bf16", out=o, lse_out=lse)
+        hip.attn_bwd(q, k, v, o, lse, do, causal=True, mode="bf16", out=grads)
+    ms, per = _timed(torch, hip, run, steps, warmup,
+                     ("pack_kv", "fwd_bf16", "bwd_prep", "bwd_pack", "bwd_dkdv", "bwd_dq"))
+    return dict(B=B, H=H, S=S, D=D, fwd_flop=fwd_flop, bwd_flop=bwd_flop, ms=ms, per=per)
+
+
+def bench_encoder(torch, hip, steps, warmup, mode):
+    """C2: non-causal encoder attention, B=8 H=12 S=1024 D=64, fp32 in/out."""
+    B, H, S, D = 8, 12, 1024, 64
+    flop = 4.0 * B * H * S * S * D
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2)
+    q, k, v = (torch.randn((B * H, S, D), generator=g, device="cuda") for _ in range(3))
+    o = torch.empty_like(q)
+    run = lambda: hip.attn_fwd(q, k, v, causal=False, mode=mode, out=o)  # noqa: E731
+    kname = "fwd_bf16" if mode == "bf16" else "fwd_f32"
+    ms, per = _timed(torch, hip, run, steps, warmup, ("pack_kv", kname))
+    return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, kernel_ms=per[kname],
+                pack_ms=per["pack_kv"])
+
+
 def cpu_baseline(pre, seconds):
     """Time the fp64 oracle on whole (b,h) slices of the prefill workload."""
     import numpy as np
@@ -175,6 +238,13 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-bwd", action="store_true")
+    ap.add_argument("--no-encoder", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the headline leg (profiling runs of the other legs only)")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run one device copy of 1 GiB, the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -189,6 +259,27 @@ def main():
         print("bench.py: no gfx950 device visible to libgonn_hip.so", file=sys.stderr)
         sys.exit(1)
 
+    if args.copy_calib:
+        n = 1 << 28  # 2^28 floats = 1 GiB read + 1 GiB written
+        x = torch.ones(n, device="cuda")
+        y = torch.empty_like(x)
+        torch.cuda.synchronize()
+        y.copy_(x)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: {4 * n} bytes read, {4 * n} bytes written")
+        del x, y
+    if args.no_prefill:
+        if not args.no_decode:
+            log("[bench] decode C4")
+            bench_decode(torch, hip, args.steps, args.warmup)
+        if not args.no_bwd:
+            log("[bench] fwd+bwd C5")
+            bench_fwd_bwd(torch, hip, args.steps, args.warmup)
+        if not args.no_encoder:
+            for mode in ("bf16", "fp32"):
+                log(f"[bench] encoder C2 {mode}")
+                bench_encoder(torch, hip, args.steps, args.warmup, mode)
+        return
     log("[bench] prefill C3")
     pre = bench_prefill(torch, hip, args.steps, args.warmup)
     tflops = pre["flop"] / (pre["ms"] * 1e-3) / 1e12
@@ -233,6 +324,42 @@ def main():
                          "kernel_ms": round(dec["split_ms"], 5),
                          "combine_ms": round(dec["combine_ms"], 5)},
         }
+    if not args.no_bwd:
+        log("[bench] fwd+bwd C5")
+        fb = bench_fwd_bwd(torch, hip, max(args.steps // 5, 3), max(args.warmup // 2, 1))
+        per = fb["per"]
+        bwd_ms = sum(per[k] for k in ("bwd_prep", "bwd_pack", "bwd_dkdv", "bwd_dq"))
+        tot = fb["fwd_flop"] + fb["bwd_flop"]
+        line["fwd_bwd"] = {
+            "metric": "causal fwd+bwd TFLOP/s", "value": round(tot / (fb["ms"] * 1e-3) / 1e12, 3),
+            "unit": "TFLOP/s", "ms_per_step": round(fb["ms"], 4),
+            "config": {"workload": "C5 causal flash fwd+bwd, fp32 in/out, bf16 MFMA",
+                       "B": fb["B"], "H": fb["H"], "S": fb["S"], "D": fb["D"],
+                       "fwd_flop": fb["fwd_flop"], "bwd_flop": fb["bwd_flop"]},
+            "bwd_TFLOPs": round(fb["bwd_flop"] / (bwd_ms * 1e-3) / 1e12, 3),
+            "stage_ms": {k: round(v, 5) for k, v in per.items()},
+            "roofline": {"bound": "mfma", "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                         "kernel": "bwd_dkdv + bwd_dq",
+                         "achieved": round(fb["bwd_flop"] / ((per["bwd_dkdv"] + per["bwd_dq"])
+                                                             * 1e-3) / 1e12, 3),
+                         "frac": round(fb["bwd_flop"] / ((per["bwd_dkdv"] + per["bwd_dq"]) * 1e-3)
+                                       / 1e12 / PEAK_BF16_TFLOPS, 4)},
+        }
+    if not args.no_encoder:
+        line["encoder"] = {}
+        for mode, peak in (("bf16", PEAK_BF16_TFLOPS), ("fp32", PEAK_FP32_TFLOPS)):
+            log(f"[bench] encoder C2 {mode}")
+            en = bench_encoder(torch, hip, args.steps, args.warmup, mode)
+            ach = en["flop"] / (en["kernel_ms"] * 1e-3) / 1e12
+            line["encoder"][mode] = {
+                "value": round(en["flop"] / (en["ms"] * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
+                "ms_per_step": round(en["ms"], 5),
+                "config": {"workload": f"C2 encoder non-causal, fp32 in/out, {mode} MFMA",
+                           "B": en["B"], "H": en["H"], "S": en["S"], "D": en["D"]},
+                "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": peak,
+                             "unit": "TFLOP/s", "frac": round(ach / peak, 4),
+                             "kernel_ms": round(en["kernel_ms"], 5),
+                             "pack_kv_ms": round(en["pack_ms"], 5)}}
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
         line["cpu_baseline"] = cpu_baseline(pre, args.cpu_seconds)

@@ -205,12 +205,13 @@ def _shape4(t, name):
 
 
 def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None,
-             lse=True, stream=None):
+             lse=True, lse_out=None, stream=None):
     """O = softmax(scale QK^T + mask) V on device tensors.
 
     q (B,H,Sq,D) or (BH,Sq,D); k, v (.., Sk, D). fp32 mode needs float32
     inputs; bf16 mode takes float32 or bfloat16 inputs. Returns (O, LSE) with O
-    float32 like q and LSE float32 (B*H, Sq) in natural-log units (or None).
+    float32 like q and LSE float32 (B*H, Sq) in natural-log units (or None when
+    lse is False). out / lse_out may supply preallocated outputs.
     """
     torch = _torch()
     B, H, Sq, D = _shape4(q, "q")
@@ -219,7 +220,9 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
         scale = 1.0 / math.sqrt(D)
     if out is None:
         out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
-    l = torch.empty((B * H, Sq), dtype=torch.float32, device=q.device) if lse else None
+    l = lse_out
+    if l is None and lse:
+        l = torch.empty((B * H, Sq), dtype=torch.float32, device=q.device)
     a = FwdArgs(buf(q), buf(k), buf(v), buf(out), buf(l), B, H, Sq, Sk, D, float(scale),
                 int(bool(causal)), MODES[mode])
     lib = _lib.load()
@@ -232,13 +235,18 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
 
 
 def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp32",
-             stream=None):
-    """dQ, dK, dV (float32) from the saved forward tensors (all float32)."""
+             out=None, stream=None):
+    """dQ, dK, dV (float32) from the saved forward tensors (all float32).
+    out may supply preallocated (dq, dk, dv)."""
     torch = _torch()
     B, H, S, D = _shape4(q, "q")
     if scale is None:
         scale = 1.0 / math.sqrt(D)
-    dq, dk, dv = (torch.empty(q.shape, dtype=torch.float32, device=q.device) for _ in range(3))
+    if out is None:
+        dq, dk, dv = (torch.empty(q.shape, dtype=torch.float32, device=q.device)
+                      for _ in range(3))
+    else:
+        dq, dk, dv = out
     a = BwdArgs(buf(q), buf(k), buf(v), buf(o), buf(lse), buf(dO), buf(dq), buf(dk), buf(dv),
                 B, H, S, D, float(scale), int(bool(causal)), MODES[mode], 1)
     lib = _lib.load()
