@@ -10,31 +10,27 @@
 //        sequence axis against P, dS (or their transposes) taken straight from
 //        an accumulator, so each lane's 8 k-values are one 16-byte read.
 // One launch packs up to two sources; either output of a source may be null.
+//
+// HBM-bound: per element 4 (f32) or 2 (bf16) bytes read and 2 bytes written
+// per output layout. A workgroup owns 64 rows of one (b,h) slice:
+//   phase 1: each lane reads 4 consecutive elements (16 B of f32, lanes along
+//            D, fully coalesced), converts to bf16, writes them to Xb (8 B
+//            per lane, coalesced) and, for Xt, to a row-major LDS tile;
+//   phase 2: (Xt only) a lane owns 4 consecutive d and 8 output positions:
+//            eight 8-byte LDS reads (4 d of one row each), a register
+//            transpose, and four 16-byte stores; 8 consecutive lanes write one
+//            whole 128-byte segment of an Xt row.
 #include "common.h"
 #include "kernels.h"
 
 namespace gonn {
 
-template <typename T, int D>
-GONN_DEV void load8(const T* p, float* v) {
-    if constexpr (sizeof(T) == 4) {
-        const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
-        for (int i = 0; i < 4; i++) {
-            v[i] = a[i];
-            v[4 + i] = b[i];
-        }
-    } else {
-        const u16x8 a = *(const u16x8*)p;
-        for (int i = 0; i < 8; i++) v[i] = bf16_to_f32(a[i]);
-    }
-}
-
 // grid (Sp/64, BH, nsrc), 256 threads.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void pack_kernel(PackParams p) {
     constexpr int BN = 64;
-    constexpr int VS = D + 2;
-    __shared__ bf16 tile[BN * VS];
+    constexpr int TS = D + 4;  // LDS row stride (bf16): 8-byte rows, spread banks
+    __shared__ __attribute__((aligned(16))) bf16 tile[BN * TS];
     const int tid = threadIdx.x;
     const int kt = blockIdx.x, bh = blockIdx.y, which = blockIdx.z;
     const T* src = (const T*)p.src[which];
@@ -42,34 +38,60 @@ __global__ __launch_bounds__(256) void pack_kernel(PackParams p) {
     bf16* tr = (bf16*)p.tr[which];
     const int S = p.S, Sp = p.Sp;
     const size_t src0 = (size_t)bh * S * D;
-    constexpr int CH = BN * D / 8;
-    for (int c = tid; c < CH; c += 256) {
-        const int r = c / (D / 8), col = (c % (D / 8)) * 8;
+
+    constexpr int CH = BN * D / 4;  // 4-element chunks
+    constexpr int NC = CH / 256;     // per thread
+    // All of this thread's loads are issued before any store, so NC loads
+    // are in flight per lane.
+    float v[NC][4];
+    for (int n = 0; n < NC; n++) {
+        const int c = tid + n * 256;
+        const int r = c / (D / 4), col = (c % (D / 4)) * 4;
         const int key = kt * BN + r;
-        float v[8];
-        if (key < S) {
-            load8<T, D>(src + src0 + (size_t)key * D + col, v);
+        const int keyc = key < S ? key : S - 1;  // rows past S become zero below
+        const T* sp = src + src0 + (size_t)keyc * D + col;
+        if constexpr (sizeof(T) == 4) {
+            const f32x4 a = __builtin_nontemporal_load((const f32x4*)sp);
+            for (int i = 0; i < 4; i++) v[n][i] = a[i];
         } else {
-            for (int i = 0; i < 8; i++) v[i] = 0.f;
+            const uint2 a = *(const uint2*)sp;
+            v[n][0] = __uint_as_float(a.x << 16);
+            v[n][1] = __uint_as_float(a.x & 0xffff0000u);
+            v[n][2] = __uint_as_float(a.y << 16);
+            v[n][3] = __uint_as_float(a.y & 0xffff0000u);
         }
-        if (row)
-            *(bf16x8*)(row + ((size_t)bh * Sp + key) * D + col) =
-                pack8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
-        if (tr)
-            for (int i = 0; i < 8; i++) tile[r * VS + col + i] = to_bf16(v[i]);
+    }
+    typedef bf16 bf16x4 __attribute__((ext_vector_type(4)));
+    for (int n = 0; n < NC; n++) {
+        const int c = tid + n * 256;
+        const int r = c / (D / 4), col = (c % (D / 4)) * 4;
+        const int key = kt * BN + r;
+        bf16x4 b;
+        for (int i = 0; i < 4; i++) b[i] = to_bf16(key < S ? v[n][i] : 0.f);
+        if (row) *(bf16x4*)(row + ((size_t)bh * Sp + key) * D + col) = b;
+        if (tr) *(bf16x4*)(tile + r * TS + col) = b;
     }
     if (!tr) return;  // uniform for the workgroup
     __syncthreads();
-    constexpr int VC = D * BN / 8;
-    for (int c = tid; c < VC; c += 256) {
-        const int d = c / (BN / 8), j = c % (BN / 8);
-        const int grp = (j >> 1) * 16;
-        bf16x8 r;
-        for (int i = 0; i < 8; i++) {
-            const int pos = (j & 1) * 8 + i;
-            r[i] = tile[(grp + vt_pos(pos)) * VS + d];
+    // Lane -> (j: 8 output positions, d4: 4 consecutive d).
+    constexpr int NT = (D / 4) * 8;  // tasks
+    if (tid >= NT) return;
+    const int j = tid & 7, d4 = tid >> 3;
+    const int grp = (j >> 1) * 16;
+    uint2 w[8];  // w[i] = bf16 of d = 4*d4 .. 4*d4+3 for the key at position i
+    for (int i = 0; i < 8; i++) {
+        const int key = grp + vt_pos((j & 1) * 8 + i);
+        w[i] = *(const uint2*)(tile + key * TS + 4 * d4);
+    }
+    for (int r = 0; r < 4; r++) {
+        // output row d = 4*d4 + r: 8 bf16, component r of each w[i]
+        u32x4 o;
+        for (int q = 0; q < 4; q++) {
+            const uint32_t a = (r < 2) ? w[2 * q].x : w[2 * q].y;
+            const uint32_t b = (r < 2) ? w[2 * q + 1].x : w[2 * q + 1].y;
+            o[q] = (r & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
         }
-        *(bf16x8*)(tr + ((size_t)bh * D + d) * Sp + kt * BN + j * 8) = r;
+        *(u32x4*)(tr + ((size_t)bh * D + 4 * d4 + r) * Sp + kt * BN + j * 8) = o;
     }
 }
 
