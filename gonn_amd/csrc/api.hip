@@ -388,6 +388,7 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
             pp.row[0] = Kb;
             pp.src[1] = a->v.ptr;
             pp.tr[1] = Vt;
+            pp.mul[0] = pp.mul[1] = 1.f;
             pp.S = a->Sk;
             pp.Sp = Skp;
             TRYH(gonn::launch_pack(pp, 2, a->k.dtype == GONN_BF16, BH, a->D, s));
@@ -424,6 +425,10 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     p.Sp = Sp;
     p.scale = (float)a->scale;
     p.scale_log2 = (float)(a->scale * (double)gonn::kLog2e);
+    const float qsign = a->scale > 0 ? 1.f : (a->scale < 0 ? -1.f : 0.f);
+    p.c2b = (float)((a->scale == 0.0 ? 1.0 : std::fabs(a->scale)) * (double)gonn::kLog2e);
+    p.dqs = (float)a->scale;
+    p.dks = (float)std::fabs(a->scale);
     {
         ProfScope ps("bwd_prep", s);
         TRYH(gonn::launch_bwd_prep((const float*)a->o.ptr, (const float*)a->dO.ptr,
@@ -446,6 +451,8 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p1.src[1] = a->dO.ptr;
         p1.row[1] = dOb;
         p1.tr[1] = dOt;
+        p1.mul[0] = qsign;
+        p1.mul[1] = 1.f;
         p1.S = S;
         p1.Sp = Sp;
         TRYH(gonn::launch_pack(p1, 2, 0, BH, D, s));
@@ -455,6 +462,7 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p2.tr[0] = Kt;
         p2.src[1] = a->v.ptr;
         p2.row[1] = Vb;
+        p2.mul[0] = p2.mul[1] = 1.f;
         p2.S = S;
         p2.Sp = Sp;
         TRYH(gonn::launch_pack(p2, 2, 0, BH, D, s));

@@ -29,10 +29,15 @@
 // dOb, Kb, Vb and the vt_pos-permuted transposes Qt, dOt, Kt, all padded to
 // Sp rows); fp32 mode reads the caller's fp32 (BH,S,D) buffers directly with
 // v_mfma_f32_32x32x2_f32, clamping rows past S (masked or never written).
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
 namespace gonn {
+
+// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
+constexpr int kSgVALU = 0x002, kSgMFMA = 0x008, kSgDSR = 0x100;
 
 // ---------------------------------------------------------------------------
 // prep: grid ceil(BH*Sp/16), 256 threads (16 lanes per query row).
@@ -68,21 +73,41 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 
 // ---------------------------------------------------------------------------
 // bf16 dK/dV.
+//
+// One workgroup per 128-key block (32 keys per wave, held as the MFMA B
+// operand in VGPRs), query tiles of 64 streamed through LDS. One wave per
+// SIMD with the whole register file: step i runs S(i+1) = Q K^T and
+// dP(i+1) = dO V^T on MFMA (4 accumulator chains) interleaved with the VALU
+// of tile i (P = exp2(S c - L log2e), dS = P (dP - D), bf16 packs), then
+// dV^T += dO^T P and dK^T += Q^T dS for tile i (8 chains). Q/dO tiles (for
+// S, dP) run one tile ahead of the transposed Q^T/dO^T tiles and L, D (for
+// dV, dK); both stream HBM -> LDS with global_load_lds_dwordx4 into double
+// buffers the step no longer reads. Causal masks exist only on the first two
+// query tiles of a key block (q-tiles start at the block's first key).
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
-    constexpr int BN = 128;       // keys per workgroup
-    constexpr int BM = 64;        // queries per tile
-    constexpr int RST = D + 8;    // Q / dO tile row stride (bf16)
-    constexpr int TST = BM + 8;   // Q^T / dO^T tile row stride (bf16)
-    constexpr int RTILE = BM * RST, TTILE = D * TST, BUF = 2 * (RTILE + TTILE);
-    constexpr int RCH = BM * D / 8 / 256;  // 16-byte chunks per thread per tile
+    constexpr int BN = 128;      // keys per workgroup
+    constexpr int BM = 64;       // queries per tile
+    constexpr int RST = D + 8;   // Q / dO tile row stride (bf16)
+    constexpr int TST = BM + 8;  // Q^T / dO^T tile row stride (bf16)
     constexpr int NKS = D / 16;
     constexpr int NDT = D / 32;
-    __shared__ __attribute__((aligned(16))) bf16 smem[2 * BUF];
-    __shared__ float s_lse[2][BM], s_del[2][BM];
+    // LDS slots (16 B) of one tile and the load instructions that fill them.
+    constexpr int RCP = RST / 8, RCD = D / 8, NRP = BM * RCP;
+    constexpr int TCP = TST / 8, TCD = BM / 8, NTP = D * TCP;
+    constexpr int NRI = (NRP + 255) / 256, NTI = (NTP + 255) / 256;
+    constexpr int RLAST = NRP - (NRI - 1) * 256, TLAST = NTP - (NTI - 1) * 256;
+    static_assert(RLAST % 64 == 0 && TLAST % 64 == 0, "partial loads must be whole waves");
+    constexpr int RTILE = BM * RST, TTILE = D * TST;  // bf16 elements
+    __shared__ __attribute__((aligned(16))) bf16 sQ[2 * RTILE];
+    __shared__ __attribute__((aligned(16))) bf16 sdO[2 * RTILE];
+    __shared__ __attribute__((aligned(16))) bf16 sQt[2 * TTILE];
+    __shared__ __attribute__((aligned(16))) bf16 sdOt[2 * TTILE];
+    __shared__ __attribute__((aligned(16))) float sLD[2][2 * BM];  // L*log2e, then D
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, ln = lane & 31;
     const int S = p.S, Sp = p.Sp;
     int bh, kb;
@@ -90,7 +115,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     const int kw = kb * BN + wave * 32;  // first key of this wave
     const int kj = kw + ln;              // this lane's key
 
-    // K and V rows of this lane's key as MFMA B operands (k = d, column = key).
     bf16x8 kf[NKS], vf[NKS];
     {
         const bf16* kr = (const bf16*)p.k + ((size_t)bh * Sp + kj) * D + g * 8;
@@ -100,7 +124,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             vf[ks] = *(const bf16x8*)(vr + ks * 16);
         }
     }
-
     const bf16* Qg = (const bf16*)p.q + (size_t)bh * Sp * D;
     const bf16* dOg = (const bf16*)p.dO + (size_t)bh * Sp * D;
     const bf16* Qtg = (const bf16*)p.qt + (size_t)bh * D * Sp;
@@ -108,120 +131,162 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     const float* lg = p.lse2 + (size_t)bh * Sp;
     const float* dg = p.delta + (size_t)bh * Sp;
 
-    u32x4 rq[RCH], rdo[RCH], rqt[RCH], rdot[RCH];
-    float rl = 0.f, rd = 0.f;
-    auto gload = [&](int qb) {
-        const int q0 = qb * BM;
-        for (int i = 0; i < RCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-            rq[i] = *(const u32x4*)(Qg + (size_t)(q0 + row) * D + col);
-            rdo[i] = *(const u32x4*)(dOg + (size_t)(q0 + row) * D + col);
-        }
-        for (int i = 0; i < RCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (BM / 8), col = (c % (BM / 8)) * 8;
-            rqt[i] = *(const u32x4*)(Qtg + (size_t)row * Sp + q0 + col);
-            rdot[i] = *(const u32x4*)(dOtg + (size_t)row * Sp + q0 + col);
-        }
-        if (tid < BM) {
-            rl = lg[q0 + tid];
-            rd = dg[q0 + tid];
+    // Byte offsets of this thread's slots inside one tile (pad slots and
+    // lanes past the tile load a dummy chunk of the tile).
+    uint32_t roff[NRI], toff[NTI];
+    for (int i = 0; i < NRI; i++) {
+        const int pos = i * 256 + tid, r = pos / RCP, ch = pos % RCP;
+        roff[i] = (uint32_t)(((pos < NRP ? r : 0) * D + (ch < RCD ? ch : 0) * 8) * 2);
+    }
+    for (int i = 0; i < NTI; i++) {
+        const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
+        toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
+    }
+    auto dma_row = [&](int qb, int slot) {  // Q, dO rows of query tile qb
+        const char* q = (const char*)(Qg + (size_t)qb * BM * D);
+        const char* o = (const char*)(dOg + (size_t)qb * BM * D);
+        bf16* dq = sQ + slot * RTILE + wave * 64 * 8;
+        bf16* dd = sdO + slot * RTILE + wave * 64 * 8;
+        for (int i = 0; i < NRI; i++)
+            if (i < NRI - 1 || tid < RLAST) {
+                __builtin_amdgcn_global_load_lds((const void*)(q + roff[i]), (void*)(dq + i * 2048), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(o + roff[i]), (void*)(dd + i * 2048), 16, 0, 0);
+            }
+    };
+    auto dma_tr = [&](int qb, int slot) {  // Q^T, dO^T, L, D of query tile qb
+        const char* q = (const char*)(Qtg + qb * BM);
+        const char* o = (const char*)(dOtg + qb * BM);
+        bf16* dq = sQt + slot * TTILE + wave * 64 * 8;
+        bf16* dd = sdOt + slot * TTILE + wave * 64 * 8;
+        for (int i = 0; i < NTI; i++)
+            if (i < NTI - 1 || tid < TLAST) {
+                __builtin_amdgcn_global_load_lds((const void*)(q + toff[i]), (void*)(dq + i * 2048), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(o + toff[i]), (void*)(dd + i * 2048), 16, 0, 0);
+            }
+        if (wave == 0 && lane < 32) {  // 16 lanes: 64 L values; 16 lanes: 64 D values
+            const float* src = (lane < 16 ? lg : dg) + qb * BM + (lane & 15) * 4;
+            __builtin_amdgcn_global_load_lds((const void*)src, (void*)&sLD[slot][0], 16, 0, 0);
         }
     };
-    auto sstore = [&](int buf) {
-        bf16* sQ = smem + buf * BUF;
-        bf16* sdO = sQ + RTILE;
-        bf16* sQt = sdO + RTILE;
-        bf16* sdOt = sQt + TTILE;
-        for (int i = 0; i < RCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-            *(u32x4*)(sQ + row * RST + col) = rq[i];
-            *(u32x4*)(sdO + row * RST + col) = rdo[i];
-        }
-        for (int i = 0; i < RCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (BM / 8), col = (c % (BM / 8)) * 8;
-            *(u32x4*)(sQt + row * TST + col) = rqt[i];
-            *(u32x4*)(sdOt + row * TST + col) = rdot[i];
-        }
-        if (tid < BM) {
-            s_lse[buf][tid] = rl;
-            s_del[buf][tid] = rd;
-        }
+    auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
+
+    // S and dP of one query tile (64 queries x this wave's 32 keys): S[mt],
+    // dP[mt] hold queries mt*32 + 8(r/4) + 4g + r%4 of register r.
+    auto sdp = [&](int slot, f32x16* s, f32x16* dp) {
+        const bf16* q = sQ + slot * RTILE + ln * RST + g * 8;
+        const bf16* o = sdO + slot * RTILE + ln * RST + g * 8;
+        s[0] = s[1] = dp[0] = dp[1] = f32x16{};
+        for (int ks = 0; ks < NKS; ks++)
+            for (int mt = 0; mt < 2; mt++) {
+                s[mt] = mfma_bf16(*(const bf16x8*)(q + mt * 32 * RST + ks * 16), kf[ks], s[mt]);
+                dp[mt] = mfma_bf16(*(const bf16x8*)(o + mt * 32 * RST + ks * 16), vf[ks], dp[mt]);
+            }
     };
 
     f32x16 dvacc[NDT], dkacc[NDT];
     for (int t = 0; t < NDT; t++) dvacc[t] = dkacc[t] = f32x16{};
-    const float c2 = p.scale_log2;
-    // Queries below the block's first key see none of its keys.
-    const int qb0 = CAUSAL ? (kb * BN) / BM : 0;
-    const int qb1 = (S + BM - 1) / BM;
+    const float c2 = p.c2b;
+    const int qb0 = CAUSAL ? (kb * BN) / BM : 0;  // earlier queries see none of these keys
+    const int nq = (S + BM - 1) / BM - qb0;       // >= 1
 
-    if (qb0 < qb1) {
-        gload(qb0);
-        sstore(0);
-    }
-    __syncthreads();
-    for (int qb = qb0; qb < qb1; qb++) {
-        const int buf = (qb - qb0) & 1;
-        if (qb + 1 < qb1) gload(qb + 1);
-        const int q0 = qb * BM;
-        // A wave whose first key lies past the tile's last query is fully
-        // masked on this tile (wave-uniform).
-        if (!CAUSAL || kw <= q0 + BM - 1) {
-            const bf16* sQ = smem + buf * BUF;
-            const bf16* sdO = sQ + RTILE;
-            const bf16* sQt = sdO + RTILE;
-            const bf16* sdOt = sQt + TTILE;
-            // S, dP: 64 queries x 32 keys as two 32x32 tiles (mt = query half).
-            f32x16 sacc[2] = {f32x16{}, f32x16{}}, dpacc[2] = {f32x16{}, f32x16{}};
-            for (int ks = 0; ks < NKS; ks++)
-                for (int mt = 0; mt < 2; mt++) {
-                    const int off = (mt * 32 + ln) * RST + ks * 16 + g * 8;
-                    sacc[mt] = mfma_bf16(*(const bf16x8*)(sQ + off), kf[ks], sacc[mt]);
-                    dpacc[mt] = mfma_bf16(*(const bf16x8*)(sdO + off), vf[ks], dpacc[mt]);
-                }
-            const bool need_mask = CAUSAL && (q0 < kw + 31);
+    // Step i: tile qb0+i's P, dS and dV/dK; with NEXT, S/dP of tile i+1 and
+    // the loads of rows i+2 and transposes i+1.
+    auto step = [&](auto next_tag, int i, f32x16* s, f32x16* dp, f32x16* sn, f32x16* dpn) {
+        constexpr bool NEXT = decltype(next_tag)::value;
+        const int qb = qb0 + i, slot = i & 1;
+        if constexpr (NEXT) {
+            dma_row(i + 2 < nq ? qb + 2 : qb0 + nq - 1, slot);
+            dma_tr(qb + 1, slot ^ 1);
+        }
+        // Causal mask (key > query), only on the first two tiles. The exponent
+        // scale c2b is positive (a negative scale is folded into the packed
+        // Q), so a masked score of -inf gives P = 0 and dS = 0.
+        if (CAUSAL && i < 2) {
+            const int kq = kj - qb * BM - 4 * g;  // key minus this lane group's base query
             for (int mt = 0; mt < 2; mt++)
-                for (int r = 0; r < 16; r++) {
-                    const int qr = mt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    float pv = fast_exp2(__builtin_fmaf(sacc[mt][r], c2, -s_lse[buf][qr]));
-                    if (need_mask && kj > q0 + qr) pv = 0.f;
-                    sacc[mt][r] = pv;
-                    dpacc[mt][r] = pv * (dpacc[mt][r] - s_del[buf][qr]);
-                }
-            // dV^T += dO^T P and dK^T += Q^T dS over 4 k-steps of 16 queries.
-            for (int ks = 0; ks < BM / 16; ks++) {
-                const int mt = ks >> 1, b0 = (ks & 1) * 8;
-                const bf16x8 pb = pack8(sacc[mt][b0 + 0], sacc[mt][b0 + 1], sacc[mt][b0 + 2],
-                                        sacc[mt][b0 + 3], sacc[mt][b0 + 4], sacc[mt][b0 + 5],
-                                        sacc[mt][b0 + 6], sacc[mt][b0 + 7]);
-                const bf16x8 db = pack8(dpacc[mt][b0 + 0], dpacc[mt][b0 + 1], dpacc[mt][b0 + 2],
-                                        dpacc[mt][b0 + 3], dpacc[mt][b0 + 4], dpacc[mt][b0 + 5],
-                                        dpacc[mt][b0 + 6], dpacc[mt][b0 + 7]);
-                for (int t = 0; t < NDT; t++) {
-                    const int off = (t * 32 + ln) * TST + ks * 16 + g * 8;
-                    dvacc[t] = mfma_bf16(*(const bf16x8*)(sdOt + off), pb, dvacc[t]);
-                    dkacc[t] = mfma_bf16(*(const bf16x8*)(sQt + off), db, dkacc[t]);
-                }
+                for (int r = 0; r < 16; r++)
+                    s[mt][r] = kq > mt * 32 + 8 * (r >> 2) + (r & 3) ? -INFINITY : s[mt][r];
+        }
+        if constexpr (NEXT) sdp(slot ^ 1, sn, dpn);
+        // P and dS of tile i, packed to bf16 per 16-query k-step.
+        bf16x8 pb[4], db[4];
+        for (int mt = 0; mt < 2; mt++) {
+            f32x4 lse4[4], del4[4];
+            for (int j = 0; j < 4; j++) {
+                lse4[j] = *(const f32x4*)&sLD[slot][mt * 32 + 8 * j + 4 * g];
+                del4[j] = *(const f32x4*)&sLD[slot][BM + mt * 32 + 8 * j + 4 * g];
+            }
+            float pv[16], dv[16];
+            for (int r = 0; r < 16; r++) {
+                const float e = fast_exp2(__builtin_fmaf(s[mt][r], c2, -lse4[r >> 2][r & 3]));
+                pv[r] = e;
+                dv[r] = e * (dp[mt][r] - del4[r >> 2][r & 3]);
+            }
+            pb[2 * mt] = pack8(pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]);
+            pb[2 * mt + 1] = pack8(pv[8], pv[9], pv[10], pv[11], pv[12], pv[13], pv[14], pv[15]);
+            db[2 * mt] = pack8(dv[0], dv[1], dv[2], dv[3], dv[4], dv[5], dv[6], dv[7]);
+            db[2 * mt + 1] = pack8(dv[8], dv[9], dv[10], dv[11], dv[12], dv[13], dv[14], dv[15]);
+        }
+        // dV^T += dO^T P, dK^T += Q^T dS over 4 k-steps of 16 queries.
+        const bf16* qt = sQt + slot * TTILE + ln * TST + g * 8;
+        const bf16* ot = sdOt + slot * TTILE + ln * TST + g * 8;
+        for (int ks = 0; ks < BM / 16; ks++)
+            for (int t = 0; t < NDT; t++) {
+                dvacc[t] = mfma_bf16(*(const bf16x8*)(ot + t * 32 * TST + ks * 16), pb[ks], dvacc[t]);
+                dkacc[t] = mfma_bf16(*(const bf16x8*)(qt + t * 32 * TST + ks * 16), db[ks], dkacc[t]);
+            }
+        if constexpr (NEXT) {
+            // The S/dP(i+1) MFMAs carry tile i's VALU; dV/dK follow.
+            constexpr int kV = (192 + 4 * NKS - 1) / (4 * NKS);
+            __builtin_amdgcn_sched_group_barrier(kSgDSR, 4, 0);
+            for (int k = 0; k < 4 * NKS; k++) {
+                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgVALU, kV, 0);
+            }
+            for (int k = 0; k < 8 * NDT; k++) {
+                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
             }
         }
-        if (qb + 1 < qb1) sstore(buf ^ 1);
+        dma_wait();
         __syncthreads();
+    };
+    using Yes = std::integral_constant<bool, true>;
+    using No = std::integral_constant<bool, false>;
+
+    // Prologue: rows of tiles 0, 1; transposes, L, D of tile 0; S/dP of tile 0.
+    dma_row(qb0, 0);
+    if (nq > 1) dma_row(qb0 + 1, 1);
+    dma_tr(qb0, 0);
+    dma_wait();
+    __syncthreads();
+    f32x16 sA[2], dA[2], sB[2], dB[2];
+    sdp(0, sA, dA);
+    __syncthreads();  // step 0 reloads row slot 0
+
+    int i = 0;
+    for (; i + 2 < nq; i += 2) {
+        step(Yes{}, i, sA, dA, sB, dB);
+        step(Yes{}, i + 1, sB, dB, sA, dA);
+    }
+    if (i + 1 < nq) {
+        step(Yes{}, i, sA, dA, sB, dB);
+        step(No{}, i + 1, sB, dB, sA, dA);
+    } else {
+        step(No{}, i, sA, dA, sB, dB);
     }
 
     if (kj < S) {
-        const float sc = p.scale;
+        const float sc = p.dks;
         float* dkr = p.dk + ((size_t)bh * S + kj) * D;
         float* dvr = p.dv + ((size_t)bh * S + kj) * D;
         for (int t = 0; t < NDT; t++)
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 f32x4 a, b;
-                for (int i = 0; i < 4; i++) {
-                    a[i] = dkacc[t][rq4 * 4 + i] * sc;
-                    b[i] = dvacc[t][rq4 * 4 + i];
+                for (int k = 0; k < 4; k++) {
+                    a[k] = dkacc[t][rq4 * 4 + k] * sc;
+                    b[k] = dvacc[t][rq4 * 4 + k];
                 }
                 *(f32x4*)(dkr + t * 32 + rq4 * 8 + g * 4) = a;
                 *(f32x4*)(dvr + t * 32 + rq4 * 8 + g * 4) = b;
@@ -231,19 +296,34 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
 
 // ---------------------------------------------------------------------------
 // bf16 dQ.
+//
+// One workgroup per 128-query block, 32 queries per wave (the forward's
+// shape): S^T = K Q^T and dP^T = V dO^T with one QUERY per lane, so L and D
+// are lane scalars, and dQ^T += K^T dS^T. One wave per SIMD; step t runs the
+// S^T/dP^T MFMAs of key tile t+1 (4 chains) interleaved with the VALU of tile
+// t, then the dQ MFMAs of tile t. K/V tiles run one tile ahead of the K^T
+// tiles; all stream HBM -> LDS with global_load_lds_dwordx4. Masks (causal
+// diagonal, key end) exist only on the last two key tiles of a query block.
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     constexpr int BM = 128, BN = 64;
     constexpr int KST = D + 8;   // K / V tile row stride (bf16)
     constexpr int TST = BN + 8;  // K^T tile row stride (bf16)
-    constexpr int KTILE = BN * KST, TTILE = D * TST, BUF = 2 * KTILE + TTILE;
-    constexpr int KCH = BN * D / 8 / 256;
     constexpr int NKS = D / 16;
     constexpr int NDT = D / 32;
-    __shared__ __attribute__((aligned(16))) bf16 smem[2 * BUF];
+    constexpr int RCP = KST / 8, RCD = D / 8, NRP = BN * RCP;
+    constexpr int TCP = TST / 8, TCD = BN / 8, NTP = D * TCP;
+    constexpr int NRI = (NRP + 255) / 256, NTI = (NTP + 255) / 256;
+    constexpr int RLAST = NRP - (NRI - 1) * 256, TLAST = NTP - (NTI - 1) * 256;
+    static_assert(RLAST % 64 == 0 && TLAST % 64 == 0, "partial loads must be whole waves");
+    constexpr int RTILE = BN * KST, TTILE = D * TST;
+    __shared__ __attribute__((aligned(16))) bf16 sK[2 * RTILE];
+    __shared__ __attribute__((aligned(16))) bf16 sV[2 * RTILE];
+    __shared__ __attribute__((aligned(16))) bf16 sKt[2 * TTILE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, ln = lane & 31;
     const int S = p.S, Sp = p.Sp;
     int bh, qb;
@@ -265,97 +345,143 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
 
     int kend = S;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
-    const int ntiles = (kend + BN - 1) / BN;
+    const int nt = (kend + BN - 1) / BN;
     const bf16* Kg = (const bf16*)p.k + (size_t)bh * Sp * D;
     const bf16* Vg = (const bf16*)p.v + (size_t)bh * Sp * D;
     const bf16* Ktg = (const bf16*)p.kt + (size_t)bh * D * Sp;
 
-    u32x4 rk[KCH], rv[KCH], rkt[KCH];
-    auto gload = [&](int kt) {
-        for (int i = 0; i < KCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-            rk[i] = *(const u32x4*)(Kg + (size_t)(kt * BN + row) * D + col);
-            rv[i] = *(const u32x4*)(Vg + (size_t)(kt * BN + row) * D + col);
-        }
-        for (int i = 0; i < KCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (BN / 8), col = (c % (BN / 8)) * 8;
-            rkt[i] = *(const u32x4*)(Ktg + (size_t)row * Sp + kt * BN + col);
-        }
+    uint32_t roff[NRI], toff[NTI];
+    for (int i = 0; i < NRI; i++) {
+        const int pos = i * 256 + tid, r = pos / RCP, ch = pos % RCP;
+        roff[i] = (uint32_t)(((pos < NRP ? r : 0) * D + (ch < RCD ? ch : 0) * 8) * 2);
+    }
+    for (int i = 0; i < NTI; i++) {
+        const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
+        toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
+    }
+    auto dma_row = [&](int kt, int slot) {  // K, V rows of key tile kt
+        const char* k = (const char*)(Kg + (size_t)kt * BN * D);
+        const char* v = (const char*)(Vg + (size_t)kt * BN * D);
+        bf16* dk = sK + slot * RTILE + wave * 64 * 8;
+        bf16* dv = sV + slot * RTILE + wave * 64 * 8;
+        for (int i = 0; i < NRI; i++)
+            if (i < NRI - 1 || tid < RLAST) {
+                __builtin_amdgcn_global_load_lds((const void*)(k + roff[i]), (void*)(dk + i * 2048), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(v + roff[i]), (void*)(dv + i * 2048), 16, 0, 0);
+            }
     };
-    auto sstore = [&](int buf) {
-        bf16* sK = smem + buf * BUF;
-        bf16* sV = sK + KTILE;
-        bf16* sKt = sV + KTILE;
-        for (int i = 0; i < KCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (D / 8), col = (c % (D / 8)) * 8;
-            *(u32x4*)(sK + row * KST + col) = rk[i];
-            *(u32x4*)(sV + row * KST + col) = rv[i];
-        }
-        for (int i = 0; i < KCH; i++) {
-            const int c = tid + i * 256;
-            const int row = c / (BN / 8), col = (c % (BN / 8)) * 8;
-            *(u32x4*)(sKt + row * TST + col) = rkt[i];
-        }
+    auto dma_tr = [&](int kt, int slot) {  // K^T of key tile kt
+        const char* k = (const char*)(Ktg + kt * BN);
+        bf16* dk = sKt + slot * TTILE + wave * 64 * 8;
+        for (int i = 0; i < NTI; i++)
+            if (i < NTI - 1 || tid < TLAST)
+                __builtin_amdgcn_global_load_lds((const void*)(k + toff[i]), (void*)(dk + i * 2048), 16, 0, 0);
+    };
+    auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
+
+    auto sdp = [&](int slot, f32x16* s, f32x16* dp) {
+        const bf16* k = sK + slot * RTILE + ln * KST + g * 8;
+        const bf16* v = sV + slot * RTILE + ln * KST + g * 8;
+        s[0] = s[1] = dp[0] = dp[1] = f32x16{};
+        for (int ks = 0; ks < NKS; ks++)
+            for (int mt = 0; mt < 2; mt++) {
+                s[mt] = mfma_bf16(*(const bf16x8*)(k + mt * 32 * KST + ks * 16), qf[ks], s[mt]);
+                dp[mt] = mfma_bf16(*(const bf16x8*)(v + mt * 32 * KST + ks * 16), df[ks], dp[mt]);
+            }
+    };
+    // Masks of key tile kt on S^T: key >= S, or causal key > query. The
+    // exponent scale c2b is positive, so -inf gives P = 0 and dS = 0.
+    auto needs_mask = [&](int kt) {
+        const int kbase = kt * BN;
+        return (kbase + BN > S) || (CAUSAL && kbase + BN - 1 > q0 + wave * 32);
+    };
+    auto mask = [&](int kt, f32x16* s) {
+        const int kbase = kt * BN + 4 * g;
+        for (int mt = 0; mt < 2; mt++)
+            for (int r = 0; r < 16; r++) {
+                const int key = kbase + mt * 32 + 8 * (r >> 2) + (r & 3);
+                const bool off = key >= S || (CAUSAL && key > qi);
+                s[mt][r] = off ? -INFINITY : s[mt][r];
+            }
     };
 
     f32x16 dqacc[NDT];
     for (int t = 0; t < NDT; t++) dqacc[t] = f32x16{};
-    const float c2 = p.scale_log2;
+    const float c2 = p.c2b;
 
-    gload(0);
-    sstore(0);
-    __syncthreads();
-    for (int kt = 0; kt < ntiles; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < ntiles) gload(kt + 1);
-        const bf16* sK = smem + buf * BUF;
-        const bf16* sV = sK + KTILE;
-        const bf16* sKt = sV + KTILE;
-
-        f32x16 sacc[2] = {f32x16{}, f32x16{}}, dpacc[2] = {f32x16{}, f32x16{}};
-        for (int ks = 0; ks < NKS; ks++)
-            for (int mt = 0; mt < 2; mt++) {
-                const int off = (mt * 32 + ln) * KST + ks * 16 + g * 8;
-                sacc[mt] = mfma_bf16(*(const bf16x8*)(sK + off), qf[ks], sacc[mt]);
-                dpacc[mt] = mfma_bf16(*(const bf16x8*)(sV + off), df[ks], dpacc[mt]);
-            }
-        const int kbase = kt * BN;
-        const bool need_mask = (kbase + BN > S) || (CAUSAL && kbase + BN - 1 > q0 + wave * 32);
-        for (int mt = 0; mt < 2; mt++)
-            for (int r = 0; r < 16; r++) {
-                float pv = fast_exp2(__builtin_fmaf(sacc[mt][r], c2, -lq));
-                if (need_mask) {
-                    const int key = kbase + mt * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (key >= S || (CAUSAL && key > qi)) pv = 0.f;
-                }
-                dpacc[mt][r] = pv * (dpacc[mt][r] - dl);
-            }
-        // dQ^T += K^T dS^T over 4 k-steps of 16 keys.
-        for (int ks = 0; ks < BN / 16; ks++) {
-            const int mt = ks >> 1, b0 = (ks & 1) * 8;
-            const bf16x8 db = pack8(dpacc[mt][b0 + 0], dpacc[mt][b0 + 1], dpacc[mt][b0 + 2],
-                                    dpacc[mt][b0 + 3], dpacc[mt][b0 + 4], dpacc[mt][b0 + 5],
-                                    dpacc[mt][b0 + 6], dpacc[mt][b0 + 7]);
-            for (int t = 0; t < NDT; t++) {
-                const int off = (t * 32 + ln) * TST + ks * 16 + g * 8;
-                dqacc[t] = mfma_bf16(*(const bf16x8*)(sKt + off), db, dqacc[t]);
-            }
+    auto step = [&](auto next_tag, int t, f32x16* s, f32x16* dp, f32x16* sn, f32x16* dpn) {
+        constexpr bool NEXT = decltype(next_tag)::value;
+        const int slot = t & 1;
+        if constexpr (NEXT) {
+            dma_row(t + 2 < nt ? t + 2 : nt - 1, slot);
+            dma_tr(t + 1, slot ^ 1);
+            sdp(slot ^ 1, sn, dpn);
         }
-        if (kt + 1 < ntiles) sstore(buf ^ 1);
+        bf16x8 db[4];
+        for (int mt = 0; mt < 2; mt++) {
+            float d[16];
+            for (int r = 0; r < 16; r++) {
+                const float e = fast_exp2(__builtin_fmaf(s[mt][r], c2, -lq));
+                d[r] = e * (dp[mt][r] - dl);
+            }
+            db[2 * mt] = pack8(d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7]);
+            db[2 * mt + 1] = pack8(d[8], d[9], d[10], d[11], d[12], d[13], d[14], d[15]);
+        }
+        // dQ^T += K^T dS^T over 4 k-steps of 16 keys.
+        const bf16* kt_ = sKt + slot * TTILE + ln * TST + g * 8;
+        for (int ks = 0; ks < BN / 16; ks++)
+            for (int d = 0; d < NDT; d++)
+                dqacc[d] = mfma_bf16(*(const bf16x8*)(kt_ + d * 32 * TST + ks * 16), db[ks], dqacc[d]);
+        if constexpr (NEXT) {
+            constexpr int kV = (160 + 4 * NKS - 1) / (4 * NKS);
+            __builtin_amdgcn_sched_group_barrier(kSgDSR, 4, 0);
+            for (int k = 0; k < 4 * NKS; k++) {
+                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgVALU, kV, 0);
+            }
+            for (int k = 0; k < 4 * NDT; k++) {
+                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
+                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
+            }
+            if (needs_mask(t + 1)) mask(t + 1, sn);
+        }
+        dma_wait();
         __syncthreads();
+    };
+    using Yes = std::integral_constant<bool, true>;
+    using No = std::integral_constant<bool, false>;
+
+    dma_row(0, 0);
+    if (nt > 1) dma_row(1, 1);
+    dma_tr(0, 0);
+    dma_wait();
+    __syncthreads();
+    f32x16 sA[2], dA[2], sB[2], dB[2];
+    sdp(0, sA, dA);
+    if (needs_mask(0)) mask(0, sA);
+    __syncthreads();  // step 0 reloads row slot 0
+
+    int t = 0;
+    for (; t + 2 < nt; t += 2) {
+        step(Yes{}, t, sA, dA, sB, dB);
+        step(Yes{}, t + 1, sB, dB, sA, dA);
+    }
+    if (t + 1 < nt) {
+        step(Yes{}, t, sA, dA, sB, dB);
+        step(No{}, t + 1, sB, dB, sA, dA);
+    } else {
+        step(No{}, t, sA, dA, sB, dB);
     }
 
     if (qi < S) {
-        const float sc = p.scale;
+        const float sc = p.dqs;
         float* dqr = p.dq + ((size_t)bh * S + qi) * D;
-        for (int t = 0; t < NDT; t++)
+        for (int d = 0; d < NDT; d++)
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 f32x4 a;
-                for (int i = 0; i < 4; i++) a[i] = dqacc[t][rq4 * 4 + i] * sc;
-                *(f32x4*)(dqr + t * 32 + rq4 * 8 + g * 4) = a;
+                for (int k = 0; k < 4; k++) a[k] = dqacc[d][rq4 * 4 + k] * sc;
+                *(f32x4*)(dqr + d * 32 + rq4 * 8 + g * 4) = a;
             }
     }
 }

@@ -9,7 +9,8 @@
 //        of 16 permuted by vt_pos: an MFMA operand that contracts over the
 //        sequence axis against P, dS (or their transposes) taken straight from
 //        an accumulator, so each lane's 8 k-values are one 16-byte read.
-// One launch packs up to two sources; either output of a source may be null.
+// One launch packs up to two sources, each times a factor (1, or the sign of
+// the scale for the backward's Q); either output of a source may be null.
 //
 // HBM-bound: per element 4 (f32) or 2 (bf16) bytes read and 2 bytes written
 // per output layout. A workgroup owns 64 rows of one (b,h) slice:
@@ -37,6 +38,7 @@ __global__ __launch_bounds__(256) void pack_kernel(PackParams p) {
     bf16* row = (bf16*)p.row[which];
     bf16* tr = (bf16*)p.tr[which];
     const int S = p.S, Sp = p.Sp;
+    const float mul = p.mul[which];
     const size_t src0 = (size_t)bh * S * D;
 
     constexpr int CH = BN * D / 4;  // 4-element chunks
@@ -67,7 +69,7 @@ __global__ __launch_bounds__(256) void pack_kernel(PackParams p) {
         const int r = c / (D / 4), col = (c % (D / 4)) * 4;
         const int key = kt * BN + r;
         bf16x4 b;
-        for (int i = 0; i < 4; i++) b[i] = to_bf16(key < S ? v[n][i] : 0.f);
+        for (int i = 0; i < 4; i++) b[i] = to_bf16(key < S ? v[n][i] * mul : 0.f);
         if (row) *(bf16x4*)(row + ((size_t)bh * Sp + key) * D + col) = b;
         if (tr) *(bf16x4*)(tile + r * TS + col) = b;
     }

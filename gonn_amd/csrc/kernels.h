@@ -32,11 +32,13 @@ struct DecodeParams {
 
 // Up to two sources packed by one launch (attn_pack.hip): src[i] (BH,S,D)
 // f32 or bf16 -> row[i] (BH,Sp,D) bf16 and/or tr[i] (BH,D,Sp) bf16
-// (transposed, 16-groups permuted by vt_pos). Null outputs are skipped.
+// (transposed, 16-groups permuted by vt_pos), times mul[i]. Null outputs are
+// skipped.
 struct PackParams {
     const void* src[2];
     void* row[2];
     void* tr[2];
+    float mul[2];  // each source is multiplied by mul before rounding to bf16
     int S, Sp;
 };
 
@@ -57,8 +59,12 @@ struct BwdParams {
     float* dk;
     float* dv;
     int BH, S, Sp;
-    float scale;       // signed scale
-    float scale_log2;  // scale * log2(e)
+    float scale;       // signed scale (fp32 kernels)
+    float scale_log2;  // scale * log2(e) (fp32 kernels)
+    // bf16 kernels: Q is packed times sign(scale) (0 for a zero scale), so
+    // the exponent scale is positive: c2b = (scale ? |scale| : 1) * log2(e);
+    // outputs dQ = dqs * acc, dK = dks * acc with dqs = scale, dks = |scale|.
+    float c2b, dqs, dks;
 };
 
 hipError_t launch_pack(const PackParams& p, int nsrc, int in_bf16, int BH, int D, hipStream_t s);
