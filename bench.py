@@ -56,13 +56,14 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def load_traffic(kernel: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE and
-    WRITE_SIZE runs, scaled by a copy-kernel calibration); None if absent."""
+def load_traffic(key: str):
+    """HBM bytes per launch of `kernel:workload` measured by rocprofv3 --pmc
+    (FETCH_SIZE and WRITE_SIZE passes, scaled by the 1 GiB copy calibration,
+    profiles/README.md); None if absent."""
     try:
         with open(TRAFFIC_FILE) as f:
             t = json.load(f)
-        return t.get(kernel, {}).get("bytes_per_launch")
+        return t.get(key, {}).get("bytes_per_launch")
     except (OSError, ValueError):
         return None
 
@@ -302,7 +303,7 @@ def main():
                    "flop_per_step": pre["flop"], "wall_s": round(pre["wall_s"], 4)},
         "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-                     "traffic": load_traffic("fwd_bf16"), "kernel": "fwd_bf16_kernel",
+                     "traffic": load_traffic("fwd_bf16:C3"), "kernel": "fwd_bf16_kernel",
                      "kernel_ms": round(pre["kernel_ms"], 5),
                      "pack_kv_ms": round(pre["pack_ms"], 5)},
     }
@@ -319,7 +320,7 @@ def main():
                        "mean_len": dec["mean_len"]},
             "roofline": {"bound": "hbm", "achieved": round(kgbs, 2), "peak": PEAK_HBM_GBS,
                          "unit": "GB/s", "frac": round(kgbs / PEAK_HBM_GBS, 4),
-                         "traffic": load_traffic("decode_split"),
+                         "traffic": load_traffic("decode_split:C4"),
                          "kernel": "decode_split_kernel",
                          "kernel_ms": round(dec["split_ms"], 5),
                          "combine_ms": round(dec["combine_ms"], 5)},
@@ -340,6 +341,8 @@ def main():
             "stage_ms": {k: round(v, 5) for k, v in per.items()},
             "roofline": {"bound": "mfma", "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "kernel": "bwd_dkdv + bwd_dq",
+                         "traffic": (load_traffic("bwd_dkdv:C5") or 0) + (load_traffic("bwd_dq:C5") or 0)
+                         or None,
                          "achieved": round(fb["bwd_flop"] / ((per["bwd_dkdv"] + per["bwd_dq"])
                                                              * 1e-3) / 1e12, 3),
                          "frac": round(fb["bwd_flop"] / ((per["bwd_dkdv"] + per["bwd_dq"]) * 1e-3)
