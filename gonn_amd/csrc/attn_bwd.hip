@@ -81,7 +81,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 // of tile i (P = exp2(S c - L log2e), dS = P (dP - D), bf16 packs), then
 // dV^T += dO^T P and dK^T += Q^T dS for tile i (8 chains). Q/dO tiles (for
 // S, dP) run one tile ahead of the transposed Q^T/dO^T tiles and L, D (for
-// dV, dK); both stream HBM -> LDS with global_load_lds_dwordx4 into double
+// dV, dK); both stream HBM -> LDS with buffer_load_dwordx4 ... lds into double
 // buffers the step no longer reads. Causal masks exist only on the first two
 // query tiles of a key block (q-tiles start at the block's first key).
 // ---------------------------------------------------------------------------
@@ -142,33 +142,37 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
         toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
     }
+    const uint32_t slice = (uint32_t)Sp * D * 2;  // bytes of one (b,h) slice
+    const brsrc rq = make_rsrc(Qg, slice), rdo = make_rsrc(dOg, slice);
+    const brsrc rqt = make_rsrc(Qtg, slice), rdot = make_rsrc(dOtg, slice);
+    const brsrc rl = make_rsrc(lg, (uint32_t)Sp * 4), rd = make_rsrc(dg, (uint32_t)Sp * 4);
     auto dma_row = [&](int qb, int slot) {  // Q, dO rows of query tile qb
-        const char* q = (const char*)(Qg + (size_t)qb * BM * D);
-        const char* o = (const char*)(dOg + (size_t)qb * BM * D);
-        bf16* dq = sQ + slot * RTILE + wave * 64 * 8;
-        bf16* dd = sdO + slot * RTILE + wave * 64 * 8;
+        const uint32_t so = (uint32_t)qb * BM * D * 2;
+        const bf16* dq = sQ + slot * RTILE + wave * 64 * 8;
+        const bf16* dd = sdO + slot * RTILE + wave * 64 * 8;
         for (int i = 0; i < NRI; i++)
             if (i < NRI - 1 || tid < RLAST) {
-                __builtin_amdgcn_global_load_lds((const void*)(q + roff[i]), (void*)(dq + i * 2048), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(o + roff[i]), (void*)(dd + i * 2048), 16, 0, 0);
+                dma16(rq, dq + i * 2048, roff[i], so);
+                dma16(rdo, dd + i * 2048, roff[i], so);
             }
     };
     auto dma_tr = [&](int qb, int slot) {  // Q^T, dO^T, L, D of query tile qb
-        const char* q = (const char*)(Qtg + qb * BM);
-        const char* o = (const char*)(dOtg + qb * BM);
-        bf16* dq = sQt + slot * TTILE + wave * 64 * 8;
-        bf16* dd = sdOt + slot * TTILE + wave * 64 * 8;
+        const uint32_t so = (uint32_t)qb * BM * 2;
+        const bf16* dq = sQt + slot * TTILE + wave * 64 * 8;
+        const bf16* dd = sdOt + slot * TTILE + wave * 64 * 8;
         for (int i = 0; i < NTI; i++)
             if (i < NTI - 1 || tid < TLAST) {
-                __builtin_amdgcn_global_load_lds((const void*)(q + toff[i]), (void*)(dq + i * 2048), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(o + toff[i]), (void*)(dd + i * 2048), 16, 0, 0);
+                dma16(rqt, dq + i * 2048, toff[i], so);
+                dma16(rdot, dd + i * 2048, toff[i], so);
             }
-        if (wave == 0 && lane < 32) {  // 16 lanes: 64 L values; 16 lanes: 64 D values
-            const float* src = (lane < 16 ? lg : dg) + qb * BM + (lane & 15) * 4;
-            __builtin_amdgcn_global_load_lds((const void*)src, (void*)&sLD[slot][0], 16, 0, 0);
+        // Wave 0: lanes 0-15 load the 64 L values (bytes 0-255 of sLD[slot]),
+        // lanes 16-31 the 64 D values (bytes 256-511).
+        if (wave == 0) {
+            if (lane < 16) dma16(rl, &sLD[slot][0], (lane & 15) * 16, (uint32_t)qb * BM * 4);
+            else if (lane < 32) dma16(rd, &sLD[slot][0], (lane & 15) * 16, (uint32_t)qb * BM * 4);
         }
     };
-    auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
+    auto dma_wait = [] { GONN_VMCNT(0); };
 
     // S and dP of one query tile (64 queries x this wave's 32 keys): S[mt],
     // dP[mt] hold queries mt*32 + 8(r/4) + 4g + r%4 of register r.
@@ -302,7 +306,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
 // are lane scalars, and dQ^T += K^T dS^T. One wave per SIMD; step t runs the
 // S^T/dP^T MFMAs of key tile t+1 (4 chains) interleaved with the VALU of tile
 // t, then the dQ MFMAs of tile t. K/V tiles run one tile ahead of the K^T
-// tiles; all stream HBM -> LDS with global_load_lds_dwordx4. Masks (causal
+// tiles; all stream HBM -> LDS with buffer_load_dwordx4 ... lds. Masks (causal
 // diagonal, key end) exist only on the last two key tiles of a query block.
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL>
@@ -359,25 +363,25 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
         const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
         toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
     }
+    const uint32_t slice = (uint32_t)Sp * D * 2;  // bytes of one (b,h) slice
+    const brsrc rk = make_rsrc(Kg, slice), rv = make_rsrc(Vg, slice), rkt = make_rsrc(Ktg, slice);
     auto dma_row = [&](int kt, int slot) {  // K, V rows of key tile kt
-        const char* k = (const char*)(Kg + (size_t)kt * BN * D);
-        const char* v = (const char*)(Vg + (size_t)kt * BN * D);
-        bf16* dk = sK + slot * RTILE + wave * 64 * 8;
-        bf16* dv = sV + slot * RTILE + wave * 64 * 8;
+        const uint32_t so = (uint32_t)kt * BN * D * 2;
+        const bf16* dk = sK + slot * RTILE + wave * 64 * 8;
+        const bf16* dv = sV + slot * RTILE + wave * 64 * 8;
         for (int i = 0; i < NRI; i++)
             if (i < NRI - 1 || tid < RLAST) {
-                __builtin_amdgcn_global_load_lds((const void*)(k + roff[i]), (void*)(dk + i * 2048), 16, 0, 0);
-                __builtin_amdgcn_global_load_lds((const void*)(v + roff[i]), (void*)(dv + i * 2048), 16, 0, 0);
+                dma16(rk, dk + i * 2048, roff[i], so);
+                dma16(rv, dv + i * 2048, roff[i], so);
             }
     };
     auto dma_tr = [&](int kt, int slot) {  // K^T of key tile kt
-        const char* k = (const char*)(Ktg + kt * BN);
-        bf16* dk = sKt + slot * TTILE + wave * 64 * 8;
+        const uint32_t so = (uint32_t)kt * BN * 2;
+        const bf16* dk = sKt + slot * TTILE + wave * 64 * 8;
         for (int i = 0; i < NTI; i++)
-            if (i < NTI - 1 || tid < TLAST)
-                __builtin_amdgcn_global_load_lds((const void*)(k + toff[i]), (void*)(dk + i * 2048), 16, 0, 0);
+            if (i < NTI - 1 || tid < TLAST) dma16(rkt, dk + i * 2048, toff[i], so);
     };
-    auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };  // vmcnt(0)
+    auto dma_wait = [] { GONN_VMCNT(0); };
 
     auto sdp = [&](int slot, f32x16* s, f32x16* dp) {
         const bf16* k = sK + slot * RTILE + ln * KST + g * 8;

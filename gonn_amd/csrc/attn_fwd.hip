@@ -40,7 +40,7 @@ namespace gonn {
 // Pipeline (one barrier per 64-key tile): K and V have separate double
 // buffers in LDS and V lags K by one tile. K(t+2) and V(t+1) stream from HBM
 // straight into the LDS buffers step t no longer reads
-// (global_load_lds_dwordx4: lane L of a wave writes 16 bytes at dst + 16 L),
+// (buffer_load_dwordx4 ... lds: lane L of a wave writes 16 bytes at dst + 16 L),
 // so no VGPRs stage them. The tiles keep a padded row stride (one spare
 // 16-byte slot per row: conflict-free MFMA operand reads); the lanes that
 // land on a pad slot load a dummy chunk.
@@ -132,24 +132,20 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_kernel(FwdParams p) {
         const int pos = i * 256 + tid, row = pos / VCP, ch = pos % VCP;
         voff[i] = (uint32_t)(((pos < NVP ? row : 0) * Skp + (ch < VCD ? ch : 0) * 8) * 2);
     }
+    const brsrc krs = make_rsrc(Kg, (uint32_t)Skp * D * 2);
+    const brsrc vrs = make_rsrc(Vg, (uint32_t)Skp * D * 2);
     auto dma_k = [&](int kt, int buf) {
-        const char* src = (const char*)(Kg + (size_t)kt * BN * D);
-        bf16* dst = sKb + buf * KTILE + wave * 64 * 8;
+        const bf16* dst = sKb + buf * KTILE + wave * 64 * 8;
         for (int i = 0; i < NKI; i++)
-            if (i < NKI - 1 || tid < KLAST)
-                __builtin_amdgcn_global_load_lds((const void*)(src + koff[i]),
-                                                 (void*)(dst + i * 256 * 8), 16, 0, 0);
+            if (i < NKI - 1 || tid < KLAST) dma16(krs, dst + i * 256 * 8, koff[i], kt * BN * D * 2);
     };
     auto dma_v = [&](int kt, int buf) {
-        const char* src = (const char*)(Vg + kt * BN);
-        bf16* dst = sVb + buf * VTILE + wave * 64 * 8;
+        const bf16* dst = sVb + buf * VTILE + wave * 64 * 8;
         for (int i = 0; i < NVI; i++)
-            if (i < NVI - 1 || tid < VLAST)
-                __builtin_amdgcn_global_load_lds((const void*)(src + voff[i]),
-                                                 (void*)(dst + i * 256 * 8), 16, 0, 0);
+            if (i < NVI - 1 || tid < VLAST) dma16(vrs, dst + i * 256 * 8, voff[i], kt * BN * 2);
     };
-    // Wait for this thread's LDS-DMA loads (s_waitcnt vmcnt(0)).
-    auto dma_wait = [] { __builtin_amdgcn_s_waitcnt(0x0F70); };
+    // Wait for this thread's tile loads.
+    auto dma_wait = [] { GONN_VMCNT(0); };
     // S^T (64 keys x 32 queries) of one K tile as two 32x32 tiles.
     auto qk = [&](int buf, f32x16* s) {
         const bf16* sK = sKb + buf * KTILE + ln * KST + g * 8;

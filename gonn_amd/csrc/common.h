@@ -109,4 +109,24 @@ GONN_DEV int vt_pos(int o) {
     return (o >= 4 && o < 8) ? o + 4 : ((o >= 8 && o < 12) ? o - 4 : o);
 }
 
+// ---- HBM -> LDS tile loads (buffer_load_dwordx4 ... lds) ----
+// A raw buffer resource over [base, base + bytes): stride 0, reads past the
+// end return zero. The fourth descriptor word selects 32-bit raw access.
+typedef __amdgpu_buffer_rsrc_t brsrc;
+GONN_DEV brsrc make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+// Every lane reads 16 bytes at voff + soff of the buffer; lane L of the wave
+// writes them to LDS at lds + 16 L (lds must be wave-uniform). The load
+// counts in vmcnt only. The MUBUF form is used rather than
+// global_load_lds: the compiler models the latter as a FLAT access that may
+// also touch LDS, which turns every later LDS-read wait into lgkmcnt(0)
+// while a tile load is in flight.
+GONN_DEV void dma16(brsrc r, const void* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)const_cast<void*>(lds), 16, voff, soff, 0, 0);
+}
+// s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained), n < 16.
+#define GONN_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
 }  // namespace gonn
