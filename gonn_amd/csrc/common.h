@@ -99,6 +99,11 @@ GONN_DEV void map_block(int L, int nblk, int BH, bool reverse, int& bh, int& blk
     bh = idx / nblk;
     const int r = idx - bh * nblk;
     blk = reverse ? (nblk - 1 - r) : r;
+    // The integer division runs on the VALU; pin the (uniform) results to
+    // SGPRs so buffer resources built from them stay scalar (a resource in
+    // VGPRs makes the compiler wrap every buffer load in a readfirstlane loop).
+    bh = __builtin_amdgcn_readfirstlane(bh);
+    blk = __builtin_amdgcn_readfirstlane(blk);
 }
 
 // Key position inside a 16-key group of the transposed-V (Vt) layout. The
@@ -117,14 +122,22 @@ GONN_DEV brsrc make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 // Every lane reads 16 bytes at voff + soff of the buffer; lane L of the wave
-// writes them to LDS at lds + 16 L (lds must be wave-uniform). The load
-// counts in vmcnt only. The MUBUF form is used rather than
-// global_load_lds: the compiler models the latter as a FLAT access that may
-// also touch LDS, which turns every later LDS-read wait into lgkmcnt(0)
-// while a tile load is in flight.
+// writes them to LDS at lds + 16 L (lds must be wave-uniform). The load counts
+// in vmcnt only; callers wait with GONN_VMCNT and publish with a barrier.
+//
+// Issued from inline asm on purpose: the compiler treats an LDS-DMA load as a
+// possible writer of any LDS address it cannot disambiguate, and then waits
+// for all of them (vmcnt(0)) before the next ds_read, which turns a load
+// meant to run a whole step ahead into a synchronous one. Hidden in asm, the
+// load is invisible to the compiler's wait insertion; every buffer read
+// after it is ordered by the explicit wait + barrier of the kernel's
+// pipeline. M0 is set inside the statement; the compiler sets M0 itself
+// before each of its own M0 uses (these kernels make none).
 GONN_DEV void dma16(brsrc r, const void* lds, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)const_cast<void*>(lds), 16, voff, soff, 0, 0);
+    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory");
 }
 // s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained), n < 16.
 #define GONN_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
