@@ -148,28 +148,29 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     const brsrc rl = make_rsrc(lg, (uint32_t)Sp * 4), rd = make_rsrc(dg, (uint32_t)Sp * 4);
     auto dma_row = [&](int qb, int slot) {  // Q, dO rows of query tile qb
         const uint32_t so = (uint32_t)qb * BM * D * 2;
-        const bf16* dq = sQ + slot * RTILE + wave * 64 * 8;
-        const bf16* dd = sdO + slot * RTILE + wave * 64 * 8;
+        const uint32_t dq = lds_addr(sQ) + (slot * RTILE + wave * 512) * 2;
+        const uint32_t dd = lds_addr(sdO) + (slot * RTILE + wave * 512) * 2;
         for (int i = 0; i < NRI; i++)
             if (i < NRI - 1 || tid < RLAST) {
-                dma16(rq, dq + i * 2048, roff[i], so);
-                dma16(rdo, dd + i * 2048, roff[i], so);
+                dma16(rq, dq + i * 4096, roff[i], so);
+                dma16(rdo, dd + i * 4096, roff[i], so);
             }
     };
     auto dma_tr = [&](int qb, int slot) {  // Q^T, dO^T, L, D of query tile qb
         const uint32_t so = (uint32_t)qb * BM * 2;
-        const bf16* dq = sQt + slot * TTILE + wave * 64 * 8;
-        const bf16* dd = sdOt + slot * TTILE + wave * 64 * 8;
+        const uint32_t dq = lds_addr(sQt) + (slot * TTILE + wave * 512) * 2;
+        const uint32_t dd = lds_addr(sdOt) + (slot * TTILE + wave * 512) * 2;
         for (int i = 0; i < NTI; i++)
             if (i < NTI - 1 || tid < TLAST) {
-                dma16(rqt, dq + i * 2048, toff[i], so);
-                dma16(rdot, dd + i * 2048, toff[i], so);
+                dma16(rqt, dq + i * 4096, toff[i], so);
+                dma16(rdot, dd + i * 4096, toff[i], so);
             }
         // Wave 0: lanes 0-15 load the 64 L values (bytes 0-255 of sLD[slot]),
         // lanes 16-31 the 64 D values (bytes 256-511).
         if (wave == 0) {
-            if (lane < 16) dma16(rl, &sLD[slot][0], (lane & 15) * 16, (uint32_t)qb * BM * 4);
-            else if (lane < 32) dma16(rd, &sLD[slot][0], (lane & 15) * 16, (uint32_t)qb * BM * 4);
+            const uint32_t dl = lds_addr(sLD) + slot * 2 * BM * 4;
+            if (lane < 16) dma16(rl, dl, (lane & 15) * 16, (uint32_t)qb * BM * 4);
+            else if (lane < 32) dma16(rd, dl, (lane & 15) * 16, (uint32_t)qb * BM * 4);
         }
     };
     auto dma_wait = [] { GONN_VMCNT(0); };
@@ -367,19 +368,19 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     const brsrc rk = make_rsrc(Kg, slice), rv = make_rsrc(Vg, slice), rkt = make_rsrc(Ktg, slice);
     auto dma_row = [&](int kt, int slot) {  // K, V rows of key tile kt
         const uint32_t so = (uint32_t)kt * BN * D * 2;
-        const bf16* dk = sK + slot * RTILE + wave * 64 * 8;
-        const bf16* dv = sV + slot * RTILE + wave * 64 * 8;
+        const uint32_t dk = lds_addr(sK) + (slot * RTILE + wave * 512) * 2;
+        const uint32_t dv = lds_addr(sV) + (slot * RTILE + wave * 512) * 2;
         for (int i = 0; i < NRI; i++)
             if (i < NRI - 1 || tid < RLAST) {
-                dma16(rk, dk + i * 2048, roff[i], so);
-                dma16(rv, dv + i * 2048, roff[i], so);
+                dma16(rk, dk + i * 4096, roff[i], so);
+                dma16(rv, dv + i * 4096, roff[i], so);
             }
     };
     auto dma_tr = [&](int kt, int slot) {  // K^T of key tile kt
         const uint32_t so = (uint32_t)kt * BN * 2;
-        const bf16* dk = sKt + slot * TTILE + wave * 64 * 8;
+        const uint32_t dk = lds_addr(sKt) + (slot * TTILE + wave * 512) * 2;
         for (int i = 0; i < NTI; i++)
-            if (i < NTI - 1 || tid < TLAST) dma16(rkt, dk + i * 2048, toff[i], so);
+            if (i < NTI - 1 || tid < TLAST) dma16(rkt, dk + i * 4096, toff[i], so);
     };
     auto dma_wait = [] { GONN_VMCNT(0); };
 

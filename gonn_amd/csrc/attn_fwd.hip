@@ -134,15 +134,17 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_kernel(FwdParams p) {
     }
     const brsrc krs = make_rsrc(Kg, (uint32_t)Skp * D * 2);
     const brsrc vrs = make_rsrc(Vg, (uint32_t)Skp * D * 2);
+    // LDS byte address of this wave's first slot in K / Vt buffer 0.
+    const uint32_t kl = lds_addr(sKb) + wave * 64 * 16, vl = lds_addr(sVb) + wave * 64 * 16;
     auto dma_k = [&](int kt, int buf) {
-        const bf16* dst = sKb + buf * KTILE + wave * 64 * 8;
+        const uint32_t dst = kl + buf * KTILE * 2;
         for (int i = 0; i < NKI; i++)
-            if (i < NKI - 1 || tid < KLAST) dma16(krs, dst + i * 256 * 8, koff[i], kt * BN * D * 2);
+            if (i < NKI - 1 || tid < KLAST) dma16(krs, dst + i * 4096, koff[i], kt * BN * D * 2);
     };
     auto dma_v = [&](int kt, int buf) {
-        const bf16* dst = sVb + buf * VTILE + wave * 64 * 8;
+        const uint32_t dst = vl + buf * VTILE * 2;
         for (int i = 0; i < NVI; i++)
-            if (i < NVI - 1 || tid < VLAST) dma16(vrs, dst + i * 256 * 8, voff[i], kt * BN * 2);
+            if (i < NVI - 1 || tid < VLAST) dma16(vrs, dst + i * 4096, voff[i], kt * BN * 2);
     };
     // Wait for this thread's tile loads.
     auto dma_wait = [] { GONN_VMCNT(0); };

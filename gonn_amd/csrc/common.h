@@ -122,7 +122,7 @@ GONN_DEV brsrc make_rsrc(const void* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
 }
 // Every lane reads 16 bytes at voff + soff of the buffer; lane L of the wave
-// writes them to LDS at lds + 16 L (lds must be wave-uniform). The load counts
+// writes them to LDS byte address lds + 16 L (lds must be wave-uniform). The load counts
 // in vmcnt only; callers wait with GONN_VMCNT and publish with a barrier.
 //
 // Issued from inline asm on purpose: the compiler treats an LDS-DMA load as a
@@ -133,11 +133,15 @@ GONN_DEV brsrc make_rsrc(const void* base, uint32_t bytes) {
 // after it is ordered by the explicit wait + barrier of the kernel's
 // pipeline. M0 is set inside the statement; the compiler sets M0 itself
 // before each of its own M0 uses (these kernels make none).
-GONN_DEV void dma16(brsrc r, const void* lds, uint32_t voff, uint32_t soff) {
-    const uint32_t m0 = __builtin_amdgcn_readfirstlane(
-        (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)lds);
+GONN_DEV void dma16(brsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :: "s"(m0), "v"(voff), "s"(r), "s"(soff) : "memory");
+                 :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+// LDS byte address of a __shared__ object (apply to the array itself, so the
+// address-space cast folds to a constant).
+GONN_DEV uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
 // s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained), n < 16.
 #define GONN_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
