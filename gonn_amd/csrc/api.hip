@@ -365,7 +365,6 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
     p.BH = BH;
     p.Sq = a->Sq;
     p.Sk = a->Sk;
-    p.nqb = (a->Sq + 127) / 128;
     if (a->scale == 0.0) {  // all scores 0: uniform weights; Q is zeroed
         p.qsign = 0.f;
         p.scale_abs = 1.f;

@@ -28,6 +28,7 @@
 //        masked.
 //  fp32: v_mfma_f32_32x32x2_f32 straight from the fp32 K/V (no pack).
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "kernels.h"
@@ -67,6 +68,23 @@ constexpr float kLazyLog2 = 8.0f;
 
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgVALU = 0x002, kSgMFMA = 0x008, kSgDSR = 0x100;
+
+// Forces x to be computed at this point of the program (an empty asm that
+// reads it): keeps hand-scheduled VALU work from being sunk to its uses.
+template <typename T>
+GONN_DEV void pin(const T& x) {
+    asm volatile("" ::"v"(x));
+}
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <typename F, int... I>
+GONN_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+GONN_DEV void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 template <int D, bool CAUSAL, typename QT>
 __global__ __launch_bounds__(256, 2) void fwd_bf16_kernel(FwdParams p) {
@@ -322,6 +340,393 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_kernel(FwdParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// bf16-MFMA forward for D = 128, NW waves (32 query rows each) per workgroup:
+// NW = 4 runs two workgroups per CU, NW = 8 one.
+//
+// Three-stage software pipeline. Step t issues, with no dependency between
+// them inside the step:
+//   MFMA  O^T += V(t)^T P(t)            (P(t) packed by step t-1)
+//   MFMA  S^T(t+2) = K(t+2) Q^T          (K(t+2) landed by the end of step t-1)
+//   VALU  P(t+1) = exp2(S^T(t+1) c - mc) packed to bf16, row sums
+// so the MFMA stream never waits on the softmax of the tile it is computing.
+//
+// The softmax VALU work is the binding cost next to the MFMAs on gfx950 (an
+// exp2 occupies the SIMD ~13 cycles, a plain VALU op ~2.5, an MFMA 32), so
+// the common path is one FMA, one exp2, half a bf16 pack and half a v_dot2 per
+// score, and no per-tile row max: P = exp2(s c - mc) is exact for any offset
+// mc, which only has to keep P bounded. A tile whose row sum exceeds 2^14 (or
+// is not finite) takes a rare, wave-uniform branch that computes the tile max,
+// moves mc to it, recomputes the tile's P and rescales l and O by
+// alpha = 2^(old - new). Otherwise every score is below mc + 14, so P, l and O
+// stay far inside fp32 range, and their relative precision does not depend
+// on mc. The first tile (prologue) uses its exact max.
+//
+// LDS: rings of K tiles (64 keys x D) and Vt tiles (D x 64 keys) filled
+// straight from HBM/L2 by buffer_load ... lds, one barrier per step. Rows
+// keep one spare 16-byte chunk (conflict-free MFMA operand reads with one
+// address register per ring); lanes that land on a spare chunk load a dummy.
+//  NW = 8: 4-slot rings; step t loads K(t+4) and V(t+2), two steps ahead.
+//  NW = 4: 2-slot rings (two workgroups share the CU's LDS); step t loads
+//          K(t+3) and V(t+1), one step ahead.
+// In steady state the loads are spread over the MFMA stream so the texture
+// unit drains them in the background.
+// ---------------------------------------------------------------------------
+constexpr float kSumBound = 16384.f;  // 2^14: row-sum bound of one 64-key tile
+// Causal: pair q-blocks (nqb-1-j, j) in one workgroup.
+constexpr bool kFwdPairBlocks = false;
+
+template <int NW, bool CAUSAL, typename QT>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParams p) {
+    constexpr int D = 128, BM = NW * 32, BN = 64, NT = NW * 64;
+    constexpr int NKS = D / 16, NDT = D / 32;
+    constexpr int KST = D + 8, VST = BN + 8;          // padded row strides (bf16)
+    constexpr uint32_t KTB = BN * KST * 2, VTB = D * VST * 2;  // slot bytes
+    constexpr int NSLOT = NW == 8 ? 4 : 2;
+    constexpr int KLEAD = NW == 8 ? 4 : 3, VLEAD = NW == 8 ? 2 : 1;  // load distance (tiles)
+    __shared__ __attribute__((aligned(16))) bf16 sKb[NSLOT * BN * KST];
+    __shared__ __attribute__((aligned(16))) bf16 sVb[NSLOT * D * VST];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5, ln = lane & 31;
+    // Causal: workgroup j of a head runs q-block nqb-1-j, then q-block j, so
+    // every workgroup covers 2 nqb + 2 key tiles (one pass for the middle
+    // block of an odd nqb) and the grid has no long tail; both blocks share
+    // the head's K/V in the XCD's L2. Non-causal: one q-block each.
+    constexpr bool PAIR = CAUSAL && kFwdPairBlocks;
+    const int nwg = PAIR ? (p.nqb + 1) / 2 : p.nqb;
+    int bh, pj;
+    map_block(blockIdx.x, nwg, p.BH, CAUSAL && !PAIR, bh, pj);
+    const int Sq = p.Sq, Sk = p.Sk, Skp = p.Skp;
+    // Per q-block state (set by each pass): first query row of the block and
+    // of this wave, this lane's query row, number of 64-key tiles.
+    int q0 = 0, qw = 0, qi = 0, ntiles = 0;
+    bf16x8 qf[NKS];  // Q[qi][16ks + 8g .. +7] * sign(scale), in bf16
+
+    // ---- tile loads: instruction i of thread tid fills 16-byte chunk
+    // position i*NT + tid of a padded tile (K: 64 x 17 positions, Vt:
+    // 128 x 9); the last instruction of a tile covers its first waves only ----
+    constexpr int KCP = KST / 8, NKP = BN * KCP, VCP = VST / 8, NVP = D * VCP;
+    constexpr int NKI = (NKP + NT - 1) / NT, NVI = (NVP + NT - 1) / NT;  // loads per tile
+    constexpr int KLAST = NKP - (NKI - 1) * NT, VLAST = NVP - (NVI - 1) * NT;
+    static_assert(KLAST % 64 == 0 && VLAST % 64 == 0, "partial loads must be whole waves");
+    static_assert(NKI == NVI, "K and Vt tiles take the same number of loads");
+    uint32_t koff[NKI], voff[NVI];
+    for (int i = 0; i < NKI; i++) {
+        const int pos = i * NT + tid;
+        const int kr = pos / KCP, kc = pos % KCP;
+        koff[i] = (uint32_t)((((pos < NKP) ? kr : 0) * D + (kc < D / 8 ? kc : 0) * 8) * 2);
+        const int vr = pos / VCP, vc = pos % VCP;
+        voff[i] = (uint32_t)((((pos < NVP) ? vr : 0) * Skp + (vc < BN / 8 ? vc : 0) * 8) * 2);
+    }
+    // Waves that issue the last (partial) load of a K / Vt tile.
+    const uint32_t klast = wave * 64 < KLAST, vlast = wave * 64 < VLAST;
+    const bf16* Kg = (const bf16*)p.k + (size_t)bh * Skp * D;
+    const bf16* Vg = (const bf16*)p.v + (size_t)bh * D * Skp;
+    const brsrc krs = make_rsrc(Kg, (uint32_t)Skp * D * 2);
+    const brsrc vrs = make_rsrc(Vg, (uint32_t)Skp * D * 2);
+    const uint32_t kl = lds_addr(sKb) + wave * 1024, vl = lds_addr(sVb) + wave * 1024;
+    // Load i of K / Vt tile kt into ring slot `slot`.
+    auto dma_ki = [&](int kt, int slot, int i) {
+        if (i < NKI - 1) dma16(krs, kl + slot * KTB + i * NT * 16, koff[i], kt * BN * D * 2);
+        else dma16_if(krs, kl + slot * KTB + i * NT * 16, koff[i], kt * BN * D * 2, klast);
+    };
+    auto dma_vi = [&](int kt, int slot, int i) {
+        if (i < NVI - 1) dma16(vrs, vl + slot * VTB + i * NT * 16, voff[i], kt * BN * 2);
+        else dma16_if(vrs, vl + slot * VTB + i * NT * 16, voff[i], kt * BN * 2, vlast);
+    };
+    auto dma_k = [&](int kt, int slot) {
+        for (int i = 0; i < NKI; i++) dma_ki(kt, slot, i);
+    };
+    auto dma_v = [&](int kt, int slot) {
+        for (int i = 0; i < NVI; i++) dma_vi(kt, slot, i);
+    };
+    // Waits count loads conservatively (NKI - 1 per tile): a wave with the
+    // extra load keeps fewer of its newest loads in flight than it could,
+    // which only waits longer, and the count stays a compile-time immediate.
+    constexpr int NL = NKI - 1;
+
+    // ---- MFMA operand reads: K row mt*32 + ln, Vt row dt*32 + ln; chunk
+    // 2ks + g (bytes from a slot's start) ----
+    const uint32_t kq = (uint32_t)(ln * KST + g * 8) * 2, vq = (uint32_t)(ln * VST + g * 8) * 2;
+    const char* sKc = (const char*)sKb;
+    const char* sVc = (const char*)sVb;
+    auto kfrag = [&](uint32_t base, int ks, int mt) {
+        return *(const bf16x8*)(sKc + (base + kq) + (mt * 32 * KST + ks * 16) * 2);
+    };
+    auto vfrag = [&](uint32_t base, int ks, int dt) {
+        return *(const bf16x8*)(sVc + (base + vq) + (dt * 32 * VST + ks * 16) * 2);
+    };
+
+    f32x16 oacc[NDT];
+    // mc: this lane's running offset (log2 units); l: row sum relative to it.
+    float mc = 0.f, l = 0.f, alpha = 1.f;
+    const float c2 = p.scale_log2;
+
+    auto mask = [&](int kt, f32x16* s) {
+        const int kb = kt * BN + 4 * g;
+        for (int mt = 0; mt < 2; mt++)
+            for (int r = 0; r < 16; r++) {
+                const int key = kb + mt * 32 + 8 * (r >> 2) + (r & 3);
+                const bool off = key >= Sk || (CAUSAL && key > qi);
+                s[mt][r] = off ? -INFINITY : s[mt][r];
+            }
+    };
+    auto needs_mask = [&](int kt) {
+        const int kb = kt * BN;
+        return (kb + BN > Sk) || (CAUSAL && kb + BN - 1 > qw);
+    };
+    auto tile_max = [&](const f32x16* s) {
+        float t8[8];
+        for (int i = 0; i < 8; i++)
+            t8[i] = fmaxf(fmaxf(s[i >> 2][(i & 3) * 4 + 0], s[i >> 2][(i & 3) * 4 + 1]),
+                          fmaxf(s[i >> 2][(i & 3) * 4 + 2], s[i >> 2][(i & 3) * 4 + 3]));
+        const float mx = fmaxf(fmaxf(fmaxf(t8[0], t8[1]), fmaxf(t8[2], t8[3])),
+                               fmaxf(fmaxf(t8[4], t8[5]), fmaxf(t8[6], t8[7])));
+        return pair_max32(mx);
+    };
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 one2 = {(__bf16)1.0f, (__bf16)1.0f};
+    // P = exp2(s c - mc) of score pair k (0..15) of a tile: the packed bf16
+    // word; the row sum of the packed values is added into part[k & 3].
+    auto p_pair = [&](const f32x16* s, int k, float* part) {
+        const int mt = k >> 3, r = (k & 7) * 2;
+        const float e0 = fast_exp2(__builtin_fmaf(s[mt][r], c2, -mc));
+        const float e1 = fast_exp2(__builtin_fmaf(s[mt][r + 1], c2, -mc));
+        const bf16x2 pr = {to_bf16(e0), to_bf16(e1)};
+        part[k & 3] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, part[k & 3], false);
+        return __builtin_bit_cast(uint32_t, pr);
+    };
+    // Whole-tile P and row sum (prologue and the rare rescale branch).
+    auto p_tile = [&](const f32x16* s, u32x4* pk) {
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < 16; k++) pk[k >> 2][k & 3] = p_pair(s, k, part);
+        return (part[0] + part[1]) + (part[2] + part[3]);
+    };
+    u32x4 pp[4];  // P of the tile PV consumes next, bf16 pairs per 32-bit word
+
+    // One pipeline step (see the header). sA <- S^T(t+2), sB = S^T(t+1);
+    // pp holds P(t) and is overwritten with P(t+1) 16 keys at a time, each
+    // part after the PV MFMAs that read it were issued.
+    //
+    // The step is scheduled by hand: slot e issues the LDS read of MFMA e+3,
+    // MFMA e, possibly one tile load and the softmax micro-op mapped to it,
+    // and a sched_barrier keeps the compiler from regrouping slots (left to
+    // itself it serialises the S^T chains behind their LDS reads). MFMA order
+    // per 16-key PV k-step j: PV(j, dt = 0..3), then S^T k-steps 2j and 2j+1
+    // (mt = 0, 1), so six accumulator chains interleave.
+    //
+    // SS (steady state: both tile loads of the step are needed) spreads the
+    // loads over the stream; otherwise the needed ones are issued up front.
+    auto step = [&](auto ha_tag, auto hb_tag, auto ss_tag, int t, f32x16* sA, f32x16* sB) {
+        constexpr bool HA = decltype(ha_tag)::value;
+        constexpr bool HB = decltype(hb_tag)::value;
+        constexpr bool SS = decltype(ss_tag)::value;
+        const int kslot = (t + KLEAD) & (NSLOT - 1), vslot = (t + VLEAD) & (NSLOT - 1);
+        const bool dk = SS || t + KLEAD < ntiles, dv = SS || t + VLEAD < ntiles;
+        if constexpr (!SS) {
+            if (dk) dma_k(t + KLEAD, kslot);
+            if (dv) dma_v(t + VLEAD, vslot);
+        }
+        // Diagonal / key-end tiles only (a wave-uniform branch ahead of the
+        // step's MFMA stream).
+        if constexpr (HB)
+            if (needs_mask(t + 1)) mask(t + 1, sB);
+        const uint32_t vb = (uint32_t)(t & (NSLOT - 1)) * VTB;
+        const uint32_t kb = (uint32_t)((t + 2) & (NSLOT - 1)) * KTB;
+
+        constexpr int GW = HA ? 8 : 4;     // MFMAs per PV k-step group
+        constexpr int NM = 4 * GW;         // MFMAs in the step
+        constexpr int NU = HB ? 16 : 0;    // softmax micro-ops (one score pair each)
+        constexpr int LA = 3;              // LDS read lead (MFMAs)
+        constexpr int NDMA = 2 * NKI;      // tile loads of a steady-state step
+        bf16x8 opr[4];
+        auto fetch = [&](auto E) {
+            constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
+            if constexpr (w < 4) opr[e & 3] = vfrag(vb, j, w);
+            else opr[e & 3] = kfrag(kb, 2 * j + ((w - 4) >> 1), (w - 4) & 1);
+        };
+        auto issue = [&](auto E) {
+            constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
+            if constexpr (w < 4) {
+                oacc[w] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pp[j]), oacc[w]);
+            } else {
+                constexpr int kk = 2 * j + ((w - 4) >> 1), mt = (w - 4) & 1;
+                sA[mt] = mfma_bf16(opr[e & 3], qf[kk], kk == 0 ? f32x16{} : sA[mt]);
+            }
+        };
+        float part[4] = {0.f, 0.f, 0.f, 0.f};
+        // Slot of score pair k (16 keys j = k / 4 of P(t+1)): after the PV
+        // MFMAs of k-step j; past the stream's end when there is no S^T part.
+        auto uslot = [](int k) { return (k >> 2) * GW + 4 + (k & 3); };
+        auto uop = [&](auto U) {
+            constexpr int k = decltype(U)::value;
+            pp[k >> 2][k & 3] = p_pair(sB, k, part);
+            pin(pp[k >> 2][k & 3]);
+            pin(part[k & 3]);
+        };
+        static_for<LA>([&](auto E) { fetch(E); });
+        static_for<NM>([&](auto E) {
+            constexpr int e = decltype(E)::value;
+            if constexpr (e + LA < NM) fetch(std::integral_constant<int, e + LA>{});
+            issue(E);
+            // Tile loads at slots 1, 1 + NM/NDMA, ... alternating K and V.
+            if constexpr (SS && e % (NM / NDMA) == 1 && e / (NM / NDMA) < NDMA) {
+                constexpr int d = e / (NM / NDMA);
+                if constexpr (d % 2 == 0) dma_ki(t + KLEAD, kslot, d / 2);
+                else dma_vi(t + VLEAD, vslot, d / 2);
+            }
+            // Micro-op k computes score pair k; its results are pinned (an
+            // empty asm) so IR passes cannot sink the work out of its slot.
+            static_for<NU>([&](auto U) {
+                if constexpr (uslot(decltype(U)::value) == e) uop(U);
+            });
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        static_for<NU>([&](auto U) {
+            if constexpr (uslot(decltype(U)::value) >= NM) uop(U);
+        });
+        if constexpr (HB) {
+            float ts = (part[0] + part[1]) + (part[2] + part[3]);
+            alpha = 1.f;
+            // Rare: the tile's P is not bounded by the current offset (or is
+            // not finite). Move the offset to the tile max and redo the tile.
+            if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound))) {
+                const float mx = tile_max(sB) * c2;
+                const float mnew = mx > mc + kLazyLog2 ? mx : mc;
+                alpha = fast_exp2(mc - mnew);
+                mc = mnew;
+                ts = p_tile(sB, pp);
+            }
+            l = l * alpha + ts;
+        }
+
+        if constexpr (NW == 8) {
+            if (dk) GONN_VMCNT(2 * NL);
+            else if (dv) GONN_VMCNT(NL);
+            else GONN_VMCNT(0);
+        } else {
+            GONN_VMCNT(0);
+        }
+        __syncthreads();
+        if constexpr (HB) {
+            if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
+                for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
+        }
+    };
+    using Yes = std::integral_constant<bool, true>;
+    using No = std::integral_constant<bool, false>;
+
+    f32x16 s0[2], s1[2];
+    for (int pass = 0; pass < (PAIR ? 2 : 1); pass++) {
+    const int qb = !PAIR ? pj : (pass == 0 ? p.nqb - 1 - pj : pj);
+    if (pass == 1 && qb == p.nqb - 1 - pj) break;
+    q0 = qb * BM;
+    qw = q0 + wave * 32;
+    qi = qw + ln;
+    {
+        const QT* qrow = (const QT*)p.q + ((size_t)bh * Sq + (qi < Sq ? qi : 0)) * D;
+        const float sg = qi < Sq ? p.qsign : 0.f;
+        for (int ks = 0; ks < NKS; ks++) {
+            const int d0 = ks * 16 + g * 8;
+            float v[8];
+            if constexpr (sizeof(QT) == 4) {
+                const f32x4 a = *(const f32x4*)(qrow + d0), b = *(const f32x4*)(qrow + d0 + 4);
+                for (int i = 0; i < 4; i++) { v[i] = a[i]; v[4 + i] = b[i]; }
+            } else {
+                const u16x8 a = *(const u16x8*)(qrow + d0);
+                for (int i = 0; i < 8; i++) v[i] = bf16_to_f32(a[i]);
+            }
+            qf[ks] = pack8(v[0] * sg, v[1] * sg, v[2] * sg, v[3] * sg, v[4] * sg, v[5] * sg,
+                           v[6] * sg, v[7] * sg);
+        }
+    }
+    {
+        int kend = Sk;
+        if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
+        ntiles = (kend + BN - 1) / BN;
+    }
+    for (int dt = 0; dt < NDT; dt++) oacc[dt] = f32x16{};
+    alpha = 1.f;
+
+    // ---- prologue: S^T(0) -> P(0), S^T(1); the rings hold what step 0 needs ----
+    auto qk_slot = [&](int slot, f32x16* s) {
+        s[0] = f32x16{};
+        s[1] = f32x16{};
+        for (int ks = 0; ks < NKS; ks++)
+            for (int mt = 0; mt < 2; mt++) s[mt] = mfma_bf16(kfrag(slot * KTB, ks, mt), qf[ks], s[mt]);
+    };
+    auto last = [&](int kt) { return kt < ntiles ? kt : ntiles - 1; };
+    if constexpr (NW == 8) {
+        dma_k(0, 0);
+        dma_k(last(1), 1);
+        dma_v(0, 0);
+        dma_k(last(2), 2);
+        dma_k(last(3), 3);
+        dma_v(last(1), 1);
+        GONN_VMCNT(3 * NL);  // Q, K(0), K(1), V(0) landed
+        __syncthreads();
+        qk_slot(0, s0);
+        if (ntiles > 1) qk_slot(1, s1);
+    } else {
+        dma_k(0, 0);
+        dma_k(last(1), 1);
+        dma_v(0, 0);
+        GONN_VMCNT(0);
+        __syncthreads();
+        qk_slot(0, s0);
+        if (ntiles > 1) qk_slot(1, s1);
+        __syncthreads();  // K(0) read by every wave: its slot takes K(2)
+        dma_k(last(2), 0);
+    }
+    // First tile: exact offset (its max; key 0 is never masked, so it is
+    // finite).
+    if (needs_mask(0)) mask(0, s0);
+    mc = tile_max(s0) * c2;
+    l = p_tile(s0, pp);
+    if constexpr (NW == 8) GONN_VMCNT(2 * NL);  // K(2) landed (K(3), V(1) may be in flight)
+    else GONN_VMCNT(0);
+    __syncthreads();
+
+    // Steady state while both loads of a step are needed: t + KLEAD < ntiles.
+    int t = 0;
+    for (; t + KLEAD + 1 < ntiles; t += 2) {
+        step(Yes{}, Yes{}, Yes{}, t, s0, s1);
+        step(Yes{}, Yes{}, Yes{}, t + 1, s1, s0);
+    }
+    for (; t + 3 < ntiles; t += 2) {
+        step(Yes{}, Yes{}, No{}, t, s0, s1);
+        step(Yes{}, Yes{}, No{}, t + 1, s1, s0);
+    }
+    const int rem = ntiles - t;
+    if (rem == 3) {
+        step(Yes{}, Yes{}, No{}, t, s0, s1);
+        step(No{}, Yes{}, No{}, t + 1, s1, s0);
+        step(No{}, No{}, No{}, t + 2, s0, s1);
+    } else if (rem == 2) {
+        step(No{}, Yes{}, No{}, t, s0, s1);
+        step(No{}, No{}, No{}, t + 1, s1, s0);
+    } else {
+        step(No{}, No{}, No{}, t, s0, s1);
+    }
+
+    const float lt = pair_sum32(l);
+    if (qi < Sq) {
+        const float inv = 1.f / lt;
+        float* orow = p.o + ((size_t)bh * Sq + qi) * D;
+        for (int dt = 0; dt < NDT; dt++)
+            for (int rq = 0; rq < 4; rq++) {
+                f32x4 v;
+                for (int i = 0; i < 4; i++) v[i] = oacc[dt][rq * 4 + i] * inv;
+                *(f32x4*)(orow + dt * 32 + rq * 8 + g * 4) = v;
+            }
+        // LSE = (mc + log2 l) * ln 2, natural-log units of the scaled scores.
+        if (p.lse && g == 0) p.lse[(size_t)bh * Sq + qi] = (mc + fast_log2(lt)) * kLn2;
+    }
+    }  // pass
+}
+
+// ---------------------------------------------------------------------------
 // fp32-MFMA forward (32 keys per tile).
 // k-slot map of the QK^T product: step ks, group g <-> d = g*(D/2) + ks, so a
 // lane reads its K row and holds its Q row as contiguous runs of floats.
@@ -464,16 +869,34 @@ static void launch_bf16_d(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t
         fwd_bf16_kernel<D, C, float><<<grid, 256, 0, s>>>(p);
 }
 
-hipError_t launch_fwd(const FwdParams& p, int mode, int D, int causal, int q_bf16,
+// Waves per workgroup of the D = 128 bf16 forward (4: two workgroups per CU;
+// 8: one).
+constexpr int kFwdWaves = 4;
+
+template <bool C>
+static void launch_bf16_d128(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t s) {
+    if (q_bf16)
+        fwd_bf16_d128_kernel<kFwdWaves, C, bf16><<<grid, kFwdWaves * 64, 0, s>>>(p);
+    else
+        fwd_bf16_d128_kernel<kFwdWaves, C, float><<<grid, kFwdWaves * 64, 0, s>>>(p);
+}
+
+hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_bf16,
                       hipStream_t s) {
-    dim3 grid(p.nqb * p.BH);
+    FwdParams p = p_in;
+    // Query rows per workgroup.
+    const int bm = (mode == 1 && D == 128) ? kFwdWaves * 32 : 128;
+    p.nqb = (p.Sq + bm - 1) / bm;
+    // The bf16 D = 128 causal kernel pairs q-blocks (nqb-1-j, j) per workgroup.
+    const bool paired = mode == 1 && D == 128 && causal && kFwdPairBlocks;
+    dim3 grid((paired ? (p.nqb + 1) / 2 : p.nqb) * p.BH);
     if (mode == 1) {
         if (D == 64) {
             if (causal) launch_bf16_d<64, true>(p, q_bf16, grid, s);
             else launch_bf16_d<64, false>(p, q_bf16, grid, s);
         } else if (D == 128) {
-            if (causal) launch_bf16_d<128, true>(p, q_bf16, grid, s);
-            else launch_bf16_d<128, false>(p, q_bf16, grid, s);
+            if (causal) launch_bf16_d128<true>(p, q_bf16, grid, s);
+            else launch_bf16_d128<false>(p, q_bf16, grid, s);
         } else {
             return hipErrorInvalidValue;
         }

@@ -138,6 +138,18 @@ GONN_DEV void dma16(brsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
                  :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff)
                  : "memory");
 }
+// dma16 when the wave-uniform `on` is non-zero. The skip is a scalar branch
+// inside the asm statement, so the caller's code stays one basic block (an
+// exec-masked branch around the load would split the hand-scheduled MFMA
+// stream and perturb register allocation).
+GONN_DEV void dma16_if(brsrc r, uint32_t lds, uint32_t voff, uint32_t soff, uint32_t on) {
+    asm volatile(
+        "s_cmp_eq_u32 %4, 0\n\ts_cbranch_scc1 1f\n\t"
+        "s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds\n1:"
+        :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff),
+           "s"(__builtin_amdgcn_readfirstlane(on))
+        : "memory", "scc");
+}
 // LDS byte address of a __shared__ object (apply to the array itself, so the
 // address-space cast folds to a constant).
 GONN_DEV uint32_t lds_addr(const void* p) {

@@ -156,8 +156,14 @@ def test_c5_fwd_bwd_full_size():
     assert_close(dk[:, rows], rk[:, rows], mode, "C5 dK")
     assert_close(dv[:, rows], rv[:, rows], mode, "C5 dV")
     # Identities over the full output (fp64 sums of the fp32 results).
+    # Error model of sum_j dV_j - sum_i dO_i = sum_i dO_i (sum_j P~_ij - 1):
+    # the bf16 P~ and the LSE error (~1e-3, up to 7e-3 on the first rows)
+    # give per-row deviations eps_i ~ 1.5e-3, so each of the 32 x 128 column
+    # sums is ~N(0, sqrt(8192) * 1.5e-3 = 0.14); the largest of 4096 lands near
+    # 0.5. atol 1.0 (~7 sigma) still flags any dropped or repeated key tile,
+    # which moves a column sum by O(10).
     np.testing.assert_allclose(dv.astype(np.float64).sum(axis=1),
-                               g.astype(np.float64).sum(axis=1), atol=0.5, rtol=1e-3)
+                               g.astype(np.float64).sum(axis=1), atol=1.0, rtol=1e-3)
     assert np.abs(dk.astype(np.float64).sum(axis=1)).max() < 0.5
     say("C5 determinism")
     _, _, dq2, dk2, dv2 = _fwd_bwd(q, k, v, g, True, mode)
