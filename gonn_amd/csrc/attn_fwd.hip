@@ -374,6 +374,8 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_kernel(FwdParams p) {
 constexpr float kSumBound = 16384.f;  // 2^14: row-sum bound of one 64-key tile
 // Causal: pair q-blocks (nqb-1-j, j) in one workgroup.
 constexpr bool kFwdPairBlocks = false;
+// Wave issue priority (s_setprio) during a step's MFMA stream.
+constexpr int kFwdStreamPrio = 1;
 
 template <int NW, bool CAUSAL, typename QT>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParams p) {
@@ -396,7 +398,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     constexpr bool PAIR = CAUSAL && kFwdPairBlocks;
     const int nwg = PAIR ? (p.nqb + 1) / 2 : p.nqb;
     int bh, pj;
-    map_block(blockIdx.x, nwg, p.BH, CAUSAL && !PAIR, bh, pj);
+    map_block(blockIdx.x, nwg, p.BH, CAUSAL && !PAIR, bh, pj, CAUSAL && !PAIR ? p.hgroup : 1);
     const int Sq = p.Sq, Sk = p.Sk, Skp = p.Skp;
     // Per q-block state (set by each pass): first query row of the block and
     // of this wave, this lane's query row, number of 64-key tiles.
@@ -517,8 +519,21 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     // (mt = 0, 1), so six accumulator chains interleave.
     //
     // SS (steady state: both tile loads of the step are needed) spreads the
-    // loads over the stream; otherwise the needed ones are issued up front.
-    auto step = [&](auto ha_tag, auto hb_tag, auto ss_tag, int t, f32x16* sA, f32x16* sB) {
+    // loads over the first half of the stream; otherwise the needed ones are
+    // issued up front.
+    //
+    // GB (NW = 8, waves 4-7): the wave group runs half a step behind waves
+    // 0-3: its barrier (and the wait for its loads) sits in the middle of its
+    // MFMA stream instead of at the end, so on every SIMD one wave's barrier,
+    // tile-load wait and step start overlap the other wave's MFMAs. Both
+    // groups still meet once per step at the same barrier instance k (group
+    // A at the end of step k, group B halfway through step k): tiles for step
+    // k are waited for by every wave before instance k-1, and a ring slot is
+    // refilled in step j only after instance j-1, by which both groups are
+    // done with the tile of step j-2 it held.
+    const bool gB = NW == 8 && wave >= 4;  // wave-uniform
+    auto step = [&](auto ha_tag, auto hb_tag, auto ss_tag, int t, f32x16* sA,
+                    f32x16* sB) __attribute__((always_inline)) {
         constexpr bool HA = decltype(ha_tag)::value;
         constexpr bool HB = decltype(hb_tag)::value;
         constexpr bool SS = decltype(ss_tag)::value;
@@ -537,6 +552,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
 
         constexpr int GW = HA ? 8 : 4;     // MFMAs per PV k-step group
         constexpr int NM = 4 * GW;         // MFMAs in the step
+        constexpr int MID = NM / 2;        // group B's barrier: before slot MID
         constexpr int NU = HB ? 16 : 0;    // softmax micro-ops (one score pair each)
         constexpr int LA = 3;              // LDS read lead (MFMAs)
         constexpr int NDMA = 2 * NKI;      // tile loads of a steady-state step
@@ -556,36 +572,85 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
             }
         };
         float part[4] = {0.f, 0.f, 0.f, 0.f};
-        // Slot of score pair k (16 keys j = k / 4 of P(t+1)): after the PV
-        // MFMAs of k-step j; past the stream's end when there is no S^T part.
+        // Score pair k (16 keys j = k / 4 of P(t+1)) in three micro-ops two
+        // slots apart so no slot waits on a dependent VALU result: (0) the
+        // FMA s c - mc, (1) exp2, (2) bf16 pack into pp and row sum. Stage 2
+        // lands in slot uslot(k), after the PV MFMAs of k-step j read pp[j];
+        // micro-ops past the stream's end run after it.
         auto uslot = [](int k) { return (k >> 2) * GW + 4 + (k & 3); };
-        auto uop = [&](auto U) {
-            constexpr int k = decltype(U)::value;
-            pp[k >> 2][k & 3] = p_pair(sB, k, part);
-            pin(pp[k >> 2][k & 3]);
-            pin(part[k & 3]);
+        float ua[16][2], ub[16][2];
+        auto uop = [&](auto U, auto S) {
+            constexpr int k = decltype(U)::value, stage = decltype(S)::value;
+            constexpr int mt = k >> 3, r = (k & 7) * 2;
+            if constexpr (stage == 0) {
+                ua[k][0] = __builtin_fmaf(sB[mt][r], c2, -mc);
+                ua[k][1] = __builtin_fmaf(sB[mt][r + 1], c2, -mc);
+                pin(ua[k][0]);
+                pin(ua[k][1]);
+            } else if constexpr (stage == 1) {
+                ub[k][0] = fast_exp2(ua[k][0]);
+                ub[k][1] = fast_exp2(ua[k][1]);
+                pin(ub[k][0]);
+                pin(ub[k][1]);
+            } else {
+                const bf16x2 pr = {to_bf16(ub[k][0]), to_bf16(ub[k][1])};
+                part[k & 3] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, part[k & 3], false);
+                pp[k >> 2][k & 3] = __builtin_bit_cast(uint32_t, pr);
+                pin(pp[k >> 2][k & 3]);
+                pin(part[k & 3]);
+            }
         };
+        // Run the micro-ops of slot e (stage st of pair k sits at slot
+        // uslot(k) - 2 + st); e = NM runs everything past the stream's end.
+        auto uops_at = [&](auto E) {
+            constexpr int e = decltype(E)::value;
+            static_for<3>([&](auto S) {
+                static_for<NU>([&](auto U) {
+                    constexpr int at = uslot(decltype(U)::value) - 2 + decltype(S)::value;
+                    if constexpr (e < NM ? at == e : at >= NM) uop(U, S);
+                });
+            });
+        };
+        // Raised issue priority over the MFMA stream: on a SIMD shared with
+        // the other workgroup's wave, that wave's step start and barrier
+        // then fill the gaps of this stream rather than delay it.
+        __builtin_amdgcn_s_setprio(kFwdStreamPrio);
         static_for<LA>([&](auto E) { fetch(E); });
+        auto wait_loads = [&] {
+            if constexpr (NW == 8) {
+                if (dk) GONN_VMCNT(2 * NL);
+                else if (dv) GONN_VMCNT(NL);
+                else GONN_VMCNT(0);
+            } else {
+                GONN_VMCNT(0);
+            }
+        };
         static_for<NM>([&](auto E) {
             constexpr int e = decltype(E)::value;
+            if constexpr (NW == 8 && e == MID) {
+                if (gB) {
+                    wait_loads();
+                    __syncthreads();
+                }
+            }
             if constexpr (e + LA < NM) fetch(std::integral_constant<int, e + LA>{});
             issue(E);
-            // Tile loads at slots 1, 1 + NM/NDMA, ... alternating K and V.
-            if constexpr (SS && e % (NM / NDMA) == 1 && e / (NM / NDMA) < NDMA) {
-                constexpr int d = e / (NM / NDMA);
+            // Tile loads at slots 1, 1 + DS, ..., alternating K and V; with
+            // NW = 8 all before slot MID (group B waits for them there).
+            constexpr int DSPAN = NW == 8 ? MID : NM;
+            constexpr int DS = DSPAN / NDMA > 0 ? DSPAN / NDMA : 1;
+            if constexpr (SS && e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
+                constexpr int d = (e - 1) / DS;
                 if constexpr (d % 2 == 0) dma_ki(t + KLEAD, kslot, d / 2);
                 else dma_vi(t + VLEAD, vslot, d / 2);
             }
-            // Micro-op k computes score pair k; its results are pinned (an
-            // empty asm) so IR passes cannot sink the work out of its slot.
-            static_for<NU>([&](auto U) {
-                if constexpr (uslot(decltype(U)::value) == e) uop(U);
-            });
+            // Softmax micro-ops; their results are pinned (an empty asm) so
+            // IR passes cannot sink the work out of its slot.
+            uops_at(E);
             __builtin_amdgcn_sched_barrier(0);
         });
-        static_for<NU>([&](auto U) {
-            if constexpr (uslot(decltype(U)::value) >= NM) uop(U);
-        });
+        uops_at(std::integral_constant<int, NM>{});
+        __builtin_amdgcn_s_setprio(0);
         if constexpr (HB) {
             float ts = (part[0] + part[1]) + (part[2] + part[3]);
             alpha = 1.f;
@@ -601,14 +666,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
             l = l * alpha + ts;
         }
 
-        if constexpr (NW == 8) {
-            if (dk) GONN_VMCNT(2 * NL);
-            else if (dv) GONN_VMCNT(NL);
-            else GONN_VMCNT(0);
-        } else {
-            GONN_VMCNT(0);
+        if (!gB) {
+            wait_loads();
+            __syncthreads();
         }
-        __syncthreads();
         if constexpr (HB) {
             if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
                 for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
@@ -689,25 +750,27 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     __syncthreads();
 
     // Steady state while both loads of a step are needed: t + KLEAD < ntiles.
-    int t = 0;
-    for (; t + KLEAD + 1 < ntiles; t += 2) {
-        step(Yes{}, Yes{}, Yes{}, t, s0, s1);
-        step(Yes{}, Yes{}, Yes{}, t + 1, s1, s0);
-    }
-    for (; t + 3 < ntiles; t += 2) {
-        step(Yes{}, Yes{}, No{}, t, s0, s1);
-        step(Yes{}, Yes{}, No{}, t + 1, s1, s0);
-    }
-    const int rem = ntiles - t;
-    if (rem == 3) {
-        step(Yes{}, Yes{}, No{}, t, s0, s1);
-        step(No{}, Yes{}, No{}, t + 1, s1, s0);
-        step(No{}, No{}, No{}, t + 2, s0, s1);
-    } else if (rem == 2) {
-        step(No{}, Yes{}, No{}, t, s0, s1);
-        step(No{}, No{}, No{}, t + 1, s1, s0);
-    } else {
-        step(No{}, No{}, No{}, t, s0, s1);
+    {
+        int t = 0;
+        for (; t + KLEAD + 1 < ntiles; t += 2) {
+            step(Yes{}, Yes{}, Yes{}, t, s0, s1);
+            step(Yes{}, Yes{}, Yes{}, t + 1, s1, s0);
+        }
+        for (; t + 3 < ntiles; t += 2) {
+            step(Yes{}, Yes{}, No{}, t, s0, s1);
+            step(Yes{}, Yes{}, No{}, t + 1, s1, s0);
+        }
+        const int rem = ntiles - t;
+        if (rem == 3) {
+            step(Yes{}, Yes{}, No{}, t, s0, s1);
+            step(No{}, Yes{}, No{}, t + 1, s1, s0);
+            step(No{}, No{}, No{}, t + 2, s0, s1);
+        } else if (rem == 2) {
+            step(No{}, Yes{}, No{}, t, s0, s1);
+            step(No{}, No{}, No{}, t + 1, s1, s0);
+        } else {
+            step(No{}, No{}, No{}, t, s0, s1);
+        }
     }
 
     const float lt = pair_sum32(l);
@@ -890,6 +953,20 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
     // The bf16 D = 128 causal kernel pairs q-blocks (nqb-1-j, j) per workgroup.
     const bool paired = mode == 1 && D == 128 && causal && kFwdPairBlocks;
     dim3 grid((paired ? (p.nqb + 1) / 2 : p.nqb) * p.BH);
+    // Causal dispatch groups: about one XCD's worth of workgroup slots
+    // (CUs / 8 XCDs x 2 resident workgroups) of q-blocks per group.
+    p.hgroup = 1;
+    if (causal && mode == 1 && D == 128 && !paired) {
+        static int cus = 0;
+        if (!cus) {
+            int dev = 0;
+            if (hipGetDevice(&dev) != hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+                cus = 256;
+        }
+        const int slots = cus / 8 * (8 / kFwdWaves);
+        p.hgroup = slots / p.nqb > 1 ? slots / p.nqb : 1;
+    }
     if (mode == 1) {
         if (D == 64) {
             if (causal) launch_bf16_d<64, true>(p, q_bf16, grid, s);

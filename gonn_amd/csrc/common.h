@@ -89,12 +89,32 @@ GONN_DEV float row_sum16(float x) {
 // slice's K/V (or Q/dO) run on the same XCD and share its L2. Within a slice
 // the block order is reversed when `reverse` is set, which puts the longest
 // causal blocks first.
-GONN_DEV void map_block(int L, int nblk, int BH, bool reverse, int& bh, int& blk) {
+//
+// hgroup > 1 (causal grids): the blocks of hgroup consecutive slices of an
+// XCD are dispatched interleaved, longest first (block nblk-1 of each slice,
+// then nblk-2, ...). With hgroup * nblk close to the XCD's workgroup slots,
+// each group's long blocks start together and its short blocks fill in
+// behind them, so the grid ends without a tail of long blocks, while only
+// about one group's K/V is live in the XCD's L2 at a time.
+GONN_DEV void map_block(int L, int nblk, int BH, bool reverse, int& bh, int& blk,
+                        int hgroup = 1) {
     const int N = nblk * BH;
     int idx = L;
     if ((N & 7) == 0) {
         const int per = N >> 3;
         idx = (L & 7) * per + (L >> 3);
+        if (hgroup > 1 && per % nblk == 0) {
+            // XCD-local position i among its Hx whole slices.
+            const int x = L & 7, i = L >> 3, Hx = per / nblk;
+            const int gsz = hgroup * nblk, gi = i / gsz, r = i - gi * gsz;
+            const int gh = Hx - gi * hgroup < hgroup ? Hx - gi * hgroup : hgroup;
+            const int rank = r / gh, hs = r - rank * gh;
+            bh = x * Hx + gi * hgroup + hs;
+            blk = reverse ? (nblk - 1 - rank) : rank;
+            bh = __builtin_amdgcn_readfirstlane(bh);
+            blk = __builtin_amdgcn_readfirstlane(blk);
+            return;
+        }
     }
     bh = idx / nblk;
     const int r = idx - bh * nblk;

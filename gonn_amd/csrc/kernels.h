@@ -16,6 +16,7 @@ struct FwdParams {
     float scale_log2;  // |scale| * log2(e)
     float scale_abs;   // |scale|
     float qsign;       // sign(scale) (Q is negated for a negative scale)
+    int hgroup;        // slices whose blocks are dispatched interleaved (map_block)
 };
 
 struct DecodeParams {
