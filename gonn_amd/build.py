@@ -3,7 +3,9 @@
     python -m gonn_amd.build          # or: python gonn_amd/build.py
 
 Every .hip file under gonn_amd/csrc is compiled with hipcc for gfx950 only and
-linked into one shared library exposing the C ABI of include/gonn_hip.h.
+linked into one shared library exposing the C ABI of include/gonn_hip.h. The
+C++ host mirror of GoNN's attention seam (gonn_amd/host/*.cpp) is built on
+top of it as gonn_amd/libgonn_host.so.
 Packed-fp32 VALU instructions are disabled for device code; hipcc's host pass
 reports that feature as unknown, which is harmless.
 """
@@ -56,6 +58,25 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
+HOST_LIB = os.path.join(HERE, "libgonn_host.so")
+HOST_SRC = os.path.join(HERE, "host")
+
+
+def build_host(verbose: bool = False) -> str:
+    """The C++ host mirror of GoNN's attention seam (gonn_amd/host) as
+    libgonn_host.so, linked against libgonn_hip.so (found next to it)."""
+    srcs = sorted(os.path.join(HOST_SRC, f) for f in os.listdir(HOST_SRC) if f.endswith(".cpp"))
+    tmp = HOST_LIB + ".tmp"
+    cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+           "-I", HOST_SRC, "-I", os.path.join(os.path.dirname(HERE), "include"), *srcs,
+           "-L", HERE, "-lgonn_hip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    subprocess.run(cmd, check=True)
+    os.replace(tmp, HOST_LIB)
+    return HOST_LIB
+
+
 def build(verbose: bool = False) -> str:
     os.makedirs(BUILD, exist_ok=True)
     srcs = sources()
@@ -67,6 +88,7 @@ def build(verbose: bool = False) -> str:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)
     os.replace(tmp, LIB)
+    build_host(verbose)
     return LIB
 
 

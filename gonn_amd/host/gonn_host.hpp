@@ -1,0 +1,149 @@
+// gonn_host.hpp -- C++ host mirror of GoNN's attention seam over the C ABI.
+//
+// GoNN's host side for this path is Go: the cgo wrappers backend/cuda/cuda.go
+// (flash entry points :125-194) and the build-tagged nn seam
+// nn/flashattn_cuda.go:13-38, called from MultiHeadAttention.Forward /
+// ForwardFused (nn/attention.go:107-180). This header restates that layer in
+// C++ on top of include/gonn_hip.h, with the same names, argument meaning and
+// error behaviour:
+//
+//   gonn::hip  (backend/hip, the counterpart of backend/cuda/cuda.go)
+//     Available, Supports, SetMode, FlashAttnF64, FlashAttnF64Fwd,
+//     FlashAttnF64Bwd, BenchFlashAttnF64
+//   gonn::nn   (nn/flashattn_hip.go + the fused branch of nn/attention.go)
+//     Tensor, Linear, fusedAttnAvailable, fusedAttnSupports, fusedAttnF64,
+//     fusedAttnDiff, MultiHeadAttention::{Forward, ForwardFused}
+//
+// Where the Go code panics (slice length mismatch, checkQKVDims, a failed
+// device call surfaced by the new ABI's status codes) these throw:
+// std::invalid_argument for argument errors, gonn::hip::Error for a non-zero
+// ABI status. Tensors hold host float64 data, like tensor.Tensor
+// (tensor/tensor.go:22-23). The attention core only runs on the device: with
+// no library or no gfx950 device the fused calls throw, there is no CPU
+// attention path in this library.
+#pragma once
+
+#include <array>
+#include <functional>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace gonn {
+namespace hip {
+
+// A non-zero status from the C ABI (GONN_E_* or a hipError_t value).
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& where);
+};
+
+// cuda.go has no Available(): the Go cuda build returns true at compile time
+// (nn/flashattn_cuda.go:13). This is a runtime device query.
+bool Available();
+// Head-dim / shape predicate replacing the D == 64 gate of nn/attention.go:129.
+bool Supports(int D, int Tq, int Tk);
+// 0 = fp32-MFMA (default), 1 = bf16-MFMA, for the f64 entry points.
+void SetMode(int mode);
+int Mode();
+
+// cuda.go:128-140: O = softmax(scale Q K^T + causal mask) V on flat
+// (BH, S, d) float64 data; O is caller-allocated.
+void FlashAttnF64(const std::vector<double>& Q, const std::vector<double>& K,
+                  const std::vector<double>& V, std::vector<double>& O, int BH, int S, int d,
+                  double scale, bool causal);
+
+struct FwdOut {
+    std::vector<double> O;  // (BH, S, d)
+    std::vector<double> L;  // (BH, S) log-sum-exp, natural log
+};
+// cuda.go:144-160.
+FwdOut FlashAttnF64Fwd(const std::vector<double>& Q, const std::vector<double>& K,
+                       const std::vector<double>& V, int BH, int S, int d, double scale,
+                       bool causal);
+
+struct BwdOut {
+    std::vector<double> dQ, dK, dV;
+};
+// cuda.go:162-184.
+BwdOut FlashAttnF64Bwd(const std::vector<double>& Q, const std::vector<double>& K,
+                       const std::vector<double>& V, const std::vector<double>& O,
+                       const std::vector<double>& L, const std::vector<double>& dO, int BH,
+                       int S, int d, double scale, bool causal);
+
+// cuda.go:188-194: mean milliseconds of `iters` device-resident forwards.
+double BenchFlashAttnF64(int BH, int S, int d, int iters, bool causal);
+
+}  // namespace hip
+
+namespace nn {
+
+// Host float64 tensor, row-major (tensor/tensor.go:22-23).
+struct Tensor {
+    std::vector<double> Data;
+    std::vector<int> Shape;
+
+    static Tensor New(std::vector<double> data, std::vector<int> shape);
+    static Tensor Zeros(std::vector<int> shape);
+    size_t Numel() const;
+    // Reshape keeps the data (tensor/ops_shape.go:5-51).
+    Tensor Reshape(std::vector<int> shape) const;
+    // Permute(0, 2, 1, 3) of a 4-D tensor, materialised as a copy the way
+    // tensor/ops_shape.go:64-107 does.
+    Tensor Permute0213() const;
+};
+
+// y = x W^T + b (nn/linear.go:40-59); W is (out, in), b (out) or empty.
+struct Linear {
+    Tensor W;
+    std::vector<double> B;
+    Tensor Forward(const Tensor& x) const;
+};
+
+bool fusedAttnAvailable();
+bool fusedAttnSupports(int D, int Tq, int Tk);
+// nn/flashattn_cuda.go:17-21.
+std::vector<double> fusedAttnF64(const std::vector<double>& Q, const std::vector<double>& K,
+                                 const std::vector<double>& V, int BH, int S, int D,
+                                 double scale, bool causal);
+
+// What nn/flashattn_cuda.go:26-38 returns: the output tensor and the custom
+// autograd node tensor.MakeNode(out, "FlashAttn", ...) attaches to it. The
+// node keeps the inputs, O and L, and maps the upstream gradient to
+// (dQ, dK, dV) with the device backward.
+struct FlashAttnNode {
+    std::string Op = "FlashAttn";
+    std::function<std::array<Tensor, 3>(const Tensor& grad)> Backward;
+};
+struct DiffOut {
+    Tensor Out;
+    FlashAttnNode Node;
+};
+DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
+                      double scale, bool causal);
+
+// nn.MultiHeadAttention with the fused core (nn/attention.go:38-180).
+// Weights are given explicitly: GoNN draws them from Go's math/rand stream
+// (nn/linear.go:20-36).
+class MultiHeadAttention {
+  public:
+    int EmbedDim, NumHeads, HeadDim, KDim, VDim;
+    Linear QProj, KProj, VProj, OutProj;
+
+    MultiHeadAttention(int embedDim, int numHeads, Linear q, Linear k, Linear v, Linear out);
+
+    // Forward (nn/attention.go:107-148) through the differentiable fused core;
+    // the node of the last call is kept in LastNode for a backward pass.
+    Tensor Forward(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
+    // ForwardFused (nn/attention.go:159-180): inference core, no node.
+    Tensor ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
+
+    FlashAttnNode LastNode;
+
+  private:
+    void checkQKVDims(const Tensor& q, const Tensor& k, const Tensor& v) const;
+    void requireFused(int D, int Tq, int Tk) const;
+};
+
+}  // namespace nn
+}  // namespace gonn

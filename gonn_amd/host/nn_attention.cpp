@@ -1,0 +1,202 @@
+// nn_attention.cpp -- gonn::nn: the fused attention seam and the fused branch
+// of MultiHeadAttention, mirroring nn/flashattn_cuda.go:13-38 and
+// nn/attention.go:83-180 over gonn::hip.
+#include <cmath>
+#include <memory>
+#include <string>
+#include <utility>
+
+#include "gonn_host.hpp"
+
+namespace gonn {
+namespace nn {
+
+namespace {
+
+std::string shape_str(const std::vector<int>& s) {
+    std::string r = "[";
+    for (size_t i = 0; i < s.size(); i++) r += (i ? " " : "") + std::to_string(s[i]);
+    return r + "]";
+}
+
+size_t prod(const std::vector<int>& s) {
+    size_t n = 1;
+    for (int x : s) {
+        if (x < 0) throw std::invalid_argument("tensor: negative dimension");
+        n *= (size_t)x;
+    }
+    return n;
+}
+
+}  // namespace
+
+Tensor Tensor::New(std::vector<double> data, std::vector<int> shape) {
+    if (data.size() != prod(shape))
+        throw std::invalid_argument("tensor.New: data length " + std::to_string(data.size()) +
+                                    " does not match shape " + shape_str(shape));
+    Tensor t;
+    t.Data = std::move(data);
+    t.Shape = std::move(shape);
+    return t;
+}
+
+Tensor Tensor::Zeros(std::vector<int> shape) {
+    const size_t n = prod(shape);
+    return New(std::vector<double>(n, 0.0), std::move(shape));
+}
+
+size_t Tensor::Numel() const { return Data.size(); }
+
+Tensor Tensor::Reshape(std::vector<int> shape) const {
+    if (prod(shape) != Data.size())
+        throw std::invalid_argument("Reshape: cannot reshape " + shape_str(Shape) + " to " +
+                                    shape_str(shape));
+    return New(Data, std::move(shape));
+}
+
+Tensor Tensor::Permute0213() const {
+    if (Shape.size() != 4) throw std::invalid_argument("Permute: need a 4-D tensor");
+    const int A = Shape[0], B = Shape[1], C = Shape[2], D = Shape[3];
+    std::vector<double> out(Data.size());
+    for (int a = 0; a < A; a++)
+        for (int b = 0; b < B; b++)
+            for (int c = 0; c < C; c++) {
+                const double* src = &Data[(((size_t)a * B + b) * C + c) * D];
+                double* dst = &out[(((size_t)a * C + c) * B + b) * D];
+                for (int d = 0; d < D; d++) dst[d] = src[d];
+            }
+    return New(std::move(out), {A, C, B, D});
+}
+
+Tensor Linear::Forward(const Tensor& x) const {
+    if (W.Shape.size() != 2) throw std::invalid_argument("Linear: W must be (out, in)");
+    const int out = W.Shape[0], in = W.Shape[1];
+    if (x.Shape.empty() || x.Shape.back() != in)
+        throw std::invalid_argument("Linear: input shape " + shape_str(x.Shape) +
+                                    ", want (..., " + std::to_string(in) + ")");
+    if (!B.empty() && (int)B.size() != out) throw std::invalid_argument("Linear: bias length");
+    const size_t N = x.Numel() / (size_t)in;
+    std::vector<double> y(N * (size_t)out);
+    // y[n][o] = sum_i x[n][i] W[o][i] (+ b[o]), the x @ W^T + b of
+    // nn/linear.go:53-57, summed in input order.
+    for (size_t n = 0; n < N; n++) {
+        const double* xr = &x.Data[n * in];
+        for (int o = 0; o < out; o++) {
+            const double* wr = &W.Data[(size_t)o * in];
+            double acc = 0.0;
+            for (int i = 0; i < in; i++) acc += xr[i] * wr[i];
+            y[n * out + o] = B.empty() ? acc : acc + B[o];
+        }
+    }
+    std::vector<int> shape = x.Shape;
+    shape.back() = out;
+    return Tensor::New(std::move(y), std::move(shape));
+}
+
+bool fusedAttnAvailable() { return hip::Available(); }
+
+bool fusedAttnSupports(int D, int Tq, int Tk) { return hip::Supports(D, Tq, Tk); }
+
+std::vector<double> fusedAttnF64(const std::vector<double>& Q, const std::vector<double>& K,
+                                 const std::vector<double>& V, int BH, int S, int D,
+                                 double scale, bool causal) {
+    std::vector<double> O(Q.size(), 0.0);
+    hip::FlashAttnF64(Q, K, V, O, BH, S, D, scale, causal);
+    return O;
+}
+
+DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
+                      double scale, bool causal) {
+    hip::FwdOut f = hip::FlashAttnF64Fwd(qp.Data, kp.Data, vp.Data, BH, S, D, scale, causal);
+    DiffOut r;
+    r.Out = Tensor::New(f.O, qp.Shape);
+    // The node's closure holds the inputs and the saved O and L, as the Go
+    // closure captures them (nn/flashattn_cuda.go:29-37).
+    auto saved = std::make_shared<std::array<Tensor, 3>>(std::array<Tensor, 3>{qp, kp, vp});
+    auto O = std::make_shared<std::vector<double>>(std::move(f.O));
+    auto L = std::make_shared<std::vector<double>>(std::move(f.L));
+    r.Node.Backward = [saved, O, L, BH, S, D, scale, causal](const Tensor& grad) {
+        const Tensor &q = (*saved)[0], &k = (*saved)[1], &v = (*saved)[2];
+        hip::BwdOut b =
+            hip::FlashAttnF64Bwd(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH, S, D, scale, causal);
+        return std::array<Tensor, 3>{Tensor::New(std::move(b.dQ), q.Shape),
+                                     Tensor::New(std::move(b.dK), k.Shape),
+                                     Tensor::New(std::move(b.dV), v.Shape)};
+    };
+    return r;
+}
+
+MultiHeadAttention::MultiHeadAttention(int embedDim, int numHeads, Linear q, Linear k, Linear v,
+                                       Linear out)
+    : EmbedDim(embedDim), NumHeads(numHeads), HeadDim(0), KDim(0), VDim(0),
+      QProj(std::move(q)), KProj(std::move(k)), VProj(std::move(v)), OutProj(std::move(out)) {
+    // nn/attention.go:45-58
+    if (numHeads <= 0 || embedDim % numHeads != 0)
+        throw std::invalid_argument("MultiHeadAttention: embedDim must be divisible by numHeads");
+    HeadDim = embedDim / numHeads;
+    KDim = KProj.W.Shape.size() == 2 ? KProj.W.Shape[1] : 0;
+    VDim = VProj.W.Shape.size() == 2 ? VProj.W.Shape[1] : 0;
+}
+
+// nn/attention.go:83-103
+void MultiHeadAttention::checkQKVDims(const Tensor& q, const Tensor& k, const Tensor& v) const {
+    const int kd = KDim ? KDim : EmbedDim, vd = VDim ? VDim : EmbedDim;
+    if (q.Shape.size() != 3 || q.Shape[2] != EmbedDim)
+        throw std::invalid_argument("MultiHeadAttention: q shape " + shape_str(q.Shape) +
+                                    ", want (B, Tq, " + std::to_string(EmbedDim) + ")");
+    if (k.Shape.size() != 3 || k.Shape[2] != kd)
+        throw std::invalid_argument("MultiHeadAttention: k shape " + shape_str(k.Shape) +
+                                    ", want (B, Tk, kdim=" + std::to_string(kd) + ")");
+    if (v.Shape.size() != 3 || v.Shape[2] != vd)
+        throw std::invalid_argument("MultiHeadAttention: v shape " + shape_str(v.Shape) +
+                                    ", want (B, Tk, vdim=" + std::to_string(vd) + ")");
+    if (k.Shape[1] != v.Shape[1])
+        throw std::invalid_argument("MultiHeadAttention: k and v sequence lengths differ (" +
+                                    std::to_string(k.Shape[1]) + " vs " +
+                                    std::to_string(v.Shape[1]) + ")");
+}
+
+// The reference takes its CPU core when the gate at nn/attention.go:129 is
+// false; this library has no CPU attention core, so the gate failing is an
+// error here.
+void MultiHeadAttention::requireFused(int D, int Tq, int Tk) const {
+    if (!fusedAttnAvailable())
+        throw hip::Error(-5, "nn: fused attention needs libgonn_hip.so and a gfx950 device");
+    if (!fusedAttnSupports(D, Tq, Tk) || Tq != Tk)
+        throw std::invalid_argument("nn: the fused core needs D in {64, 128} and Tq == Tk, got D=" +
+                                    std::to_string(D) + " Tq=" + std::to_string(Tq) +
+                                    " Tk=" + std::to_string(Tk));
+}
+
+Tensor MultiHeadAttention::Forward(const Tensor& q, const Tensor& k, const Tensor& v,
+                                   bool causal) {
+    checkQKVDims(q, k, v);
+    const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1], H = NumHeads, D = HeadDim;
+    requireFused(D, Tq, Tk);
+    // project; (B, T, H, D) -> (B, H, T, D)   nn/attention.go:115-122
+    const Tensor qp = QProj.Forward(q).Reshape({B, Tq, H, D}).Permute0213();
+    const Tensor kp = KProj.Forward(k).Reshape({B, Tk, H, D}).Permute0213();
+    const Tensor vp = VProj.Forward(v).Reshape({B, Tk, H, D}).Permute0213();
+    const double scale = 1.0 / std::sqrt((double)D);
+    DiffOut f = fusedAttnDiff(qp, kp, vp, B * H, Tq, D, scale, causal);
+    LastNode = f.Node;
+    const Tensor ctx = f.Out.Permute0213().Reshape({B, Tq, EmbedDim});  // :130-131
+    return OutProj.Forward(ctx);                                         // :132
+}
+
+Tensor MultiHeadAttention::ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v,
+                                        bool causal) {
+    checkQKVDims(q, k, v);
+    const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1], H = NumHeads, D = HeadDim;
+    requireFused(D, Tq, Tk);
+    const Tensor qp = QProj.Forward(q).Reshape({B, Tq, H, D}).Permute0213();
+    const Tensor kp = KProj.Forward(k).Reshape({B, Tk, H, D}).Permute0213();
+    const Tensor vp = VProj.Forward(v).Reshape({B, Tk, H, D}).Permute0213();
+    const double scale = 1.0 / std::sqrt((double)D);
+    std::vector<double> O = fusedAttnF64(qp.Data, kp.Data, vp.Data, B * H, Tq, D, scale, causal);
+    const Tensor ctx = Tensor::New(std::move(O), {B, H, Tq, D}).Permute0213().Reshape({B, Tq, EmbedDim});
+    return OutProj.Forward(ctx);
+}
+
+}  // namespace nn
+}  // namespace gonn

@@ -1,0 +1,322 @@
+// host_test.cpp -- tests of the C++ host mirror (gonn_amd/host) of GoNN's
+// attention seam, checked against the fp64 oracle (oracle/liboracle.so, the
+// test-only C restatement of GoNN's CPU attention).
+//
+//   host_test cpu   argument checks, shape ops, Linear vs the oracle, the
+//                   no-device error path (no GPU calls)
+//   host_test gpu   MultiHeadAttention (config C1 and a D = 128 variant)
+//                   Forward / ForwardFused vs the oracle's MHA, fusedAttnDiff's
+//                   backward vs the oracle's autograd, in both MFMA modes
+//
+// Mirrors the reference's checks: benchmark/mha/main.go:55-73 (ForwardFused
+// vs Forward), nn/attention_test.go (shape panics), benchmark/flashbwd
+// (gradients). Tolerances: fp32-MFMA max-abs 1e-4; bf16-MFMA
+// |got - ref| <= 2e-2 + 1e-2 |ref|. Exit status 0 = all passed.
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "gonn_hip.h"
+#include "gonn_host.hpp"
+
+extern "C" {
+int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O, double* LSE,
+                    int BH, int H, int Sq, int Sk, int D, double scale, int causal,
+                    const int* kv_len, const int* rows, int nrows);
+int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V, const double* dO,
+                             double* dQ, double* dK, double* dV, int BH, int S, int D,
+                             double scale, int causal);
+int oracle_linear(const double* x, const double* W, const double* b, double* y, int N, int in,
+                  int out);
+void oracle_heads(const double* in, double* out, int B, int T, int H, int D, int dir);
+}
+
+using gonn::nn::Linear;
+using gonn::nn::MultiHeadAttention;
+using gonn::nn::Tensor;
+
+static int g_fail = 0;
+
+#define CHECK(cond, ...)                                  \
+    do {                                                  \
+        if (!(cond)) {                                    \
+            std::printf("FAIL %s:%d: ", __FILE__, __LINE__); \
+            std::printf(__VA_ARGS__);                     \
+            std::printf("\n");                            \
+            g_fail++;                                     \
+        }                                                 \
+    } while (0)
+
+// splitmix64 -> Box-Muller N(0,1), a documented deterministic stream.
+struct Rng {
+    uint64_t s;
+    explicit Rng(uint64_t seed) : s(seed) {}
+    uint64_t next() {
+        uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+        z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+        z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+        return z ^ (z >> 31);
+    }
+    double uniform() { return ((next() >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+    double normal() {
+        const double u = uniform(), v = uniform();
+        return std::sqrt(-2.0 * std::log(u)) * std::cos(6.283185307179586 * v);
+    }
+    std::vector<double> normals(size_t n, double mul = 1.0) {
+        std::vector<double> x(n);
+        for (auto& e : x) e = normal() * mul;
+        return x;
+    }
+};
+
+template <typename F>
+static bool throws_invalid(F f) {
+    try {
+        f();
+    } catch (const std::invalid_argument&) {
+        return true;
+    } catch (...) {
+        return false;
+    }
+    return false;
+}
+
+// max |got - ref| and whether every element is within atol + rtol |ref|.
+static bool close(const std::vector<double>& got, const std::vector<double>& ref, double atol,
+                  double rtol, const char* what) {
+    if (got.size() != ref.size()) {
+        std::printf("[%s] size %zu vs %zu\n", what, got.size(), ref.size());
+        return false;
+    }
+    double mx = 0.0;
+    bool ok = true;
+    for (size_t i = 0; i < got.size(); i++) {
+        const double e = std::fabs(got[i] - ref[i]);
+        if (!(e <= atol + rtol * std::fabs(ref[i]))) ok = false;
+        if (e > mx || std::isnan(e)) mx = e;
+    }
+    std::printf("[%s] max_abs %.3e (atol %.0e rtol %.0e)\n", what, mx, atol, rtol);
+    return ok;
+}
+
+static Linear make_linear(Rng& r, int out, int in) {
+    Linear l;
+    l.W = Tensor::New(r.normals((size_t)out * in, 1.0 / std::sqrt((double)in)), {out, in});
+    l.B = r.normals(out, 0.1);
+    return l;
+}
+
+// The oracle's MHA forward: projections, split heads, core, merge, output.
+static std::vector<double> oracle_mha(const MultiHeadAttention& m, const Tensor& q,
+                                      const Tensor& k, const Tensor& v, bool causal) {
+    const int B = q.Shape[0], T = q.Shape[1], E = m.EmbedDim, H = m.NumHeads, D = m.HeadDim;
+    auto lin = [](const Linear& l, const Tensor& x) {
+        const int out = l.W.Shape[0], in = l.W.Shape[1], N = (int)(x.Numel() / in);
+        std::vector<double> y((size_t)N * out);
+        oracle_linear(x.Data.data(), l.W.Data.data(), l.B.data(), y.data(), N, in, out);
+        return y;
+    };
+    std::vector<double> qp = lin(m.QProj, q), kp = lin(m.KProj, k), vp = lin(m.VProj, v);
+    std::vector<double> qh(qp.size()), kh(kp.size()), vh(vp.size()), o(qp.size()), ctx(qp.size());
+    oracle_heads(qp.data(), qh.data(), B, T, H, D, 0);
+    oracle_heads(kp.data(), kh.data(), B, T, H, D, 0);
+    oracle_heads(vp.data(), vh.data(), B, T, H, D, 0);
+    oracle_attn_fwd(qh.data(), kh.data(), vh.data(), o.data(), nullptr, B * H, H, T, T, D,
+                    1.0 / std::sqrt((double)D), causal ? 1 : 0, nullptr, nullptr, 0);
+    oracle_heads(o.data(), ctx.data(), B, T, H, D, 1);
+    Tensor c = Tensor::New(ctx, {B, T, E});
+    return lin(m.OutProj, c);
+}
+
+static void test_cpu() {
+    // Supports: the head dims the kernels cover (replaces D == 64 at
+    // nn/attention.go:129).
+    CHECK(gonn::hip::Supports(64, 128, 128) && gonn::hip::Supports(128, 7, 300), "Supports 64/128");
+    CHECK(!gonn::hip::Supports(32, 128, 128) && !gonn::hip::Supports(256, 128, 128),
+          "Supports rejects other D");
+    CHECK(!gonn::hip::Supports(64, 0, 128), "Supports rejects empty");
+
+    // Mode switching and its error.
+    const int m0 = gonn::hip::Mode();
+    gonn::hip::SetMode(1);
+    CHECK(gonn::hip::Mode() == 1, "SetMode(1)");
+    gonn::hip::SetMode(m0);
+    bool threw = false;
+    try {
+        gonn::hip::SetMode(7);
+    } catch (const gonn::hip::Error& e) {
+        threw = e.code == GONN_E_INVALID;
+    }
+    CHECK(threw, "SetMode(7) throws GONN_E_INVALID");
+
+    // Short slices panic in Go; they throw invalid_argument here, before any
+    // device work.
+    std::vector<double> a(8 * 16 * 64, 0.0), shortv(10, 0.0), o(a.size());
+    CHECK(throws_invalid([&] { gonn::hip::FlashAttnF64(a, shortv, a, o, 8, 16, 64, 0.125, true); }),
+          "FlashAttnF64 short K");
+    CHECK(throws_invalid([&] { gonn::hip::FlashAttnF64Fwd(a, a, a, 0, 16, 64, 0.125, true); }),
+          "FlashAttnF64Fwd BH = 0");
+    CHECK(throws_invalid([&] {
+              gonn::hip::FlashAttnF64Bwd(a, a, a, a, shortv, a, 8, 16, 64, 0.125, true);
+          }),
+          "FlashAttnF64Bwd short L");
+
+    // Tensor shape ops and the head split match the oracle's Permute copy.
+    Rng r(11);
+    Tensor x = Tensor::New(r.normals(2 * 5 * 3 * 4), {2, 5, 3, 4});
+    Tensor p = x.Permute0213();
+    CHECK(p.Shape == std::vector<int>({2, 3, 5, 4}), "Permute shape");
+    std::vector<double> ref(x.Numel());
+    oracle_heads(x.Data.data(), ref.data(), 2, 5, 3, 4, 0);
+    CHECK(p.Data == ref, "Permute0213 == oracle split heads");
+    CHECK(p.Permute0213().Data == x.Data, "Permute0213 is an involution");
+    CHECK(throws_invalid([&] { x.Reshape({7, 7}); }), "Reshape size check");
+    CHECK(throws_invalid([&] { Tensor::New(std::vector<double>(5), {2, 3}); }), "New size check");
+
+    // Linear vs the oracle's Linear.Forward.
+    Linear l = make_linear(r, 24, 40);
+    Tensor in = Tensor::New(r.normals(3 * 7 * 40), {3, 7, 40});
+    Tensor y = l.Forward(in);
+    std::vector<double> yref(3 * 7 * 24);
+    oracle_linear(in.Data.data(), l.W.Data.data(), l.B.data(), yref.data(), 21, 40, 24);
+    CHECK(y.Shape == std::vector<int>({3, 7, 24}), "Linear shape");
+    CHECK(close(y.Data, yref, 1e-12, 0.0, "Linear vs oracle"), "Linear vs oracle");
+
+    // MultiHeadAttention construction and checkQKVDims (nn/attention.go:45-103).
+    CHECK(throws_invalid([&] {
+              MultiHeadAttention(30, 4, make_linear(r, 30, 30), make_linear(r, 30, 30),
+                                 make_linear(r, 30, 30), make_linear(r, 30, 30));
+          }),
+          "embedDim %% numHeads");
+    MultiHeadAttention m(32, 4, make_linear(r, 32, 32), make_linear(r, 32, 32),
+                         make_linear(r, 32, 32), make_linear(r, 32, 32));
+    Tensor q = Tensor::New(r.normals(2 * 6 * 32), {2, 6, 32});
+    Tensor qbad = Tensor::New(r.normals(2 * 6 * 31), {2, 6, 31});
+    Tensor k5 = Tensor::New(r.normals(2 * 5 * 32), {2, 5, 32});
+    CHECK(throws_invalid([&] { m.Forward(qbad, q, q, false); }), "q feature dim");
+    CHECK(throws_invalid([&] { m.Forward(q, q, k5, false); }), "k/v length mismatch");
+
+    // Without a device the fused core reports GONN_E_NODEVICE rather than
+    // running anywhere else.
+    if (!gonn::hip::Available()) {
+        int code = 0;
+        try {
+            m.Forward(q, q, q, true);
+        } catch (const gonn::hip::Error& e) {
+            code = e.code;
+        }
+        CHECK(code == GONN_E_NODEVICE, "Forward without device: code %d", code);
+        code = 0;
+        try {
+            std::vector<double> z(4 * 8 * 64, 0.0), oz(z.size());
+            gonn::hip::FlashAttnF64(z, z, z, oz, 4, 8, 64, 0.125, false);
+        } catch (const gonn::hip::Error& e) {
+            code = e.code;
+        }
+        CHECK(code == GONN_E_NODEVICE, "FlashAttnF64 without device: code %d", code);
+    }
+}
+
+static void test_gpu() {
+    CHECK(gonn::hip::Available(), "no gfx950 device");
+    if (!gonn::hip::Available()) return;
+    struct Cfg {
+        const char* name;
+        int B, T, E, H;
+        bool causal;
+    };
+    // C1: B=2, S=128, d_model=256, 4 heads, causal; and a
+    // D = 128 variant with a ragged length.
+    const Cfg cfgs[] = {{"C1 D=64", 2, 128, 256, 4, true},
+                        {"D=128 T=77", 2, 77, 512, 4, true},
+                        {"D=64 non-causal", 1, 200, 128, 2, false}};
+    for (const Cfg& c : cfgs) {
+        Rng r(1000 + c.T);
+        const double ws = 1.0 / std::sqrt((double)c.E);
+        auto lin = [&] {
+            Linear l;
+            l.W = Tensor::New(r.normals((size_t)c.E * c.E, ws), {c.E, c.E});
+            l.B = r.normals(c.E, ws);
+            return l;
+        };
+        MultiHeadAttention m(c.E, c.H, lin(), lin(), lin(), lin());
+        const size_t n = (size_t)c.B * c.T * c.E;
+        Tensor q = Tensor::New(r.normals(n, ws), {c.B, c.T, c.E});
+        Tensor k = Tensor::New(r.normals(n, ws), {c.B, c.T, c.E});
+        Tensor v = Tensor::New(r.normals(n, ws), {c.B, c.T, c.E});
+        const std::vector<double> ref = oracle_mha(m, q, k, v, c.causal);
+        for (int mode = 0; mode < 2; mode++) {
+            gonn::hip::SetMode(mode);
+            const double atol = mode ? 2e-2 : 1e-4, rtol = mode ? 1e-2 : 0.0;
+            const std::string tag = std::string(c.name) + (mode ? " bf16" : " fp32");
+            Tensor out = m.Forward(q, k, v, c.causal);
+            CHECK(out.Shape == std::vector<int>({c.B, c.T, c.E}), "%s shape", tag.c_str());
+            CHECK(close(out.Data, ref, atol, rtol, (tag + " Forward").c_str()), "%s Forward",
+                  tag.c_str());
+            // benchmark/mha/main.go:55-73: ForwardFused agrees with Forward.
+            Tensor ff = m.ForwardFused(q, k, v, c.causal);
+            CHECK(close(ff.Data, out.Data, 0.0, 0.0, (tag + " ForwardFused == Forward").c_str()),
+                  "%s ForwardFused", tag.c_str());
+        }
+    }
+    // fusedAttnDiff: the node's backward vs the oracle's autograd.
+    for (int D : {64, 128}) {
+        Rng r(77 + D);
+        const int BH = 3, S = 97;
+        const size_t n = (size_t)BH * S * D;
+        Tensor qp = Tensor::New(r.normals(n), {1, BH, S, D});
+        Tensor kp = Tensor::New(r.normals(n), {1, BH, S, D});
+        Tensor vp = Tensor::New(r.normals(n), {1, BH, S, D});
+        Tensor g = Tensor::New(r.normals(n), {1, BH, S, D});
+        const double scale = 1.0 / std::sqrt((double)D);
+        std::vector<double> ro(n), rq(n), rk(n), rv(n);
+        oracle_attn_fwd(qp.Data.data(), kp.Data.data(), vp.Data.data(), ro.data(), nullptr, BH, 1,
+                        S, S, D, scale, 1, nullptr, nullptr, 0);
+        oracle_attn_bwd_autograd(qp.Data.data(), kp.Data.data(), vp.Data.data(), g.Data.data(),
+                                 rq.data(), rk.data(), rv.data(), BH, S, D, scale, 1);
+        for (int mode = 0; mode < 2; mode++) {
+            gonn::hip::SetMode(mode);
+            const double atol = mode ? 2e-2 : 1e-4, rtol = mode ? 1e-2 : 0.0;
+            const std::string tag = "fusedAttnDiff D=" + std::to_string(D) + (mode ? " bf16" : " fp32");
+            auto f = gonn::nn::fusedAttnDiff(qp, kp, vp, BH, S, D, scale, true);
+            CHECK(f.Node.Op == "FlashAttn", "node op");
+            CHECK(close(f.Out.Data, ro, atol, rtol, (tag + " O").c_str()), "%s O", tag.c_str());
+            auto grads = f.Node.Backward(g);
+            CHECK(close(grads[0].Data, rq, atol, rtol, (tag + " dQ").c_str()), "%s dQ", tag.c_str());
+            CHECK(close(grads[1].Data, rk, atol, rtol, (tag + " dK").c_str()), "%s dK", tag.c_str());
+            CHECK(close(grads[2].Data, rv, atol, rtol, (tag + " dV").c_str()), "%s dV", tag.c_str());
+        }
+    }
+    gonn::hip::SetMode(0);
+    // The fused gate: Tq != Tk is outside the seam's contract.
+    {
+        Rng r(5);
+        Linear l;
+        l.W = Tensor::New(r.normals(64 * 64, 0.125), {64, 64});
+        MultiHeadAttention m(64, 1, l, l, l, l);
+        Tensor q = Tensor::New(r.normals(1 * 8 * 64), {1, 8, 64});
+        Tensor k = Tensor::New(r.normals(1 * 9 * 64), {1, 9, 64});
+        CHECK(throws_invalid([&] { m.Forward(q, k, k, false); }), "Tq != Tk rejected");
+    }
+}
+
+int main(int argc, char** argv) {
+    const std::string what = argc > 1 ? argv[1] : "cpu";
+    try {
+        if (what == "cpu") test_cpu();
+        else if (what == "gpu") test_gpu();
+        else {
+            std::printf("usage: host_test cpu|gpu\n");
+            return 2;
+        }
+    } catch (const std::exception& e) {
+        std::printf("FAIL: uncaught exception: %s\n", e.what());
+        return 1;
+    }
+    std::printf("%s: %s (%d failures)\n", what.c_str(), g_fail ? "FAILED" : "ok", g_fail);
+    return g_fail ? 1 : 0;
+}
