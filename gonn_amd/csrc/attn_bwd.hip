@@ -75,15 +75,26 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 // bf16 dK/dV.
 //
 // One workgroup per 128-key block (32 keys per wave, held as the MFMA B
-// operand in VGPRs), query tiles of 64 streamed through LDS. One wave per
-// SIMD with the whole register file: step i runs S(i+1) = Q K^T and
-// dP(i+1) = dO V^T on MFMA (4 accumulator chains) interleaved with the VALU
-// of tile i (P = exp2(S c - L log2e), dS = P (dP - D), bf16 packs), then
-// dV^T += dO^T P and dK^T += Q^T dS for tile i (8 chains). Q/dO tiles (for
-// S, dP) run one tile ahead of the transposed Q^T/dO^T tiles and L, D (for
-// dV, dK); both stream HBM -> LDS with buffer_load_dwordx4 ... lds into double
-// buffers the step no longer reads. Causal masks exist only on the first two
-// query tiles of a key block (q-tiles start at the block's first key).
+// operand in VGPRs), query tiles of 64 streamed through LDS, one wave per
+// SIMD with the full register file. Three-stage software pipeline: step i
+// issues, with no dependency between them inside the step,
+//   MFMA  S(i+1) = Q K^T, dP(i+1) = dO V^T        (row tiles of query tile i+1)
+//   VALU  P(i) = exp2(S c - L log2e), dS(i) = P (dP - D), packed to bf16
+//   MFMA  dV^T += dO^T P(i-1), dK^T += Q^T dS(i-1) (transposed tiles of i-1)
+// so no MFMA waits on the VALU of its own step. P(i) / dS(i) overwrite
+// P(i-1) / dS(i-1) 16 queries at a time, after the dV / dK MFMAs that read
+// those 16 queries were issued. The step is scheduled by hand: slot e issues
+// the LDS read of MFMA e+3, MFMA e, a tile load and the VALU micro-ops mapped
+// to it, fenced by sched_barrier (the compiler's own schedule serialises
+// MFMA chains behind their LDS reads). MFMA order per 16-query k-step ks:
+// dV(ks, d-tiles), dK(ks, d-tiles), then a quarter of S/dP(i+1): 4 NDT + 4
+// accumulator chains interleave.
+//
+// LDS: 2-slot rings. Step i loads row tile i+2 into the slot row tile i left
+// (read by step i-1), transposed tile i into the slot of tile i-2, and L/D of
+// tile i+1; all land by the end of step i (one barrier per step). Causal
+// masks exist only on the first two query tiles of a key block (its query
+// tiles start at the block's first key).
 // ---------------------------------------------------------------------------
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
@@ -100,6 +111,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     constexpr int RLAST = NRP - (NRI - 1) * 256, TLAST = NTP - (NTI - 1) * 256;
     static_assert(RLAST % 64 == 0 && TLAST % 64 == 0, "partial loads must be whole waves");
     constexpr int RTILE = BM * RST, TTILE = D * TST;  // bf16 elements
+    constexpr uint32_t RTB = RTILE * 2, TTB = TTILE * 2;
     __shared__ __attribute__((aligned(16))) bf16 sQ[2 * RTILE];
     __shared__ __attribute__((aligned(16))) bf16 sdO[2 * RTILE];
     __shared__ __attribute__((aligned(16))) bf16 sQt[2 * TTILE];
@@ -142,144 +154,239 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
         toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
     }
+    const uint32_t rlast = wave * 64 < RLAST, tlast = wave * 64 < TLAST;  // wave-uniform
     const uint32_t slice = (uint32_t)Sp * D * 2;  // bytes of one (b,h) slice
     const brsrc rq = make_rsrc(Qg, slice), rdo = make_rsrc(dOg, slice);
     const brsrc rqt = make_rsrc(Qtg, slice), rdot = make_rsrc(dOtg, slice);
     const brsrc rl = make_rsrc(lg, (uint32_t)Sp * 4), rd = make_rsrc(dg, (uint32_t)Sp * 4);
-    auto dma_row = [&](int qb, int slot) {  // Q, dO rows of query tile qb
+    const uint32_t lq = lds_addr(sQ) + wave * 1024, ldo = lds_addr(sdO) + wave * 1024;
+    const uint32_t lqt = lds_addr(sQt) + wave * 1024, ldot = lds_addr(sdOt) + wave * 1024;
+    // Load j of the row tiles (Q: j < NRI, dO: j >= NRI) of query tile qb.
+    auto dma_row = [&](int qb, int slot, int j) {
         const uint32_t so = (uint32_t)qb * BM * D * 2;
-        const uint32_t dq = lds_addr(sQ) + (slot * RTILE + wave * 512) * 2;
-        const uint32_t dd = lds_addr(sdO) + (slot * RTILE + wave * 512) * 2;
-        for (int i = 0; i < NRI; i++)
-            if (i < NRI - 1 || tid < RLAST) {
-                dma16(rq, dq + i * 4096, roff[i], so);
-                dma16(rdo, dd + i * 4096, roff[i], so);
-            }
+        const int i = j % NRI;
+        const brsrc r = j < NRI ? rq : rdo;
+        const uint32_t dst = (j < NRI ? lq : ldo) + slot * RTB + i * 4096;
+        if (i < NRI - 1) dma16(r, dst, roff[i], so);
+        else dma16_if(r, dst, roff[i], so, rlast);
     };
-    auto dma_tr = [&](int qb, int slot) {  // Q^T, dO^T, L, D of query tile qb
+    // Load j of the transposed tiles (Q^T: j < NTI, dO^T: j >= NTI).
+    auto dma_tr = [&](int qb, int slot, int j) {
         const uint32_t so = (uint32_t)qb * BM * 2;
-        const uint32_t dq = lds_addr(sQt) + (slot * TTILE + wave * 512) * 2;
-        const uint32_t dd = lds_addr(sdOt) + (slot * TTILE + wave * 512) * 2;
-        for (int i = 0; i < NTI; i++)
-            if (i < NTI - 1 || tid < TLAST) {
-                dma16(rqt, dq + i * 4096, toff[i], so);
-                dma16(rdot, dd + i * 4096, toff[i], so);
-            }
-        // Wave 0: lanes 0-15 load the 64 L values (bytes 0-255 of sLD[slot]),
-        // lanes 16-31 the 64 D values (bytes 256-511).
+        const int i = j % NTI;
+        const brsrc r = j < NTI ? rqt : rdot;
+        const uint32_t dst = (j < NTI ? lqt : ldot) + slot * TTB + i * 4096;
+        if (i < NTI - 1) dma16(r, dst, toff[i], so);
+        else dma16_if(r, dst, toff[i], so, tlast);
+    };
+    // L and D of query tile qb: wave 0, lanes 0-15 load the 64 L values
+    // (bytes 0-255 of sLD[slot]), lanes 16-31 the 64 D values (256-511).
+    auto dma_ld = [&](int qb, int slot) {
         if (wave == 0) {
             const uint32_t dl = lds_addr(sLD) + slot * 2 * BM * 4;
             if (lane < 16) dma16(rl, dl, (lane & 15) * 16, (uint32_t)qb * BM * 4);
             else if (lane < 32) dma16(rd, dl, (lane & 15) * 16, (uint32_t)qb * BM * 4);
         }
     };
-    auto dma_wait = [] { GONN_VMCNT(0); };
 
-    // S and dP of one query tile (64 queries x this wave's 32 keys): S[mt],
-    // dP[mt] hold queries mt*32 + 8(r/4) + 4g + r%4 of register r.
-    auto sdp = [&](int slot, f32x16* s, f32x16* dp) {
-        const bf16* q = sQ + slot * RTILE + ln * RST + g * 8;
-        const bf16* o = sdO + slot * RTILE + ln * RST + g * 8;
-        s[0] = s[1] = dp[0] = dp[1] = f32x16{};
-        for (int ks = 0; ks < NKS; ks++)
-            for (int mt = 0; mt < 2; mt++) {
-                s[mt] = mfma_bf16(*(const bf16x8*)(q + mt * 32 * RST + ks * 16), kf[ks], s[mt]);
-                dp[mt] = mfma_bf16(*(const bf16x8*)(o + mt * 32 * RST + ks * 16), vf[ks], dp[mt]);
-            }
-    };
+    // ---- MFMA operand reads (bytes from a slot's start) ----
+    const uint32_t rq0 = (uint32_t)(ln * RST + g * 8) * 2, tq0 = (uint32_t)(ln * TST + g * 8) * 2;
+    const char* cQ = (const char*)sQ;
+    const char* cdO = (const char*)sdO;
+    const char* cQt = (const char*)sQt;
+    const char* cdOt = (const char*)sdOt;
 
     f32x16 dvacc[NDT], dkacc[NDT];
     for (int t = 0; t < NDT; t++) dvacc[t] = dkacc[t] = f32x16{};
     const float c2 = p.c2b;
     const int qb0 = CAUSAL ? (kb * BN) / BM : 0;  // earlier queries see none of these keys
     const int nq = (S + BM - 1) / BM - qb0;       // >= 1
+    u32x4 pp[4], pd[4];  // P and dS of the tile dV/dK consume next, bf16 pairs per word
 
-    // Step i: tile qb0+i's P, dS and dV/dK; with NEXT, S/dP of tile i+1 and
-    // the loads of rows i+2 and transposes i+1.
-    auto step = [&](auto next_tag, int i, f32x16* s, f32x16* dp, f32x16* sn, f32x16* dpn) {
-        constexpr bool NEXT = decltype(next_tag)::value;
-        const int qb = qb0 + i, slot = i & 1;
-        if constexpr (NEXT) {
-            dma_row(i + 2 < nq ? qb + 2 : qb0 + nq - 1, slot);
-            dma_tr(qb + 1, slot ^ 1);
-        }
-        // Causal mask (key > query), only on the first two tiles. The exponent
-        // scale c2b is positive (a negative scale is folded into the packed
-        // Q), so a masked score of -inf gives P = 0 and dS = 0.
-        if (CAUSAL && i < 2) {
-            const int kq = kj - qb * BM - 4 * g;  // key minus this lane group's base query
-            for (int mt = 0; mt < 2; mt++)
-                for (int r = 0; r < 16; r++)
-                    s[mt][r] = kq > mt * 32 + 8 * (r >> 2) + (r & 3) ? -INFINITY : s[mt][r];
-        }
-        if constexpr (NEXT) sdp(slot ^ 1, sn, dpn);
-        // P and dS of tile i, packed to bf16 per 16-query k-step.
-        bf16x8 pb[4], db[4];
-        for (int mt = 0; mt < 2; mt++) {
-            f32x4 lse4[4], del4[4];
-            for (int j = 0; j < 4; j++) {
-                lse4[j] = *(const f32x4*)&sLD[slot][mt * 32 + 8 * j + 4 * g];
-                del4[j] = *(const f32x4*)&sLD[slot][BM + mt * 32 + 8 * j + 4 * g];
-            }
-            float pv[16], dv[16];
-            for (int r = 0; r < 16; r++) {
-                const float e = fast_exp2(__builtin_fmaf(s[mt][r], c2, -lse4[r >> 2][r & 3]));
-                pv[r] = e;
-                dv[r] = e * (dp[mt][r] - del4[r >> 2][r & 3]);
-            }
-            pb[2 * mt] = pack8(pv[0], pv[1], pv[2], pv[3], pv[4], pv[5], pv[6], pv[7]);
-            pb[2 * mt + 1] = pack8(pv[8], pv[9], pv[10], pv[11], pv[12], pv[13], pv[14], pv[15]);
-            db[2 * mt] = pack8(dv[0], dv[1], dv[2], dv[3], dv[4], dv[5], dv[6], dv[7]);
-            db[2 * mt + 1] = pack8(dv[8], dv[9], dv[10], dv[11], dv[12], dv[13], dv[14], dv[15]);
-        }
-        // dV^T += dO^T P, dK^T += Q^T dS over 4 k-steps of 16 queries.
-        const bf16* qt = sQt + slot * TTILE + ln * TST + g * 8;
-        const bf16* ot = sdOt + slot * TTILE + ln * TST + g * 8;
-        for (int ks = 0; ks < BM / 16; ks++)
-            for (int t = 0; t < NDT; t++) {
-                dvacc[t] = mfma_bf16(*(const bf16x8*)(ot + t * 32 * TST + ks * 16), pb[ks], dvacc[t]);
-                dkacc[t] = mfma_bf16(*(const bf16x8*)(qt + t * 32 * TST + ks * 16), db[ks], dkacc[t]);
-            }
-        if constexpr (NEXT) {
-            // The S/dP(i+1) MFMAs carry tile i's VALU; dV/dK follow.
-            constexpr int kV = (192 + 4 * NKS - 1) / (4 * NKS);
-            __builtin_amdgcn_sched_group_barrier(kSgDSR, 4, 0);
-            for (int k = 0; k < 4 * NKS; k++) {
-                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgVALU, kV, 0);
-            }
-            for (int k = 0; k < 8 * NDT; k++) {
-                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    // One pipeline step. sA <- S(i+1), dA <- dP(i+1); sB, dB = S(i), dP(i).
+    auto step = [&](auto ha_tag, auto hb_tag, auto hc_tag, int i, f32x16* sA, f32x16* dA,
+                    f32x16* sB, f32x16* dB) __attribute__((always_inline)) {
+        constexpr bool HA = decltype(ha_tag)::value;  // S/dP of tile i+1
+        constexpr bool HB = decltype(hb_tag)::value;  // P/dS of tile i
+        constexpr bool HC = decltype(hc_tag)::value;  // dV/dK of tile i-1
+        const int qb = qb0 + i;
+        // Loads for the next step: row tile i+2, transposed tile i, L/D i+1.
+        const bool dr = HA && i + 2 < nq, dt = HB, dl = HA;
+        if (dl) dma_ld(qb + 1, (i + 1) & 1);
+        // Causal mask (key > query), only on the first two tiles. The
+        // exponent scale c2b is positive (a negative scale is folded into
+        // the packed Q), so a masked score of -inf gives P = 0 and dS = 0.
+        if constexpr (HB) {
+            if (CAUSAL && i < 2) {
+                const int kq = kj - qb * BM - 4 * g;  // key minus the lane group's base query
+                for (int mt = 0; mt < 2; mt++)
+                    for (int r = 0; r < 16; r++)
+                        sB[mt][r] = kq > mt * 32 + 8 * (r >> 2) + (r & 3) ? -INFINITY : sB[mt][r];
             }
         }
-        dma_wait();
+        const uint32_t rsl = (uint32_t)((i + 1) & 1) * RTB;   // row tile i+1
+        const uint32_t tsl = (uint32_t)((i + 1) & 1) * TTB;   // transposed tile i-1
+        const int lsl = i & 1;                                 // L/D of tile i
+
+        constexpr int HCn = HC ? 2 * NDT : 0, HAn = HA ? NKS : 0;
+        constexpr int GW = HCn + HAn;  // MFMAs per 16-query k-step group
+        constexpr int NM = 4 * GW;
+        constexpr int LA = 3;
+        constexpr int NDMA = 2 * NRI + 2 * NTI;
+        bf16x8 opr[4];
+        auto fetch = [&](auto E) {
+            constexpr int e = decltype(E)::value, ks = e / GW, w = e % GW;
+            if constexpr (w < HCn) {
+                constexpr int t = w % NDT;
+                const char* base = (w < NDT ? cdOt : cQt) + tsl + tq0;
+                opr[e & 3] = *(const bf16x8*)(base + (t * 32 * TST + ks * 16) * 2);
+            } else {
+                constexpr int u = w - HCn, kk = ks * (NKS / 4) + u / 4, mt = u & 1;
+                const char* base = ((u & 2) ? cdO : cQ) + rsl + rq0;
+                opr[e & 3] = *(const bf16x8*)(base + (mt * 32 * RST + kk * 16) * 2);
+            }
+        };
+        auto issue = [&](auto E) {
+            constexpr int e = decltype(E)::value, ks = e / GW, w = e % GW;
+            if constexpr (w < HCn) {
+                constexpr int t = w % NDT;
+                if constexpr (w < NDT)
+                    dvacc[t] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pp[ks]), dvacc[t]);
+                else
+                    dkacc[t] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pd[ks]), dkacc[t]);
+            } else {
+                constexpr int u = w - HCn, kk = ks * (NKS / 4) + u / 4, mt = u & 1;
+                if constexpr (u & 2)
+                    dA[mt] = mfma_bf16(opr[e & 3], vf[kk], kk == 0 ? f32x16{} : dA[mt]);
+                else
+                    sA[mt] = mfma_bf16(opr[e & 3], kf[kk], kk == 0 ? f32x16{} : sA[mt]);
+            }
+        };
+        // VALU of tile i in 8 groups k = mt*4 + j4 (registers 4 j4 .. +3 of
+        // sB/dB[mt], queries mt*32 + 8 j4 + 4g + 0..3), each in five
+        // micro-ops: R (read L, D), A0/A1 (exp2 of two scores), B0/B1 (dS of
+        // two scores, bf16 pairs of P and dS). Group k fills words of k-step
+        // ks = k/2: its B micro-ops sit after the dV/dK MFMAs of ks.
+        f32x4 uL[8], uD[8];
+        float ue[8][4];
+        auto ub = [](int k, int st) {  // slot of micro-op st (0 R, 1 A0, 2 A1, 3 B0, 4 B1)
+            int b0 = (k >> 1) * GW + (HCn ? HCn - 1 : 0) + 2 * (k & 1);
+            const int off[5] = {-5, -3, -2, 0, 1};
+            const int s = b0 + off[st];
+            return s < 0 ? 0 : s;
+        };
+        auto uop = [&](auto K, auto ST) {
+            constexpr int k = decltype(K)::value, st = decltype(ST)::value;
+            constexpr int mt = k >> 2, j4 = k & 3, ks = k >> 1, w0 = (j4 & 1) * 2;
+            if constexpr (st == 0) {
+                uL[k] = *(const f32x4*)&sLD[lsl][mt * 32 + 8 * j4 + 4 * g];
+                uD[k] = *(const f32x4*)&sLD[lsl][BM + mt * 32 + 8 * j4 + 4 * g];
+            } else if constexpr (st <= 2) {
+                constexpr int e0 = (st - 1) * 2;
+                for (int e = e0; e < e0 + 2; e++) {
+                    ue[k][e] = fast_exp2(__builtin_fmaf(sB[mt][4 * j4 + e], c2, -uL[k][e]));
+                    pin(ue[k][e]);
+                }
+            } else {
+                constexpr int e0 = (st - 3) * 2;
+                const float d0 = ue[k][e0] * (dB[mt][4 * j4 + e0] - uD[k][e0]);
+                const float d1 = ue[k][e0 + 1] * (dB[mt][4 * j4 + e0 + 1] - uD[k][e0 + 1]);
+                const bf16x2 pr = {to_bf16(ue[k][e0]), to_bf16(ue[k][e0 + 1])};
+                const bf16x2 dr2 = {to_bf16(d0), to_bf16(d1)};
+                pp[ks][w0 + e0 / 2] = __builtin_bit_cast(uint32_t, pr);
+                pd[ks][w0 + e0 / 2] = __builtin_bit_cast(uint32_t, dr2);
+                pin(pp[ks][w0 + e0 / 2]);
+                pin(pd[ks][w0 + e0 / 2]);
+            }
+        };
+        auto uops_at = [&](auto E) {
+            constexpr int e = decltype(E)::value;
+            if constexpr (HB) {
+                static_for<5>([&](auto ST) {
+                    static_for<8>([&](auto K) {
+                        constexpr int at = ub(decltype(K)::value, decltype(ST)::value);
+                        if constexpr (e < NM ? at == e : at >= NM) uop(K, ST);
+                    });
+                });
+            }
+        };
+        static_for<LA>([&](auto E) {
+            if constexpr (decltype(E)::value < NM) fetch(E);
+        });
+        static_for<NM>([&](auto E) {
+            constexpr int e = decltype(E)::value;
+            if constexpr (e + LA < NM) fetch(std::integral_constant<int, e + LA>{});
+            issue(E);
+            // Tile loads spread over the stream: slots 1, 1 + DS, ...
+            constexpr int DS = NM / NDMA > 0 ? NM / NDMA : 1;
+            if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
+                constexpr int d = (e - 1) / DS;
+                if constexpr (d < 2 * NRI) {
+                    if (dr) dma_row(qb + 2, i & 1, d);
+                } else {
+                    if (dt) dma_tr(qb, i & 1, d - 2 * NRI);
+                }
+            }
+            uops_at(E);
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        // Loads not placed in the stream (a step with too few MFMAs).
+        static_for<NDMA>([&](auto Dd) {
+            constexpr int d = decltype(Dd)::value;
+            constexpr int DS = NM / NDMA > 0 ? NM / NDMA : 1;
+            if constexpr (NM == 0 || 1 + d * DS >= NM) {
+                if constexpr (d < 2 * NRI) {
+                    if (dr) dma_row(qb + 2, i & 1, d);
+                } else {
+                    if (dt) dma_tr(qb, i & 1, d - 2 * NRI);
+                }
+            }
+        });
+        uops_at(std::integral_constant<int, NM>{});
+        GONN_VMCNT(0);
         __syncthreads();
     };
     using Yes = std::integral_constant<bool, true>;
     using No = std::integral_constant<bool, false>;
 
-    // Prologue: rows of tiles 0, 1; transposes, L, D of tile 0; S/dP of tile 0.
-    dma_row(qb0, 0);
-    if (nq > 1) dma_row(qb0 + 1, 1);
-    dma_tr(qb0, 0);
-    dma_wait();
+    // Prologue: row tiles 0, 1 and L/D of tile 0; S/dP of tile 0.
+    for (int j = 0; j < 2 * NRI; j++) dma_row(qb0, 0, j);
+    if (nq > 1)
+        for (int j = 0; j < 2 * NRI; j++) dma_row(qb0 + 1, 1, j);
+    dma_ld(qb0, 0);
+    GONN_VMCNT(0);
     __syncthreads();
-    f32x16 sA[2], dA[2], sB[2], dB[2];
-    sdp(0, sA, dA);
-    __syncthreads();  // step 0 reloads row slot 0
+    f32x16 sX[2], dX[2], sY[2], dY[2];
+    for (int mt = 0; mt < 2; mt++) sX[mt] = dX[mt] = f32x16{};
+    for (int kk = 0; kk < NKS; kk++)
+        for (int mt = 0; mt < 2; mt++) {
+            sX[mt] = mfma_bf16(*(const bf16x8*)(cQ + rq0 + (mt * 32 * RST + kk * 16) * 2), kf[kk], sX[mt]);
+            dX[mt] = mfma_bf16(*(const bf16x8*)(cdO + rq0 + (mt * 32 * RST + kk * 16) * 2), vf[kk], dX[mt]);
+        }
+    __syncthreads();  // row slot 0 is reloaded by step 0
 
-    int i = 0;
-    for (; i + 2 < nq; i += 2) {
-        step(Yes{}, i, sA, dA, sB, dB);
-        step(Yes{}, i + 1, sB, dB, sA, dA);
-    }
-    if (i + 1 < nq) {
-        step(Yes{}, i, sA, dA, sB, dB);
-        step(No{}, i + 1, sB, dB, sA, dA);
+    // Steps 0 .. nq: step i has S/dP(i+1) while i+1 < nq, P/dS(i) while
+    // i < nq, dV/dK(i-1) from i = 1.
+    if (nq == 1) {
+        step(No{}, Yes{}, No{}, 0, sY, dY, sX, dX);
+        step(No{}, No{}, Yes{}, 1, sX, dX, sY, dY);
     } else {
-        step(No{}, i, sA, dA, sB, dB);
+        step(Yes{}, Yes{}, No{}, 0, sY, dY, sX, dX);
+        int i = 1;
+        for (; i + 2 < nq; i += 2) {
+            step(Yes{}, Yes{}, Yes{}, i, sX, dX, sY, dY);
+            step(Yes{}, Yes{}, Yes{}, i + 1, sY, dY, sX, dX);
+        }
+        // i = nq-2 or nq-1 remain (then the final dV/dK step)
+        if (i + 1 < nq) {
+            step(Yes{}, Yes{}, Yes{}, i, sX, dX, sY, dY);
+            step(No{}, Yes{}, Yes{}, i + 1, sY, dY, sX, dX);
+            step(No{}, No{}, Yes{}, i + 2, sX, dX, sY, dY);
+        } else {
+            step(No{}, Yes{}, Yes{}, i, sX, dX, sY, dY);
+            step(No{}, No{}, Yes{}, i + 1, sY, dY, sX, dX);
+        }
     }
 
     if (kj < S) {

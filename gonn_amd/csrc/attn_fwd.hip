@@ -28,7 +28,6 @@
 //        masked.
 //  fp32: v_mfma_f32_32x32x2_f32 straight from the fp32 K/V (no pack).
 #include <type_traits>
-#include <utility>
 
 #include "common.h"
 #include "kernels.h"
@@ -69,22 +68,6 @@ constexpr float kLazyLog2 = 8.0f;
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgVALU = 0x002, kSgMFMA = 0x008, kSgDSR = 0x100;
 
-// Forces x to be computed at this point of the program (an empty asm that
-// reads it): keeps hand-scheduled VALU work from being sunk to its uses.
-template <typename T>
-GONN_DEV void pin(const T& x) {
-    asm volatile("" ::"v"(x));
-}
-
-// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
-template <typename F, int... I>
-GONN_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-    (f(std::integral_constant<int, I>{}), ...);
-}
-template <int N, typename F>
-GONN_DEV void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
 
 template <int D, bool CAUSAL, typename QT>
 __global__ __launch_bounds__(256, 2) void fwd_bf16_kernel(FwdParams p) {

@@ -14,6 +14,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 typedef __bf16 bf16;
 typedef bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -177,5 +180,23 @@ GONN_DEV uint32_t lds_addr(const void* p) {
 }
 // s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained), n < 16.
 #define GONN_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
+// ---- hand scheduling helpers ----
+// Forces x to be computed at this point of the program (an empty asm that
+// reads it): keeps hand-scheduled VALU work from being sunk to its uses.
+template <typename T>
+GONN_DEV void pin(const T& x) {
+    asm volatile("" ::"v"(x));
+}
+
+// Compile-time loop: f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <typename F, int... I>
+GONN_DEV void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+GONN_DEV void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 }  // namespace gonn
