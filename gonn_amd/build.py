@@ -35,7 +35,12 @@ CFLAGS = [
 # (one extra v_max per operand) and v_max3 is not formed. No value on that
 # path is NaN (masked scores are -inf), so the file is built with relaxed NaN
 # handling and the IEEE mode bit off, which turns the reductions into v_max3.
-FILE_FLAGS = {"attn_fwd.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"]}
+FILE_FLAGS = {
+    "attn_fwd.hip": ["-fno-honor-nans", "-mno-amdgpu-ieee"],
+    # MFMAs with VGPR accumulators (the score tiles the VALU reads); the file
+    # header gives the reason.
+    "attn_bwd_dq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 
 
 def sources():

@@ -22,7 +22,8 @@
 //         from those registers;
 //   dq    one workgroup per 128-query block, 32 queries per wave (the forward
 //         kernel's shape): S^T = K Q^T and dP^T = V dO^T with one QUERY per
-//         lane, so L_i and D_i are lane scalars; dQ^T += K^T dS^T.
+//         lane, so L_i and D_i are lane scalars; dQ^T += K^T dS^T. The bf16
+//         dQ kernel is in attn_bwd_dq.hip (built with other MFMA flags).
 // Causal work skips fully masked tiles and masks only diagonal ones.
 //
 // bf16 mode reads the packed bf16 operands of attn_pack.hip (row-major Qb,
@@ -35,9 +36,6 @@
 #include "kernels.h"
 
 namespace gonn {
-
-// Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
-constexpr int kSgVALU = 0x002, kSgMFMA = 0x008, kSgDSR = 0x100;
 
 // ---------------------------------------------------------------------------
 // prep: grid ceil(BH*Sp/16), 256 threads (16 lanes per query row).
@@ -96,6 +94,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 // masks exist only on the first two query tiles of a key block (its query
 // tiles start at the block's first key).
 // ---------------------------------------------------------------------------
+constexpr int kDkdvLookahead = 3;
+
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     constexpr int BN = 128;      // keys per workgroup
@@ -232,19 +232,20 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         constexpr int HCn = HC ? 2 * NDT : 0, HAn = HA ? NKS : 0;
         constexpr int GW = HCn + HAn;  // MFMAs per 16-query k-step group
         constexpr int NM = 4 * GW;
-        constexpr int LA = 3;
+        constexpr int LA = kDkdvLookahead;  // LDS operand lead (MFMA slots)
+        constexpr int NO = LA < 4 ? 4 : 8;
         constexpr int NDMA = 2 * NRI + 2 * NTI;
-        bf16x8 opr[4];
+        bf16x8 opr[NO];
         auto fetch = [&](auto E) {
             constexpr int e = decltype(E)::value, ks = e / GW, w = e % GW;
             if constexpr (w < HCn) {
                 constexpr int t = w % NDT;
                 const char* base = (w < NDT ? cdOt : cQt) + tsl + tq0;
-                opr[e & 3] = *(const bf16x8*)(base + (t * 32 * TST + ks * 16) * 2);
+                opr[e % NO] = *(const bf16x8*)(base + (t * 32 * TST + ks * 16) * 2);
             } else {
                 constexpr int u = w - HCn, kk = ks * (NKS / 4) + u / 4, mt = u & 1;
                 const char* base = ((u & 2) ? cdO : cQ) + rsl + rq0;
-                opr[e & 3] = *(const bf16x8*)(base + (mt * 32 * RST + kk * 16) * 2);
+                opr[e % NO] = *(const bf16x8*)(base + (mt * 32 * RST + kk * 16) * 2);
             }
         };
         auto issue = [&](auto E) {
@@ -252,15 +253,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             if constexpr (w < HCn) {
                 constexpr int t = w % NDT;
                 if constexpr (w < NDT)
-                    dvacc[t] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pp[ks]), dvacc[t]);
+                    dvacc[t] = mfma_bf16(opr[e % NO], __builtin_bit_cast(bf16x8, pp[ks]), dvacc[t]);
                 else
-                    dkacc[t] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pd[ks]), dkacc[t]);
+                    dkacc[t] = mfma_bf16(opr[e % NO], __builtin_bit_cast(bf16x8, pd[ks]), dkacc[t]);
             } else {
                 constexpr int u = w - HCn, kk = ks * (NKS / 4) + u / 4, mt = u & 1;
                 if constexpr (u & 2)
-                    dA[mt] = mfma_bf16(opr[e & 3], vf[kk], kk == 0 ? f32x16{} : dA[mt]);
+                    dA[mt] = mfma_bf16(opr[e % NO], vf[kk], kk == 0 ? f32x16{} : dA[mt]);
                 else
-                    sA[mt] = mfma_bf16(opr[e & 3], kf[kk], kk == 0 ? f32x16{} : sA[mt]);
+                    sA[mt] = mfma_bf16(opr[e % NO], kf[kk], kk == 0 ? f32x16{} : sA[mt]);
             }
         };
         // VALU of tile i in 8 groups k = mt*4 + j4 (registers 4 j4 .. +3 of
@@ -402,198 +403,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
                 }
                 *(f32x4*)(dkr + t * 32 + rq4 * 8 + g * 4) = a;
                 *(f32x4*)(dvr + t * 32 + rq4 * 8 + g * 4) = b;
-            }
-    }
-}
-
-// ---------------------------------------------------------------------------
-// bf16 dQ.
-//
-// One workgroup per 128-query block, 32 queries per wave (the forward's
-// shape): S^T = K Q^T and dP^T = V dO^T with one QUERY per lane, so L and D
-// are lane scalars, and dQ^T += K^T dS^T. One wave per SIMD; step t runs the
-// S^T/dP^T MFMAs of key tile t+1 (4 chains) interleaved with the VALU of tile
-// t, then the dQ MFMAs of tile t. K/V tiles run one tile ahead of the K^T
-// tiles; all stream HBM -> LDS with buffer_load_dwordx4 ... lds. Masks (causal
-// diagonal, key end) exist only on the last two key tiles of a query block.
-// ---------------------------------------------------------------------------
-template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
-    constexpr int BM = 128, BN = 64;
-    constexpr int KST = D + 8;   // K / V tile row stride (bf16)
-    constexpr int TST = BN + 8;  // K^T tile row stride (bf16)
-    constexpr int NKS = D / 16;
-    constexpr int NDT = D / 32;
-    constexpr int RCP = KST / 8, RCD = D / 8, NRP = BN * RCP;
-    constexpr int TCP = TST / 8, TCD = BN / 8, NTP = D * TCP;
-    constexpr int NRI = (NRP + 255) / 256, NTI = (NTP + 255) / 256;
-    constexpr int RLAST = NRP - (NRI - 1) * 256, TLAST = NTP - (NTI - 1) * 256;
-    static_assert(RLAST % 64 == 0 && TLAST % 64 == 0, "partial loads must be whole waves");
-    constexpr int RTILE = BN * KST, TTILE = D * TST;
-    __shared__ __attribute__((aligned(16))) bf16 sK[2 * RTILE];
-    __shared__ __attribute__((aligned(16))) bf16 sV[2 * RTILE];
-    __shared__ __attribute__((aligned(16))) bf16 sKt[2 * TTILE];
-
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int g = lane >> 5, ln = lane & 31;
-    const int S = p.S, Sp = p.Sp;
-    int bh, qb;
-    map_block(blockIdx.x, Sp / BM, p.BH, CAUSAL, bh, qb);
-    const int q0 = qb * BM;
-    const int qi = q0 + wave * 32 + ln;  // this lane's query (< Sp)
-
-    bf16x8 qf[NKS], df[NKS];
-    {
-        const bf16* qr = (const bf16*)p.q + ((size_t)bh * Sp + qi) * D + g * 8;
-        const bf16* dr = (const bf16*)p.dO + ((size_t)bh * Sp + qi) * D + g * 8;
-        for (int ks = 0; ks < NKS; ks++) {
-            qf[ks] = *(const bf16x8*)(qr + ks * 16);
-            df[ks] = *(const bf16x8*)(dr + ks * 16);
-        }
-    }
-    const float lq = p.lse2[(size_t)bh * Sp + qi];
-    const float dl = p.delta[(size_t)bh * Sp + qi];
-
-    int kend = S;
-    if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
-    const int nt = (kend + BN - 1) / BN;
-    const bf16* Kg = (const bf16*)p.k + (size_t)bh * Sp * D;
-    const bf16* Vg = (const bf16*)p.v + (size_t)bh * Sp * D;
-    const bf16* Ktg = (const bf16*)p.kt + (size_t)bh * D * Sp;
-
-    uint32_t roff[NRI], toff[NTI];
-    for (int i = 0; i < NRI; i++) {
-        const int pos = i * 256 + tid, r = pos / RCP, ch = pos % RCP;
-        roff[i] = (uint32_t)(((pos < NRP ? r : 0) * D + (ch < RCD ? ch : 0) * 8) * 2);
-    }
-    for (int i = 0; i < NTI; i++) {
-        const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
-        toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
-    }
-    const uint32_t slice = (uint32_t)Sp * D * 2;  // bytes of one (b,h) slice
-    const brsrc rk = make_rsrc(Kg, slice), rv = make_rsrc(Vg, slice), rkt = make_rsrc(Ktg, slice);
-    auto dma_row = [&](int kt, int slot) {  // K, V rows of key tile kt
-        const uint32_t so = (uint32_t)kt * BN * D * 2;
-        const uint32_t dk = lds_addr(sK) + (slot * RTILE + wave * 512) * 2;
-        const uint32_t dv = lds_addr(sV) + (slot * RTILE + wave * 512) * 2;
-        for (int i = 0; i < NRI; i++)
-            if (i < NRI - 1 || tid < RLAST) {
-                dma16(rk, dk + i * 4096, roff[i], so);
-                dma16(rv, dv + i * 4096, roff[i], so);
-            }
-    };
-    auto dma_tr = [&](int kt, int slot) {  // K^T of key tile kt
-        const uint32_t so = (uint32_t)kt * BN * 2;
-        const uint32_t dk = lds_addr(sKt) + (slot * TTILE + wave * 512) * 2;
-        for (int i = 0; i < NTI; i++)
-            if (i < NTI - 1 || tid < TLAST) dma16(rkt, dk + i * 4096, toff[i], so);
-    };
-    auto dma_wait = [] { GONN_VMCNT(0); };
-
-    auto sdp = [&](int slot, f32x16* s, f32x16* dp) {
-        const bf16* k = sK + slot * RTILE + ln * KST + g * 8;
-        const bf16* v = sV + slot * RTILE + ln * KST + g * 8;
-        s[0] = s[1] = dp[0] = dp[1] = f32x16{};
-        for (int ks = 0; ks < NKS; ks++)
-            for (int mt = 0; mt < 2; mt++) {
-                s[mt] = mfma_bf16(*(const bf16x8*)(k + mt * 32 * KST + ks * 16), qf[ks], s[mt]);
-                dp[mt] = mfma_bf16(*(const bf16x8*)(v + mt * 32 * KST + ks * 16), df[ks], dp[mt]);
-            }
-    };
-    // Masks of key tile kt on S^T: key >= S, or causal key > query. The
-    // exponent scale c2b is positive, so -inf gives P = 0 and dS = 0.
-    auto needs_mask = [&](int kt) {
-        const int kbase = kt * BN;
-        return (kbase + BN > S) || (CAUSAL && kbase + BN - 1 > q0 + wave * 32);
-    };
-    auto mask = [&](int kt, f32x16* s) {
-        const int kbase = kt * BN + 4 * g;
-        for (int mt = 0; mt < 2; mt++)
-            for (int r = 0; r < 16; r++) {
-                const int key = kbase + mt * 32 + 8 * (r >> 2) + (r & 3);
-                const bool off = key >= S || (CAUSAL && key > qi);
-                s[mt][r] = off ? -INFINITY : s[mt][r];
-            }
-    };
-
-    f32x16 dqacc[NDT];
-    for (int t = 0; t < NDT; t++) dqacc[t] = f32x16{};
-    const float c2 = p.c2b;
-
-    auto step = [&](auto next_tag, int t, f32x16* s, f32x16* dp, f32x16* sn, f32x16* dpn) {
-        constexpr bool NEXT = decltype(next_tag)::value;
-        const int slot = t & 1;
-        if constexpr (NEXT) {
-            dma_row(t + 2 < nt ? t + 2 : nt - 1, slot);
-            dma_tr(t + 1, slot ^ 1);
-            sdp(slot ^ 1, sn, dpn);
-        }
-        bf16x8 db[4];
-        for (int mt = 0; mt < 2; mt++) {
-            float d[16];
-            for (int r = 0; r < 16; r++) {
-                const float e = fast_exp2(__builtin_fmaf(s[mt][r], c2, -lq));
-                d[r] = e * (dp[mt][r] - dl);
-            }
-            db[2 * mt] = pack8(d[0], d[1], d[2], d[3], d[4], d[5], d[6], d[7]);
-            db[2 * mt + 1] = pack8(d[8], d[9], d[10], d[11], d[12], d[13], d[14], d[15]);
-        }
-        // dQ^T += K^T dS^T over 4 k-steps of 16 keys.
-        const bf16* kt_ = sKt + slot * TTILE + ln * TST + g * 8;
-        for (int ks = 0; ks < BN / 16; ks++)
-            for (int d = 0; d < NDT; d++)
-                dqacc[d] = mfma_bf16(*(const bf16x8*)(kt_ + d * 32 * TST + ks * 16), db[ks], dqacc[d]);
-        if constexpr (NEXT) {
-            constexpr int kV = (160 + 4 * NKS - 1) / (4 * NKS);
-            __builtin_amdgcn_sched_group_barrier(kSgDSR, 4, 0);
-            for (int k = 0; k < 4 * NKS; k++) {
-                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgVALU, kV, 0);
-            }
-            for (int k = 0; k < 4 * NDT; k++) {
-                __builtin_amdgcn_sched_group_barrier(kSgMFMA, 1, 0);
-                __builtin_amdgcn_sched_group_barrier(kSgDSR, 1, 0);
-            }
-            if (needs_mask(t + 1)) mask(t + 1, sn);
-        }
-        dma_wait();
-        __syncthreads();
-    };
-    using Yes = std::integral_constant<bool, true>;
-    using No = std::integral_constant<bool, false>;
-
-    dma_row(0, 0);
-    if (nt > 1) dma_row(1, 1);
-    dma_tr(0, 0);
-    dma_wait();
-    __syncthreads();
-    f32x16 sA[2], dA[2], sB[2], dB[2];
-    sdp(0, sA, dA);
-    if (needs_mask(0)) mask(0, sA);
-    __syncthreads();  // step 0 reloads row slot 0
-
-    int t = 0;
-    for (; t + 2 < nt; t += 2) {
-        step(Yes{}, t, sA, dA, sB, dB);
-        step(Yes{}, t + 1, sB, dB, sA, dA);
-    }
-    if (t + 1 < nt) {
-        step(Yes{}, t, sA, dA, sB, dB);
-        step(No{}, t + 1, sB, dB, sA, dA);
-    } else {
-        step(No{}, t, sA, dA, sB, dB);
-    }
-
-    if (qi < S) {
-        const float sc = p.dqs;
-        float* dqr = p.dq + ((size_t)bh * S + qi) * D;
-        for (int d = 0; d < NDT; d++)
-            for (int rq4 = 0; rq4 < 4; rq4++) {
-                f32x4 a;
-                for (int k = 0; k < 4; k++) a[k] = dqacc[d][rq4 * 4 + k] * sc;
-                *(f32x4*)(dqr + d * 32 + rq4 * 8 + g * 4) = a;
             }
     }
 }
@@ -898,8 +707,8 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipS
 hipError_t launch_bwd_dq(const BwdParams& p, int mode, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0) return hipErrorInvalidValue;
     const dim3 grid((p.Sp / 128) * p.BH);
-    if (mode == 1) GONN_BWD_LAUNCH(bwd_dq_bf16_kernel);
-    else GONN_BWD_LAUNCH(bwd_dq_f32_kernel);
+    if (mode == 1) return launch_bwd_dq_bf16(p, D, causal, s);
+    GONN_BWD_LAUNCH(bwd_dq_f32_kernel);
     return hipGetLastError();
 }
 

@@ -79,6 +79,8 @@ hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, fl
                            float* delta, int BH, int S, int Sp, int D, hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdParams& p, int mode, int D, int causal, hipStream_t s);
+// bf16 dQ (attn_bwd_dq.hip); launch_bwd_dq dispatches mode 1 here.
+hipError_t launch_bwd_dq_bf16(const BwdParams& p, int D, int causal, hipStream_t s);
 // Sequence padding of the backward's workspace layouts.
 constexpr int kBwdPad = 128;
 
