@@ -95,6 +95,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 // tiles start at the block's first key).
 // ---------------------------------------------------------------------------
 constexpr int kDkdvLookahead = 3;
+constexpr int kDkdvDmaSpan = 40;  // slots over which a step's tile loads are spread (0: all)
 
 template <int D, bool CAUSAL>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
@@ -161,23 +162,23 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     const brsrc rl = make_rsrc(lg, (uint32_t)Sp * 4), rd = make_rsrc(dg, (uint32_t)Sp * 4);
     const uint32_t lq = lds_addr(sQ) + wave * 1024, ldo = lds_addr(sdO) + wave * 1024;
     const uint32_t lqt = lds_addr(sQt) + wave * 1024, ldot = lds_addr(sdOt) + wave * 1024;
-    // Load j of the row tiles (Q: j < NRI, dO: j >= NRI) of query tile qb.
-    auto dma_row = [&](int qb, int slot, int j) {
+    // Load j of the row tiles (Q: j < NRI, dO: j >= NRI) of query tile qb,
+    // issued when the wave-uniform `on` is set (a scalar branch inside the
+    // load statement keeps the step one basic block).
+    auto dma_row = [&](int qb, int slot, int j, uint32_t on) {
         const uint32_t so = (uint32_t)qb * BM * D * 2;
         const int i = j % NRI;
         const brsrc r = j < NRI ? rq : rdo;
         const uint32_t dst = (j < NRI ? lq : ldo) + slot * RTB + i * 4096;
-        if (i < NRI - 1) dma16(r, dst, roff[i], so);
-        else dma16_if(r, dst, roff[i], so, rlast);
+        dma16_if(r, dst, roff[i], so, i < NRI - 1 ? on : on & rlast);
     };
     // Load j of the transposed tiles (Q^T: j < NTI, dO^T: j >= NTI).
-    auto dma_tr = [&](int qb, int slot, int j) {
+    auto dma_tr = [&](int qb, int slot, int j, uint32_t on) {
         const uint32_t so = (uint32_t)qb * BM * 2;
         const int i = j % NTI;
         const brsrc r = j < NTI ? rqt : rdot;
         const uint32_t dst = (j < NTI ? lqt : ldot) + slot * TTB + i * 4096;
-        if (i < NTI - 1) dma16(r, dst, toff[i], so);
-        else dma16_if(r, dst, toff[i], so, tlast);
+        dma16_if(r, dst, toff[i], so, i < NTI - 1 ? on : on & tlast);
     };
     // L and D of query tile qb: wave 0, lanes 0-15 load the 64 L values
     // (bytes 0-255 of sLD[slot]), lanes 16-31 the 64 D values (256-511).
@@ -205,20 +206,24 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
 
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     // One pipeline step. sA <- S(i+1), dA <- dP(i+1); sB, dB = S(i), dP(i).
-    auto step = [&](auto ha_tag, auto hb_tag, auto hc_tag, int i, f32x16* sA, f32x16* dA,
-                    f32x16* sB, f32x16* dB) __attribute__((always_inline)) {
+    auto step = [&](auto ha_tag, auto hb_tag, auto hc_tag, auto mk_tag, int i, f32x16* sA,
+                    f32x16* dA, f32x16* sB, f32x16* dB) __attribute__((always_inline)) {
         constexpr bool HA = decltype(ha_tag)::value;  // S/dP of tile i+1
         constexpr bool HB = decltype(hb_tag)::value;  // P/dS of tile i
         constexpr bool HC = decltype(hc_tag)::value;  // dV/dK of tile i-1
+        constexpr bool MK = decltype(mk_tag)::value;  // tile i may need the causal mask
         const int qb = qb0 + i;
         // Loads for the next step: row tile i+2, transposed tile i, L/D i+1.
-        const bool dr = HA && i + 2 < nq, dt = HB, dl = HA;
+        const uint32_t dr = HA && i + 2 < nq, dt = HB;
+        const bool dl = HA;
         if (dl) dma_ld(qb + 1, (i + 1) & 1);
-        // Causal mask (key > query), only on the first two tiles. The
-        // exponent scale c2b is positive (a negative scale is folded into
-        // the packed Q), so a masked score of -inf gives P = 0 and dS = 0.
-        if constexpr (HB) {
-            if (CAUSAL && i < 2) {
+        // Causal mask (key > query), only on the first two tiles (steps with
+        // MK set; kept out of the other steps, where the selects would pull
+        // every score out of its accumulator registers). The exponent scale
+        // c2b is positive (a negative scale is folded into the packed Q), so
+        // a masked score of -inf gives P = 0 and dS = 0.
+        if constexpr (HB && MK) {
+            if (i < 2) {
                 const int kq = kj - qb * BM - 4 * g;  // key minus the lane group's base query
                 for (int mt = 0; mt < 2; mt++)
                     for (int r = 0; r < 16; r++)
@@ -235,6 +240,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         constexpr int LA = kDkdvLookahead;  // LDS operand lead (MFMA slots)
         constexpr int NO = LA < 4 ? 4 : 8;
         constexpr int NDMA = 2 * NRI + 2 * NTI;
+        constexpr int SPAN = kDkdvDmaSpan > 0 && kDkdvDmaSpan < NM ? kDkdvDmaSpan : NM;
+        constexpr int DS = SPAN / NDMA > 0 ? SPAN / NDMA : 1;
         bf16x8 opr[NO];
         auto fetch = [&](auto E) {
             constexpr int e = decltype(E)::value, ks = e / GW, w = e % GW;
@@ -319,15 +326,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             constexpr int e = decltype(E)::value;
             if constexpr (e + LA < NM) fetch(std::integral_constant<int, e + LA>{});
             issue(E);
-            // Tile loads spread over the stream: slots 1, 1 + DS, ...
-            constexpr int DS = NM / NDMA > 0 ? NM / NDMA : 1;
+            // Tile loads spread over the first SPAN slots: 1, 1 + DS, ...
             if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
                 constexpr int d = (e - 1) / DS;
-                if constexpr (d < 2 * NRI) {
-                    if (dr) dma_row(qb + 2, i & 1, d);
-                } else {
-                    if (dt) dma_tr(qb, i & 1, d - 2 * NRI);
-                }
+                if constexpr (d < 2 * NRI) dma_row(qb + 2, i & 1, d, dr);
+                else dma_tr(qb, i & 1, d - 2 * NRI, dt);
             }
             uops_at(E);
             __builtin_amdgcn_sched_barrier(0);
@@ -335,13 +338,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         // Loads not placed in the stream (a step with too few MFMAs).
         static_for<NDMA>([&](auto Dd) {
             constexpr int d = decltype(Dd)::value;
-            constexpr int DS = NM / NDMA > 0 ? NM / NDMA : 1;
             if constexpr (NM == 0 || 1 + d * DS >= NM) {
-                if constexpr (d < 2 * NRI) {
-                    if (dr) dma_row(qb + 2, i & 1, d);
-                } else {
-                    if (dt) dma_tr(qb, i & 1, d - 2 * NRI);
-                }
+                if constexpr (d < 2 * NRI) dma_row(qb + 2, i & 1, d, dr);
+                else dma_tr(qb, i & 1, d - 2 * NRI, dt);
             }
         });
         uops_at(std::integral_constant<int, NM>{});
@@ -352,9 +351,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     using No = std::integral_constant<bool, false>;
 
     // Prologue: row tiles 0, 1 and L/D of tile 0; S/dP of tile 0.
-    for (int j = 0; j < 2 * NRI; j++) dma_row(qb0, 0, j);
-    if (nq > 1)
-        for (int j = 0; j < 2 * NRI; j++) dma_row(qb0 + 1, 1, j);
+    for (int j = 0; j < 2 * NRI; j++) dma_row(qb0, 0, j, 1);
+    for (int j = 0; j < 2 * NRI; j++) dma_row(qb0 + 1, 1, j, nq > 1);
     dma_ld(qb0, 0);
     GONN_VMCNT(0);
     __syncthreads();
@@ -369,24 +367,32 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
 
     // Steps 0 .. nq: step i has S/dP(i+1) while i+1 < nq, P/dS(i) while
     // i < nq, dV/dK(i-1) from i = 1.
+    // Even steps write S/dP into sY/dY and read sX/dX, odd steps the reverse.
+    // Steps 0 and 1 carry the causal mask; the loop starts at step 2.
+    using Mk = std::integral_constant<bool, CAUSAL>;
     if (nq == 1) {
-        step(No{}, Yes{}, No{}, 0, sY, dY, sX, dX);
-        step(No{}, No{}, Yes{}, 1, sX, dX, sY, dY);
+        step(No{}, Yes{}, No{}, Mk{}, 0, sY, dY, sX, dX);
+        step(No{}, No{}, Yes{}, No{}, 1, sX, dX, sY, dY);
+    } else if (nq == 2) {
+        step(Yes{}, Yes{}, No{}, Mk{}, 0, sY, dY, sX, dX);
+        step(No{}, Yes{}, Yes{}, Mk{}, 1, sX, dX, sY, dY);
+        step(No{}, No{}, Yes{}, No{}, 2, sY, dY, sX, dX);
     } else {
-        step(Yes{}, Yes{}, No{}, 0, sY, dY, sX, dX);
-        int i = 1;
+        step(Yes{}, Yes{}, No{}, Mk{}, 0, sY, dY, sX, dX);
+        step(Yes{}, Yes{}, Yes{}, Mk{}, 1, sX, dX, sY, dY);
+        int i = 2;
         for (; i + 2 < nq; i += 2) {
-            step(Yes{}, Yes{}, Yes{}, i, sX, dX, sY, dY);
-            step(Yes{}, Yes{}, Yes{}, i + 1, sY, dY, sX, dX);
+            step(Yes{}, Yes{}, Yes{}, No{}, i, sY, dY, sX, dX);
+            step(Yes{}, Yes{}, Yes{}, No{}, i + 1, sX, dX, sY, dY);
         }
         // i = nq-2 or nq-1 remain (then the final dV/dK step)
         if (i + 1 < nq) {
-            step(Yes{}, Yes{}, Yes{}, i, sX, dX, sY, dY);
-            step(No{}, Yes{}, Yes{}, i + 1, sY, dY, sX, dX);
-            step(No{}, No{}, Yes{}, i + 2, sX, dX, sY, dY);
+            step(Yes{}, Yes{}, Yes{}, No{}, i, sY, dY, sX, dX);
+            step(No{}, Yes{}, Yes{}, No{}, i + 1, sX, dX, sY, dY);
+            step(No{}, No{}, Yes{}, No{}, i + 2, sY, dY, sX, dX);
         } else {
-            step(No{}, Yes{}, Yes{}, i, sX, dX, sY, dY);
-            step(No{}, No{}, Yes{}, i + 1, sY, dY, sX, dX);
+            step(No{}, Yes{}, Yes{}, No{}, i, sY, dY, sX, dX);
+            step(No{}, No{}, Yes{}, No{}, i + 1, sX, dX, sY, dY);
         }
     }
 
