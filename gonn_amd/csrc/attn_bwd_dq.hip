@@ -36,6 +36,19 @@ namespace gonn {
 // a step to arrive (an L2 miss takes about a microsecond); the dP^T
 // accumulator starts at -D, which saves the subtraction per score.
 // ---------------------------------------------------------------------------
+// Softmax micro-ops of one 16-key k-step (4 score pairs): j -> pair, kind
+// (0 / 1: FMA + exp2 of score 0 / 1 of the pair, 2: products + bf16 pack).
+constexpr int kDqPairOf[12] = {0, 0, 1, 1, 0, 2, 2, 1, 3, 3, 2, 3};
+constexpr int kDqKindOf[12] = {0, 1, 0, 1, 2, 0, 1, 2, 0, 1, 2, 2};
+// Slot of micro-op j of k-step q in a step of GW MFMAs per k-step whose
+// first HCn MFMAs of each group are the dQ products reading pd[q].
+template <int GW, int HCn>
+constexpr int dq_uop_slot(int q, int j) {
+    int s = q * GW + (j * GW) / 12;
+    if (kDqKindOf[j] == 2 && HCn > 0 && s < q * GW + HCn - 1) s = q * GW + HCn - 1;
+    return s;
+}
+
 constexpr int kDqDmaSpan = 24;     // slots over which the step's tile loads are spread
 constexpr int kDqLookahead = 3;    // LDS operand lead (deeper measured no faster)
 constexpr bool kDqFragsInAgpr = true;
@@ -198,22 +211,20 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
             }
         };
         // dS of tile t as 16 score pairs k (registers (k%8)*2, +1 of
-        // sB/dB[k/8]; 16-key k-step k/4 of the dQ product), each in two
-        // micro-ops: A (exp2 of the pair), B (dS, bf16 pair into pd).
+        // sB/dB[k/8]; 16-key k-step k/4 of the dQ product), each in three
+        // micro-ops: E0 / E1 (FMA + exp2 of one score, ~20 VALU cycles) and
+        // P (two products and the bf16 pair into pd, ~12 cycles). The 12
+        // micro-ops of k-step q are spread one per MFMA slot over its group
+        // of GW slots, so no slot carries more VALU than its MFMA hides; a
+        // P micro-op of k-step q comes after the dQ MFMAs that read pd[q].
         float ue[16][2];
-        auto ub = [](int k, int st) {
-            const int b = (k >> 2) * GW + (HCn ? HCn - 1 : 0) + (k & 3);
-            const int s = st == 0 ? b - 2 : b;
-            return s < 0 ? 0 : s;
-        };
-        auto uop = [&](auto K, auto ST) {
-            constexpr int k = decltype(K)::value, st = decltype(ST)::value;
-            constexpr int mt = k >> 3, r = (k & 7) * 2;
-            if constexpr (st == 0) {
-                ue[k][0] = fast_exp2(__builtin_fmaf(sB[mt][r], c2, -lq));
-                ue[k][1] = fast_exp2(__builtin_fmaf(sB[mt][r + 1], c2, -lq));
-                pin(ue[k][0]);
-                pin(ue[k][1]);
+        auto uop = [&](auto Q, auto J) {
+            constexpr int q = decltype(Q)::value, j = decltype(J)::value;
+            constexpr int k = 4 * q + kDqPairOf[j], mt = k >> 3, r = (k & 7) * 2;
+            if constexpr (kDqKindOf[j] < 2) {
+                constexpr int h = kDqKindOf[j];
+                ue[k][h] = fast_exp2(__builtin_fmaf(sB[mt][r + h], c2, -lq));
+                pin(ue[k][h]);
             } else {
                 const float d0 = ue[k][0] * dB[mt][r];
                 const float d1 = ue[k][1] * dB[mt][r + 1];
@@ -225,10 +236,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
         auto uops_at = [&](auto E) {
             constexpr int e = decltype(E)::value;
             if constexpr (HB) {
-                static_for<2>([&](auto ST) {
-                    static_for<16>([&](auto K) {
-                        constexpr int at = ub(decltype(K)::value, decltype(ST)::value);
-                        if constexpr (e < NM ? at == e : at >= NM) uop(K, ST);
+                static_for<4>([&](auto Q) {
+                    static_for<12>([&](auto J) {
+                        constexpr int at = dq_uop_slot<GW, HCn>(decltype(Q)::value, decltype(J)::value);
+                        if constexpr (e < NM ? at == e : at >= NM) uop(Q, J);
                     });
                 });
             }
