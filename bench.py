@@ -27,6 +27,7 @@ import json
 import math
 import os
 import platform
+import statistics
 import sys
 import time
 
@@ -68,6 +69,22 @@ def load_traffic(key: str):
         return None
 
 
+def _run_steps(torch, run, steps):
+    """Time `steps` back-to-back calls on the current stream with an event
+    before each call and one after the last: (mean ms, median ms, wall s).
+    The mean is the span of the whole run over `steps`."""
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i].record()
+        run()
+    ev[steps].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
+    return ev[0].elapsed_time(ev[steps]) / steps, statistics.median(per), wall
+
+
 def bench_prefill(torch, hip, steps, warmup):
     B, H, S, D = 4, 32, 4096, 128
     flop = 4.0 * B * H * S * S * D * 0.5
@@ -81,15 +98,7 @@ def bench_prefill(torch, hip, steps, warmup):
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    e0.record()
-    for _ in range(steps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_time(e1) / steps
+    ms, med, wall = _run_steps(torch, run, steps)
     # per-kernel pass (events recorded by the library around each stage)
     hip.profile_reset()
     hip.profile_enable(True)
@@ -102,7 +111,7 @@ def bench_prefill(torch, hip, steps, warmup):
     hip.profile_reset()
     # The library splits a large forward into head chunks (one pack and one
     # attention launch each): per-launch time and FLOP, launches per step.
-    return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, wall_s=wall,
+    return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, median_ms=med, wall_s=wall,
                 kernel_ms=kt / max(kn, 1), pack_ms=pt / max(pn, 1),
                 launches=max(kn, 1) / steps, q=q, k=k, v=v)
 
@@ -123,13 +132,7 @@ def bench_decode(torch, hip, steps, warmup):
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms, med, _ = _run_steps(torch, run, steps)
     hip.profile_reset()
     hip.profile_enable(True)
     for _ in range(steps):
@@ -141,7 +144,7 @@ def bench_decode(torch, hip, steps, warmup):
     hip.profile_reset()
     del kc, vc
     return dict(B=B, H=H, Lmax=Lmax, D=D, mean_len=float(lens.mean()), bytes=nbytes, ms=ms,
-                split_ms=st / max(sn, 1), combine_ms=ct / max(cn, 1))
+                median_ms=med, split_ms=st / max(sn, 1), combine_ms=ct / max(cn, 1))
 
 
 def _timed(torch, hip, run, steps, warmup, stages):
@@ -151,13 +154,7 @@ def _timed(torch, hip, run, steps, warmup, stages):
     for _ in range(warmup):
         run()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        run()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms, med, _ = _run_steps(torch, run, steps)
     hip.profile_reset()
     hip.profile_enable(True)
     for _ in range(steps):
@@ -170,7 +167,7 @@ def _timed(torch, hip, run, steps, warmup, stages):
         per[st] = t / max(n, 1)
         launches[st] = max(n, 1) / steps
     hip.profile_reset()
-    return ms, per, launches
+    return (ms, med), per, launches
 
 
 def bench_fwd_bwd(torch, hip, steps, warmup):
@@ -187,11 +184,12 @@ def bench_fwd_bwd(torch, hip, steps, warmup):
     def run():
         hip.attn_fwd(q, k, v, causal=True, mode="bf16", out=o, lse_out=lse)
         hip.attn_bwd(q, k, v, o, lse, do, causal=True, mode="bf16", out=grads)
-    ms, per, nl = _timed(torch, hip, run, steps, warmup,
+    (ms, med), per, nl = _timed(torch, hip, run, steps, warmup,
                          ("pack_kv", "fwd_bf16", "bwd_prep", "bwd_pack", "bwd_dkdv", "bwd_dq"))
     # stage times per step (a stage may be several launches)
     per = {k: v * nl[k] for k, v in per.items()}
-    return dict(B=B, H=H, S=S, D=D, fwd_flop=fwd_flop, bwd_flop=bwd_flop, ms=ms, per=per)
+    return dict(B=B, H=H, S=S, D=D, fwd_flop=fwd_flop, bwd_flop=bwd_flop, ms=ms, median_ms=med,
+                per=per)
 
 
 def bench_encoder(torch, hip, steps, warmup, mode):
@@ -204,8 +202,8 @@ def bench_encoder(torch, hip, steps, warmup, mode):
     o = torch.empty_like(q)
     run = lambda: hip.attn_fwd(q, k, v, causal=False, mode=mode, out=o)  # noqa: E731
     kname = "fwd_bf16" if mode == "bf16" else "fwd_f32"
-    ms, per, nl = _timed(torch, hip, run, steps, warmup, ("pack_kv", kname))
-    return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, kernel_ms=per[kname],
+    (ms, med), per, nl = _timed(torch, hip, run, steps, warmup, ("pack_kv", kname))
+    return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, median_ms=med, kernel_ms=per[kname],
                 pack_ms=per["pack_kv"], launches=nl[kname])
 
 
@@ -299,6 +297,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(pre["ms"], 5),
+        "median_ms_per_step": round(pre["median_ms"], 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -321,7 +320,8 @@ def main():
         kgbs = dec["bytes"] / (dec["split_ms"] * 1e-3) / 1e9
         line["decode"] = {
             "metric": "decode HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
-            "ms_per_step": round(dec["ms"], 5), "bytes_per_step": dec["bytes"],
+            "ms_per_step": round(dec["ms"], 5), "median_ms_per_step": round(dec["median_ms"], 5),
+            "bytes_per_step": dec["bytes"],
             "config": {"workload": "C4 split-KV decode, bf16 cache", "B": dec["B"],
                        "H": dec["H"], "Lmax": dec["Lmax"], "D": dec["D"],
                        "mean_len": dec["mean_len"]},
@@ -341,6 +341,7 @@ def main():
         line["fwd_bwd"] = {
             "metric": "causal fwd+bwd TFLOP/s", "value": round(tot / (fb["ms"] * 1e-3) / 1e12, 3),
             "unit": "TFLOP/s", "ms_per_step": round(fb["ms"], 4),
+            "median_ms_per_step": round(fb["median_ms"], 4),
             "config": {"workload": "C5 causal flash fwd+bwd, fp32 in/out, bf16 MFMA",
                        "B": fb["B"], "H": fb["H"], "S": fb["S"], "D": fb["D"],
                        "fwd_flop": fb["fwd_flop"], "bwd_flop": fb["bwd_flop"]},
@@ -363,7 +364,7 @@ def main():
             ach = en["flop"] / en["launches"] / (en["kernel_ms"] * 1e-3) / 1e12
             line["encoder"][mode] = {
                 "value": round(en["flop"] / (en["ms"] * 1e-3) / 1e12, 3), "unit": "TFLOP/s",
-                "ms_per_step": round(en["ms"], 5),
+                "ms_per_step": round(en["ms"], 5), "median_ms_per_step": round(en["median_ms"], 5),
                 "config": {"workload": f"C2 encoder non-causal, fp32 in/out, {mode} MFMA",
                            "B": en["B"], "H": en["H"], "S": en["S"], "D": en["D"]},
                 "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": peak,

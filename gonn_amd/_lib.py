@@ -36,6 +36,9 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_flash_attn_f64", "gonn_hip_flash_attn_f64_fwd", "gonn_hip_flash_attn_f64_bwd",
     "gonn_hip_bench_flash_attn_f64", "gonn_hip_profile_enable", "gonn_hip_profile_reset",
     "gonn_hip_profile_read", "gonn_hip_selftest_mfma",
+    "gonn_hip_kvcache_create", "gonn_hip_kvcache_free", "gonn_hip_kvcache_reset",
+    "gonn_hip_kvcache_lengths", "gonn_hip_kvcache_append", "gonn_hip_kvcache_append_f64",
+    "gonn_hip_kvcache_attend", "gonn_hip_kvcache_attend_f64",
 )
 
 
@@ -116,6 +119,16 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_selftest_mfma.restype = i
     lib.gonn_hip_profile_enable.argtypes = [i]
     lib.gonn_hip_profile_read.argtypes = [ctypes.c_char_p, dp, ctypes.POINTER(i)]
+    ip = ctypes.POINTER(i)
+    lib.gonn_hip_kvcache_create.argtypes = [ctypes.POINTER(vp), i, i, i, i]
+    lib.gonn_hip_kvcache_free.argtypes = [vp]
+    lib.gonn_hip_kvcache_reset.argtypes = [vp]
+    lib.gonn_hip_kvcache_lengths.argtypes = [vp, ip]
+    lib.gonn_hip_kvcache_append.argtypes = [vp, ctypes.POINTER(Buf), ctypes.POINTER(Buf), i, ip, vp]
+    lib.gonn_hip_kvcache_append_f64.argtypes = [vp, dp, dp, i, ip]
+    lib.gonn_hip_kvcache_attend.argtypes = [vp, ctypes.POINTER(Buf), ctypes.POINTER(Buf),
+                                            ctypes.c_double, vp]
+    lib.gonn_hip_kvcache_attend_f64.argtypes = [vp, dp, dp, ctypes.c_double]
     _lib = lib
     return lib
 

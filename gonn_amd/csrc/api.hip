@@ -6,12 +6,14 @@
 // (backend/cuda/gonn_cuda.cu:466-560) but check every runtime call.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <new>
 #include <vector>
 
 #include "../../include/gonn_hip.h"
@@ -276,6 +278,74 @@ int run_fwd_f32(DevMem& mem, const float* q, const float* k, const float* v, flo
 }
 
 bool shim_args_ok(int BH, int S, int d) { return BH > 0 && S > 0 && d > 0 && d <= 128; }
+
+}  // namespace
+
+// The KV-cache handle of the C ABI (opaque to callers).
+struct gonn_kvcache {
+    int B = 0, H = 0, Lmax = 0, D = 0;
+    void* k = nullptr;    // bf16 (B,H,Lmax,D)
+    void* v = nullptr;
+    int* d_len = nullptr;  // device int32[B]: cached positions per sequence
+    int* d_pc = nullptr;   // device int32[2B]: positions and counts of an append
+    void* ws = nullptr;    // decode workspace
+    size_t ws_bytes = 0;
+    std::vector<int> h_len;  // host copy of the lengths (authoritative)
+    std::vector<int> h_pc;
+};
+
+namespace {
+
+void kv_release(gonn_kvcache* c) {
+    void* ptrs[] = {c->k, c->v, c->d_len, c->d_pc, c->ws};
+    for (void* p : ptrs)
+        if (p) (void)hipFree(p);
+    c->k = c->v = c->ws = nullptr;
+    c->d_len = c->d_pc = nullptr;
+}
+
+gonn_attn_decode_args kv_decode_args(const gonn_kvcache* c) {
+    gonn_attn_decode_args a{};
+    const size_t n = (size_t)c->B * c->H * c->Lmax * c->D;
+    a.kcache = {c->k, n * 2, GONN_BF16};
+    a.vcache = {c->v, n * 2, GONN_BF16};
+    a.kv_len = {c->d_len, (size_t)c->B * 4, GONN_I32};
+    a.B = c->B;
+    a.H = c->H;
+    a.Lmax = c->Lmax;
+    a.D = c->D;
+    a.split_keys = 0;
+    return a;
+}
+
+// Checks an append of T rows per sequence (counts: host int[B] or null = T);
+// fills c->h_pc with (positions, counts).
+int kv_check_append(gonn_kvcache* c, int T, const int* counts) {
+    if (T <= 0) return GONN_E_INVALID;
+    c->h_pc.assign(2 * (size_t)c->B, 0);
+    for (int b = 0; b < c->B; b++) {
+        const int n = counts ? counts[b] : T;
+        if (n < 0 || n > T) return GONN_E_INVALID;
+        if ((long long)c->h_len[b] + n > c->Lmax) return GONN_E_INVALID;
+        c->h_pc[b] = c->h_len[b];
+        c->h_pc[c->B + b] = n;
+    }
+    return GONN_OK;
+}
+
+// Launches the append (k, v device, f32 or bf16 (B,H,T,D)) and advances the
+// lengths; synchronous.
+int kv_append_dev(gonn_kvcache* c, const void* k, const void* v, int src_bf16, int T,
+                  hipStream_t s) {
+    TRYH(hipMemcpyAsync(c->d_pc, c->h_pc.data(), 2 * (size_t)c->B * sizeof(int),
+                        hipMemcpyHostToDevice, s));
+    TRYH(gonn::launch_kv_append(k, v, src_bf16, c->k, c->v, c->d_pc, c->d_pc + c->B, c->B, c->H,
+                                T, c->Lmax, c->D, s));
+    for (int b = 0; b < c->B; b++) c->h_len[b] += c->h_pc[c->B + b];
+    TRYH(hipMemcpyAsync(c->d_len, c->h_len.data(), (size_t)c->B * sizeof(int),
+                        hipMemcpyHostToDevice, s));
+    return herr(hipStreamSynchronize(s));
+}
 
 }  // namespace
 
@@ -762,6 +832,115 @@ int gonn_hip_profile_read(const char* kernel, double* total_ms, int* count) {
 int gonn_hip_selftest_mfma(void) {
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
     return gonn::selftest_mfma();
+}
+
+// ---- KV cache ---------------------------------------------------------------
+
+int gonn_hip_kvcache_create(gonn_kvcache** out, int B, int H, int Lmax, int D) {
+    if (!out) return GONN_E_INVALID;
+    *out = nullptr;
+    if (B <= 0 || H <= 0 || Lmax <= 0 || D <= 0) return GONN_E_INVALID;
+    if (!head_dim_ok(D)) return GONN_E_UNSUPPORTED;
+    const size_t n = (size_t)B * H * Lmax * D;
+    if ((double)n * 2 >= 9.0e18 || (double)B * H * Lmax >= 2147483647.0) return GONN_E_UNSUPPORTED;
+    if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    if (fail_alloc_injected()) return GONN_E_INJECTED;
+    gonn_kvcache* c = new (std::nothrow) gonn_kvcache;
+    if (!c) return GONN_E_NOMEM;
+    c->B = B;
+    c->H = H;
+    c->Lmax = Lmax;
+    c->D = D;
+    c->h_len.assign(B, 0);
+    gonn_attn_decode_args a = kv_decode_args(c);
+    c->ws_bytes = decode_ws(&a);
+    const size_t bytes[] = {n * 2, n * 2, (size_t)B * 4, (size_t)B * 8, c->ws_bytes};
+    void** slots[] = {&c->k, &c->v, (void**)&c->d_len, (void**)&c->d_pc, &c->ws};
+    for (int i = 0; i < 5; i++) {
+        if (hipMalloc(slots[i], bytes[i] ? bytes[i] : 16) != hipSuccess) {
+            (void)hipGetLastError();
+            *slots[i] = nullptr;
+            kv_release(c);
+            delete c;
+            return GONN_E_NOMEM;
+        }
+    }
+    const hipError_t e = hipMemset(c->d_len, 0, (size_t)B * 4);
+    if (e != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+        kv_release(c);
+        delete c;
+        return herr(e != hipSuccess ? e : hipErrorUnknown);
+    }
+    *out = c;
+    return GONN_OK;
+}
+
+int gonn_hip_kvcache_free(gonn_kvcache* c) {
+    if (!c) return GONN_OK;
+    kv_release(c);
+    delete c;
+    return GONN_OK;
+}
+
+int gonn_hip_kvcache_reset(gonn_kvcache* c) {
+    if (!c) return GONN_E_INVALID;
+    std::fill(c->h_len.begin(), c->h_len.end(), 0);
+    TRYH(hipMemcpy(c->d_len, c->h_len.data(), (size_t)c->B * 4, hipMemcpyHostToDevice));
+    return GONN_OK;
+}
+
+int gonn_hip_kvcache_lengths(const gonn_kvcache* c, int* len) {
+    if (!c || !len) return GONN_E_INVALID;
+    for (int b = 0; b < c->B; b++) len[b] = c->h_len[b];
+    return GONN_OK;
+}
+
+int gonn_hip_kvcache_append(gonn_kvcache* c, const gonn_buf* k, const gonn_buf* v, int T,
+                            const int* counts, void* stream) {
+    if (!c || !k || !v) return GONN_E_INVALID;
+    if (k->dtype != v->dtype || (k->dtype != GONN_F32 && k->dtype != GONN_BF16))
+        return GONN_E_INVALID;
+    if (T <= 0) return GONN_E_INVALID;
+    const size_t n = (size_t)c->B * c->H * T * c->D;
+    if (!buf_ok(*k, n, k->dtype) || !buf_ok(*v, n, v->dtype)) return GONN_E_INVALID;
+    if (((uintptr_t)k->ptr | (uintptr_t)v->ptr) & 15) return GONN_E_INVALID;
+    TRY(kv_check_append(c, T, counts));
+    return kv_append_dev(c, k->ptr, v->ptr, k->dtype == GONN_BF16, T, (hipStream_t)stream);
+}
+
+int gonn_hip_kvcache_append_f64(gonn_kvcache* c, const double* k, const double* v, int T,
+                                const int* counts) {
+    if (!c || !k || !v) return GONN_E_INVALID;
+    TRY(kv_check_append(c, T, counts));
+    const size_t rows = (size_t)c->B * c->H * T;
+    DevMem mem;
+    float *kd = nullptr, *vd = nullptr;
+    TRY(upload_padded(mem, k, rows, c->D, c->D, &kd));
+    TRY(upload_padded(mem, v, rows, c->D, c->D, &vd));
+    return kv_append_dev(c, kd, vd, 0, T, nullptr);
+}
+
+int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, double scale,
+                            void* stream) {
+    if (!c || !q || !o) return GONN_E_INVALID;
+    gonn_attn_decode_args a = kv_decode_args(c);
+    a.q = *q;
+    a.o = *o;
+    a.scale = scale;
+    return gonn_hip_attn_decode(&a, c->ws, c->ws_bytes, stream);
+}
+
+int gonn_hip_kvcache_attend_f64(gonn_kvcache* c, const double* q, double* o, double scale) {
+    if (!c || !q || !o) return GONN_E_INVALID;
+    const size_t rows = (size_t)c->B * c->H;
+    DevMem mem;
+    float* qd = nullptr;
+    void* od = nullptr;
+    TRY(upload_padded(mem, q, rows, c->D, c->D, &qd));
+    TRY(mem.alloc(&od, rows * c->D * sizeof(float)));
+    gonn_buf qb{qd, rows * c->D * 4, GONN_F32}, ob{od, rows * c->D * 4, GONN_F32};
+    TRY(gonn_hip_kvcache_attend(c, &qb, &ob, scale, nullptr));
+    return download_padded(mem, (const float*)od, rows, c->D, c->D, o);
 }
 
 }  // extern "C"

@@ -20,7 +20,9 @@
 //  * each lane row runs its own online softmax in log2 units (scale*log2e is
 //    folded into q); the 16 lane rows of a workgroup merge through LDS and
 //    write one partial (m, l, o[D]) per split;
-//  * combine kernel: per (b,h), O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s.
+//  * combine kernel: per (b,h), O = sum_s 2^(m_s-M) o_s / sum_s 2^(m_s-M) l_s;
+//  * kv_append kernel: writes new K/V rows (f32 or bf16) into the bf16 cache
+//    at each sequence's current length (the KV-cache handle of the C ABI).
 #include "common.h"
 #include "kernels.h"
 
@@ -145,6 +147,57 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeParams p) {
         O = __builtin_fmaf(w, po[(size_t)s * D + tid], O);
     }
     p.o[(size_t)bh * D + tid] = ns > 0 ? O / L : 0.f;
+}
+
+// KV-cache append: row t < cnt[b] of (b, h) in the sources (B,H,T,D), f32 or
+// bf16, goes to position pos[b] + t of the bf16 cache (B,H,Lmax,D); rows at
+// or past Lmax are dropped (the host rejects such appends beforehand). One
+// thread per 8 elements of K and of V (one 16-byte store each).
+template <typename ST>
+__global__ __launch_bounds__(256) void kv_append_kernel(const ST* __restrict__ ks,
+                                                        const ST* __restrict__ vs, bf16* kc,
+                                                        bf16* vc, const int* __restrict__ pos,
+                                                        const int* __restrict__ cnt, int H,
+                                                        int T, int Lmax, int D, size_t nchunk) {
+    const size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= nchunk) return;
+    const int cpr = D / 8;  // 16-byte chunks per row
+    const size_t row = c / cpr;
+    const int e0 = (int)(c % cpr) * 8;
+    const int t = (int)(row % T);
+    const size_t bh = row / T;
+    const int b = (int)(bh / H);
+    if (t >= cnt[b]) return;
+    const int dst_t = pos[b] + t;
+    if (dst_t < 0 || dst_t >= Lmax) return;
+    const size_t src = row * D + e0, dst = (bh * Lmax + dst_t) * D + e0;
+    bf16x8 kk, vv;
+    if constexpr (sizeof(ST) == 4) {
+        const f32x4 k0 = *(const f32x4*)(ks + src), k1 = *(const f32x4*)(ks + src + 4);
+        const f32x4 v0 = *(const f32x4*)(vs + src), v1 = *(const f32x4*)(vs + src + 4);
+        kk = pack8(k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]);
+        vv = pack8(v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]);
+    } else {
+        kk = *(const bf16x8*)(ks + src);
+        vv = *(const bf16x8*)(vs + src);
+    }
+    *(bf16x8*)(kc + dst) = kk;
+    *(bf16x8*)(vc + dst) = vv;
+}
+
+hipError_t launch_kv_append(const void* ks, const void* vs, int src_bf16, void* kc, void* vc,
+                            const int* pos, const int* cnt, int B, int H, int T, int Lmax,
+                            int D, hipStream_t s) {
+    if (D % 8 != 0 || B <= 0 || H <= 0 || T <= 0) return hipErrorInvalidValue;
+    const size_t nchunk = (size_t)B * H * T * (D / 8);
+    const unsigned grid = (unsigned)((nchunk + 255) / 256);
+    if (src_bf16)
+        kv_append_kernel<bf16><<<grid, 256, 0, s>>>((const bf16*)ks, (const bf16*)vs, (bf16*)kc,
+                                                    (bf16*)vc, pos, cnt, H, T, Lmax, D, nchunk);
+    else
+        kv_append_kernel<float><<<grid, 256, 0, s>>>((const float*)ks, (const float*)vs, (bf16*)kc,
+                                                     (bf16*)vc, pos, cnt, H, T, Lmax, D, nchunk);
+    return hipGetLastError();
 }
 
 hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStream_t s) {

@@ -73,6 +73,12 @@ hipError_t launch_fwd(const FwdParams& p, int mode, int D, int causal, int q_bf1
                       hipStream_t s);
 hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStream_t s);
 hipError_t launch_decode_combine(const DecodeParams& p, int D, hipStream_t s);
+// KV-cache append (attn_decode.hip): row t < cnt[b] of the (B,H,T,D) sources
+// (f32, or bf16 when src_bf16) to position pos[b] + t of the bf16 cache
+// (B,H,Lmax,D). pos and cnt are device int32[B].
+hipError_t launch_kv_append(const void* ks, const void* vs, int src_bf16, void* kc, void* vc,
+                            const int* pos, const int* cnt, int B, int H, int T, int Lmax,
+                            int D, hipStream_t s);
 // Backward stages: prep (lse2, delta), then dK/dV (one workgroup per key
 // block) and dQ (one workgroup per query block), both deterministic.
 hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, float* lse2,

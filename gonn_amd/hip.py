@@ -14,6 +14,9 @@ Two layers, both over the C ABI (include/gonn_hip.h):
 2. The device-resident API on torch device tensors (torch only supplies
    device memory and the current HIP stream):
        attn_fwd, attn_bwd, attn_decode
+
+3. KVCache: a device KV cache handle for incremental decoding (new; the
+   reference has none), with host fp64 and device-tensor methods.
 """
 from __future__ import annotations
 
@@ -279,6 +282,113 @@ def attn_decode(q, kcache, vcache, kv_len, *, scale=None, split_keys: int = 0, o
     return out
 
 
+# ---------------------------------------------------------------------------
+# KV cache (incremental decoding)
+# ---------------------------------------------------------------------------
+class KVCache:
+    """One attention layer's device KV cache (gonn_hip_kvcache_*): bf16 K/V of
+    B sequences x H heads, up to Lmax positions of head dim D, plus each
+    sequence's length. New relative to the reference, which has no KV cache;
+    attend() is ForwardMasked with a key-padding mask (nn/attention.go:305-341)
+    over the cached positions of each sequence.
+
+    Host fp64 methods (the cgo-style path): append_f64, attend_f64.
+    Device methods on torch tensors: append, attend.
+    """
+
+    def __init__(self, B: int, H: int, Lmax: int, D: int):
+        self.B, self.H, self.Lmax, self.D = int(B), int(H), int(Lmax), int(D)
+        self._h = ctypes.c_void_p()
+        check(_lib.load().gonn_hip_kvcache_create(ctypes.byref(self._h), self.B, self.H,
+                                                  self.Lmax, self.D), "KVCache")
+
+    def close(self) -> None:
+        if self._h:
+            check(_lib.load().gonn_hip_kvcache_free(self._h), "KVCache.close")
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _live(self):
+        if not self._h:
+            raise ValueError("KVCache: closed")
+        return self._h
+
+    def reset(self) -> None:
+        check(_lib.load().gonn_hip_kvcache_reset(self._live()), "KVCache.reset")
+
+    def lengths(self) -> np.ndarray:
+        out = np.zeros(self.B, dtype=np.int32)
+        check(_lib.load().gonn_hip_kvcache_lengths(
+            self._live(), out.ctypes.data_as(ctypes.POINTER(ctypes.c_int))), "KVCache.lengths")
+        return out
+
+    def _counts(self, counts, T):
+        if counts is None:
+            return None, None
+        c = np.ascontiguousarray(counts, dtype=np.int32)
+        if c.shape != (self.B,):
+            raise ValueError(f"KVCache: counts must have {self.B} entries")
+        return c, c.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+
+    def append_f64(self, k, v, counts=None) -> None:
+        """k, v host (B,H,T,D) float64; sequence b takes its first counts[b]
+        rows (all T when counts is None)."""
+        k = np.ascontiguousarray(k, dtype=np.float64)
+        v = np.ascontiguousarray(v, dtype=np.float64)
+        if k.ndim != 4 or k.shape != v.shape or k.shape[:2] != (self.B, self.H) \
+                or k.shape[3] != self.D:
+            raise ValueError(f"KVCache.append_f64: k, v must be ({self.B},{self.H},T,{self.D})")
+        c, cp = self._counts(counts, k.shape[2])
+        check(_lib.load().gonn_hip_kvcache_append_f64(self._live(), _p(k), _p(v), k.shape[2],
+                                                       cp), "KVCache.append_f64")
+
+    def attend_f64(self, q, scale=None) -> np.ndarray:
+        """q host (B,H,D) float64 -> o (B,H,D) float64."""
+        q = np.ascontiguousarray(q, dtype=np.float64)
+        if q.shape != (self.B, self.H, self.D):
+            raise ValueError(f"KVCache.attend_f64: q must be ({self.B},{self.H},{self.D})")
+        if scale is None:
+            scale = 1.0 / math.sqrt(self.D)
+        o = np.zeros_like(q)
+        check(_lib.load().gonn_hip_kvcache_attend_f64(self._live(), _p(q), _p(o), float(scale)),
+              "KVCache.attend_f64")
+        return o
+
+    def append(self, k, v, counts=None, stream=None) -> None:
+        """k, v device (B,H,T,D) float32 or bfloat16 (both the same dtype)."""
+        if k.dim() != 4 or tuple(k.shape) != tuple(v.shape):
+            raise ValueError("KVCache.append: k, v must be (B,H,T,D) of the same shape")
+        c, cp = self._counts(counts, k.shape[2])
+        kb, vb = buf(k), buf(v)
+        check(_lib.load().gonn_hip_kvcache_append(self._live(), ctypes.byref(kb),
+                                                   ctypes.byref(vb), int(k.shape[2]), cp,
+                                                   _stream(stream)), "KVCache.append")
+
+    def attend(self, q, scale=None, out=None, stream=None):
+        """q device (B,H,D) float32/bfloat16 -> o (B,H,D) float32."""
+        torch = _torch()
+        if scale is None:
+            scale = 1.0 / math.sqrt(self.D)
+        if out is None:
+            out = torch.empty((self.B, self.H, self.D), dtype=torch.float32, device=q.device)
+        qb, ob = buf(q), buf(out)
+        check(_lib.load().gonn_hip_kvcache_attend(self._live(), ctypes.byref(qb),
+                                                   ctypes.byref(ob), float(scale),
+                                                   _stream(stream)), "KVCache.attend")
+        return out
+
+
 __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
            "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "BenchFlashAttnF64",
-           "attn_fwd", "attn_bwd", "attn_decode", "buf", "GonnHipError"]
+           "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "buf", "GonnHipError"]

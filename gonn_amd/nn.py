@@ -135,6 +135,39 @@ class MultiHeadAttention:
 
     forward = forward_fused
 
+    # ---- incremental decoding (new: the reference has no KV cache) ----
+    def new_cache(self, batch: int, max_len: int) -> "hip.KVCache":
+        """A device KV cache for this layer: batch sequences, max_len positions."""
+        return hip.KVCache(batch, self.NumHeads, max_len, self.HeadDim)
+
+    def forward_incremental(self, x, cache: "hip.KVCache"):
+        """Causal self-attention of new tokens x (B, T, E) over the tokens the
+        cache holds plus themselves: each new position is projected, its K/V
+        appended, and its query attended over the cache (one position at a
+        time, so position t sees exactly the positions <= t). Output row t
+        equals row (cached + t) of forward_fused(seq, seq, seq, causal=True)
+        over the whole sequence (top-left causal mask, nn/attention.go:185-196,
+        is what the cache realises)."""
+        x = np.asarray(x, dtype=np.float64)
+        E = self.EmbedDim
+        if x.ndim != 3 or x.shape[2] != E:
+            raise ValueError(f"MultiHeadAttention: x shape {x.shape}, want (B, T, {E})")
+        B, T, _ = x.shape
+        H, D = self.NumHeads, self.HeadDim
+        if (cache.B, cache.H, cache.D) != (B, H, D):
+            raise ValueError(f"MultiHeadAttention: cache is ({cache.B},{cache.H},*,{cache.D}), "
+                             f"want ({B},{H},*,{D})")
+        qp = self._split(self.QProj.forward(x))
+        kp = self._split(self.KProj.forward(x))
+        vp = self._split(self.VProj.forward(x))
+        scale = 1.0 / math.sqrt(D)
+        ctx = np.empty((B, H, T, D))
+        for t in range(T):
+            cache.append_f64(kp[:, :, t:t + 1, :], vp[:, :, t:t + 1, :])
+            ctx[:, :, t, :] = cache.attend_f64(qp[:, :, t, :], scale)
+        ctx = ctx.transpose(0, 2, 1, 3).reshape(B, T, E)
+        return self.OutProj.forward(ctx)
+
 
 def attn_decode(q, kcache, vcache, kv_len, scale=None, split_keys: int = 0):
     """KV-cache decode on device tensors: ForwardMasked with a key-padding mask

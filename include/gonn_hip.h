@@ -157,6 +157,46 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
  * :261-272) on the post-projection core with pad[b][t] = (t >= kv_len[b]).  */
 int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_bytes, void* stream);
 
+/* ---- KV cache for incremental decoding ----------------------------------
+ * New: the reference has no KV cache (its decoder recomputes attention over
+ * the whole prefix through MultiHeadAttention.Forward). A handle owns one
+ * attention layer's device cache: K and V of B sequences x H heads, up to
+ * Lmax positions of head dim D, bf16 (B,H,Lmax,D), and the number of cached
+ * positions of each sequence. Appending writes new positions at each
+ * sequence's length; attending runs the split-KV decode of one query per
+ * (b, h) over the cached positions, i.e. ForwardMasked with a key-padding
+ * mask (nn/attention.go:305-341, :261-272) on the post-projection core; a
+ * sequence with no cached position gets o = 0. Calls on one handle are not
+ * reentrant; different handles are independent. For callers that cannot
+ * hold device pointers (cgo), the _f64 variants take host arrays.        */
+typedef struct gonn_kvcache gonn_kvcache;
+
+/* D must be 64 or 128 (GONN_E_UNSUPPORTED otherwise); GONN_E_NODEVICE
+ * without a gfx950 device. *out is NULL on failure.                       */
+int gonn_hip_kvcache_create(gonn_kvcache** out, int B, int H, int Lmax, int D);
+/* Frees the handle and its device memory (NULL is allowed).              */
+int gonn_hip_kvcache_free(gonn_kvcache* c);
+/* Drops every cached position (lengths back to 0).                       */
+int gonn_hip_kvcache_reset(gonn_kvcache* c);
+/* Copies the B current lengths into len[B].                              */
+int gonn_hip_kvcache_lengths(const gonn_kvcache* c, int* len);
+/* Appends new positions: k, v are (B,H,T,D) device buffers, GONN_F32 or
+ * GONN_BF16 (both the same, 16-byte aligned); sequence b takes its first
+ * counts[b] rows (host int[B]; NULL = T for every sequence). An append that
+ * would take a sequence past Lmax returns GONN_E_INVALID and writes nothing.
+ * Synchronous with respect to `stream`.                                   */
+int gonn_hip_kvcache_append(gonn_kvcache* c, const gonn_buf* k, const gonn_buf* v, int T,
+                            const int* counts, void* stream);
+/* As gonn_hip_kvcache_append with host fp64 (B,H,T,D) arrays.            */
+int gonn_hip_kvcache_append_f64(gonn_kvcache* c, const double* k, const double* v, int T,
+                                const int* counts);
+/* o (B,H,D) = softmax(scale q . K^T) V over each sequence's cached
+ * positions; q: GONN_F32 or GONN_BF16 (B,H,D), o: GONN_F32 (B,H,D).      */
+int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, double scale,
+                            void* stream);
+/* As gonn_hip_kvcache_attend with host fp64 q and o (B,H,D); synchronous. */
+int gonn_hip_kvcache_attend_f64(gonn_kvcache* c, const double* q, double* o, double scale);
+
 /* ---- device buffers ------------------------------------------------------
  * Replace gonn_dev_alloc / gonn_dev_free / gonn_dev_upload / gonn_dev_download
  * (backend/cuda/gonn_cuda.h:77-80) for the attention path. The f64 transfer

@@ -249,3 +249,26 @@ def test_bench_refuses_multi_gpu():
                          capture_output=True, text=True)
     assert out.returncode == 2
     assert "one GPU" in out.stderr
+
+
+def test_kvcache_argument_and_device_checks():
+    """Bad arguments are rejected before the device is touched; with no gfx950
+    device, creating a cache fails with GONN_E_NODEVICE (no CPU fallback)."""
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    assert lib.gonn_hip_kvcache_create(None, 1, 1, 8, 64) == GONN_E_INVALID
+    assert lib.gonn_hip_kvcache_create(ctypes.byref(h), 0, 1, 8, 64) == GONN_E_INVALID
+    assert lib.gonn_hip_kvcache_create(ctypes.byref(h), 1, 1, 0, 64) == GONN_E_INVALID
+    assert lib.gonn_hip_kvcache_create(ctypes.byref(h), 1, 1, 8, 96) == GONN_E_UNSUPPORTED
+    assert not h.value
+    assert lib.gonn_hip_kvcache_free(None) == 0
+    assert lib.gonn_hip_kvcache_reset(None) == GONN_E_INVALID
+    assert lib.gonn_hip_kvcache_lengths(None, None) == GONN_E_INVALID
+    assert lib.gonn_hip_kvcache_append_f64(None, None, None, 1, None) == GONN_E_INVALID
+    assert lib.gonn_hip_kvcache_attend_f64(None, None, None, 1.0) == GONN_E_INVALID
+    if not hip.Available():
+        assert lib.gonn_hip_kvcache_create(ctypes.byref(h), 1, 1, 8, 64) == GONN_E_NODEVICE
+        assert not h.value
+        with pytest.raises(hip.GonnHipError) as ei:
+            hip.KVCache(1, 1, 8, 64)
+        assert ei.value.code == GONN_E_NODEVICE
