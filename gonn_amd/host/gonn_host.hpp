@@ -9,10 +9,11 @@
 //
 //   gonn::hip  (backend/hip, the counterpart of backend/cuda/cuda.go)
 //     Available, Supports, SetMode, FlashAttnF64, FlashAttnF64Fwd,
-//     FlashAttnF64Bwd, BenchFlashAttnF64
+//     FlashAttnF64Bwd, BenchFlashAttnF64, KVCache (new)
 //   gonn::nn   (nn/flashattn_hip.go + the fused branch of nn/attention.go)
 //     Tensor, Linear, fusedAttnAvailable, fusedAttnSupports, fusedAttnF64,
-//     fusedAttnDiff, MultiHeadAttention::{Forward, ForwardFused}
+//     fusedAttnDiff, MultiHeadAttention::{Forward, ForwardFused,
+//     NewCache, ForwardIncremental (new)}
 //
 // Where the Go code panics (slice length mismatch, checkQKVDims, a failed
 // device call surfaced by the new ABI's status codes) these throw:
@@ -73,6 +74,37 @@ BwdOut FlashAttnF64Bwd(const std::vector<double>& Q, const std::vector<double>& 
 
 // cuda.go:188-194: mean milliseconds of `iters` device-resident forwards.
 double BenchFlashAttnF64(int BH, int S, int d, int iters, bool causal);
+
+// Device KV cache of one attention layer (gonn_hip_kvcache_*). New: the
+// reference has no KV cache. Attend is ForwardMasked with a key-padding mask
+// (nn/attention.go:305-341) over each sequence's cached positions; a sequence
+// with none gets zeros. Move-only; frees its device memory on destruction.
+class KVCache {
+  public:
+    KVCache(int B, int H, int Lmax, int D);
+    ~KVCache();
+    KVCache(KVCache&& o) noexcept;
+    KVCache& operator=(KVCache&& o) noexcept;
+    KVCache(const KVCache&) = delete;
+    KVCache& operator=(const KVCache&) = delete;
+
+    // k, v: flat (B,H,T,D) fp64; sequence b takes its first counts[b] rows
+    // (all T when counts is empty). Past Lmax: throws Error, nothing written.
+    void Append(const std::vector<double>& k, const std::vector<double>& v, int T,
+                const std::vector<int>& counts = {});
+    // q: flat (B,H,D) fp64 -> o (B,H,D).
+    std::vector<double> Attend(const std::vector<double>& q, double scale) const;
+    std::vector<int> Lengths() const;
+    void Reset();
+    int B() const { return B_; }
+    int H() const { return H_; }
+    int Lmax() const { return Lmax_; }
+    int D() const { return D_; }
+
+  private:
+    void* h_ = nullptr;
+    int B_, H_, Lmax_, D_;
+};
 
 }  // namespace hip
 
@@ -139,6 +171,14 @@ class MultiHeadAttention {
     Tensor ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
 
     FlashAttnNode LastNode;
+
+    // Incremental decoding (new: the reference has no KV cache). A cache of
+    // `batch` sequences and `maxLen` positions for this layer.
+    hip::KVCache NewCache(int batch, int maxLen) const;
+    // Causal self-attention of new tokens x (B, T, E) over the cached tokens
+    // plus themselves, one position at a time; row t equals row (cached + t)
+    // of Forward(seq, seq, seq, causal=true) over the whole sequence.
+    Tensor ForwardIncremental(const Tensor& x, hip::KVCache& cache);
 
   private:
     void checkQKVDims(const Tensor& q, const Tensor& k, const Tensor& v) const;

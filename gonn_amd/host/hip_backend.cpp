@@ -106,5 +106,68 @@ double BenchFlashAttnF64(int BH, int S, int d, int iters, bool causal) {
     return ms;
 }
 
+KVCache::KVCache(int B, int H, int Lmax, int D) : B_(B), H_(H), Lmax_(Lmax), D_(D) {
+    gonn_kvcache* c = nullptr;
+    check(gonn_hip_kvcache_create(&c, B, H, Lmax, D), "KVCache");
+    h_ = c;
+}
+
+KVCache::~KVCache() {
+    if (h_) (void)gonn_hip_kvcache_free((gonn_kvcache*)h_);
+}
+
+KVCache::KVCache(KVCache&& o) noexcept
+    : h_(o.h_), B_(o.B_), H_(o.H_), Lmax_(o.Lmax_), D_(o.D_) {
+    o.h_ = nullptr;
+}
+
+KVCache& KVCache::operator=(KVCache&& o) noexcept {
+    if (this != &o) {
+        if (h_) (void)gonn_hip_kvcache_free((gonn_kvcache*)h_);
+        h_ = o.h_;
+        B_ = o.B_;
+        H_ = o.H_;
+        Lmax_ = o.Lmax_;
+        D_ = o.D_;
+        o.h_ = nullptr;
+    }
+    return *this;
+}
+
+void KVCache::Append(const std::vector<double>& k, const std::vector<double>& v, int T,
+                     const std::vector<int>& counts) {
+    if (!h_) throw std::invalid_argument("hip: KVCache: moved-from cache");
+    if (T <= 0) throw std::invalid_argument("hip: KVCache.Append: T must be >= 1");
+    const size_t n = (size_t)B_ * H_ * T * D_;
+    need(k, n, "KVCache.Append k");
+    need(v, n, "KVCache.Append v");
+    if (!counts.empty() && (int)counts.size() != B_)
+        throw std::invalid_argument("hip: KVCache.Append: counts needs B entries");
+    check(gonn_hip_kvcache_append_f64((gonn_kvcache*)h_, k.data(), v.data(), T,
+                                      counts.empty() ? nullptr : counts.data()),
+          "KVCache.Append");
+}
+
+std::vector<double> KVCache::Attend(const std::vector<double>& q, double scale) const {
+    if (!h_) throw std::invalid_argument("hip: KVCache: moved-from cache");
+    const size_t n = (size_t)B_ * H_ * D_;
+    need(q, n, "KVCache.Attend q");
+    std::vector<double> o(n, 0.0);
+    check(gonn_hip_kvcache_attend_f64((gonn_kvcache*)h_, q.data(), o.data(), scale),
+          "KVCache.Attend");
+    return o;
+}
+
+std::vector<int> KVCache::Lengths() const {
+    std::vector<int> len(B_, 0);
+    if (h_) check(gonn_hip_kvcache_lengths((const gonn_kvcache*)h_, len.data()), "KVCache.Lengths");
+    return len;
+}
+
+void KVCache::Reset() {
+    if (!h_) throw std::invalid_argument("hip: KVCache: moved-from cache");
+    check(gonn_hip_kvcache_reset((gonn_kvcache*)h_), "KVCache.Reset");
+}
+
 }  // namespace hip
 }  // namespace gonn

@@ -198,5 +198,40 @@ Tensor MultiHeadAttention::ForwardFused(const Tensor& q, const Tensor& k, const 
     return OutProj.Forward(ctx);
 }
 
+hip::KVCache MultiHeadAttention::NewCache(int batch, int maxLen) const {
+    return hip::KVCache(batch, NumHeads, maxLen, HeadDim);
+}
+
+Tensor MultiHeadAttention::ForwardIncremental(const Tensor& x, hip::KVCache& cache) {
+    if (x.Shape.size() != 3 || x.Shape[2] != EmbedDim)
+        throw std::invalid_argument("MultiHeadAttention: x shape " + shape_str(x.Shape) +
+                                    ", want (B, T, " + std::to_string(EmbedDim) + ")");
+    const int B = x.Shape[0], T = x.Shape[1], H = NumHeads, D = HeadDim;
+    if (cache.B() != B || cache.H() != H || cache.D() != D)
+        throw std::invalid_argument("MultiHeadAttention: cache shape does not match (B, H, D)");
+    // project all new tokens, (B, T, H, D) -> (B, H, T, D)
+    const Tensor qp = QProj.Forward(x).Reshape({B, T, H, D}).Permute0213();
+    const Tensor kp = KProj.Forward(x).Reshape({B, T, H, D}).Permute0213();
+    const Tensor vp = VProj.Forward(x).Reshape({B, T, H, D}).Permute0213();
+    const double scale = 1.0 / std::sqrt((double)D);
+    std::vector<double> ctx((size_t)B * H * T * D);
+    std::vector<double> kt((size_t)B * H * D), vt(kt.size()), qt(kt.size());
+    for (int t = 0; t < T; t++) {
+        for (size_t bh = 0; bh < (size_t)B * H; bh++)
+            for (int d = 0; d < D; d++) {
+                const size_t src = (bh * T + t) * D + d;
+                kt[bh * D + d] = kp.Data[src];
+                vt[bh * D + d] = vp.Data[src];
+                qt[bh * D + d] = qp.Data[src];
+            }
+        cache.Append(kt, vt, 1);
+        const std::vector<double> o = cache.Attend(qt, scale);
+        for (size_t bh = 0; bh < (size_t)B * H; bh++)
+            for (int d = 0; d < D; d++) ctx[(bh * T + t) * D + d] = o[bh * D + d];
+    }
+    const Tensor merged = Tensor::New(std::move(ctx), {B, H, T, D}).Permute0213().Reshape({B, T, EmbedDim});
+    return OutProj.Forward(merged);
+}
+
 }  // namespace nn
 }  // namespace gonn

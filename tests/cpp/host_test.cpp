@@ -218,6 +218,23 @@ static void test_cpu() {
             code = e.code;
         }
         CHECK(code == GONN_E_NODEVICE, "FlashAttnF64 without device: code %d", code);
+        code = 0;
+        try {
+            gonn::hip::KVCache c(2, 2, 16, 64);
+        } catch (const gonn::hip::Error& e) {
+            code = e.code;
+        }
+        CHECK(code == GONN_E_NODEVICE, "KVCache without device: code %d", code);
+    }
+    // The cache checks its arguments before the device.
+    {
+        int code = 0;
+        try {
+            gonn::hip::KVCache c(2, 2, 16, 96);
+        } catch (const gonn::hip::Error& e) {
+            code = e.code;
+        }
+        CHECK(code == GONN_E_UNSUPPORTED, "KVCache D=96: code %d", code);
     }
 }
 
@@ -301,6 +318,55 @@ static void test_gpu() {
         Tensor q = Tensor::New(r.normals(1 * 8 * 64), {1, 8, 64});
         Tensor k = Tensor::New(r.normals(1 * 9 * 64), {1, 9, 64});
         CHECK(throws_invalid([&] { m.Forward(q, k, k, false); }), "Tq != Tk rejected");
+    }
+    // Incremental decoding: ForwardIncremental over a KV cache in two chunks
+    // equals the causal rows of the oracle's MHA over the whole sequence (the
+    // cache holds bf16 K/V: bf16 bar).
+    for (int H : {4, 2}) {
+        const int B = 2, T = 24, E = 256;
+        Rng r(2000 + H);
+        const double ws = 1.0 / std::sqrt((double)E);
+        auto lin = [&] {
+            Linear l;
+            l.W = Tensor::New(r.normals((size_t)E * E, ws), {E, E});
+            l.B = r.normals(E, 0.1);
+            return l;
+        };
+        MultiHeadAttention m(E, H, lin(), lin(), lin(), lin());
+        Tensor x = Tensor::New(r.normals((size_t)B * T * E), {B, T, E});
+        const std::vector<double> ref = oracle_mha(m, x, x, x, true);
+        gonn::hip::KVCache cache = m.NewCache(B, 32);
+        auto part = [&](int t0, int t1) {
+            std::vector<double> d((size_t)B * (t1 - t0) * E);
+            for (int b = 0; b < B; b++)
+                for (int t = t0; t < t1; t++)
+                    for (int e = 0; e < E; e++)
+                        d[((size_t)b * (t1 - t0) + (t - t0)) * E + e] = x.Data[((size_t)b * T + t) * E + e];
+            return Tensor::New(std::move(d), {B, t1 - t0, E});
+        };
+        const Tensor y1 = m.ForwardIncremental(part(0, 10), cache);
+        const Tensor y2 = m.ForwardIncremental(part(10, T), cache);
+        CHECK(cache.Lengths() == std::vector<int>({T, T}), "cache lengths");
+        std::vector<double> got((size_t)B * T * E);
+        for (int b = 0; b < B; b++)
+            for (int t = 0; t < T; t++)
+                for (int e = 0; e < E; e++)
+                    got[((size_t)b * T + t) * E + e] =
+                        t < 10 ? y1.Data[((size_t)b * 10 + t) * E + e]
+                               : y2.Data[((size_t)b * (T - 10) + (t - 10)) * E + e];
+        const std::string tag = "ForwardIncremental H=" + std::to_string(H);
+        CHECK(close(got, ref, 2e-2, 1e-2, tag.c_str()), "%s", tag.c_str());
+        // past Lmax: rejected, nothing written
+        bool threw = false;
+        try {
+            std::vector<double> z((size_t)B * H * 20 * (E / H), 0.0);
+            cache.Append(z, z, 20);
+        } catch (const gonn::hip::Error& e) {
+            threw = e.code == GONN_E_INVALID;
+        }
+        CHECK(threw && cache.Lengths() == std::vector<int>({T, T}), "append past Lmax rejected");
+        cache.Reset();
+        CHECK(cache.Lengths() == std::vector<int>({0, 0}), "Reset");
     }
 }
 
