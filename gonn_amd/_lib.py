@@ -38,7 +38,7 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_profile_read", "gonn_hip_selftest_mfma",
     "gonn_hip_kvcache_create", "gonn_hip_kvcache_free", "gonn_hip_kvcache_reset",
     "gonn_hip_kvcache_lengths", "gonn_hip_kvcache_append", "gonn_hip_kvcache_append_f64",
-    "gonn_hip_kvcache_attend", "gonn_hip_kvcache_attend_f64",
+    "gonn_hip_kvcache_attend", "gonn_hip_kvcache_attend_f64", "gonn_hip_flash_attn_f64_ex",
 )
 
 
@@ -59,7 +59,7 @@ class FwdArgs(ctypes.Structure):
     _fields_ = [("q", Buf), ("k", Buf), ("v", Buf), ("o", Buf), ("lse", Buf),
                 ("B", ctypes.c_int), ("H", ctypes.c_int), ("Sq", ctypes.c_int),
                 ("Sk", ctypes.c_int), ("D", ctypes.c_int), ("scale", ctypes.c_double),
-                ("causal", ctypes.c_int), ("mode", ctypes.c_int)]
+                ("causal", ctypes.c_int), ("mode", ctypes.c_int), ("kv_len", Buf)]
 
 
 class BwdArgs(ctypes.Structure):
@@ -129,6 +129,8 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_kvcache_attend.argtypes = [vp, ctypes.POINTER(Buf), ctypes.POINTER(Buf),
                                             ctypes.c_double, vp]
     lib.gonn_hip_kvcache_attend_f64.argtypes = [vp, dp, dp, ctypes.c_double]
+    lib.gonn_hip_flash_attn_f64_ex.argtypes = [dp, dp, dp, dp, dp, i, i, i, i, i, ctypes.c_double,
+                                               i, ip]
     _lib = lib
     return lib
 

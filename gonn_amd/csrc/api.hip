@@ -122,6 +122,7 @@ int check_fwd(const gonn_attn_fwd_args* a) {
     }
     if (!buf_ok(a->o, nq, GONN_F32)) return GONN_E_INVALID;
     if (a->lse.ptr && !buf_ok(a->lse, BH * a->Sq, GONN_F32)) return GONN_E_INVALID;
+    if (a->kv_len.ptr && !buf_ok(a->kv_len, (size_t)a->B, GONN_I32)) return GONN_E_INVALID;
     return GONN_OK;
 }
 
@@ -279,6 +280,33 @@ int run_fwd_f32(DevMem& mem, const float* q, const float* k, const float* v, flo
 
 bool shim_args_ok(int BH, int S, int d) { return BH > 0 && S > 0 && d > 0 && d <= 128; }
 
+// General forward on device f32 buffers: B sequences x H heads, Sq x Sk,
+// optional device kv_len[B].
+int run_fwd_f32_ex(DevMem& mem, const float* q, const float* k, const float* v, float* o,
+                   float* lse, int B, int H, int Sq, int Sk, int dp, double scale, int causal,
+                   const int* kv_len) {
+    gonn_attn_fwd_args a{};
+    const size_t BH = (size_t)B * H, nq = BH * Sq * dp, nk = BH * Sk * dp;
+    a.q = {(void*)q, nq * 4, GONN_F32};
+    a.k = {(void*)k, nk * 4, GONN_F32};
+    a.v = {(void*)v, nk * 4, GONN_F32};
+    a.o = {(void*)o, nq * 4, GONN_F32};
+    a.lse = {(void*)lse, lse ? BH * Sq * 4 : 0, GONN_F32};
+    a.kv_len = {(void*)kv_len, kv_len ? (size_t)B * 4 : 0, GONN_I32};
+    a.B = B;
+    a.H = H;
+    a.Sq = Sq;
+    a.Sk = Sk;
+    a.D = dp;
+    a.scale = scale;
+    a.causal = causal;
+    a.mode = current_mode();
+    const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_FWD, &a);
+    void* ws = nullptr;
+    if (wsb) TRY(mem.alloc(&ws, wsb));
+    return gonn_hip_attn_fwd(&a, ws, wsb, nullptr);
+}
+
 }  // namespace
 
 // The KV-cache handle of the C ABI (opaque to callers).
@@ -435,6 +463,8 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
     p.BH = BH;
     p.Sq = a->Sq;
     p.Sk = a->Sk;
+    p.H = a->H;
+    p.kv_len = a->kv_len.ptr ? (const int*)a->kv_len.ptr : nullptr;
     if (a->scale == 0.0) {  // all scores 0: uniform weights; Q is zeroed
         p.qsign = 0.f;
         p.scale_abs = 1.f;
@@ -701,6 +731,32 @@ int gonn_hip_flash_attn_f64_fwd(const double* Q, const double* K, const double* 
     TRY(run_fwd_f32(mem, q, k, v, o, l, BH, S, dp, scale, causal));
     TRY(download_padded(mem, o, rows, d, dp, O));
     TRY(download_padded(mem, l, rows, 1, 1, L));
+    return herr(hipDeviceSynchronize());
+}
+
+int gonn_hip_flash_attn_f64_ex(const double* Q, const double* K, const double* V, double* O,
+                               double* L, int B, int H, int Sq, int Sk, int d, double scale,
+                               int causal, const int* kv_len) {
+    if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || d <= 0 || d > 128) return GONN_E_INVALID;
+    if (!Q || !K || !V || !O || !std::isfinite(scale)) return GONN_E_INVALID;
+    if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    DevMem mem;
+    const int dp = pad_dim(d);
+    const size_t rq = (size_t)B * H * Sq, rk = (size_t)B * H * Sk;
+    float *q, *k, *v, *o, *l = nullptr;
+    int* kl = nullptr;
+    TRY(upload_padded(mem, Q, rq, d, dp, &q));
+    TRY(upload_padded(mem, K, rk, d, dp, &k));
+    TRY(upload_padded(mem, V, rk, d, dp, &v));
+    TRY(mem.alloc((void**)&o, rq * dp * 4));
+    if (L) TRY(mem.alloc((void**)&l, rq * 4));
+    if (kv_len) {
+        TRY(mem.alloc((void**)&kl, (size_t)B * 4));
+        TRYH(hipMemcpy(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice));
+    }
+    TRY(run_fwd_f32_ex(mem, q, k, v, o, l, B, H, Sq, Sk, dp, scale, causal, kl));
+    TRY(download_padded(mem, o, rq, d, dp, O));
+    if (L) TRY(download_padded(mem, l, rq, 1, 1, L));
     return herr(hipDeviceSynchronize());
 }
 

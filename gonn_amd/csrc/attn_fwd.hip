@@ -65,6 +65,27 @@ namespace gonn {
 // ---------------------------------------------------------------------------
 constexpr float kLazyLog2 = 8.0f;
 
+// Keys of slice bh that take part: Sk, or the sequence's kv_len clamped to
+// [0, Sk] (a prefix key-padding mask).
+GONN_DEV int fwd_keys(const FwdParams& p, int bh) {
+    if (!p.kv_len) return p.Sk;
+    int l = p.kv_len[bh / p.H];
+    l = l < 0 ? 0 : (l > p.Sk ? p.Sk : l);
+    return __builtin_amdgcn_readfirstlane(l);
+}
+
+// Rows q0 .. q0 + rows - 1 of slice bh when the slice has no key at all:
+// O = 0, LSE = -inf.
+template <int D>
+GONN_DEV void fwd_empty_rows(const FwdParams& p, int bh, int q0, int rows) {
+    const int r1 = q0 + rows < p.Sq ? q0 + rows : p.Sq;
+    if (r1 <= q0) return;
+    float* o = p.o + ((size_t)bh * p.Sq + q0) * D;
+    for (int i = threadIdx.x; i < (r1 - q0) * D; i += blockDim.x) o[i] = 0.f;
+    if (p.lse)
+        for (int r = q0 + threadIdx.x; r < r1; r += blockDim.x) p.lse[(size_t)bh * p.Sq + r] = -INFINITY;
+}
+
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgVALU = 0x002, kSgMFMA = 0x008, kSgDSR = 0x100;
 
@@ -87,7 +108,11 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_kernel(FwdParams p) {
     map_block(blockIdx.x, p.nqb, p.BH, CAUSAL, bh, qb);
     const int q0 = qb * BM;
     const int qi = q0 + wave * 32 + ln;  // this lane's query row
-    const int Sq = p.Sq, Sk = p.Sk, Skp = p.Skp;
+    const int Sq = p.Sq, Sk = fwd_keys(p, bh), Skp = p.Skp;
+    if (Sk == 0) {  // uniform: the whole slice is padded
+        fwd_empty_rows<D>(p, bh, q0, BM);
+        return;
+    }
 
     // Q fragment: qf[ks] = Q[qi][16ks + 8g .. +7] in bf16.
     bf16x8 qf[NKS];
@@ -382,7 +407,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     const int nwg = PAIR ? (p.nqb + 1) / 2 : p.nqb;
     int bh, pj;
     map_block(blockIdx.x, nwg, p.BH, CAUSAL && !PAIR, bh, pj, CAUSAL && !PAIR ? p.hgroup : 1);
-    const int Sq = p.Sq, Sk = p.Sk, Skp = p.Skp;
+    const int Sq = p.Sq, Sk = fwd_keys(p, bh), Skp = p.Skp;
+    if (Sk == 0) {  // uniform: the whole slice is padded
+        fwd_empty_rows<D>(p, bh, (PAIR ? p.nqb - 1 - pj : pj) * BM, BM);
+        if (PAIR && p.nqb - 1 - pj != pj) fwd_empty_rows<D>(p, bh, pj * BM, BM);
+        return;
+    }
     // Per q-block state (set by each pass): first query row of the block and
     // of this wave, this lane's query row, number of 64-key tiles.
     int q0 = 0, qw = 0, qi = 0, ntiles = 0;
@@ -793,7 +823,11 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(FwdParams p) {
     map_block(blockIdx.x, p.nqb, p.BH, CAUSAL, bh, qb);
     const int q0 = qb * BM;
     const int qi = q0 + wave * 32 + ln;
-    const int Sq = p.Sq, Sk = p.Sk;
+    const int Sq = p.Sq, Sk = fwd_keys(p, bh), Ss = p.Sk;  // keys taking part, slice stride
+    if (Sk == 0) {  // uniform: the whole slice is padded
+        fwd_empty_rows<D>(p, bh, q0, BM);
+        return;
+    }
 
     float qf[HD];
     {
@@ -808,8 +842,8 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(FwdParams p) {
     int kend = Sk;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
     const int ntiles = (kend + BN - 1) / BN;
-    const float* Kg = (const float*)p.k + (size_t)bh * Sk * D;
-    const float* Vg = (const float*)p.v + (size_t)bh * Sk * D;
+    const float* Kg = (const float*)p.k + (size_t)bh * Ss * D;
+    const float* Vg = (const float*)p.v + (size_t)bh * Ss * D;
 
     f32x4 kreg[CH], vreg[CH];
     auto gload = [&](int kt) {

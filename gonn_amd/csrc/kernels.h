@@ -17,6 +17,8 @@ struct FwdParams {
     float scale_abs;   // |scale|
     float qsign;       // sign(scale) (Q is negated for a negative scale)
     int hgroup;        // slices whose blocks are dispatched interleaved (map_block)
+    const int* kv_len; // [BH / H] valid keys per sequence, or null (all Sk)
+    int H;             // heads per sequence (slice bh belongs to sequence bh / H)
 };
 
 struct DecodeParams {

@@ -133,6 +133,30 @@ def FlashAttnF64Bwd(Q, K, V, O, L, dO, BH: int, S: int, d: int, scale: float, ca
     return dQ, dK, dV
 
 
+def FlashAttnF64Ex(Q, K, V, B: int, H: int, Sq: int, Sk: int, d: int, scale: float,
+                   causal: bool, kv_len=None, lse: bool = False):
+    """General fused forward on host fp64 arrays (new; the reference seam is
+    Tq == Tk only): Q (B*H,Sq,d), K/V (B*H,Sk,d), optional prefix key padding
+    kv_len[B] (keys t >= kv_len[b] masked, ForwardMasked semantics). Returns
+    O, or (O, L) when lse is set."""
+    Q = _f64(Q, B * H * Sq * d, "FlashAttnF64Ex Q")
+    K = _f64(K, B * H * Sk * d, "FlashAttnF64Ex K")
+    V = _f64(V, B * H * Sk * d, "FlashAttnF64Ex V")
+    O = np.zeros(B * H * Sq * d)
+    L = np.zeros(B * H * Sq) if lse else None
+    kl = None
+    if kv_len is not None:
+        kl = np.ascontiguousarray(kv_len, dtype=np.int32)
+        if kl.shape != (B,):
+            raise ValueError(f"FlashAttnF64Ex: kv_len must have {B} entries")
+    check(_lib.load().gonn_hip_flash_attn_f64_ex(
+        _p(Q), _p(K), _p(V), _p(O), _p(L) if L is not None else None, B, H, Sq, Sk, d,
+        float(scale), int(bool(causal)),
+        kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None),
+        "FlashAttnF64Ex")
+    return (O, L) if lse else O
+
+
 def BenchFlashAttnF64(BH: int, S: int, d: int, iters: int, causal: bool) -> float:
     """Device-resident, event-timed forward; mean ms per launch."""
     ms = float(_lib.load().gonn_hip_bench_flash_attn_f64(BH, S, d, iters, int(bool(causal))))
@@ -208,13 +232,15 @@ def _shape4(t, name):
 
 
 def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None,
-             lse=True, lse_out=None, stream=None):
+             lse=True, lse_out=None, kv_len=None, stream=None):
     """O = softmax(scale QK^T + mask) V on device tensors.
 
     q (B,H,Sq,D) or (BH,Sq,D); k, v (.., Sk, D). fp32 mode needs float32
     inputs; bf16 mode takes float32 or bfloat16 inputs. Returns (O, LSE) with O
     float32 like q and LSE float32 (B*H, Sq) in natural-log units (or None when
-    lse is False). out / lse_out may supply preallocated outputs.
+    lse is False). out / lse_out may supply preallocated outputs. kv_len: an
+    optional int32 device tensor (B,) of valid keys per sequence (prefix key
+    padding; a 3-D q counts each slice as its own sequence).
     """
     torch = _torch()
     B, H, Sq, D = _shape4(q, "q")
@@ -227,7 +253,7 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
     if l is None and lse:
         l = torch.empty((B * H, Sq), dtype=torch.float32, device=q.device)
     a = FwdArgs(buf(q), buf(k), buf(v), buf(out), buf(l), B, H, Sq, Sk, D, float(scale),
-                int(bool(causal)), MODES[mode])
+                int(bool(causal)), MODES[mode], buf(kv_len) if kv_len is not None else Buf())
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_FWD, ctypes.byref(a))
@@ -390,5 +416,6 @@ class KVCache:
 
 
 __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
-           "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "BenchFlashAttnF64",
-           "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "buf", "GonnHipError"]
+           "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex",
+           "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "buf",
+           "GonnHipError"]

@@ -75,6 +75,15 @@ BwdOut FlashAttnF64Bwd(const std::vector<double>& Q, const std::vector<double>& 
 // cuda.go:188-194: mean milliseconds of `iters` device-resident forwards.
 double BenchFlashAttnF64(int BH, int S, int d, int iters, bool causal);
 
+// New (the reference seam is Tq == Tk only): the general fused forward for
+// the wider gate, cross-attention (Sq != Sk, top-left causal) and a prefix
+// key-padding mask kvLen[B] (empty = none). Q (B*H,Sq,d), K/V (B*H,Sk,d);
+// returns O (B*H,Sq,d).
+std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vector<double>& K,
+                                   const std::vector<double>& V, int B, int H, int Sq, int Sk,
+                                   int d, double scale, bool causal,
+                                   const std::vector<int>& kvLen = {});
+
 // Device KV cache of one attention layer (gonn_hip_kvcache_*). New: the
 // reference has no KV cache. Attend is ForwardMasked with a key-padding mask
 // (nn/attention.go:305-341) over each sequence's cached positions; a sequence
@@ -167,8 +176,15 @@ class MultiHeadAttention {
     // Forward (nn/attention.go:107-148) through the differentiable fused core;
     // the node of the last call is kept in LastNode for a backward pass.
     Tensor Forward(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
-    // ForwardFused (nn/attention.go:159-180): inference core, no node.
+    // ForwardFused (nn/attention.go:159-180): inference core, no node. Also
+    // takes Tq != Tk (cross-attention), which the reference's gate sends to
+    // its CPU path.
     Tensor ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
+    // ForwardMasked (nn/attention.go:305-341) on the fused core with causal
+    // and a (B, Tk) key-padding mask (nonzero = ignore; the padded keys of a
+    // row must be a suffix). An empty keyPad means none. Inference only.
+    Tensor ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
+                         const Tensor& keyPad);
 
     FlashAttnNode LastNode;
 
@@ -183,6 +199,8 @@ class MultiHeadAttention {
   private:
     void checkQKVDims(const Tensor& q, const Tensor& k, const Tensor& v) const;
     void requireFused(int D, int Tq, int Tk) const;
+    Tensor fusedGeneral(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
+                        const std::vector<int>& kvLen);
 };
 
 }  // namespace nn

@@ -106,6 +106,26 @@ double BenchFlashAttnF64(int BH, int S, int d, int iters, bool causal) {
     return ms;
 }
 
+std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vector<double>& K,
+                                   const std::vector<double>& V, int B, int H, int Sq, int Sk,
+                                   int d, double scale, bool causal,
+                                   const std::vector<int>& kvLen) {
+    if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || d <= 0)
+        throw std::invalid_argument("hip: FlashAttnF64Ex: B, H, Sq, Sk, d must be >= 1");
+    const size_t nq = (size_t)B * H * Sq * d, nk = (size_t)B * H * Sk * d;
+    need(Q, nq, "FlashAttnF64Ex Q");
+    need(K, nk, "FlashAttnF64Ex K");
+    need(V, nk, "FlashAttnF64Ex V");
+    if (!kvLen.empty() && (int)kvLen.size() != B)
+        throw std::invalid_argument("hip: FlashAttnF64Ex: kvLen needs B entries");
+    std::vector<double> O(nq, 0.0);
+    check(gonn_hip_flash_attn_f64_ex(Q.data(), K.data(), V.data(), O.data(), nullptr, B, H, Sq,
+                                     Sk, d, scale, causal ? 1 : 0,
+                                     kvLen.empty() ? nullptr : kvLen.data()),
+          "FlashAttnF64Ex");
+    return O;
+}
+
 KVCache::KVCache(int B, int H, int Lmax, int D) : B_(B), H_(H), Lmax_(Lmax), D_(D) {
     gonn_kvcache* c = nullptr;
     check(gonn_hip_kvcache_create(&c, B, H, Lmax, D), "KVCache");

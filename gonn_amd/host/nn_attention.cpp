@@ -184,10 +184,60 @@ Tensor MultiHeadAttention::Forward(const Tensor& q, const Tensor& k, const Tenso
     return OutProj.Forward(ctx);                                         // :132
 }
 
+Tensor MultiHeadAttention::fusedGeneral(const Tensor& q, const Tensor& k, const Tensor& v,
+                                        bool causal, const std::vector<int>& kvLen) {
+    const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1], H = NumHeads, D = HeadDim;
+    if (!fusedAttnAvailable())
+        throw hip::Error(-5, "nn: fused attention needs libgonn_hip.so and a gfx950 device");
+    if (!fusedAttnSupports(D, Tq, Tk))
+        throw std::invalid_argument("nn: the fused core needs D in {64, 128}, got D=" +
+                                    std::to_string(D));
+    const Tensor qp = QProj.Forward(q).Reshape({B, Tq, H, D}).Permute0213();
+    const Tensor kp = KProj.Forward(k).Reshape({B, Tk, H, D}).Permute0213();
+    const Tensor vp = VProj.Forward(v).Reshape({B, Tk, H, D}).Permute0213();
+    const double scale = 1.0 / std::sqrt((double)D);
+    std::vector<double> O =
+        hip::FlashAttnF64Ex(qp.Data, kp.Data, vp.Data, B, H, Tq, Tk, D, scale, causal, kvLen);
+    const Tensor ctx = Tensor::New(std::move(O), {B, H, Tq, D}).Permute0213().Reshape({B, Tq, EmbedDim});
+    return OutProj.Forward(ctx);
+}
+
+Tensor MultiHeadAttention::ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v,
+                                         bool causal, const Tensor& keyPad) {
+    checkQKVDims(q, k, v);
+    const int B = q.Shape[0], Tk = k.Shape[1];
+    std::vector<int> kvLen;
+    if (!keyPad.Data.empty()) {
+        // keyPaddingMaskAdd's shape check, nn/attention.go:262-264
+        if (keyPad.Shape.size() != 2 || keyPad.Shape[0] != B || keyPad.Shape[1] != Tk)
+            throw std::invalid_argument("MultiHeadAttention: key padding mask shape " +
+                                        shape_str(keyPad.Shape) + ", want (B, Tk) = (" +
+                                        std::to_string(B) + ", " + std::to_string(Tk) + ")");
+        kvLen.assign(B, Tk);
+        for (int b = 0; b < B; b++) {
+            const double* row = &keyPad.Data[(size_t)b * Tk];
+            int n = Tk;
+            for (int t = 0; t < Tk; t++)
+                if (row[t] != 0) {
+                    n = t;
+                    break;
+                }
+            for (int t = n; t < Tk; t++)
+                if (row[t] == 0)
+                    throw std::invalid_argument(
+                        "nn: the fused core takes key padding masks whose padded keys are a "
+                        "suffix of the row");
+            kvLen[b] = n;
+        }
+    }
+    return fusedGeneral(q, k, v, causal, kvLen);
+}
+
 Tensor MultiHeadAttention::ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v,
                                         bool causal) {
     checkQKVDims(q, k, v);
     const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1], H = NumHeads, D = HeadDim;
+    if (Tq != Tk) return fusedGeneral(q, k, v, causal, {});
     requireFused(D, Tq, Tk);
     const Tensor qp = QProj.Forward(q).Reshape({B, Tq, H, D}).Permute0213();
     const Tensor kp = KProj.Forward(k).Reshape({B, Tk, H, D}).Permute0213();

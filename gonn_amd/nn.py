@@ -123,17 +123,56 @@ class MultiHeadAttention:
         H, D = self.NumHeads, self.HeadDim
         if not fused_attn_available():
             raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
-        if Tq != Tk:
-            raise ValueError("nn: the fused core needs Tq == Tk (flash-attention seam contract)")
+        return self._fused(q, k, v, causal, None)
+
+    forward = forward_fused
+
+    def _fused(self, q, k, v, causal, kv_len):
+        B, Tq, _ = q.shape
+        Tk = k.shape[1]
+        H, D = self.NumHeads, self.HeadDim
         qp = self._split(self.QProj.forward(q))
         kp = self._split(self.KProj.forward(k))
         vp = self._split(self.VProj.forward(v))
         scale = 1.0 / math.sqrt(D)
-        O = fused_attn_f64(qp, kp, vp, B * H, Tq, D, scale, causal)
+        if Tq == Tk and kv_len is None:
+            O = fused_attn_f64(qp, kp, vp, B * H, Tq, D, scale, causal)
+        else:
+            # the wider gate: cross-attention and / or prefix key padding
+            O = hip.FlashAttnF64Ex(qp, kp, vp, B, H, Tq, Tk, D, scale, causal, kv_len=kv_len)
         ctx = O.reshape(B, H, Tq, D).transpose(0, 2, 1, 3).reshape(B, Tq, self.EmbedDim)
         return self.OutProj.forward(ctx)
 
-    forward = forward_fused
+    def forward_masked(self, q, k, v, causal: bool = False, key_padding_mask=None,
+                       attn_mask=None, dropout: float = 0.0):
+        """ForwardMasked (nn/attention.go:305-341) on the fused core: causal
+        and a (B, Tk) key-padding mask (nonzero = ignore the key) whose padded
+        keys form a suffix of each row, which is how padded batches look. An
+        additive attn_mask, attention dropout or a padding mask with holes are
+        not fused (the reference always runs ForwardMasked on its CPU path;
+        this library has none) and raise ValueError."""
+        if attn_mask is not None or dropout:
+            raise ValueError("nn: the fused core takes no additive attn mask or dropout")
+        q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+        self._check(q, k, v)
+        if not fused_attn_available():
+            raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
+        kv_len = None
+        if key_padding_mask is not None:
+            m = np.asarray(key_padding_mask)
+            B, Tk = q.shape[0], k.shape[1]
+            if m.shape != (B, Tk):
+                raise ValueError(f"MultiHeadAttention: key padding mask shape {m.shape}, "
+                                 f"want (B, Tk) = ({B}, {Tk})")
+            kv_len = np.empty(B, dtype=np.int32)
+            for b in range(B):
+                nz = np.nonzero(m[b])[0]
+                n = int(nz[0]) if nz.size else Tk
+                if np.any(m[b, n:] == 0):
+                    raise ValueError("nn: the fused core takes key padding masks whose padded "
+                                     "keys are a suffix of the row")
+                kv_len[b] = n
+        return self._fused(q, k, v, causal, kv_len)
 
     # ---- incremental decoding (new: the reference has no KV cache) ----
     def new_cache(self, batch: int, max_len: int) -> "hip.KVCache":

@@ -75,13 +75,21 @@ typedef struct {
 } gonn_buf;
 
 /* Forward: O = softmax(scale * Q K^T + mask) V, plus LSE.
- * q, k, v: GONN_F32 or GONN_BF16. o: GONN_F32. lse: GONN_F32 or ptr NULL. */
+ * q, k, v: GONN_F32 or GONN_BF16. o: GONN_F32. lse: GONN_F32 or ptr NULL.
+ * kv_len: optional GONN_I32 device array [B] (ptr NULL = none): keys
+ * t >= kv_len[b] are masked for every head and query of sequence b (a
+ * prefix key-padding mask, nn/attention.go:261-272), combined with the
+ * causal mask as ForwardMasked adds both (nn/attention.go:321-330). Values
+ * are clamped to [0, Sk]; a sequence with kv_len 0 gets O = 0 and
+ * LSE = -inf (the reference's fully masked row, a uniform average, is
+ * outside this library's definition). */
 typedef struct {
     gonn_buf q, k, v, o, lse;
     int B, H, Sq, Sk, D;
     double scale;
     int causal;
     int mode; /* gonn_attn_mode */
+    gonn_buf kv_len;
 } gonn_attn_fwd_args;
 
 /* Backward from the saved forward tensors: dQ, dK, dV (all GONN_F32).
@@ -229,6 +237,15 @@ int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* 
                                 const double* O, const double* L, const double* dO,
                                 double* dQ, double* dK, double* dV,
                                 int BH, int S, int d, double scale, int causal);
+/* New (the reference's fused seam is Tq == Tk, causal-or-not only): the
+ * general forward on host fp64 arrays for the wider fused gate, i.e.
+ * cross-attention (Sq != Sk, top-left causal mask when causal) and
+ * ForwardMasked with a prefix key-padding mask (nn/attention.go:305-341):
+ * Q (B*H, Sq, d), K, V (B*H, Sk, d), O (B*H, Sq, d); L (B*H, Sq) natural-log
+ * LSE or NULL; kv_len host int[B] (keys t >= kv_len[b] masked) or NULL.   */
+int gonn_hip_flash_attn_f64_ex(const double* Q, const double* K, const double* V, double* O,
+                               double* L, int B, int H, int Sq, int Sk, int d, double scale,
+                               int causal, const int* kv_len);
 /* backend/cuda/gonn_cuda.h:63, gonn_cuda.cu:532-560: device-resident,
  * event-timed forward; returns mean ms per launch, or a negative value on
  * error. Inputs are zero-filled like the reference's benchmark.           */

@@ -110,10 +110,13 @@ static Linear make_linear(Rng& r, int out, int in) {
     return l;
 }
 
-// The oracle's MHA forward: projections, split heads, core, merge, output.
+// The oracle's MHA forward: projections, split heads, core, merge, output;
+// Tq and Tk may differ, kvLen (empty = none) is a prefix key-padding mask.
 static std::vector<double> oracle_mha(const MultiHeadAttention& m, const Tensor& q,
-                                      const Tensor& k, const Tensor& v, bool causal) {
-    const int B = q.Shape[0], T = q.Shape[1], E = m.EmbedDim, H = m.NumHeads, D = m.HeadDim;
+                                      const Tensor& k, const Tensor& v, bool causal,
+                                      const std::vector<int>& kvLen = {}) {
+    const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1], E = m.EmbedDim, H = m.NumHeads,
+              D = m.HeadDim;
     auto lin = [](const Linear& l, const Tensor& x) {
         const int out = l.W.Shape[0], in = l.W.Shape[1], N = (int)(x.Numel() / in);
         std::vector<double> y((size_t)N * out);
@@ -122,13 +125,14 @@ static std::vector<double> oracle_mha(const MultiHeadAttention& m, const Tensor&
     };
     std::vector<double> qp = lin(m.QProj, q), kp = lin(m.KProj, k), vp = lin(m.VProj, v);
     std::vector<double> qh(qp.size()), kh(kp.size()), vh(vp.size()), o(qp.size()), ctx(qp.size());
-    oracle_heads(qp.data(), qh.data(), B, T, H, D, 0);
-    oracle_heads(kp.data(), kh.data(), B, T, H, D, 0);
-    oracle_heads(vp.data(), vh.data(), B, T, H, D, 0);
-    oracle_attn_fwd(qh.data(), kh.data(), vh.data(), o.data(), nullptr, B * H, H, T, T, D,
-                    1.0 / std::sqrt((double)D), causal ? 1 : 0, nullptr, nullptr, 0);
-    oracle_heads(o.data(), ctx.data(), B, T, H, D, 1);
-    Tensor c = Tensor::New(ctx, {B, T, E});
+    oracle_heads(qp.data(), qh.data(), B, Tq, H, D, 0);
+    oracle_heads(kp.data(), kh.data(), B, Tk, H, D, 0);
+    oracle_heads(vp.data(), vh.data(), B, Tk, H, D, 0);
+    oracle_attn_fwd(qh.data(), kh.data(), vh.data(), o.data(), nullptr, B * H, H, Tq, Tk, D,
+                    1.0 / std::sqrt((double)D), causal ? 1 : 0,
+                    kvLen.empty() ? nullptr : kvLen.data(), nullptr, 0);
+    oracle_heads(o.data(), ctx.data(), B, Tq, H, D, 1);
+    Tensor c = Tensor::New(ctx, {B, Tq, E});
     return lin(m.OutProj, c);
 }
 
@@ -318,6 +322,36 @@ static void test_gpu() {
         Tensor q = Tensor::New(r.normals(1 * 8 * 64), {1, 8, 64});
         Tensor k = Tensor::New(r.normals(1 * 9 * 64), {1, 9, 64});
         CHECK(throws_invalid([&] { m.Forward(q, k, k, false); }), "Tq != Tk rejected");
+    }
+    // The wider gate: cross-attention (Tq != Tk) through ForwardFused and a
+    // suffix key-padding mask through ForwardMasked, against the oracle.
+    for (bool causal : {false, true}) {
+        const int B = 3, Tq = 40, Tk = 64, E = 256, H = 4;
+        Rng r(3000 + causal);
+        const double ws = 1.0 / std::sqrt((double)E);
+        auto lin = [&] {
+            Linear l;
+            l.W = Tensor::New(r.normals((size_t)E * E, ws), {E, E});
+            l.B = r.normals(E, 0.1);
+            return l;
+        };
+        MultiHeadAttention m(E, H, lin(), lin(), lin(), lin());
+        Tensor q = Tensor::New(r.normals((size_t)B * Tq * E), {B, Tq, E});
+        Tensor mem = Tensor::New(r.normals((size_t)B * Tk * E), {B, Tk, E});
+        const std::string tag = causal ? " causal" : "";
+        const Tensor y = m.ForwardFused(q, mem, mem, causal);
+        CHECK(close(y.Data, oracle_mha(m, q, mem, mem, causal), 1e-4, 0.0,
+                    ("cross ForwardFused" + tag).c_str()), "cross ForwardFused%s", tag.c_str());
+        Tensor pad = Tensor::Zeros({B, Tk});
+        for (int t = 50; t < Tk; t++) pad.Data[(size_t)1 * Tk + t] = 1.0;
+        for (int t = 7; t < Tk; t++) pad.Data[(size_t)2 * Tk + t] = 1.0;
+        const Tensor ym = m.ForwardMasked(q, mem, mem, causal, pad);
+        CHECK(close(ym.Data, oracle_mha(m, q, mem, mem, causal, {Tk, 50, 7}), 1e-4, 0.0,
+                    ("ForwardMasked" + tag).c_str()), "ForwardMasked%s", tag.c_str());
+        Tensor holes = pad;
+        holes.Data[3] = 1.0;
+        CHECK(throws_invalid([&] { m.ForwardMasked(q, mem, mem, causal, holes); }),
+              "padding mask with holes rejected");
     }
     // Incremental decoding: ForwardIncremental over a KV cache in two chunks
     // equals the causal rows of the oracle's MHA over the whole sequence (the

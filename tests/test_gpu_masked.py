@@ -1,0 +1,116 @@
+"""GPU parity of the wider fused gate: cross-attention (Sq != Sk, top-left
+causal mask) and ForwardMasked's prefix key padding on the fused forward.
+
+Reference semantics: causalMaskAdd (nn/attention.go:185-196) and
+keyPaddingMaskAdd (:261-272) both add -1e30, which gives masked keys an
+exactly-zero weight in fp64; ForwardMasked adds both (:321-330). The oracle
+restates that (attn_oracle.c), so the GPU output is compared with it at the
+bar of the arithmetic mode (fp32-MFMA max-abs 1e-4; bf16-MFMA 2e-2 + 1e-2|ref|).
+A sequence with no valid key is defined here as O = 0, LSE = -inf.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._util import assert_close, randn, say
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_fwd_kv_len_and_cross_shapes(mode, D, causal):
+    from gonn_amd import hip
+    B, H, Sq, Sk = 3, 2, 70, 150
+    lens = np.array([150, 37, 0], dtype=np.int32)
+    say(f"[masked] fwd mode={mode} D={D} causal={causal} Sq={Sq} Sk={Sk} lens={list(lens)}")
+    q = randn((B * H, Sq, D), 800 + D)
+    k = randn((B * H, Sk, D), 801 + D)
+    v = randn((B * H, Sk, D), 802 + D)
+    dev = [torch.from_numpy(x).cuda().reshape(B, H, -1, D) for x in (q, k, v)]
+    kl = torch.from_numpy(lens).cuda()
+    o, l = hip.attn_fwd(*dev, causal=causal, mode=mode, kv_len=kl)
+    torch.cuda.synchronize()
+    o = o.reshape(B * H, Sq, D).cpu().numpy()
+    l = l.cpu().numpy()
+    ro, rl = oracle.attn_fwd(q, k, v, 1.0 / math.sqrt(D), causal, kv_len=lens, H=H)
+    live = np.repeat(lens > 0, H)
+    assert_close(o[live], ro[live], mode, f"O kv_len {mode} D={D} causal={causal}")
+    assert_close(l[live], rl[live], mode, f"LSE kv_len {mode} D={D} causal={causal}")
+    assert np.all(o[~live] == 0.0) and np.all(np.isneginf(l[~live]))
+
+
+def test_fwd_kv_len_clamped_and_absent_equal_full():
+    """kv_len >= Sk for every sequence is the same as no kv_len (bit-identical)."""
+    from gonn_amd import hip
+    B, H, S, D = 2, 4, 200, 128
+    dev = [torch.from_numpy(randn((B, H, S, D), 810 + i)).cuda() for i in range(3)]
+    o0, l0 = hip.attn_fwd(*dev, causal=True, mode="bf16")
+    kl = torch.tensor([S, S + 1000], dtype=torch.int32, device="cuda")
+    o1, l1 = hip.attn_fwd(*dev, causal=True, mode="bf16", kv_len=kl)
+    torch.cuda.synchronize()
+    assert torch.equal(o0, o1) and torch.equal(l0, l1)
+
+
+@pytest.mark.parametrize("d", [64, 100, 128])
+def test_f64_ex_entry(d):
+    from gonn_amd import hip
+    B, H, Sq, Sk = 2, 3, 33, 90
+    lens = np.array([90, 12], dtype=np.int32)
+    say(f"[masked] FlashAttnF64Ex d={d}")
+    q = randn((B * H, Sq, d), 820 + d).astype(np.float64)
+    k = randn((B * H, Sk, d), 821 + d).astype(np.float64)
+    v = randn((B * H, Sk, d), 822 + d).astype(np.float64)
+    for causal in (False, True):
+        O, L = hip.FlashAttnF64Ex(q, k, v, B, H, Sq, Sk, d, 1.0 / math.sqrt(d), causal,
+                                  kv_len=lens, lse=True)
+        ro, rl = oracle.attn_fwd(q, k, v, 1.0 / math.sqrt(d), causal, kv_len=lens, H=H)
+        assert_close(O.reshape(ro.shape), ro, "fp32", f"FlashAttnF64Ex d={d} causal={causal}")
+        assert_close(L.reshape(rl.shape), rl, "fp32", f"FlashAttnF64Ex LSE d={d} causal={causal}")
+
+
+def _params(E, seed):
+    s = 1.0 / math.sqrt(E)
+    p = {}
+    for i, n in enumerate(("q", "k", "v", "o")):
+        p["W" + n] = randn((E, E), seed + 2 * i).astype(np.float64) * s
+        p["b" + n] = randn((E,), seed + 2 * i + 1).astype(np.float64) * 0.1
+    return p
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_mha_forward_masked_and_cross_attention(causal):
+    from gonn_amd import nn
+    E, H, B, Tq, Tk = 256, 4, 3, 40, 64
+    say(f"[masked] MHA forward_masked / cross causal={causal}")
+    p = _params(E, 840)
+    mha = nn.MultiHeadAttention(E, H, p["Wq"], p["bq"], p["Wk"], p["bk"], p["Wv"], p["bv"],
+                                p["Wo"], p["bo"])
+    x = randn((B, Tk, E), 850).astype(np.float64)
+    mem = randn((B, Tk, E), 851).astype(np.float64)
+    q = randn((B, Tq, E), 852).astype(np.float64)
+    pad = np.zeros((B, Tk))
+    pad[1, 50:] = 1
+    pad[2, 7:] = 1
+    # self-attention with key padding (Tq == Tk)
+    got = mha.forward_masked(x, x, x, causal=causal, key_padding_mask=pad)
+    ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, key_pad=pad)
+    assert_close(got, ref, "fp32", f"forward_masked causal={causal}")
+    # cross-attention (Tq != Tk), with and without padding
+    got = mha.forward_fused(q, mem, mem, causal)
+    ref = oracle.mha_fwd(q, mem, mem, p, H, causal=causal)
+    assert_close(got, ref, "fp32", f"cross-attention causal={causal}")
+    got = mha.forward_masked(q, mem, mem, causal=causal, key_padding_mask=pad)
+    ref = oracle.mha_fwd(q, mem, mem, p, H, causal=causal, key_pad=pad)
+    assert_close(got, ref, "fp32", f"cross-attention + padding causal={causal}")
+    holes = pad.copy()
+    holes[0, 3] = 1
+    with pytest.raises(ValueError):
+        mha.forward_masked(x, x, x, key_padding_mask=holes)
+    with pytest.raises(ValueError):
+        mha.forward_masked(x, x, x, attn_mask=np.zeros((Tk, Tk)))
