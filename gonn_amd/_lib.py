@@ -21,6 +21,7 @@ GONN_E_WORKSPACE = -3
 GONN_E_NOMEM = -4
 GONN_E_NODEVICE = -5
 GONN_E_INJECTED = -6
+GONN_E_BLAS = -7
 
 GONN_F32, GONN_BF16, GONN_F64, GONN_I32 = 0, 1, 2, 3
 GONN_ATTN_FP32_MFMA, GONN_ATTN_BF16_MFMA = 0, 1
@@ -39,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_kvcache_create", "gonn_hip_kvcache_free", "gonn_hip_kvcache_reset",
     "gonn_hip_kvcache_lengths", "gonn_hip_kvcache_append", "gonn_hip_kvcache_append_f64",
     "gonn_hip_kvcache_attend", "gonn_hip_kvcache_attend_f64", "gonn_hip_flash_attn_f64_ex",
+    "gonn_hip_gemm_f64", "gonn_hip_gemm_f64_dev",
 )
 
 
@@ -131,6 +133,9 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_kvcache_attend_f64.argtypes = [vp, dp, dp, ctypes.c_double]
     lib.gonn_hip_flash_attn_f64_ex.argtypes = [dp, dp, dp, dp, dp, i, i, i, i, i, ctypes.c_double,
                                                i, ip]
+    lib.gonn_hip_gemm_f64.argtypes = [dp, dp, dp, i, i, i, i, i, i]
+    lib.gonn_hip_gemm_f64_dev.argtypes = [ctypes.POINTER(Buf), ctypes.POINTER(Buf),
+                                          ctypes.POINTER(Buf), i, i, i, i, i, i, vp]
     _lib = lib
     return lib
 

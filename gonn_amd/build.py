@@ -72,7 +72,7 @@ def build_host(verbose: bool = False) -> str:
     libgonn_host.so, linked against libgonn_hip.so (found next to it)."""
     srcs = sorted(os.path.join(HOST_SRC, f) for f in os.listdir(HOST_SRC) if f.endswith(".cpp"))
     tmp = HOST_LIB + ".tmp"
-    cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra",
+    cmd = ["g++", "-std=c++17", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-pthread",
            "-I", HOST_SRC, "-I", os.path.join(os.path.dirname(HERE), "include"), *srcs,
            "-L", HERE, "-lgonn_hip", "-Wl,-rpath,$ORIGIN", "-o", tmp]
     if verbose:
@@ -88,7 +88,8 @@ def build(verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
     tmp = LIB + ".tmp"
-    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs,
+           "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"]
     if verbose:
         print(" ".join(cmd), flush=True)
     subprocess.run(cmd, check=True)

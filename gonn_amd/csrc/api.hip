@@ -390,6 +390,7 @@ const char* gonn_hip_strerror(int code) {
         case GONN_E_NOMEM: return "device allocation failed";
         case GONN_E_NODEVICE: return "no usable gfx950 device";
         case GONN_E_INJECTED: return "failure injected by GONN_HIP_FAIL_ALLOC";
+        case GONN_E_BLAS: return "rocBLAS call failed";
         default: break;
     }
     if (code > 0) return hipGetErrorString((hipError_t)code);

@@ -157,6 +157,22 @@ def FlashAttnF64Ex(Q, K, V, B: int, H: int, Sq: int, Sk: int, d: int, scale: flo
     return (O, L) if lse else O
 
 
+def Gemm(a, b, batch: int, m: int, k: int, n: int, transA: bool = False,
+         transB: bool = False) -> np.ndarray:
+    """backend.Backend.Gemm (backend/backend.go:61-78) on the device: row-major
+    batched C = op(A) op(B) of host float64 data (A: batch*m*k, B: batch*k*n
+    elements); returns the batch*m*n result (flat), like cuda.go:42-67."""
+    a = _f64(a, batch * m * k, "Gemm A")
+    b = _f64(b, batch * k * n, "Gemm B")
+    out = np.zeros(batch * m * n)
+    if out.size == 0:
+        return out
+    check(_lib.load().gonn_hip_gemm_f64(_p(a) if a.size else None, _p(b) if b.size else None,
+                                        _p(out), batch, m, k, n, int(bool(transA)),
+                                        int(bool(transB))), "Gemm")
+    return out
+
+
 def BenchFlashAttnF64(BH: int, S: int, d: int, iters: int, causal: bool) -> float:
     """Device-resident, event-timed forward; mean ms per launch."""
     ms = float(_lib.load().gonn_hip_bench_flash_attn_f64(BH, S, d, iters, int(bool(causal))))
@@ -416,6 +432,6 @@ class KVCache:
 
 
 __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
-           "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex",
+           "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex", "Gemm",
            "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "buf",
            "GonnHipError"]

@@ -10,6 +10,8 @@
 //   gonn::hip  (backend/hip, the counterpart of backend/cuda/cuda.go)
 //     Available, Supports, SetMode, FlashAttnF64, FlashAttnF64Fwd,
 //     FlashAttnF64Bwd, BenchFlashAttnF64, KVCache (new)
+//   gonn::backend  (backend/backend.go:61-118: Backend, NewCPU, Use, Current;
+//     NewHIP is the counterpart of backend/cuda's Backend(), cuda.go:30-67)
 //   gonn::nn   (nn/flashattn_hip.go + the fused branch of nn/attention.go)
 //     Tensor, Linear, fusedAttnAvailable, fusedAttnSupports, fusedAttnF64,
 //     fusedAttnDiff, MultiHeadAttention::{Forward, ForwardFused,
@@ -26,6 +28,7 @@
 
 #include <array>
 #include <functional>
+#include <memory>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -117,6 +120,34 @@ class KVCache {
 
 }  // namespace hip
 
+namespace backend {
+
+// backend/backend.go:61-78: row-major batched C = op(A) op(B) of `batch`
+// contiguous matrix pairs; op(A) is (m,k) (stored (k,m) when transA), op(B)
+// (k,n) (stored (n,k) when transB); returns the batch*m*n result.
+class Backend {
+public:
+    virtual ~Backend() = default;
+    virtual std::string Name() const = 0;
+    virtual std::vector<double> Gemm(const std::vector<double>& a, const std::vector<double>& b,
+                                     int batch, int m, int k, int n, bool transA,
+                                     bool transB) const = 0;
+    virtual void Synchronize() const = 0;
+};
+
+// The host loop backend (backend/cpu.go), the default.
+std::shared_ptr<Backend> NewCPU();
+// The device GEMM (gonn_hip_gemm_f64). Throws gonn::hip::Error with
+// GONN_E_NODEVICE when no gfx950 device is present; a failed device GEMM
+// throws gonn::hip::Error (cuda.go:62-64 panics).
+std::shared_ptr<Backend> NewHIP();
+// Swap the process-wide backend and return the previous one (backend.go:108-118).
+// Safe for concurrent use.
+std::shared_ptr<Backend> Use(std::shared_ptr<Backend> b);
+std::shared_ptr<Backend> Current();
+
+}  // namespace backend
+
 namespace nn {
 
 // Host float64 tensor, row-major (tensor/tensor.go:22-23).
@@ -134,7 +165,9 @@ struct Tensor {
     Tensor Permute0213() const;
 };
 
-// y = x W^T + b (nn/linear.go:40-59); W is (out, in), b (out) or empty.
+// y = x W^T + b (nn/linear.go:40-59); W is (out, in), b (out) or empty. The
+// product runs on backend::Current(), as tensor.MatMul dispatches its GEMM
+// (tensor/dispatch.go:111-113).
 struct Linear {
     Tensor W;
     std::vector<double> B;

@@ -76,18 +76,11 @@ Tensor Linear::Forward(const Tensor& x) const {
                                     ", want (..., " + std::to_string(in) + ")");
     if (!B.empty() && (int)B.size() != out) throw std::invalid_argument("Linear: bias length");
     const size_t N = x.Numel() / (size_t)in;
-    std::vector<double> y(N * (size_t)out);
-    // y[n][o] = sum_i x[n][i] W[o][i] (+ b[o]), the x @ W^T + b of
-    // nn/linear.go:53-57, summed in input order.
-    for (size_t n = 0; n < N; n++) {
-        const double* xr = &x.Data[n * in];
-        for (int o = 0; o < out; o++) {
-            const double* wr = &W.Data[(size_t)o * in];
-            double acc = 0.0;
-            for (int i = 0; i < in; i++) acc += xr[i] * wr[i];
-            y[n * out + o] = B.empty() ? acc : acc + B[o];
-        }
-    }
+    // x (N, in) @ W^T: op(B) is W stored (out, in), so transB.
+    std::vector<double> y = backend::Current()->Gemm(x.Data, W.Data, 1, (int)N, in, out, false, true);
+    if (!B.empty())
+        for (size_t n = 0; n < N; n++)
+            for (int o = 0; o < out; o++) y[n * out + o] += B[o];
     std::vector<int> shape = x.Shape;
     shape.back() = out;
     return Tensor::New(std::move(y), std::move(shape));

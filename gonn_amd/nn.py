@@ -23,7 +23,7 @@ import math
 
 import numpy as np
 
-from . import hip
+from . import backend, hip
 
 
 def fused_attn_available() -> bool:
@@ -75,10 +75,16 @@ class Linear:
         self.b = None if b is None else np.asarray(b, dtype=np.float64)
 
     def forward(self, x):
-        y = x.reshape(-1, x.shape[-1]) @ self.W.T
+        # x2 @ W^T through the current backend (tensor.MatMul -> dispatchGemm,
+        # tensor/dispatch.go:111-113): W is stored (out, in), so op(B) = W^T.
+        x = np.asarray(x, dtype=np.float64)
+        out, inp = self.W.shape
+        x2 = x.reshape(-1, inp)
+        y = backend.Current().Gemm(x2, self.W, 1, x2.shape[0], inp, out, False, True)
+        y = y.reshape(x2.shape[0], out)
         if self.b is not None:
             y = y + self.b
-        return y.reshape(*x.shape[:-1], self.W.shape[0])
+        return y.reshape(*x.shape[:-1], out)
 
 
 class MultiHeadAttention:

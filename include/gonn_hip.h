@@ -53,7 +53,8 @@ enum {
     GONN_E_WORKSPACE = -3,   /* workspace missing or smaller than required      */
     GONN_E_NOMEM = -4,       /* device allocation failed                        */
     GONN_E_NODEVICE = -5,    /* no usable gfx950 device                         */
-    GONN_E_INJECTED = -6     /* failure forced by GONN_HIP_FAIL_ALLOC=1         */
+    GONN_E_INJECTED = -6,    /* failure forced by GONN_HIP_FAIL_ALLOC=1         */
+    GONN_E_BLAS = -7         /* a rocBLAS call failed (GEMM)                    */
 };
 
 /* ---- element types and arithmetic modes --------------------------------- */
@@ -204,6 +205,19 @@ int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, dou
                             void* stream);
 /* As gonn_hip_kvcache_attend with host fp64 q and o (B,H,D); synchronous. */
 int gonn_hip_kvcache_attend_f64(gonn_kvcache* c, const double* q, double* o, double scale);
+
+/* ---- fp64 GEMM of the backend -------------------------------------------
+ * backend.Backend.Gemm (backend/backend.go:61-78) on the device: row-major
+ * batched C = op(A) op(B); op(A) (m,k) stored (m,k), or (k,m) when transA;
+ * op(B) (k,n) stored (k,n), or (n,k) when transB; C (m,n); `batch`
+ * contiguous pairs. Replaces gonn_gemm (backend/cuda/gonn_cuda.h:36,
+ * gonn_cuda.cu:147-177): host fp64 in and out, synchronous, serialised on
+ * an internal workspace like the reference's. The _dev variant takes
+ * GONN_F64 device buffers and a stream.                                   */
+int gonn_hip_gemm_f64(const double* A, const double* B, double* C, int batch, int m, int k, int n,
+                      int transA, int transB);
+int gonn_hip_gemm_f64_dev(const gonn_buf* A, const gonn_buf* B, gonn_buf* C, int batch, int m,
+                          int k, int n, int transA, int transB, void* stream);
 
 /* ---- device buffers ------------------------------------------------------
  * Replace gonn_dev_alloc / gonn_dev_free / gonn_dev_upload / gonn_dev_download

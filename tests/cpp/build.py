@@ -13,7 +13,7 @@ OUT = os.path.join(HERE, "host_test")
 
 def build(verbose: bool = False) -> str:
     pkg, orc = os.path.join(ROOT, "gonn_amd"), os.path.join(ROOT, "oracle")
-    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra",
+    cmd = ["g++", "-std=c++17", "-O2", "-Wall", "-Wextra", "-pthread",
            "-I", os.path.join(pkg, "host"), "-I", os.path.join(ROOT, "include"),
            os.path.join(HERE, "host_test.cpp"), "-o", OUT + ".tmp",
            "-L", pkg, "-lgonn_host", "-lgonn_hip", "-L", orc, "-loracle",

@@ -18,6 +18,7 @@
 #include <cstring>
 #include <functional>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "gonn_hip.h"
@@ -136,6 +137,85 @@ static std::vector<double> oracle_mha(const MultiHeadAttention& m, const Tensor&
     return lin(m.OutProj, c);
 }
 
+// op(X) materialised by explicit transposition, then the textbook triple
+// loop: the brute-force check of the backends' strided GEMM.
+static std::vector<double> naive_gemm(const std::vector<double>& a, const std::vector<double>& b,
+                                      int batch, int m, int k, int n, bool ta, bool tb) {
+    std::vector<double> c((size_t)batch * m * n);
+    std::vector<double> A((size_t)m * k), B((size_t)k * n);
+    for (int z = 0; z < batch; z++) {
+        for (int i = 0; i < m; i++)
+            for (int p = 0; p < k; p++)
+                A[(size_t)i * k + p] = ta ? a[(size_t)z * m * k + (size_t)p * m + i]
+                                          : a[(size_t)z * m * k + (size_t)i * k + p];
+        for (int p = 0; p < k; p++)
+            for (int j = 0; j < n; j++)
+                B[(size_t)p * n + j] = tb ? b[(size_t)z * k * n + (size_t)j * k + p]
+                                          : b[(size_t)z * k * n + (size_t)p * n + j];
+        for (int i = 0; i < m; i++)
+            for (int j = 0; j < n; j++) {
+                double s = 0.0;
+                for (int p = 0; p < k; p++) s += A[(size_t)i * k + p] * B[(size_t)p * n + j];
+                c[(size_t)z * m * n + (size_t)i * n + j] = s;
+            }
+    }
+    return c;
+}
+
+struct GemmCase {
+    int batch, m, k, n;
+    bool ta, tb;
+};
+// backend/backend_test.go:54-66, plus a transA-only batched case.
+static const GemmCase kGemmCases[] = {{1, 3, 4, 5, false, false}, {1, 3, 4, 5, true, false},
+                                      {1, 3, 4, 5, false, true},  {1, 3, 4, 5, true, true},
+                                      {4, 2, 3, 2, false, false}, {4, 2, 3, 2, true, true},
+                                      {2, 1, 1, 1, false, false}, {3, 5, 2, 4, false, true},
+                                      {3, 5, 7, 4, true, false}};
+
+static void test_backend_cpu(Rng& r) {
+    namespace be = gonn::backend;
+    auto cpu = be::NewCPU();
+    CHECK(cpu->Name() == "cpu" && be::Current()->Name() == "cpu", "default backend is cpu");
+    for (const GemmCase& c : kGemmCases) {
+        const auto a = r.normals((size_t)c.batch * c.m * c.k);
+        const auto b = r.normals((size_t)c.batch * c.k * c.n);
+        const auto got = cpu->Gemm(a, b, c.batch, c.m, c.k, c.n, c.ta, c.tb);
+        CHECK(close(got, naive_gemm(a, b, c.batch, c.m, c.k, c.n, c.ta, c.tb), 1e-12, 0.0,
+                    "cpu Gemm vs naive"),
+              "cpu Gemm %d %d %d %d %d %d", c.batch, c.m, c.k, c.n, c.ta, c.tb);
+    }
+    CHECK(cpu->Gemm({}, {}, 0, 3, 4, 5, false, false).empty(), "Gemm batch=0 is empty");
+    CHECK(throws_invalid([&] { cpu->Gemm(std::vector<double>(5), std::vector<double>(20), 1, 2, 3, 4, false, false); }),
+          "Gemm short A");
+
+    // backend_test.go:90-111: Use/Current from several threads, then restored.
+    auto start = be::Current();
+    std::vector<std::thread> ts;
+    bool nil_seen = false;
+    for (int g = 0; g < 8; g++)
+        ts.emplace_back([&] {
+            for (int i = 0; i < 1000; i++) {
+                auto prev = be::Use(be::NewCPU());
+                if (!be::Current()) nil_seen = true;
+                be::Use(prev);
+            }
+        });
+    for (auto& t : ts) t.join();
+    be::Use(start);
+    CHECK(!nil_seen && be::Current() == start, "Use/Current concurrent");
+
+    if (!gonn::hip::Available()) {
+        int code = 0;
+        try {
+            be::NewHIP();
+        } catch (const gonn::hip::Error& e) {
+            code = e.code;
+        }
+        CHECK(code == GONN_E_NODEVICE, "NewHIP without device: code %d", code);
+    }
+}
+
 static void test_cpu() {
     // Supports: the head dims the kernels cover (replaces D == 64 at
     // nn/attention.go:129).
@@ -189,6 +269,7 @@ static void test_cpu() {
     oracle_linear(in.Data.data(), l.W.Data.data(), l.B.data(), yref.data(), 21, 40, 24);
     CHECK(y.Shape == std::vector<int>({3, 7, 24}), "Linear shape");
     CHECK(close(y.Data, yref, 1e-12, 0.0, "Linear vs oracle"), "Linear vs oracle");
+    test_backend_cpu(r);
 
     // MultiHeadAttention construction and checkQKVDims (nn/attention.go:45-103).
     CHECK(throws_invalid([&] {
@@ -240,6 +321,52 @@ static void test_cpu() {
         }
         CHECK(code == GONN_E_UNSUPPORTED, "KVCache D=96: code %d", code);
     }
+}
+
+// The HIP backend's GEMM (gonn_hip_gemm_f64) against the host loop at the
+// reference's GPU-vs-CPU bar of 1e-10 (tensor/cuda_dispatch_test.go:127-131),
+// and the MHA with its projections on it against the oracle.
+static void test_backend_gpu() {
+    namespace be = gonn::backend;
+    auto dev = be::NewHIP();
+    auto cpu = be::NewCPU();
+    CHECK(dev->Name() == "hip", "NewHIP name");
+    Rng r(77);
+    std::vector<GemmCase> cases(std::begin(kGemmCases), std::end(kGemmCases));
+    cases.push_back({1, 31, 17, 23, false, false});  // cuda_dispatch_test.go:119
+    cases.push_back({6, 8, 5, 7, false, false});     // the (2,3,8,5)@(2,3,5,7) batch
+    cases.push_back({2, 130, 257, 66, true, true});
+    for (const GemmCase& c : cases) {
+        const auto a = r.normals((size_t)c.batch * c.m * c.k);
+        const auto b = r.normals((size_t)c.batch * c.k * c.n);
+        const auto got = dev->Gemm(a, b, c.batch, c.m, c.k, c.n, c.ta, c.tb);
+        CHECK(close(got, cpu->Gemm(a, b, c.batch, c.m, c.k, c.n, c.ta, c.tb), 1e-10, 0.0,
+                    "hip Gemm vs cpu"),
+              "hip Gemm %d %d %d %d %d %d", c.batch, c.m, c.k, c.n, c.ta, c.tb);
+    }
+    const auto z = dev->Gemm(std::vector<double>(0), std::vector<double>(0), 2, 3, 0, 4, false, false);
+    CHECK(z.size() == 24 && z == std::vector<double>(24, 0.0), "hip Gemm k=0 gives zeros");
+
+    const int B = 2, T = 128, E = 256, H = 4;
+    const double ws = 1.0 / std::sqrt((double)E);
+    auto lin = [&] {
+        Linear l;
+        l.W = Tensor::New(r.normals((size_t)E * E, ws), {E, E});
+        l.B = r.normals(E, ws);
+        return l;
+    };
+    MultiHeadAttention m(E, H, lin(), lin(), lin(), lin());
+    Tensor x = Tensor::New(r.normals((size_t)B * T * E, ws), {B, T, E});
+    const std::vector<double> ref = oracle_mha(m, x, x, x, true);
+    gonn::hip::SetMode(0);
+    const Tensor on_cpu = m.ForwardFused(x, x, x, true);
+    auto prev = be::Use(dev);
+    const Tensor on_dev = m.ForwardFused(x, x, x, true);
+    be::Use(prev);
+    CHECK(close(on_dev.Data, ref, 1e-4, 0.0, "MHA, projections on the HIP backend"),
+          "MHA on HIP backend vs oracle");
+    CHECK(close(on_dev.Data, on_cpu.Data, 1e-9, 0.0, "MHA HIP backend vs CPU backend"),
+          "MHA HIP backend vs CPU backend");
 }
 
 static void test_gpu() {
@@ -402,6 +529,7 @@ static void test_gpu() {
         cache.Reset();
         CHECK(cache.Lengths() == std::vector<int>({0, 0}), "Reset");
     }
+    test_backend_gpu();
 }
 
 int main(int argc, char** argv) {

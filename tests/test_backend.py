@@ -1,0 +1,111 @@
+"""The backend contract around the attention core (backend/backend.go:61-78):
+the CPU backend's row-major batched GEMM against a naive triple loop at
+1e-12 (the reference's own bar, backend/backend_test.go:47-86), backend
+selection (Use / Current), and the device GEMM entry point's argument and
+no-device paths (no CPU fallback)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from gonn_amd import _lib, backend, hip
+from gonn_amd._lib import GONN_E_INVALID, GONN_E_NODEVICE
+
+
+def _naive(A, B, batch, m, k, n, ta, tb):
+    A = A.reshape(batch, *((k, m) if ta else (m, k)))
+    B = B.reshape(batch, *((n, k) if tb else (k, n)))
+    C = np.zeros((batch, m, n))
+    for z in range(batch):
+        for i in range(m):
+            for j in range(n):
+                s = 0.0
+                for p in range(k):
+                    a = A[z, p, i] if ta else A[z, i, p]
+                    b = B[z, j, p] if tb else B[z, p, j]
+                    s += a * b
+                C[z, i, j] = s
+    return C.reshape(-1)
+
+
+# The case list of backend/backend_test.go:54-66: plain 2D in every
+# transpose combination, batched, degenerate 1x1x1.
+_CASES = [(1, 3, 4, 5, False, False), (1, 3, 4, 5, True, False), (1, 3, 4, 5, False, True),
+          (1, 3, 4, 5, True, True), (4, 2, 3, 2, False, False), (4, 2, 3, 2, True, True),
+          (2, 1, 1, 1, False, False), (3, 5, 2, 4, False, True), (3, 5, 7, 4, True, False)]
+
+
+@pytest.mark.parametrize("case", _CASES, ids=lambda c: "-".join(map(str, c)))
+def test_cpu_backend_gemm_matches_naive(case):
+    batch, m, k, n, ta, tb = case
+    rng = np.random.default_rng(7)
+    A = rng.standard_normal(batch * m * k)
+    B = rng.standard_normal(batch * k * n)
+    be = backend.NewCPU()
+    assert be.Name() == "cpu"
+    got = be.Gemm(A, B, batch, m, k, n, ta, tb)
+    ref = _naive(A, B, batch, m, k, n, ta, tb)
+    assert got.shape == ref.shape
+    assert np.max(np.abs(got - ref)) <= 1e-12
+
+
+def test_cpu_backend_empty_batch():
+    # backend_test.go:82-85: batch 0 gives an empty result.
+    assert backend.NewCPU().Gemm(np.zeros(0), np.zeros(0), 0, 3, 4, 5).size == 0
+
+
+def test_use_current_concurrent():
+    # backend_test.go:90-111: Use/Current from many threads, restored after.
+    import threading
+    start = backend.Current()
+    errs = []
+
+    def worker():
+        for _ in range(1000):
+            prev = backend.Use(backend.CPUBackend())
+            if backend.Current() is None:
+                errs.append("nil")
+                return
+            backend.Use(prev)
+
+    ts = [threading.Thread(target=worker) for _ in range(8)]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join()
+    backend.Use(start)
+    assert not errs and backend.Current().Name() == "cpu"
+
+
+def test_use_returns_previous_and_linear_dispatches():
+    calls = []
+
+    class Spy(backend.CPUBackend):
+        def Gemm(self, *a, **kw):
+            calls.append(a[2:6])
+            return super().Gemm(*a, **kw)
+
+    prev = backend.Use(Spy())
+    try:
+        from gonn_amd import nn
+        lin = nn.Linear(np.ones((3, 4)), np.zeros(3))
+        y = lin.forward(np.ones((2, 5, 4)))
+        assert y.shape == (2, 5, 3) and np.all(y == 4.0)
+        assert calls == [(1, 10, 4, 3)]
+    finally:
+        backend.Use(prev)
+    assert backend.Current() is prev
+
+
+def test_gemm_entry_checks():
+    lib = _lib.load()
+    dp = ctypes.POINTER(ctypes.c_double)
+    x = np.zeros(16)
+    p = x.ctypes.data_as(dp)
+    assert lib.gonn_hip_gemm_f64(p, p, p, -1, 2, 2, 2, 0, 0) == GONN_E_INVALID
+    assert lib.gonn_hip_gemm_f64(None, p, p, 1, 2, 2, 2, 0, 0) == GONN_E_INVALID
+    assert lib.gonn_hip_gemm_f64(p, p, p, 0, 2, 2, 2, 0, 0) == 0  # empty result
+    if not hip.Available():
+        assert lib.gonn_hip_gemm_f64(p, p, p, 1, 2, 2, 2, 0, 0) == GONN_E_NODEVICE
+        with pytest.raises(RuntimeError):
+            backend.HIPBackend()
