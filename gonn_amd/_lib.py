@@ -25,6 +25,10 @@ GONN_E_BLAS = -7
 
 GONN_F32, GONN_BF16, GONN_F64, GONN_I32 = 0, 1, 2, 3
 GONN_ATTN_FP32_MFMA, GONN_ATTN_BF16_MFMA = 0, 1
+# backend.UnaryKind / BinaryKind values (backend/backend.go:26-58): a shared ABI.
+(GONN_UN_RELU, GONN_UN_SIGMOID, GONN_UN_TANH, GONN_UN_EXP, GONN_UN_LOG, GONN_UN_GELU,
+ GONN_UN_SILU, GONN_UN_GELU_EXACT) = range(8)
+GONN_BIN_ADD, GONN_BIN_SUB, GONN_BIN_MUL, GONN_BIN_DIV = range(4)
 GONN_OP_FWD, GONN_OP_BWD, GONN_OP_DECODE = 0, 1, 2
 
 # Every symbol include/gonn_hip.h declares.
@@ -41,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_kvcache_lengths", "gonn_hip_kvcache_append", "gonn_hip_kvcache_append_f64",
     "gonn_hip_kvcache_attend", "gonn_hip_kvcache_attend_f64", "gonn_hip_flash_attn_f64_ex",
     "gonn_hip_gemm_f64", "gonn_hip_gemm_f64_dev",
+    "gonn_hip_unary_f64", "gonn_hip_binary_f64", "gonn_hip_unary_f64_dev", "gonn_hip_binary_f64_dev",
 )
 
 
@@ -136,6 +141,12 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_gemm_f64.argtypes = [dp, dp, dp, i, i, i, i, i, i]
     lib.gonn_hip_gemm_f64_dev.argtypes = [ctypes.POINTER(Buf), ctypes.POINTER(Buf),
                                           ctypes.POINTER(Buf), i, i, i, i, i, i, vp]
+    lg = ctypes.c_long
+    lib.gonn_hip_unary_f64.argtypes = [i, dp, dp, lg]
+    lib.gonn_hip_binary_f64.argtypes = [i, dp, dp, dp, lg]
+    lib.gonn_hip_unary_f64_dev.argtypes = [i, ctypes.POINTER(Buf), ctypes.POINTER(Buf), lg, vp]
+    lib.gonn_hip_binary_f64_dev.argtypes = [i, ctypes.POINTER(Buf), ctypes.POINTER(Buf),
+                                            ctypes.POINTER(Buf), lg, vp]
     _lib = lib
     return lib
 

@@ -10,14 +10,26 @@ Two implementations:
 nn.Linear (the MHA projections, nn/linear.go:40-59) multiplies through the
 current backend, as tensor.MatMul does through dispatchGemm
 (tensor/dispatch.go:111-113).
+
+The optional Elementwiser capability (backend.go:80-92: Unary, Binary on the
+UnaryKind / BinaryKind values of backend.go:26-58) is implemented by
+HIPBackend only; the CPU backend deliberately lacks it, as in the reference
+(backend_test.go:117-126). dispatch_unary / dispatch_binary and the
+DispatchPolicy thresholds restate tensor/dispatch.go:44-109.
 """
 from __future__ import annotations
 
 import threading
+from dataclasses import dataclass
 
 import numpy as np
 
 from . import hip
+
+UnaryNone = -1
+(UnaryReLU, UnarySigmoid, UnaryTanh, UnaryExp, UnaryLog, UnaryGELU, UnarySiLU,
+ UnaryGELUExact) = range(8)
+BinaryAdd, BinarySub, BinaryMul, BinaryDiv = range(4)
 
 
 class CPUBackend:
@@ -55,6 +67,22 @@ class HIPBackend:
     def Synchronize(self) -> None:
         pass  # every call of the host GEMM is synchronous
 
+    # Elementwiser. The reference declines (returns False) on any device
+    # error so the caller runs its CPU loop (cuda.go:70-106). Here only a kind
+    # without a kernel is declined; a device error raises, so a failing device
+    # never hides behind a host loop.
+    def Unary(self, kind: int, a, out) -> bool:
+        if not (0 <= kind <= UnaryGELUExact):
+            return False
+        hip.Unary(kind, a, out)
+        return True
+
+    def Binary(self, kind: int, a, b, out) -> bool:
+        if not (0 <= kind <= BinaryDiv):
+            return False
+        hip.Binary(kind, a, b, out)
+        return True
+
 
 _lock = threading.Lock()
 _current = CPUBackend()
@@ -77,3 +105,42 @@ def Use(b):
 
 def Current():
     return _current
+
+
+@dataclass(frozen=True)
+class DispatchPolicy:
+    """Minimum sizes for offloading elementwise ops (tensor/dispatch.go:44-58):
+    binary ops never dispatch by default (their host copies cost more than the
+    op)."""
+    UnaryMinElems: int = 1 << 16
+    BinaryMinElems: int = 2 ** 63 - 1
+
+
+_policy = DispatchPolicy()
+
+
+def SetDispatchPolicy(p: DispatchPolicy) -> None:
+    global _policy
+    _policy = p
+
+
+def GetDispatchPolicy() -> DispatchPolicy:
+    return _policy
+
+
+def dispatch_unary(kind: int, a, out) -> bool:
+    """tensor/dispatch.go:74-84: run out = f(a) on the current backend when the
+    op has a kernel, a is large enough and the backend has the capability;
+    False means the caller runs its own loop."""
+    if kind == UnaryNone or np.size(a) < _policy.UnaryMinElems:
+        return False
+    fn = getattr(Current(), "Unary", None)
+    return fn is not None and fn(kind, a, out)
+
+
+def dispatch_binary(kind: int, a, b, out) -> bool:
+    """tensor/dispatch.go:100-109."""
+    if np.size(a) < _policy.BinaryMinElems:
+        return False
+    fn = getattr(Current(), "Binary", None)
+    return fn is not None and fn(kind, a, b, out)

@@ -173,6 +173,36 @@ def Gemm(a, b, batch: int, m: int, k: int, n: int, transA: bool = False,
     return out
 
 
+def Unary(kind: int, a, out=None) -> np.ndarray:
+    """backend.Elementwiser.Unary on the device: out[i] = f_kind(a[i]) over host
+    float64 data (kinds: _lib.GONN_UN_*, backend/backend.go:36-45). Raises on an
+    unknown kind or a device error."""
+    a = np.ascontiguousarray(a, dtype=np.float64).reshape(-1)
+    if out is None:
+        out = np.empty_like(a)
+    elif not (isinstance(out, np.ndarray) and out.dtype == np.float64 and out.flags.c_contiguous
+              and out.size == a.size):
+        raise ValueError("Unary: out must be a contiguous float64 array of a's size")
+    if a.size:
+        check(_lib.load().gonn_hip_unary_f64(int(kind), _p(a), _p(out), a.size), "Unary")
+    return out
+
+
+def Binary(kind: int, a, b, out=None) -> np.ndarray:
+    """backend.Elementwiser.Binary on the device: out[i] = a[i] op b[i] (kinds:
+    _lib.GONN_BIN_*, backend/backend.go:51-58)."""
+    a = np.ascontiguousarray(a, dtype=np.float64).reshape(-1)
+    b = _f64(b, a.size, "Binary B").reshape(-1)
+    if out is None:
+        out = np.empty_like(a)
+    elif not (isinstance(out, np.ndarray) and out.dtype == np.float64 and out.flags.c_contiguous
+              and out.size == a.size):
+        raise ValueError("Binary: out must be a contiguous float64 array of a's size")
+    if a.size:
+        check(_lib.load().gonn_hip_binary_f64(int(kind), _p(a), _p(b), _p(out), a.size), "Binary")
+    return out
+
+
 def BenchFlashAttnF64(BH: int, S: int, d: int, iters: int, causal: bool) -> float:
     """Device-resident, event-timed forward; mean ms per launch."""
     ms = float(_lib.load().gonn_hip_bench_flash_attn_f64(BH, S, d, iters, int(bool(causal))))
@@ -433,5 +463,6 @@ class KVCache:
 
 __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
            "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex", "Gemm",
+           "Unary", "Binary",
            "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "buf",
            "GonnHipError"]

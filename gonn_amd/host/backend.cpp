@@ -1,7 +1,7 @@
 // backend.cpp -- gonn::backend, the C++ counterpart of the compute-target
 // contract of backend/backend.go:61-118 (Backend, NewCPU, Use, Current) and of
-// the CUDA backend's Gemm (backend/cuda/cuda.go:30-67), over the C ABI's
-// gonn_hip_gemm_f64.
+// the CUDA backend's Gemm and Elementwiser methods (backend/cuda/cuda.go:30-106),
+// over the C ABI's gonn_hip_gemm_f64 / gonn_hip_unary_f64 / gonn_hip_binary_f64.
 #include "gonn_host.hpp"
 
 #include <mutex>
@@ -57,7 +57,7 @@ public:
     void Synchronize() const override {}
 };
 
-class HipBackend final : public Backend {
+class HipBackend final : public Backend, public Elementwiser {
 public:
     std::string Name() const override { return "hip"; }
 
@@ -75,6 +75,27 @@ public:
 
     // Every gonn_hip_gemm_f64 call returns with its result on the host.
     void Synchronize() const override {}
+
+    bool Unary(UnaryKind kind, const std::vector<double>& a,
+               std::vector<double>& out) const override {
+        if (kind < UnaryReLU || kind > UnaryGELUExact) return false;
+        if (out.size() != a.size()) throw std::invalid_argument("hip Unary: len(out) != len(a)");
+        if (a.empty()) return true;
+        const int rc = gonn_hip_unary_f64(kind, a.data(), out.data(), (long)a.size());
+        if (rc != 0) throw hip::Error(rc, "Unary");
+        return true;
+    }
+
+    bool Binary(BinaryKind kind, const std::vector<double>& a, const std::vector<double>& b,
+                std::vector<double>& out) const override {
+        if (kind < BinaryAdd || kind > BinaryDiv) return false;
+        if (b.size() != a.size() || out.size() != a.size())
+            throw std::invalid_argument("hip Binary: operand lengths differ");
+        if (a.empty()) return true;
+        const int rc = gonn_hip_binary_f64(kind, a.data(), b.data(), out.data(), (long)a.size());
+        if (rc != 0) throw hip::Error(rc, "Binary");
+        return true;
+    }
 };
 
 std::mutex g_mu;

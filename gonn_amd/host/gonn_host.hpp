@@ -135,6 +135,35 @@ public:
     virtual void Synchronize() const = 0;
 };
 
+// backend.UnaryKind / BinaryKind (backend/backend.go:26-58); the values are
+// the C ABI's GONN_UN_* / GONN_BIN_*.
+enum UnaryKind : int {
+    UnaryNone = -1,
+    UnaryReLU = 0,
+    UnarySigmoid,
+    UnaryTanh,
+    UnaryExp,
+    UnaryLog,
+    UnaryGELU,
+    UnarySiLU,
+    UnaryGELUExact
+};
+enum BinaryKind : int { BinaryAdd = 0, BinarySub, BinaryMul, BinaryDiv };
+
+// Optional capability (backend.go:80-92): write out and return true, or
+// return false to decline (the caller runs its own loop). The HIP backend
+// declines only kinds it has no kernel for; a device error throws
+// gonn::hip::Error instead of falling back. The CPU backend does not
+// implement it (backend_test.go:117-126).
+class Elementwiser {
+public:
+    virtual ~Elementwiser() = default;
+    virtual bool Unary(UnaryKind kind, const std::vector<double>& a,
+                       std::vector<double>& out) const = 0;
+    virtual bool Binary(BinaryKind kind, const std::vector<double>& a,
+                        const std::vector<double>& b, std::vector<double>& out) const = 0;
+};
+
 // The host loop backend (backend/cpu.go), the default.
 std::shared_ptr<Backend> NewCPU();
 // The device GEMM (gonn_hip_gemm_f64). Throws gonn::hip::Error with

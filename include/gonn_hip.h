@@ -219,6 +219,33 @@ int gonn_hip_gemm_f64(const double* A, const double* B, double* C, int batch, in
 int gonn_hip_gemm_f64_dev(const gonn_buf* A, const gonn_buf* B, gonn_buf* C, int batch, int m,
                           int k, int n, int transA, int transB, void* stream);
 
+/* ---- fp64 elementwise ops of the backend --------------------------------
+ * backend.Elementwiser (backend/backend.go:80-92). The kind values are the
+ * reference's append-only ABI (backend.go:26-58, gonn_cuda.h:13-28).       */
+enum {
+    GONN_UN_RELU = 0,
+    GONN_UN_SIGMOID = 1,
+    GONN_UN_TANH = 2,
+    GONN_UN_EXP = 3,
+    GONN_UN_LOG = 4,
+    GONN_UN_GELU = 5,       /* 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) */
+    GONN_UN_SILU = 6,       /* x sigmoid(x)                                     */
+    GONN_UN_GELU_EXACT = 7  /* 0.5 x (1 + erf(x / sqrt(2)))                     */
+};
+enum { GONN_BIN_ADD = 0, GONN_BIN_SUB = 1, GONN_BIN_MUL = 2, GONN_BIN_DIV = 3 };
+
+/* C[i] = f_kind(A[i]), i < n; replaces gonn_unary (gonn_cuda.h:39-40): host
+ * fp64 in and out, synchronous, serialised on an internal workspace. An
+ * unknown kind returns GONN_E_INVALID (the Go wrapper then declines).      */
+int gonn_hip_unary_f64(int kind, const double* A, double* C, long n);
+/* C[i] = A[i] op_kind B[i]; replaces gonn_binary (gonn_cuda.h:42-43).      */
+int gonn_hip_binary_f64(int kind, const double* A, const double* B, double* C, long n);
+/* The same on GONN_F64 device buffers (16-byte aligned) on a stream; no
+ * copies, no allocation.                                                   */
+int gonn_hip_unary_f64_dev(int kind, const gonn_buf* A, gonn_buf* C, long n, void* stream);
+int gonn_hip_binary_f64_dev(int kind, const gonn_buf* A, const gonn_buf* B, gonn_buf* C, long n,
+                            void* stream);
+
 /* ---- device buffers ------------------------------------------------------
  * Replace gonn_dev_alloc / gonn_dev_free / gonn_dev_upload / gonn_dev_download
  * (backend/cuda/gonn_cuda.h:77-80) for the attention path. The f64 transfer

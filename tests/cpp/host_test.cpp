@@ -205,6 +205,9 @@ static void test_backend_cpu(Rng& r) {
     be::Use(start);
     CHECK(!nil_seen && be::Current() == start, "Use/Current concurrent");
 
+    // backend_test.go:117-126: the CPU backend is not an Elementwiser.
+    CHECK(dynamic_cast<const be::Elementwiser*>(cpu.get()) == nullptr, "cpu is not an Elementwiser");
+
     if (!gonn::hip::Available()) {
         int code = 0;
         try {
@@ -343,6 +346,50 @@ static void test_backend_gpu() {
         CHECK(close(got, cpu->Gemm(a, b, c.batch, c.m, c.k, c.n, c.ta, c.tb), 1e-10, 0.0,
                     "hip Gemm vs cpu"),
               "hip Gemm %d %d %d %d %d %d", c.batch, c.m, c.k, c.n, c.ta, c.tb);
+    }
+    // Elementwiser: f64 kernels against host libm at 1e-12
+    // (tensor/cuda_dispatch_test.go:48-106); + - * / bit-identical.
+    {
+        auto* ew = dynamic_cast<const be::Elementwiser*>(dev.get());
+        CHECK(ew != nullptr, "hip backend is an Elementwiser");
+        const size_t n = 4099;
+        std::vector<double> x = r.normals(n), y = r.normals(n), out(n);
+        for (double& v : y) v += 3.0;
+        auto host = [](int kind, double v) {
+            switch (kind) {
+                case be::UnaryReLU: return v > 0.0 ? v : 0.0;
+                case be::UnarySigmoid: return 1.0 / (1.0 + std::exp(-v));
+                case be::UnaryTanh: return std::tanh(v);
+                case be::UnaryExp: return std::exp(v);
+                case be::UnaryLog: return std::log(std::fabs(v) + 0.05);
+                case be::UnaryGELU:
+                    return 0.5 * v * (1.0 + std::tanh(std::sqrt(2.0 / M_PI) * (v + 0.044715 * v * v * v)));
+                case be::UnarySiLU: return v / (1.0 + std::exp(-v));
+                default: return 0.5 * v * (1.0 + std::erf(v / std::sqrt(2.0)));
+            }
+        };
+        for (int kind = be::UnaryReLU; kind <= be::UnaryGELUExact; kind++) {
+            std::vector<double> in = x;
+            if (kind == be::UnaryLog)
+                for (double& v : in) v = std::fabs(v) + 0.05;
+            CHECK(ew && ew->Unary((be::UnaryKind)kind, in, out), "Unary %d accepted", kind);
+            std::vector<double> ref(n);
+            for (size_t i = 0; i < n; i++) ref[i] = host(kind, x[i]);
+            CHECK(close(out, ref, 1e-12, 0.0, "hip Unary vs libm"), "Unary %d", kind);
+        }
+        CHECK(ew && !ew->Unary(be::UnaryNone, x, out), "UnaryNone declined");
+        for (int kind = be::BinaryAdd; kind <= be::BinaryDiv; kind++) {
+            CHECK(ew && ew->Binary((be::BinaryKind)kind, x, y, out), "Binary %d accepted", kind);
+            bool same = true;
+            for (size_t i = 0; i < n; i++) {
+                const double ref = kind == be::BinaryAdd ? x[i] + y[i]
+                                   : kind == be::BinarySub ? x[i] - y[i]
+                                   : kind == be::BinaryMul ? x[i] * y[i]
+                                                           : x[i] / y[i];
+                same = same && out[i] == ref;
+            }
+            CHECK(same, "Binary %d bit-identical", kind);
+        }
     }
     const auto z = dev->Gemm(std::vector<double>(0), std::vector<double>(0), 2, 3, 0, 4, false, false);
     CHECK(z.size() == 24 && z == std::vector<double>(24, 0.0), "hip Gemm k=0 gives zeros");

@@ -109,3 +109,75 @@ def test_gemm_entry_checks():
         assert lib.gonn_hip_gemm_f64(p, p, p, 1, 2, 2, 2, 0, 0) == GONN_E_NODEVICE
         with pytest.raises(RuntimeError):
             backend.HIPBackend()
+
+
+def test_kind_values_are_the_abi():
+    # backend/backend.go:26-58 and gonn_cuda.h:13-28: append-only values.
+    import re
+    from gonn_amd import _lib
+    hdr = open(__file__.rsplit("/tests/", 1)[0] + "/include/gonn_hip.h").read()
+    for name, val in re.findall(r"GONN_(UN_\w+|BIN_\w+) = (\d+)", hdr):
+        assert getattr(_lib, "GONN_" + name) == int(val)
+    assert (backend.UnaryReLU, backend.UnaryLog, backend.UnaryGELUExact) == (0, 4, 7)
+    assert (backend.BinaryAdd, backend.BinaryDiv) == (0, 3)
+
+
+def test_cpu_backend_is_not_an_elementwiser():
+    # backend_test.go:117-126: the CPU backend must not implement it.
+    cpu = backend.NewCPU()
+    assert not hasattr(cpu, "Unary") and not hasattr(cpu, "Binary")
+    x = np.ones(1 << 17)
+    out = np.zeros_like(x)
+    prevp = backend.GetDispatchPolicy()
+    backend.SetDispatchPolicy(backend.DispatchPolicy(0, 0))
+    try:
+        assert not backend.dispatch_unary(backend.UnaryExp, x, out)
+        assert not backend.dispatch_binary(backend.BinaryAdd, x, x, out)
+    finally:
+        backend.SetDispatchPolicy(prevp)
+    assert not out.any()
+
+
+def test_dispatch_policy_thresholds():
+    # tensor/dispatch.go:60-109: defaults, UnaryNone never dispatches.
+    calls = []
+
+    class Spy(backend.CPUBackend):
+        def Unary(self, kind, a, out):
+            calls.append(("u", kind, np.size(a)))
+            return True
+
+        def Binary(self, kind, a, b, out):
+            calls.append(("b", kind, np.size(a)))
+            return True
+
+    p = backend.GetDispatchPolicy()
+    assert p.UnaryMinElems == 1 << 16 and p.BinaryMinElems >= 2 ** 62
+    prev = backend.Use(Spy())
+    try:
+        small, big = np.zeros((1 << 16) - 1), np.zeros(1 << 16)
+        assert not backend.dispatch_unary(backend.UnaryTanh, small, small)
+        assert backend.dispatch_unary(backend.UnaryTanh, big, big)
+        assert not backend.dispatch_unary(backend.UnaryNone, big, big)
+        assert not backend.dispatch_binary(backend.BinaryMul, big, big, big)
+    finally:
+        backend.Use(prev)
+    assert calls == [("u", backend.UnaryTanh, 1 << 16)]
+
+
+def test_elementwise_entry_checks():
+    lib = _lib.load()
+    dp = ctypes.POINTER(ctypes.c_double)
+    x = np.zeros(8)
+    p = x.ctypes.data_as(dp)
+    assert lib.gonn_hip_unary_f64(8, p, p, 8) == GONN_E_INVALID
+    assert lib.gonn_hip_unary_f64(-1, p, p, 8) == GONN_E_INVALID
+    assert lib.gonn_hip_binary_f64(4, p, p, p, 8) == GONN_E_INVALID
+    assert lib.gonn_hip_unary_f64(0, p, p, -1) == GONN_E_INVALID
+    assert lib.gonn_hip_unary_f64(0, None, None, 0) == 0
+    assert lib.gonn_hip_binary_f64(0, None, p, p, 8) == GONN_E_INVALID
+    b = _lib.Buf(0, 0, _lib.GONN_F32)
+    assert lib.gonn_hip_unary_f64_dev(0, ctypes.byref(b), ctypes.byref(b), 4, None) == GONN_E_INVALID
+    if not hip.Available():
+        assert lib.gonn_hip_unary_f64(0, p, p, 8) == GONN_E_NODEVICE
+        assert lib.gonn_hip_binary_f64(0, p, p, p, 8) == GONN_E_NODEVICE
