@@ -11,6 +11,10 @@ GB/s, 1 MI355X".
              convention, benchmark/flashattn/main.go:138-142).
   decode     config C4: B=64 H=32 D=128, bf16 cache of 8192 positions,
              lengths ~ U[512, 8192]; bytes per step = valid K+V rows + q + o.
+  mha        config C1: nn.MultiHeadAttention forward, B=2 S=128 E=256 H=4,
+             causal, fp64 host data: projections on the host with the fused
+             core, the resident layer (weights in HBM; one upload and one
+             download per call), and the resident layer on device buffers.
   roofline   the dominant kernel of each workload, timed live with HIP events
              recorded by the library on the stream the kernel runs on.
   cpu_baseline  the fp64 oracle (a C restatement of GoNN's CPU attention op
@@ -207,6 +211,50 @@ def bench_encoder(torch, hip, steps, warmup, mode):
                 pack_ms=per["pack_kv"], launches=nl[kname])
 
 
+def bench_mha(torch, hip, steps, warmup):
+    """C1: MHA forward, three routes, ms per forward."""
+    import numpy as np
+    from gonn_amd import nn
+    B, S, E, H = 2, 128, 256, 4
+    rng = np.random.default_rng(20)
+    s = 1.0 / math.sqrt(E)
+    W = [rng.standard_normal((E, E)) * s for _ in range(4)]
+    b = [rng.standard_normal(E) * s for _ in range(4)]
+    x = rng.standard_normal((B, S, E)) * s
+    mha = nn.MultiHeadAttention(E, H, W[0], b[0], W[1], b[1], W[2], b[2], W[3], b[3])
+    hip.SetAttnMode("fp32")
+
+    def wall(fn):
+        for _ in range(warmup):
+            fn()
+        t = []
+        for _ in range(steps):
+            t0 = time.perf_counter()
+            fn()
+            t.append((time.perf_counter() - t0) * 1e3)
+        return statistics.mean(t), statistics.median(t)
+
+    host = wall(lambda: mha.forward_fused(x, x, x, True))
+    res = mha.to_device()
+    resident = wall(lambda: res.forward(x, x, x, True))
+    xd = torch.from_numpy(x).cuda()
+    ws = torch.empty(res.dev.workspace_bytes(B, S, S), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(xd)
+    run = lambda: res.dev.forward_dev(xd, xd, xd, out=out, causal=True, ws=ws)  # noqa: E731
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    dev_ms, dev_med, _ = _run_steps(torch, run, steps)
+    res.close()
+    r = lambda v: round(v, 4)  # noqa: E731
+    return {"config": {"workload": "C1 MHA forward, fp64 host data, fp32-MFMA core",
+                       "B": B, "S": S, "E": E, "H": H, "causal": True},
+            "unit": "ms per forward",
+            "host_projections_fused_core": {"ms": r(host[0]), "median_ms": r(host[1])},
+            "resident_host_data": {"ms": r(resident[0]), "median_ms": r(resident[1])},
+            "resident_device_buffers": {"ms": r(dev_ms), "median_ms": r(dev_med)}}
+
+
 def cpu_baseline(pre, seconds):
     """Time the fp64 oracle on whole (b,h) slices of the prefill workload."""
     import numpy as np
@@ -245,6 +293,7 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-bwd", action="store_true")
     ap.add_argument("--no-encoder", action="store_true")
+    ap.add_argument("--no-mha", action="store_true")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the headline leg (profiling runs of the other legs only)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -372,6 +421,9 @@ def main():
                              "kernel_ms": round(en["kernel_ms"], 5),
                              "launches_per_step": en["launches"],
                              "pack_kv_ms": round(en["pack_ms"], 5)}}
+    if not args.no_mha:
+        log("[bench] MHA C1")
+        line["mha"] = bench_mha(torch, hip, args.steps, args.warmup)
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
         line["cpu_baseline"] = cpu_baseline(pre, args.cpu_seconds)

@@ -46,6 +46,8 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_kvcache_attend", "gonn_hip_kvcache_attend_f64", "gonn_hip_flash_attn_f64_ex",
     "gonn_hip_gemm_f64", "gonn_hip_gemm_f64_dev",
     "gonn_hip_unary_f64", "gonn_hip_binary_f64", "gonn_hip_unary_f64_dev", "gonn_hip_binary_f64_dev",
+    "gonn_hip_mha_create", "gonn_hip_mha_free", "gonn_hip_mha_forward_f64",
+    "gonn_hip_mha_workspace_bytes", "gonn_hip_mha_forward_dev",
 )
 
 
@@ -147,6 +149,12 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_unary_f64_dev.argtypes = [i, ctypes.POINTER(Buf), ctypes.POINTER(Buf), lg, vp]
     lib.gonn_hip_binary_f64_dev.argtypes = [i, ctypes.POINTER(Buf), ctypes.POINTER(Buf),
                                             ctypes.POINTER(Buf), lg, vp]
+    lib.gonn_hip_mha_create.argtypes = [ctypes.POINTER(vp), i, i, i, i] + [dp] * 8
+    lib.gonn_hip_mha_free.argtypes = [vp]
+    lib.gonn_hip_mha_forward_f64.argtypes = [vp, dp, dp, dp, dp, i, i, i, i, ip]
+    lib.gonn_hip_mha_workspace_bytes.argtypes = [vp, i, i, i]
+    lib.gonn_hip_mha_workspace_bytes.restype = ctypes.c_size_t
+    lib.gonn_hip_mha_forward_dev.argtypes = [vp] + [ctypes.POINTER(Buf)] * 4 + [i, i, i, i, ctypes.POINTER(Buf), vp, ctypes.c_size_t, vp]
     _lib = lib
     return lib
 

@@ -227,6 +227,8 @@ def _dtype_code(t):
         return GONN_BF16
     if t.dtype == torch.int32:
         return GONN_I32
+    if t.dtype == torch.float64:
+        return _lib.GONN_F64
     raise TypeError(f"unsupported tensor dtype {t.dtype}")
 
 
@@ -461,8 +463,109 @@ class KVCache:
         return out
 
 
+class DeviceMHA:
+    """Device-resident multi-head attention (gonn_hip_mha_*): the forward of
+    nn.MultiHeadAttention (nn/attention.go:107-148) with its four projections'
+    weights in HBM. forward() takes host fp64 (B, T, *) arrays and makes one
+    upload and one download per call; forward_dev() runs on torch float64
+    device tensors with a caller workspace and allocates nothing.
+    New relative to the reference, whose CUDA path copies across PCIe around
+    every GEMM and around the fused core."""
+
+    def __init__(self, E: int, H: int, Wq, bq, Wk, bk, Wv, bv, Wo, bo):
+        E, H = int(E), int(H)
+        Wq, Wo = _f64(Wq, E * E, "DeviceMHA Wq"), _f64(Wo, E * E, "DeviceMHA Wo")
+        Wk = np.ascontiguousarray(Wk, dtype=np.float64)
+        Wv = np.ascontiguousarray(Wv, dtype=np.float64)
+        if Wk.ndim != 2 or Wk.shape[0] != E or Wv.ndim != 2 or Wv.shape[0] != E:
+            raise ValueError("DeviceMHA: Wk and Wv must be (E, in)")
+        self.E, self.H, self.kdim, self.vdim = E, H, int(Wk.shape[1]), int(Wv.shape[1])
+        bs = [None if b is None else _f64(b, E, "DeviceMHA bias") for b in (bq, bk, bv, bo)]
+        self._keep = (Wq, Wk, Wv, Wo, bs)
+        self._h = ctypes.c_void_p()
+        bp = [_p(b) if b is not None else None for b in bs]
+        check(_lib.load().gonn_hip_mha_create(ctypes.byref(self._h), E, H, self.kdim, self.vdim,
+                                              _p(Wq), bp[0], _p(Wk), bp[1], _p(Wv), bp[2],
+                                              _p(Wo), bp[3]), "DeviceMHA")
+        self._keep = None
+
+    def close(self) -> None:
+        if self._h:
+            check(_lib.load().gonn_hip_mha_free(self._h), "DeviceMHA.close")
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _live(self):
+        if not self._h:
+            raise ValueError("DeviceMHA: closed")
+        return self._h
+
+    def _shapes(self, q, k, v):
+        if q.ndim != 3 or q.shape[2] != self.E or k.ndim != 3 or k.shape[2] != self.kdim or \
+                v.ndim != 3 or v.shape[2] != self.vdim or k.shape[:2] != v.shape[:2] or \
+                k.shape[0] != q.shape[0]:
+            raise ValueError(f"DeviceMHA: shapes q {tuple(q.shape)} k {tuple(k.shape)} "
+                             f"v {tuple(v.shape)}")
+        return q.shape[0], q.shape[1], k.shape[1]
+
+    def forward(self, q, k, v, causal: bool = False, kv_len=None) -> np.ndarray:
+        same_k, same_v = k is q, v is k
+        q = np.ascontiguousarray(q, dtype=np.float64)
+        k = q if same_k else np.ascontiguousarray(k, dtype=np.float64)
+        v = k if same_v else np.ascontiguousarray(v, dtype=np.float64)
+        B, Tq, Tk = self._shapes(q, k, v)
+        out = np.empty((B, Tq, self.E))
+        kl = None
+        if kv_len is not None:
+            kl = np.ascontiguousarray(kv_len, dtype=np.int32)
+            if kl.shape != (B,):
+                raise ValueError(f"DeviceMHA: kv_len must have {B} entries")
+        check(_lib.load().gonn_hip_mha_forward_f64(
+            self._live(), _p(q), _p(k), _p(v), _p(out), B, Tq, Tk, int(bool(causal)),
+            kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None),
+            "DeviceMHA.forward")
+        return out
+
+    def workspace_bytes(self, B: int, Tq: int, Tk: int) -> int:
+        return int(_lib.load().gonn_hip_mha_workspace_bytes(self._live(), B, Tq, Tk))
+
+    def forward_dev(self, q, k, v, out=None, causal: bool = False, kv_len=None, ws=None):
+        """q, k, v: contiguous torch float64 CUDA tensors; kv_len: int32 CUDA
+        tensor or None; ws: a uint8 CUDA tensor of workspace_bytes() or None
+        (then one is allocated by torch); runs on torch's current stream."""
+        import torch
+        B, Tq, Tk = self._shapes(q, k, v)
+        for t in (q, k, v):
+            if t.dtype != torch.float64 or not t.is_cuda or not t.is_contiguous():
+                raise ValueError("DeviceMHA.forward_dev: inputs must be contiguous float64 CUDA tensors")
+        if out is None:
+            out = torch.empty((B, Tq, self.E), dtype=torch.float64, device=q.device)
+        need = self.workspace_bytes(B, Tq, Tk)
+        if ws is None:
+            ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        kb = buf(kv_len) if kv_len is not None else None
+        st = ctypes.c_void_p(torch.cuda.current_stream(q.device).cuda_stream)
+        check(_lib.load().gonn_hip_mha_forward_dev(
+            self._live(), ctypes.byref(buf(q)), ctypes.byref(buf(k)), ctypes.byref(buf(v)),
+            ctypes.byref(buf(out)), B, Tq, Tk, int(bool(causal)),
+            ctypes.byref(kb) if kb is not None else None, ctypes.c_void_p(ws.data_ptr()),
+            ws.numel(), st), "DeviceMHA.forward_dev")
+        return out
+
+
 __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
            "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex", "Gemm",
            "Unary", "Binary",
-           "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "buf",
+           "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "DeviceMHA", "buf",
            "GonnHipError"]

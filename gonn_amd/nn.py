@@ -87,6 +87,27 @@ class Linear:
         return y.reshape(*x.shape[:-1], out)
 
 
+def _kv_len_from_mask(key_padding_mask, B: int, Tk: int):
+    """kv_len[b] of a (B, Tk) key-padding mask (nonzero = ignore the key,
+    keyPaddingMaskAdd, nn/attention.go:261-272) whose padded keys are a
+    suffix of each row; None for no mask."""
+    if key_padding_mask is None:
+        return None
+    m = np.asarray(key_padding_mask)
+    if m.shape != (B, Tk):
+        raise ValueError(f"MultiHeadAttention: key padding mask shape {m.shape}, "
+                         f"want (B, Tk) = ({B}, {Tk})")
+    kv_len = np.empty(B, dtype=np.int32)
+    for b in range(B):
+        nz = np.nonzero(m[b])[0]
+        n = int(nz[0]) if nz.size else Tk
+        if np.any(m[b, n:] == 0):
+            raise ValueError("nn: the fused core takes key padding masks whose padded "
+                             "keys are a suffix of the row")
+        kv_len[b] = n
+    return kv_len
+
+
 class MultiHeadAttention:
     """Forward-path mirror of nn.MultiHeadAttention with the fused core.
 
@@ -163,22 +184,15 @@ class MultiHeadAttention:
         self._check(q, k, v)
         if not fused_attn_available():
             raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
-        kv_len = None
-        if key_padding_mask is not None:
-            m = np.asarray(key_padding_mask)
-            B, Tk = q.shape[0], k.shape[1]
-            if m.shape != (B, Tk):
-                raise ValueError(f"MultiHeadAttention: key padding mask shape {m.shape}, "
-                                 f"want (B, Tk) = ({B}, {Tk})")
-            kv_len = np.empty(B, dtype=np.int32)
-            for b in range(B):
-                nz = np.nonzero(m[b])[0]
-                n = int(nz[0]) if nz.size else Tk
-                if np.any(m[b, n:] == 0):
-                    raise ValueError("nn: the fused core takes key padding masks whose padded "
-                                     "keys are a suffix of the row")
-                kv_len[b] = n
+        kv_len = _kv_len_from_mask(key_padding_mask, q.shape[0], k.shape[1])
         return self._fused(q, k, v, causal, kv_len)
+
+    # ---- device-resident forward (new: weights and intermediates in HBM) ----
+    def to_device(self) -> "ResidentMultiHeadAttention":
+        """This layer with its weights uploaded once: forward / forward_masked
+        then run projections, core and output projection on the device with
+        one upload and one download per call (gonn_hip_mha_*)."""
+        return ResidentMultiHeadAttention(self)
 
     # ---- incremental decoding (new: the reference has no KV cache) ----
     def new_cache(self, batch: int, max_len: int) -> "hip.KVCache":
@@ -218,3 +232,46 @@ def attn_decode(q, kcache, vcache, kv_len, scale=None, split_keys: int = 0):
     """KV-cache decode on device tensors: ForwardMasked with a key-padding mask
     pad[b][t] = (t >= kv_len[b]) on the post-projection core."""
     return hip.attn_decode(q, kcache, vcache, kv_len, scale=scale, split_keys=split_keys)
+
+
+class ResidentMultiHeadAttention:
+    """MultiHeadAttention.forward / forward_masked on a hip.DeviceMHA: the
+    same results as the host-projection path (same fp64 GEMM order up to
+    rounding of the library GEMM, the same fused core), with the weights and
+    every intermediate in HBM."""
+
+    def __init__(self, mha: MultiHeadAttention):
+        if not fused_attn_available():
+            raise RuntimeError("nn: the resident MHA requires the HIP library and a gfx950 device")
+        self._mha = mha
+        L = (mha.QProj, mha.KProj, mha.VProj, mha.OutProj)
+        self.dev = hip.DeviceMHA(mha.EmbedDim, mha.NumHeads, *[x for l in L for x in (l.W, l.b)])
+
+    def close(self) -> None:
+        self.dev.close()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def forward(self, q, k, v, causal: bool = False):
+        same_k, same_v = k is q, v is k
+        q = np.asarray(q, dtype=np.float64)
+        k = q if same_k else np.asarray(k, dtype=np.float64)
+        v = k if same_v else np.asarray(v, dtype=np.float64)
+        self._mha._check(q, k, v)
+        return self.dev.forward(q, k, v, causal)
+
+    def forward_masked(self, q, k, v, causal: bool = False, key_padding_mask=None,
+                       attn_mask=None, dropout: float = 0.0):
+        if attn_mask is not None or dropout:
+            raise ValueError("nn: the fused core takes no additive attn mask or dropout")
+        same_k, same_v = k is q, v is k
+        q = np.asarray(q, dtype=np.float64)
+        k = q if same_k else np.asarray(k, dtype=np.float64)
+        v = k if same_v else np.asarray(v, dtype=np.float64)
+        self._mha._check(q, k, v)
+        kv_len = _kv_len_from_mask(key_padding_mask, q.shape[0], k.shape[1])
+        return self.dev.forward(q, k, v, causal, kv_len)

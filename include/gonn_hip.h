@@ -246,6 +246,34 @@ int gonn_hip_unary_f64_dev(int kind, const gonn_buf* A, gonn_buf* C, long n, voi
 int gonn_hip_binary_f64_dev(int kind, const gonn_buf* A, const gonn_buf* B, gonn_buf* C, long n,
                             void* stream);
 
+/* ---- device-resident multi-head attention -------------------------------
+ * nn.MultiHeadAttention's forward (nn/attention.go:107-148) with its weights
+ * in HBM: projections (rocBLAS fp64), head split into fp32 (B, H, T, dp),
+ * the fused core in the current MFMA mode with scale 1/sqrt(E/H), head merge,
+ * output projection. New: the reference copies across PCIe around every GEMM
+ * (tensor/dispatch.go:111-113) and around the core (gonn_cuda.cu:466-529).
+ * Weights W* are (E, in) row-major fp64 with in = E (q, out), kdim (k), vdim
+ * (v); a null bias is zero. E % H == 0 and E/H <= 128.                      */
+typedef struct gonn_mha gonn_mha;
+int gonn_hip_mha_create(gonn_mha** out, int E, int H, int kdim, int vdim, const double* Wq,
+                        const double* bq, const double* Wk, const double* bk, const double* Wv,
+                        const double* bv, const double* Wo, const double* bo);
+int gonn_hip_mha_free(gonn_mha* m);
+/* q (B, Tq, E), k (B, Tk, kdim), v (B, Tk, vdim) host fp64 -> out (B, Tq, E).
+ * kv_len: optional host int32[B], keys t >= kv_len[b] ignored (ForwardMasked
+ * key padding, nn/attention.go:261-272); causal is top-left (j > i masked).
+ * Synchronous; one upload of the inputs (once when k == q and v == k), one
+ * download. Calls on one handle are serialised on its workspace.            */
+int gonn_hip_mha_forward_f64(gonn_mha* m, const double* q, const double* k, const double* v,
+                             double* out, int B, int Tq, int Tk, int causal, const int* kv_len);
+/* The same on GONN_F64 device buffers (kv_len: GONN_I32 device buffer or
+ * null) with a caller workspace of gonn_hip_mha_workspace_bytes bytes, on
+ * `stream`; allocates nothing. Calls that share a workspace must not overlap. */
+size_t gonn_hip_mha_workspace_bytes(const gonn_mha* m, int B, int Tq, int Tk);
+int gonn_hip_mha_forward_dev(gonn_mha* m, const gonn_buf* q, const gonn_buf* k, const gonn_buf* v,
+                             gonn_buf* out, int B, int Tq, int Tk, int causal,
+                             const gonn_buf* kv_len, void* ws, size_t ws_bytes, void* stream);
+
 /* ---- device buffers ------------------------------------------------------
  * Replace gonn_dev_alloc / gonn_dev_free / gonn_dev_upload / gonn_dev_download
  * (backend/cuda/gonn_cuda.h:77-80) for the attention path. The f64 transfer

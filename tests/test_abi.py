@@ -272,3 +272,23 @@ def test_kvcache_argument_and_device_checks():
         with pytest.raises(hip.GonnHipError) as ei:
             hip.KVCache(1, 1, 8, 64)
         assert ei.value.code == GONN_E_NODEVICE
+
+
+def test_mha_handle_argument_checks():
+    import ctypes
+    from gonn_amd import hip
+    lib = _lib.load()
+    h = ctypes.c_void_p()
+    dp = ctypes.POINTER(ctypes.c_double)
+    w = np.zeros(64 * 64)
+    p = w.ctypes.data_as(dp)
+    assert lib.gonn_hip_mha_create(None, 64, 4, 64, 64, p, None, p, None, p, None, p, None) == _lib.GONN_E_INVALID
+    assert lib.gonn_hip_mha_create(ctypes.byref(h), 66, 4, 64, 64, p, None, p, None, p, None, p, None) == _lib.GONN_E_INVALID
+    assert lib.gonn_hip_mha_create(ctypes.byref(h), 64, 4, 64, 64, None, None, p, None, p, None, p, None) == _lib.GONN_E_INVALID
+    assert lib.gonn_hip_mha_create(ctypes.byref(h), 512, 2, 64, 64, p, None, p, None, p, None, p, None) == _lib.GONN_E_UNSUPPORTED
+    assert lib.gonn_hip_mha_free(None) == 0
+    assert lib.gonn_hip_mha_workspace_bytes(None, 1, 1, 1) == 0
+    assert lib.gonn_hip_mha_forward_f64(None, p, p, p, p, 1, 1, 1, 0, None) == _lib.GONN_E_INVALID
+    if not hip.Available():
+        assert lib.gonn_hip_mha_create(ctypes.byref(h), 64, 4, 64, 64, p, None, p, None, p, None, p, None) == _lib.GONN_E_NODEVICE
+        assert not h.value
