@@ -118,6 +118,36 @@ class KVCache {
     int B_, H_, Lmax_, D_;
 };
 
+// Device-resident multi-head attention (gonn_hip_mha_*): the forward of
+// nn.MultiHeadAttention (nn/attention.go:107-148) with the four projections'
+// weights in HBM. New: the reference copies across PCIe around every GEMM
+// and around the fused core. W* are (E, in) row-major; an empty bias is
+// zero. Move-only; frees its device memory on destruction.
+class DeviceMHA {
+  public:
+    DeviceMHA(int E, int H, int kdim, int vdim, const std::vector<double>& Wq,
+              const std::vector<double>& bq, const std::vector<double>& Wk,
+              const std::vector<double>& bk, const std::vector<double>& Wv,
+              const std::vector<double>& bv, const std::vector<double>& Wo,
+              const std::vector<double>& bo);
+    ~DeviceMHA();
+    DeviceMHA(DeviceMHA&& o) noexcept;
+    DeviceMHA& operator=(DeviceMHA&& o) noexcept;
+    DeviceMHA(const DeviceMHA&) = delete;
+    DeviceMHA& operator=(const DeviceMHA&) = delete;
+
+    // q (B,Tq,E), k (B,Tk,kdim), v (B,Tk,vdim) flat fp64 -> (B,Tq,E); kvLen
+    // (B entries or empty): keys t >= kvLen[b] are ignored. One upload (once
+    // for self-attention, when k and v are q itself) and one download.
+    std::vector<double> Forward(const std::vector<double>& q, const std::vector<double>& k,
+                                const std::vector<double>& v, int B, int Tq, int Tk, bool causal,
+                                const std::vector<int>& kvLen = {}) const;
+
+  private:
+    void* h_ = nullptr;
+    int E_, H_, kdim_, vdim_;
+};
+
 }  // namespace hip
 
 namespace backend {
@@ -258,11 +288,31 @@ class MultiHeadAttention {
     // of Forward(seq, seq, seq, causal=true) over the whole sequence.
     Tensor ForwardIncremental(const Tensor& x, hip::KVCache& cache);
 
+    // This layer with its weights uploaded once (new): Forward / ForwardMasked
+    // of the result run projections, core and output projection on the
+    // device with one upload and one download per call.
+    class ResidentMultiHeadAttention ToDevice() const;
+
   private:
+    friend class ResidentMultiHeadAttention;
     void checkQKVDims(const Tensor& q, const Tensor& k, const Tensor& v) const;
     void requireFused(int D, int Tq, int Tk) const;
     Tensor fusedGeneral(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
                         const std::vector<int>& kvLen);
+};
+
+// MultiHeadAttention::Forward / ForwardMasked on a hip::DeviceMHA; the same
+// shape checks and mask rules as the host-projection path.
+class ResidentMultiHeadAttention {
+  public:
+    explicit ResidentMultiHeadAttention(const MultiHeadAttention& m);
+    Tensor Forward(const Tensor& q, const Tensor& k, const Tensor& v, bool causal) const;
+    Tensor ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
+                         const Tensor& keyPad) const;
+
+  private:
+    MultiHeadAttention layer_;
+    hip::DeviceMHA dev_;
 };
 
 }  // namespace nn

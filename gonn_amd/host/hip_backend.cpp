@@ -189,5 +189,72 @@ void KVCache::Reset() {
     check(gonn_hip_kvcache_reset((gonn_kvcache*)h_), "KVCache.Reset");
 }
 
+DeviceMHA::DeviceMHA(int E, int H, int kdim, int vdim, const std::vector<double>& Wq,
+                     const std::vector<double>& bq, const std::vector<double>& Wk,
+                     const std::vector<double>& bk, const std::vector<double>& Wv,
+                     const std::vector<double>& bv, const std::vector<double>& Wo,
+                     const std::vector<double>& bo)
+    : E_(E), H_(H), kdim_(kdim), vdim_(vdim) {
+    if (E <= 0 || H <= 0 || kdim <= 0 || vdim <= 0)
+        throw std::invalid_argument("hip: DeviceMHA: dimensions must be >= 1");
+    need(Wq, (size_t)E * E, "DeviceMHA Wq");
+    need(Wk, (size_t)E * kdim, "DeviceMHA Wk");
+    need(Wv, (size_t)E * vdim, "DeviceMHA Wv");
+    need(Wo, (size_t)E * E, "DeviceMHA Wo");
+    const std::vector<double>* bs[4] = {&bq, &bk, &bv, &bo};
+    for (const auto* b : bs)
+        if (!b->empty()) need(*b, (size_t)E, "DeviceMHA bias");
+    auto bp = [](const std::vector<double>& b) { return b.empty() ? nullptr : b.data(); };
+    gonn_mha* m = nullptr;
+    check(gonn_hip_mha_create(&m, E, H, kdim, vdim, Wq.data(), bp(bq), Wk.data(), bp(bk),
+                              Wv.data(), bp(bv), Wo.data(), bp(bo)),
+          "DeviceMHA");
+    h_ = m;
+}
+
+DeviceMHA::~DeviceMHA() {
+    if (h_) (void)gonn_hip_mha_free((gonn_mha*)h_);
+}
+
+DeviceMHA::DeviceMHA(DeviceMHA&& o) noexcept
+    : h_(o.h_), E_(o.E_), H_(o.H_), kdim_(o.kdim_), vdim_(o.vdim_) {
+    o.h_ = nullptr;
+}
+
+DeviceMHA& DeviceMHA::operator=(DeviceMHA&& o) noexcept {
+    if (this != &o) {
+        if (h_) (void)gonn_hip_mha_free((gonn_mha*)h_);
+        h_ = o.h_;
+        E_ = o.E_;
+        H_ = o.H_;
+        kdim_ = o.kdim_;
+        vdim_ = o.vdim_;
+        o.h_ = nullptr;
+    }
+    return *this;
+}
+
+std::vector<double> DeviceMHA::Forward(const std::vector<double>& q, const std::vector<double>& k,
+                                       const std::vector<double>& v, int B, int Tq, int Tk,
+                                       bool causal, const std::vector<int>& kvLen) const {
+    if (!h_) throw std::invalid_argument("hip: DeviceMHA: moved-from handle");
+    if (B <= 0 || Tq <= 0 || Tk <= 0)
+        throw std::invalid_argument("hip: DeviceMHA.Forward: B, Tq, Tk must be >= 1");
+    need(q, (size_t)B * Tq * E_, "DeviceMHA.Forward q");
+    need(k, (size_t)B * Tk * kdim_, "DeviceMHA.Forward k");
+    need(v, (size_t)B * Tk * vdim_, "DeviceMHA.Forward v");
+    if (!kvLen.empty() && (int)kvLen.size() != B)
+        throw std::invalid_argument("hip: DeviceMHA.Forward: kvLen needs B entries");
+    std::vector<double> out((size_t)B * Tq * E_);
+    // Pass the same pointer for k (v) when it is the same vector as q (k), so
+    // the library uploads it once.
+    const double* kp = &k == &q ? q.data() : k.data();
+    const double* vp = &v == &k ? kp : v.data();
+    check(gonn_hip_mha_forward_f64((gonn_mha*)h_, q.data(), kp, vp, out.data(), B, Tq, Tk,
+                                   causal ? 1 : 0, kvLen.empty() ? nullptr : kvLen.data()),
+          "DeviceMHA.Forward");
+    return out;
+}
+
 }  // namespace hip
 }  // namespace gonn

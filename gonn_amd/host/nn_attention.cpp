@@ -195,34 +195,40 @@ Tensor MultiHeadAttention::fusedGeneral(const Tensor& q, const Tensor& k, const 
     return OutProj.Forward(ctx);
 }
 
+// kvLen[b] of a (B, Tk) key-padding mask (nonzero = ignore the key) whose
+// padded keys are a suffix of each row; empty for no mask.
+static std::vector<int> kv_len_from_mask(const Tensor& keyPad, int B, int Tk) {
+    std::vector<int> kvLen;
+    if (keyPad.Data.empty()) return kvLen;
+    // keyPaddingMaskAdd's shape check, nn/attention.go:262-264
+    if (keyPad.Shape.size() != 2 || keyPad.Shape[0] != B || keyPad.Shape[1] != Tk)
+        throw std::invalid_argument("MultiHeadAttention: key padding mask shape " +
+                                    shape_str(keyPad.Shape) + ", want (B, Tk) = (" +
+                                    std::to_string(B) + ", " + std::to_string(Tk) + ")");
+    kvLen.assign(B, Tk);
+    for (int b = 0; b < B; b++) {
+        const double* row = &keyPad.Data[(size_t)b * Tk];
+        int n = Tk;
+        for (int t = 0; t < Tk; t++)
+            if (row[t] != 0) {
+                n = t;
+                break;
+            }
+        for (int t = n; t < Tk; t++)
+            if (row[t] == 0)
+                throw std::invalid_argument(
+                    "nn: the fused core takes key padding masks whose padded keys are a "
+                    "suffix of the row");
+        kvLen[b] = n;
+    }
+    return kvLen;
+}
+
 Tensor MultiHeadAttention::ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v,
                                          bool causal, const Tensor& keyPad) {
     checkQKVDims(q, k, v);
     const int B = q.Shape[0], Tk = k.Shape[1];
-    std::vector<int> kvLen;
-    if (!keyPad.Data.empty()) {
-        // keyPaddingMaskAdd's shape check, nn/attention.go:262-264
-        if (keyPad.Shape.size() != 2 || keyPad.Shape[0] != B || keyPad.Shape[1] != Tk)
-            throw std::invalid_argument("MultiHeadAttention: key padding mask shape " +
-                                        shape_str(keyPad.Shape) + ", want (B, Tk) = (" +
-                                        std::to_string(B) + ", " + std::to_string(Tk) + ")");
-        kvLen.assign(B, Tk);
-        for (int b = 0; b < B; b++) {
-            const double* row = &keyPad.Data[(size_t)b * Tk];
-            int n = Tk;
-            for (int t = 0; t < Tk; t++)
-                if (row[t] != 0) {
-                    n = t;
-                    break;
-                }
-            for (int t = n; t < Tk; t++)
-                if (row[t] == 0)
-                    throw std::invalid_argument(
-                        "nn: the fused core takes key padding masks whose padded keys are a "
-                        "suffix of the row");
-            kvLen[b] = n;
-        }
-    }
+    const std::vector<int> kvLen = kv_len_from_mask(keyPad, B, Tk);
     return fusedGeneral(q, k, v, causal, kvLen);
 }
 
@@ -274,6 +280,36 @@ Tensor MultiHeadAttention::ForwardIncremental(const Tensor& x, hip::KVCache& cac
     }
     const Tensor merged = Tensor::New(std::move(ctx), {B, H, T, D}).Permute0213().Reshape({B, T, EmbedDim});
     return OutProj.Forward(merged);
+}
+
+ResidentMultiHeadAttention MultiHeadAttention::ToDevice() const {
+    return ResidentMultiHeadAttention(*this);
+}
+
+ResidentMultiHeadAttention::ResidentMultiHeadAttention(const MultiHeadAttention& m)
+    : layer_(m),
+      dev_(m.EmbedDim, m.NumHeads, m.KDim, m.VDim, m.QProj.W.Data, m.QProj.B, m.KProj.W.Data,
+           m.KProj.B, m.VProj.W.Data, m.VProj.B, m.OutProj.W.Data, m.OutProj.B) {}
+
+Tensor ResidentMultiHeadAttention::Forward(const Tensor& q, const Tensor& k, const Tensor& v,
+                                           bool causal) const {
+    layer_.checkQKVDims(q, k, v);
+    const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1];
+    const std::vector<double>& kd = &k == &q ? q.Data : k.Data;
+    const std::vector<double>& vd = &v == &k ? kd : v.Data;
+    return Tensor::New(dev_.Forward(q.Data, kd, vd, B, Tq, Tk, causal), {B, Tq, layer_.EmbedDim});
+}
+
+Tensor ResidentMultiHeadAttention::ForwardMasked(const Tensor& q, const Tensor& k,
+                                                 const Tensor& v, bool causal,
+                                                 const Tensor& keyPad) const {
+    layer_.checkQKVDims(q, k, v);
+    const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1];
+    const std::vector<int> kvLen = kv_len_from_mask(keyPad, B, Tk);
+    const std::vector<double>& kd = &k == &q ? q.Data : k.Data;
+    const std::vector<double>& vd = &v == &k ? kd : v.Data;
+    return Tensor::New(dev_.Forward(q.Data, kd, vd, B, Tq, Tk, causal, kvLen),
+                       {B, Tq, layer_.EmbedDim});
 }
 
 }  // namespace nn

@@ -216,6 +216,19 @@ static void test_backend_cpu(Rng& r) {
             code = e.code;
         }
         CHECK(code == GONN_E_NODEVICE, "NewHIP without device: code %d", code);
+        code = 0;
+        std::vector<double> w(64 * 64, 0.0);
+        try {
+            gonn::hip::DeviceMHA dm(64, 4, 64, 64, w, {}, w, {}, w, {}, w, {});
+        } catch (const gonn::hip::Error& e) {
+            code = e.code;
+        }
+        CHECK(code == GONN_E_NODEVICE, "DeviceMHA without device: code %d", code);
+    }
+    {
+        std::vector<double> w(64 * 64, 0.0), shortw(10, 0.0);
+        CHECK(throws_invalid([&] { gonn::hip::DeviceMHA(64, 4, 64, 64, w, {}, shortw, {}, w, {}, w, {}); }),
+              "DeviceMHA short Wk");
     }
 }
 
@@ -416,6 +429,54 @@ static void test_backend_gpu() {
           "MHA HIP backend vs CPU backend");
 }
 
+// The resident layer (weights in HBM) against the oracle and against the
+// host-projection path with its projections on the HIP backend.
+static void test_resident_gpu() {
+    namespace be = gonn::backend;
+    Rng r(91);
+    const int B = 2, T = 128, E = 256, H = 4;
+    const double ws = 1.0 / std::sqrt((double)E);
+    auto lin = [&](int in) {
+        Linear l;
+        l.W = Tensor::New(r.normals((size_t)E * in, 1.0 / std::sqrt((double)in)), {E, in});
+        l.B = r.normals(E, ws);
+        return l;
+    };
+    gonn::hip::SetMode(0);
+    {
+        MultiHeadAttention m(E, H, lin(E), lin(E), lin(E), lin(E));
+        Tensor x = Tensor::New(r.normals((size_t)B * T * E, ws), {B, T, E});
+        auto res = m.ToDevice();
+        const Tensor y = res.Forward(x, x, x, true);
+        CHECK(y.Shape == std::vector<int>({B, T, E}), "resident shape");
+        CHECK(close(y.Data, oracle_mha(m, x, x, x, true), 1e-4, 0.0, "resident C1 vs oracle"),
+              "resident C1 vs oracle");
+        auto prev = be::Use(be::NewHIP());
+        const Tensor hostp = m.ForwardFused(x, x, x, true);
+        be::Use(prev);
+        CHECK(close(y.Data, hostp.Data, 1e-12, 0.0, "resident == HIP-backend projections"),
+              "resident == host-projection path");
+    }
+    {
+        const int Tq = 40, Tk = 90, kdim = 96, vdim = 160;
+        MultiHeadAttention m(E, H, lin(E), lin(kdim), lin(vdim), lin(E));
+        Tensor q = Tensor::New(r.normals((size_t)B * Tq * E, ws), {B, Tq, E});
+        Tensor k = Tensor::New(r.normals((size_t)B * Tk * kdim, ws), {B, Tk, kdim});
+        Tensor v = Tensor::New(r.normals((size_t)B * Tk * vdim, ws), {B, Tk, vdim});
+        Tensor pad = Tensor::Zeros({B, Tk});
+        for (int t = 33; t < Tk; t++) pad.Data[Tk + t] = 1.0;  // sequence 1 keeps 33 keys
+        auto res = m.ToDevice();
+        const Tensor ym = res.ForwardMasked(q, k, v, true, pad);
+        CHECK(close(ym.Data, oracle_mha(m, q, k, v, true, {Tk, 33}), 1e-4, 0.0,
+                    "resident cross + key padding vs oracle"),
+              "resident cross + key padding");
+        CHECK(close(ym.Data, m.ForwardMasked(q, k, v, true, pad).Data, 1e-9, 0.0,
+                    "resident == ForwardMasked"),
+              "resident == ForwardMasked");
+        CHECK(throws_invalid([&] { res.Forward(q, q, v, false); }), "resident checkQKVDims");
+    }
+}
+
 static void test_gpu() {
     CHECK(gonn::hip::Available(), "no gfx950 device");
     if (!gonn::hip::Available()) return;
@@ -577,6 +638,7 @@ static void test_gpu() {
         CHECK(cache.Lengths() == std::vector<int>({0, 0}), "Reset");
     }
     test_backend_gpu();
+    test_resident_gpu();
 }
 
 int main(int argc, char** argv) {
