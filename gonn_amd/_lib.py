@@ -47,7 +47,7 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_gemm_f64", "gonn_hip_gemm_f64_dev",
     "gonn_hip_unary_f64", "gonn_hip_binary_f64", "gonn_hip_unary_f64_dev", "gonn_hip_binary_f64_dev",
     "gonn_hip_mha_create", "gonn_hip_mha_free", "gonn_hip_mha_forward_f64",
-    "gonn_hip_mha_workspace_bytes", "gonn_hip_mha_forward_dev",
+    "gonn_hip_mha_workspace_bytes", "gonn_hip_mha_forward_dev", "gonn_hip_flash_attn_f64_bwd_ex",
 )
 
 
@@ -76,7 +76,7 @@ class BwdArgs(ctypes.Structure):
                 ("dq", Buf), ("dk", Buf), ("dv", Buf),
                 ("B", ctypes.c_int), ("H", ctypes.c_int), ("S", ctypes.c_int),
                 ("D", ctypes.c_int), ("scale", ctypes.c_double), ("causal", ctypes.c_int),
-                ("mode", ctypes.c_int), ("deterministic", ctypes.c_int)]
+                ("mode", ctypes.c_int), ("deterministic", ctypes.c_int), ("kv_len", Buf)]
 
 
 class DecodeArgs(ctypes.Structure):
@@ -149,6 +149,7 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_unary_f64_dev.argtypes = [i, ctypes.POINTER(Buf), ctypes.POINTER(Buf), lg, vp]
     lib.gonn_hip_binary_f64_dev.argtypes = [i, ctypes.POINTER(Buf), ctypes.POINTER(Buf),
                                             ctypes.POINTER(Buf), lg, vp]
+    lib.gonn_hip_flash_attn_f64_bwd_ex.argtypes = [dp] * 9 + [i, i, i, i, ctypes.c_double, i, ip]
     lib.gonn_hip_mha_create.argtypes = [ctypes.POINTER(vp), i, i, i, i] + [dp] * 8
     lib.gonn_hip_mha_free.argtypes = [vp]
     lib.gonn_hip_mha_forward_f64.argtypes = [vp, dp, dp, dp, dp, i, i, i, i, ip]

@@ -176,6 +176,7 @@ int check_bwd(const gonn_attn_bwd_args* a) {
     for (const gonn_buf* b : in)
         if (!buf_ok(*b, n, GONN_F32)) return GONN_E_INVALID;
     if (!buf_ok(a->lse, BH * a->S, GONN_F32)) return GONN_E_INVALID;
+    if (a->kv_len.ptr && !buf_ok(a->kv_len, (size_t)a->B, GONN_I32)) return GONN_E_INVALID;
     return GONN_OK;
 }
 
@@ -529,6 +530,8 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     p.c2b = (float)((a->scale == 0.0 ? 1.0 : std::fabs(a->scale)) * (double)gonn::kLog2e);
     p.dqs = (float)a->scale;
     p.dks = (float)std::fabs(a->scale);
+    p.kv_len = a->kv_len.ptr ? (const int*)a->kv_len.ptr : nullptr;
+    p.H = a->H;
     {
         ProfScope ps("bwd_prep", s);
         TRYH(gonn::launch_bwd_prep((const float*)a->o.ptr, (const float*)a->dO.ptr,
@@ -764,9 +767,19 @@ int gonn_hip_flash_attn_f64_ex(const double* Q, const double* K, const double* V
 int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* V, const double* O,
                                 const double* L, const double* dO, double* dQ, double* dK,
                                 double* dV, int BH, int S, int d, double scale, int causal) {
-    if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O || !L || !dO || !dQ || !dK || !dV)
+    return gonn_hip_flash_attn_f64_bwd_ex(Q, K, V, O, L, dO, dQ, dK, dV, BH, 1, S, d, scale, causal,
+                                          nullptr);
+}
+
+int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const double* V,
+                                   const double* O, const double* L, const double* dO, double* dQ,
+                                   double* dK, double* dV, int B, int H, int S, int d,
+                                   double scale, int causal, const int* kv_len) {
+    if (B <= 0 || H <= 0 || !shim_args_ok(B * H, S, d) || !Q || !K || !V || !O || !L || !dO ||
+        !dQ || !dK || !dV)
         return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    const int BH = B * H;
     DevMem mem;
     const int dp = pad_dim(d);
     const size_t rows = (size_t)BH * S, n = rows * dp;
@@ -780,6 +793,11 @@ int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* 
     TRY(mem.alloc((void**)&dq, n * 4));
     TRY(mem.alloc((void**)&dk, n * 4));
     TRY(mem.alloc((void**)&dv, n * 4));
+    int* kl = nullptr;
+    if (kv_len) {
+        TRY(mem.alloc((void**)&kl, (size_t)B * 4));
+        TRYH(hipMemcpy(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice));
+    }
     gonn_attn_bwd_args a{};
     a.q = {q, n * 4, GONN_F32};
     a.k = {k, n * 4, GONN_F32};
@@ -790,8 +808,9 @@ int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* 
     a.dq = {dq, n * 4, GONN_F32};
     a.dk = {dk, n * 4, GONN_F32};
     a.dv = {dv, n * 4, GONN_F32};
-    a.B = BH;
-    a.H = 1;
+    a.kv_len = {kl, kl ? (size_t)B * 4 : 0, GONN_I32};
+    a.B = B;
+    a.H = H;
     a.S = S;
     a.D = dp;
     a.scale = scale;

@@ -127,6 +127,14 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     map_block(blockIdx.x, Sp / BN, p.BH, false, bh, kb);
     const int kw = kb * BN + wave * 32;  // first key of this wave
     const int kj = kw + ln;              // this lane's key
+    // Keys >= Skv are padded: zero probability for every query, so their dK
+    // and dV rows are 0, and the other keys' gradients do not involve them.
+    const int Skv = bwd_keys(p, bh);
+    if (kb * BN >= Skv) {
+        bwd_zero_rows<D>(p.dk, S, bh, kb * BN, BN);
+        bwd_zero_rows<D>(p.dv, S, bh, kb * BN, BN);
+        return;
+    }
 
     bf16x8 kf[NKS], vf[NKS];
     {
@@ -398,14 +406,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
 
     if (kj < S) {
         const float sc = p.dks;
+        const bool live = kj < Skv;  // a padded key of a partial block: zeros
         float* dkr = p.dk + ((size_t)bh * S + kj) * D;
         float* dvr = p.dv + ((size_t)bh * S + kj) * D;
         for (int t = 0; t < NDT; t++)
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 f32x4 a, b;
                 for (int k = 0; k < 4; k++) {
-                    a[k] = dkacc[t][rq4 * 4 + k] * sc;
-                    b[k] = dvacc[t][rq4 * 4 + k];
+                    a[k] = live ? dkacc[t][rq4 * 4 + k] * sc : 0.f;
+                    b[k] = live ? dvacc[t][rq4 * 4 + k] : 0.f;
                 }
                 *(f32x4*)(dkr + t * 32 + rq4 * 8 + g * 4) = a;
                 *(f32x4*)(dvr + t * 32 + rq4 * 8 + g * 4) = b;
@@ -436,6 +445,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
     map_block(blockIdx.x, Sp / BN, p.BH, false, bh, kb);
     const int kw = kb * BN + wave * 32;
     const int kj = kw + ln;
+    const int Skv = bwd_keys(p, bh);  // keys >= Skv are padded: dK = dV = 0
+    if (kb * BN >= Skv) {
+        bwd_zero_rows<D>(p.dk, S, bh, kb * BN, BN);
+        bwd_zero_rows<D>(p.dv, S, bh, kb * BN, BN);
+        return;
+    }
 
     float kf[HD], vf[HD];
     {
@@ -539,14 +554,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
 
     if (kj < S) {
         const float sc = p.scale;
+        const bool live = kj < Skv;
         float* dkr = p.dk + ((size_t)bh * S + kj) * D;
         float* dvr = p.dv + ((size_t)bh * S + kj) * D;
         for (int t = 0; t < NDT; t++)
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 f32x4 a, b;
                 for (int i = 0; i < 4; i++) {
-                    a[i] = dkacc[t][rq4 * 4 + i] * sc;
-                    b[i] = dvacc[t][rq4 * 4 + i];
+                    a[i] = live ? dkacc[t][rq4 * 4 + i] * sc : 0.f;
+                    b[i] = live ? dvacc[t][rq4 * 4 + i] : 0.f;
                 }
                 *(f32x4*)(dkr + t * 32 + rq4 * 8 + g * 4) = a;
                 *(f32x4*)(dvr + t * 32 + rq4 * 8 + g * 4) = b;
@@ -574,6 +590,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
     map_block(blockIdx.x, Sp / BM, p.BH, CAUSAL, bh, qb);
     const int q0 = qb * BM;
     const int qi = q0 + wave * 32 + ln;
+    const int Skv = bwd_keys(p, bh);  // keys taking part (key padding)
+    if (Skv == 0) {
+        bwd_zero_rows<D>(p.dq, S, bh, q0, BM);
+        return;
+    }
 
     float qf[HD], df[HD];
     {
@@ -591,7 +612,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
     const float lq = p.lse2[(size_t)bh * Sp + qi];
     const float dl = p.delta[(size_t)bh * Sp + qi];
 
-    int kend = S;
+    int kend = Skv;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
     const int ntiles = (kend + BN - 1) / BN;
     const float* Kg = (const float*)p.k + (size_t)bh * S * D;
@@ -643,12 +664,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
             }
         }
         const int kbase = kt * BN;
-        const bool need_mask = (kbase + BN > S) || (CAUSAL && kbase + BN - 1 > q0 + wave * 32);
+        const bool need_mask = (kbase + BN > Skv) || (CAUSAL && kbase + BN - 1 > q0 + wave * 32);
         for (int r = 0; r < 16; r++) {
             float pv = fast_exp2(__builtin_fmaf(sacc[r], c2, -lq));
             if (need_mask) {
                 const int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (key >= S || (CAUSAL && key > qi)) pv = 0.f;
+                if (key >= Skv || (CAUSAL && key > qi)) pv = 0.f;
             }
             dpacc[r] = pv * (dpacc[r] - dl);
         }

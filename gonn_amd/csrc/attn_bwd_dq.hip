@@ -80,6 +80,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     const int q0 = qb * BM;
     const int qw = q0 + wave * 32;       // first query of this wave
     const int qi = qw + ln;              // this lane's query (< Sp)
+    const int Skv = bwd_keys(p, bh);     // keys taking part (key padding)
+    if (Skv == 0) {  // no key: the forward gave O = 0; dQ = 0
+        bwd_zero_rows<D>(p.dq, S, bh, q0, BM);
+        return;
+    }
 
     bf16x8 qf[NKS], df[NKS];
     {
@@ -100,7 +105,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     f32x16 dinit;
     for (int r = 0; r < 16; r++) dinit[r] = -dl;
 
-    int kend = S;
+    int kend = Skv;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
     const int nt = (kend + BN - 1) / BN;
     const bf16* Kg = (const bf16*)p.k + (size_t)bh * Sp * D;
@@ -143,18 +148,19 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     const char* cV = (const char*)sV;
     const char* cKt = (const char*)sKt;
 
-    // Masks of key tile kt on S^T: key >= S, or causal key > query. The
-    // exponent scale c2b is positive, so -inf gives P = 0 and dS = 0.
+    // Masks of key tile kt on S^T: key >= Skv (end of the slice or key
+    // padding), or causal key > query. The exponent scale c2b is positive,
+    // so -inf gives P = 0 and dS = 0.
     auto needs_mask = [&](int kt) {
         const int kbase = kt * BN;
-        return (kbase + BN > S) || (CAUSAL && kbase + BN - 1 > qw);
+        return (kbase + BN > Skv) || (CAUSAL && kbase + BN - 1 > qw);
     };
     auto mask = [&](int kt, f32x16* s) {
         const int kbase = kt * BN + 4 * g;
         for (int mt = 0; mt < 2; mt++)
             for (int r = 0; r < 16; r++) {
                 const int key = kbase + mt * 32 + 8 * (r >> 2) + (r & 3);
-                const bool off = key >= S || (CAUSAL && key > qi);
+                const bool off = key >= Skv || (CAUSAL && key > qi);
                 s[mt][r] = off ? -INFINITY : s[mt][r];
             }
     };

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 
+#include "common.h"
+
 namespace gonn {
 
 struct FwdParams {
@@ -68,7 +70,31 @@ struct BwdParams {
     // the exponent scale is positive: c2b = (scale ? |scale| : 1) * log2(e);
     // outputs dQ = dqs * acc, dK = dks * acc with dqs = scale, dks = |scale|.
     float c2b, dqs, dks;
+    // Optional per-sequence key counts (device int32[BH / H]): keys
+    // t >= kv_len[bh / H] of slice bh are padded (ForwardMasked key padding);
+    // their dK, dV rows are zero and they add nothing to dQ.
+    const int* kv_len;
+    int H;
 };
+
+// Keys of slice bh that take part in the backward: S, or the sequence's
+// kv_len clamped to [0, S]. Wave-uniform.
+GONN_DEV int bwd_keys(const BwdParams& p, int bh) {
+    if (!p.kv_len) return p.S;
+    int l = p.kv_len[bh / p.H];
+    l = l < 0 ? 0 : (l > p.S ? p.S : l);
+    return __builtin_amdgcn_readfirstlane(l);
+}
+
+// Zero rows r0 .. r0 + rows - 1 (those below S) of the (BH, S, D) output
+// `out` for slice bh, with every thread of the workgroup.
+template <int D>
+GONN_DEV void bwd_zero_rows(float* out, int S, int bh, int r0, int rows) {
+    const int r1 = r0 + rows < S ? r0 + rows : S;
+    if (r1 <= r0) return;
+    f32x4* o = (f32x4*)(out + ((size_t)bh * S + r0) * D);
+    for (int i = threadIdx.x; i < (r1 - r0) * D / 4; i += blockDim.x) o[i] = f32x4{};
+}
 
 hipError_t launch_pack(const PackParams& p, int nsrc, int in_bf16, int BH, int D, hipStream_t s);
 hipError_t launch_fwd(const FwdParams& p, int mode, int D, int causal, int q_bf16,

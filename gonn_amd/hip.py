@@ -133,6 +133,28 @@ def FlashAttnF64Bwd(Q, K, V, O, L, dO, BH: int, S: int, d: int, scale: float, ca
     return dQ, dK, dV
 
 
+def FlashAttnF64BwdEx(Q, K, V, O, L, dO, B: int, H: int, S: int, d: int, scale: float,
+                      causal: bool, kv_len=None):
+    """General backward on host fp64 (B*H,S,d) arrays with the forward's
+    optional key padding kv_len[B] (new): returns (dQ, dK, dV). O and L come
+    from FlashAttnF64Ex(..., kv_len, lse=True) with the same kv_len."""
+    n = B * H * S * d
+    Q, K, V, O, dO = (_f64(x, n, "FlashAttnF64BwdEx") for x in (Q, K, V, O, dO))
+    L = _f64(L, B * H * S, "FlashAttnF64BwdEx L")
+    kl = None
+    if kv_len is not None:
+        kl = np.ascontiguousarray(kv_len, dtype=np.int32)
+        if kl.shape != (B,):
+            raise ValueError(f"FlashAttnF64BwdEx: kv_len must have {B} entries")
+    dQ, dK, dV = np.zeros(n), np.zeros(n), np.zeros(n)
+    check(_lib.load().gonn_hip_flash_attn_f64_bwd_ex(
+        _p(Q), _p(K), _p(V), _p(O), _p(L), _p(dO), _p(dQ), _p(dK), _p(dV), B, H, S, d,
+        float(scale), int(bool(causal)),
+        kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None),
+        "FlashAttnF64BwdEx")
+    return dQ, dK, dV
+
+
 def FlashAttnF64Ex(Q, K, V, B: int, H: int, Sq: int, Sk: int, d: int, scale: float,
                    causal: bool, kv_len=None, lse: bool = False):
     """General fused forward on host fp64 arrays (new; the reference seam is
@@ -312,9 +334,10 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
 
 
 def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp32",
-             out=None, stream=None):
+             out=None, stream=None, kv_len=None):
     """dQ, dK, dV (float32) from the saved forward tensors (all float32).
-    out may supply preallocated (dq, dk, dv)."""
+    out may supply preallocated (dq, dk, dv). kv_len: optional int32 (B,)
+    device tensor, the key padding the forward was run with."""
     torch = _torch()
     B, H, S, D = _shape4(q, "q")
     if scale is None:
@@ -325,7 +348,8 @@ def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp3
     else:
         dq, dk, dv = out
     a = BwdArgs(buf(q), buf(k), buf(v), buf(o), buf(lse), buf(dO), buf(dq), buf(dk), buf(dv),
-                B, H, S, D, float(scale), int(bool(causal)), MODES[mode], 1)
+                B, H, S, D, float(scale), int(bool(causal)), MODES[mode], 1,
+                buf(kv_len) if kv_len is not None else Buf(None, 0, GONN_I32))
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
@@ -565,7 +589,8 @@ class DeviceMHA:
 
 
 __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
-           "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex", "Gemm",
+           "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex",
+           "FlashAttnF64BwdEx", "Gemm",
            "Unary", "Binary",
            "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "DeviceMHA", "buf",
            "GonnHipError"]

@@ -86,6 +86,17 @@ std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vect
                                    const std::vector<double>& V, int B, int H, int Sq, int Sk,
                                    int d, double scale, bool causal,
                                    const std::vector<int>& kvLen = {});
+// The same forward returning O and L (B*H,Sq), for a backward.
+FwdOut FlashAttnF64ExFwd(const std::vector<double>& Q, const std::vector<double>& K,
+                         const std::vector<double>& V, int B, int H, int Sq, int Sk, int d,
+                         double scale, bool causal, const std::vector<int>& kvLen = {});
+// New: the backward of a square (S x S) forward with key padding kvLen[B]
+// (empty = none); O and L from FlashAttnF64ExFwd with the same kvLen.
+BwdOut FlashAttnF64BwdEx(const std::vector<double>& Q, const std::vector<double>& K,
+                         const std::vector<double>& V, const std::vector<double>& O,
+                         const std::vector<double>& L, const std::vector<double>& dO, int B,
+                         int H, int S, int d, double scale, bool causal,
+                         const std::vector<int>& kvLen = {});
 
 // Device KV cache of one attention layer (gonn_hip_kvcache_*). New: the
 // reference has no KV cache. Attend is ForwardMasked with a key-padding mask
@@ -252,8 +263,10 @@ struct DiffOut {
     Tensor Out;
     FlashAttnNode Node;
 };
+// kvLen (new, BH / H entries or empty): the key padding of ForwardMasked, in
+// the forward and in the node's backward.
 DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
-                      double scale, bool causal);
+                      double scale, bool causal, const std::vector<int>& kvLen = {}, int H = 1);
 
 // nn.MultiHeadAttention with the fused core (nn/attention.go:38-180).
 // Weights are given explicitly: GoNN draws them from Go's math/rand stream
@@ -274,7 +287,8 @@ class MultiHeadAttention {
     Tensor ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
     // ForwardMasked (nn/attention.go:305-341) on the fused core with causal
     // and a (B, Tk) key-padding mask (nonzero = ignore; the padded keys of a
-    // row must be a suffix). An empty keyPad means none. Inference only.
+    // row must be a suffix). An empty keyPad means none. Inference; the
+    // differentiable form is fusedAttnDiff with kvLen.
     Tensor ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
                          const Tensor& keyPad);
 

@@ -106,10 +106,9 @@ double BenchFlashAttnF64(int BH, int S, int d, int iters, bool causal) {
     return ms;
 }
 
-std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vector<double>& K,
-                                   const std::vector<double>& V, int B, int H, int Sq, int Sk,
-                                   int d, double scale, bool causal,
-                                   const std::vector<int>& kvLen) {
+FwdOut FlashAttnF64ExFwd(const std::vector<double>& Q, const std::vector<double>& K,
+                         const std::vector<double>& V, int B, int H, int Sq, int Sk, int d,
+                         double scale, bool causal, const std::vector<int>& kvLen) {
     if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || d <= 0)
         throw std::invalid_argument("hip: FlashAttnF64Ex: B, H, Sq, Sk, d must be >= 1");
     const size_t nq = (size_t)B * H * Sq * d, nk = (size_t)B * H * Sk * d;
@@ -118,12 +117,49 @@ std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vect
     need(V, nk, "FlashAttnF64Ex V");
     if (!kvLen.empty() && (int)kvLen.size() != B)
         throw std::invalid_argument("hip: FlashAttnF64Ex: kvLen needs B entries");
-    std::vector<double> O(nq, 0.0);
-    check(gonn_hip_flash_attn_f64_ex(Q.data(), K.data(), V.data(), O.data(), nullptr, B, H, Sq,
-                                     Sk, d, scale, causal ? 1 : 0,
+    FwdOut r;
+    r.O.assign(nq, 0.0);
+    r.L.assign((size_t)B * H * Sq, 0.0);
+    check(gonn_hip_flash_attn_f64_ex(Q.data(), K.data(), V.data(), r.O.data(), r.L.data(), B, H,
+                                     Sq, Sk, d, scale, causal ? 1 : 0,
                                      kvLen.empty() ? nullptr : kvLen.data()),
           "FlashAttnF64Ex");
-    return O;
+    return r;
+}
+
+std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vector<double>& K,
+                                   const std::vector<double>& V, int B, int H, int Sq, int Sk,
+                                   int d, double scale, bool causal,
+                                   const std::vector<int>& kvLen) {
+    return FlashAttnF64ExFwd(Q, K, V, B, H, Sq, Sk, d, scale, causal, kvLen).O;
+}
+
+BwdOut FlashAttnF64BwdEx(const std::vector<double>& Q, const std::vector<double>& K,
+                         const std::vector<double>& V, const std::vector<double>& O,
+                         const std::vector<double>& L, const std::vector<double>& dO, int B,
+                         int H, int S, int d, double scale, bool causal,
+                         const std::vector<int>& kvLen) {
+    if (B <= 0 || H <= 0) throw std::invalid_argument("hip: FlashAttnF64BwdEx: B, H must be >= 1");
+    shape_ok(B * H, S, d, "FlashAttnF64BwdEx");
+    const size_t n = (size_t)B * H * S * d;
+    need(Q, n, "FlashAttnF64BwdEx Q");
+    need(K, n, "FlashAttnF64BwdEx K");
+    need(V, n, "FlashAttnF64BwdEx V");
+    need(O, n, "FlashAttnF64BwdEx O");
+    need(L, (size_t)B * H * S, "FlashAttnF64BwdEx L");
+    need(dO, n, "FlashAttnF64BwdEx dO");
+    if (!kvLen.empty() && (int)kvLen.size() != B)
+        throw std::invalid_argument("hip: FlashAttnF64BwdEx: kvLen needs B entries");
+    BwdOut r;
+    r.dQ.assign(n, 0.0);
+    r.dK.assign(n, 0.0);
+    r.dV.assign(n, 0.0);
+    check(gonn_hip_flash_attn_f64_bwd_ex(Q.data(), K.data(), V.data(), O.data(), L.data(),
+                                         dO.data(), r.dQ.data(), r.dK.data(), r.dV.data(), B, H, S,
+                                         d, scale, causal ? 1 : 0,
+                                         kvLen.empty() ? nullptr : kvLen.data()),
+          "FlashAttnF64BwdEx");
+    return r;
 }
 
 KVCache::KVCache(int B, int H, int Lmax, int D) : B_(B), H_(H), Lmax_(Lmax), D_(D) {

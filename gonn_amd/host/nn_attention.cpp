@@ -99,8 +99,12 @@ std::vector<double> fusedAttnF64(const std::vector<double>& Q, const std::vector
 }
 
 DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
-                      double scale, bool causal) {
-    hip::FwdOut f = hip::FlashAttnF64Fwd(qp.Data, kp.Data, vp.Data, BH, S, D, scale, causal);
+                      double scale, bool causal, const std::vector<int>& kvLen, int H) {
+    if (H <= 0 || BH % H != 0) throw std::invalid_argument("fusedAttnDiff: BH must be a multiple of H");
+    hip::FwdOut f = kvLen.empty()
+                        ? hip::FlashAttnF64Fwd(qp.Data, kp.Data, vp.Data, BH, S, D, scale, causal)
+                        : hip::FlashAttnF64ExFwd(qp.Data, kp.Data, vp.Data, BH / H, H, S, S, D,
+                                                 scale, causal, kvLen);
     DiffOut r;
     r.Out = Tensor::New(f.O, qp.Shape);
     // The node's closure holds the inputs and the saved O and L, as the Go
@@ -108,10 +112,14 @@ DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int 
     auto saved = std::make_shared<std::array<Tensor, 3>>(std::array<Tensor, 3>{qp, kp, vp});
     auto O = std::make_shared<std::vector<double>>(std::move(f.O));
     auto L = std::make_shared<std::vector<double>>(std::move(f.L));
-    r.Node.Backward = [saved, O, L, BH, S, D, scale, causal](const Tensor& grad) {
+    r.Node.Backward = [saved, O, L, BH, S, D, scale, causal, kvLen, H](const Tensor& grad) {
         const Tensor &q = (*saved)[0], &k = (*saved)[1], &v = (*saved)[2];
         hip::BwdOut b =
-            hip::FlashAttnF64Bwd(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH, S, D, scale, causal);
+            kvLen.empty()
+                ? hip::FlashAttnF64Bwd(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH, S, D, scale,
+                                       causal)
+                : hip::FlashAttnF64BwdEx(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH / H, H, S,
+                                         D, scale, causal, kvLen);
         return std::array<Tensor, 3>{Tensor::New(std::move(b.dQ), q.Shape),
                                      Tensor::New(std::move(b.dK), k.Shape),
                                      Tensor::New(std::move(b.dV), v.Shape)};

@@ -46,25 +46,36 @@ class FusedAttnNode:
     nn/flashattn_cuda.go:29-37): holds what the backward needs and runs the
     device backward when called with the upstream gradient."""
 
-    def __init__(self, Q, K, V, O, L, BH, S, D, scale, causal):
+    def __init__(self, Q, K, V, O, L, BH, S, D, scale, causal, kv_len=None, H=1):
         self.saved = (Q, K, V, O, L)
         self.shape = (BH, S, D)
         self.scale = scale
         self.causal = causal
+        self.kv_len, self.H = kv_len, H
 
     def __call__(self, grad):
         Q, K, V, O, L = self.saved
         BH, S, D = self.shape
-        return hip.FlashAttnF64Bwd(Q, K, V, O, L, grad, BH, S, D, self.scale, self.causal)
+        if self.kv_len is None:
+            return hip.FlashAttnF64Bwd(Q, K, V, O, L, grad, BH, S, D, self.scale, self.causal)
+        return hip.FlashAttnF64BwdEx(Q, K, V, O, L, grad, BH // self.H, self.H, S, D,
+                                     self.scale, self.causal, kv_len=self.kv_len)
 
 
-def fused_attn_diff(qp, kp, vp, BH: int, S: int, D: int, scale: float, causal: bool):
-    """Differentiable core: returns (O, node) where node(dO) -> (dQ, dK, dV)."""
-    O, L = hip.FlashAttnF64Fwd(qp, kp, vp, BH, S, D, scale, causal)
+def fused_attn_diff(qp, kp, vp, BH: int, S: int, D: int, scale: float, causal: bool,
+                    kv_len=None, H: int = 1):
+    """Differentiable core: returns (O, node) where node(dO) -> (dQ, dK, dV).
+    kv_len (new): optional per-sequence key counts (BH / H entries), the key
+    padding of ForwardMasked, in the forward and the backward."""
+    if kv_len is None:
+        O, L = hip.FlashAttnF64Fwd(qp, kp, vp, BH, S, D, scale, causal)
+    else:
+        O, L = hip.FlashAttnF64Ex(qp, kp, vp, BH // H, H, S, S, D, scale, causal,
+                                  kv_len=kv_len, lse=True)
     return O, FusedAttnNode(np.ascontiguousarray(qp, dtype=np.float64).ravel(),
                             np.ascontiguousarray(kp, dtype=np.float64).ravel(),
                             np.ascontiguousarray(vp, dtype=np.float64).ravel(), O, L, BH, S, D,
-                            scale, causal)
+                            scale, causal, kv_len, H)
 
 
 class Linear:

@@ -98,7 +98,11 @@ typedef struct {
  * Sq == Sk is required (the reference backward's contract).
  * deterministic: accepted for API completeness; every mode of this library
  * is deterministic (no floating-point atomics), so 0 and 1 give
- * bit-identical results.                                                   */
+ * bit-identical results.
+ * kv_len: optional GONN_I32 device array [B] (ptr NULL = none), the same as
+ * the forward's: keys t >= kv_len[b] are padded, so their dK and dV rows are
+ * 0 and they add nothing to dQ; o and lse must come from the forward with
+ * the same kv_len. A sequence with kv_len 0 gets dQ = dK = dV = 0.         */
 typedef struct {
     gonn_buf q, k, v, o, lse, dO, dq, dk, dv;
     int B, H, S, D;
@@ -106,6 +110,7 @@ typedef struct {
     int causal;
     int mode;
     int deterministic;
+    gonn_buf kv_len;
 } gonn_attn_bwd_args;
 
 /* KV-cache decode, one query per (b, h): o[b,h] = attention of q[b,h] over
@@ -306,6 +311,14 @@ int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* 
                                 const double* O, const double* L, const double* dO,
                                 double* dQ, double* dK, double* dV,
                                 int BH, int S, int d, double scale, int causal);
+/* General fp64 backward (new): B sequences x H heads of S x S, with the
+ * forward's optional host kv_len[B] (ForwardMasked key padding, see
+ * gonn_attn_bwd_args); O and L from gonn_hip_flash_attn_f64_ex with the same
+ * kv_len. gonn_hip_flash_attn_f64_bwd is this with B = BH, H = 1, no kv_len. */
+int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const double* V,
+                                   const double* O, const double* L, const double* dO, double* dQ,
+                                   double* dK, double* dV, int B, int H, int S, int d,
+                                   double scale, int causal, const int* kv_len);
 /* New (the reference's fused seam is Tq == Tk, causal-or-not only): the
  * general forward on host fp64 arrays for the wider fused gate, i.e.
  * cross-attention (Sq != Sk, top-left causal mask when causal) and

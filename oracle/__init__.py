@@ -13,7 +13,9 @@ Pinning (each check lives in tests/test_oracle.py):
                     (nn/attention_masked_test.go:23-81), the refAttn restatement
                     of benchmark/flashattn/main.go:39-75.
   attn_bwd_autograd torch fp64 autograd, central finite differences with the
-                    flashbwd protocol (benchmark/flashbwd/main.go:32-95).
+                    flashbwd protocol (benchmark/flashbwd/main.go:32-95); with
+                    kv_len, torch fp64 autograd through an explicit key mask
+                    and exact zeros on the padded keys' dK, dV.
   attn_bwd_rows     equal to attn_bwd_autograd on every row (1e-12).
   linear / mha_fwd  torch fp64 F.linear / the composed reference sequence.
 Planted-mistake tests show each of these checks fails on a plausible bug.
@@ -47,6 +49,8 @@ def _load():
                                     ctypes.c_double, ctypes.c_int, _ip, _ip, ctypes.c_int]
     lib.oracle_attn_bwd_autograd.argtypes = [_dp] * 7 + [ctypes.c_int] * 3 + [
         ctypes.c_double, ctypes.c_int]
+    lib.oracle_attn_bwd_autograd_ex.argtypes = [_dp] * 7 + [ctypes.c_int] * 4 + [
+        ctypes.c_double, ctypes.c_int, _ip]
     lib.oracle_attn_bwd_rows.argtypes = [_dp] * 9 + [ctypes.c_int] * 3 + [
         ctypes.c_double, ctypes.c_int, _ip, ctypes.c_int, _ip, ctypes.c_int]
     lib.oracle_linear.argtypes = [_dp, _dp, _dp, _dp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
@@ -115,16 +119,23 @@ def attn_fwd(Q, K, V, scale=None, causal=False, kv_len=None, H=1, rows=None):
     return O, L
 
 
-def attn_bwd_autograd(Q, K, V, dO, scale=None, causal=False):
-    """Backward through the reference's autograd chain -> (dQ, dK, dV)."""
+def attn_bwd_autograd(Q, K, V, dO, scale=None, causal=False, kv_len=None, H=1):
+    """Backward through the reference's autograd chain -> (dQ, dK, dV).
+    kv_len: optional per-batch valid key counts (BH/H entries), the key
+    padding mask of ForwardMasked."""
     lib = _load()
     Q, K, V, dO = _c64(Q), _c64(K), _c64(V), _c64(dO)
     BH, S, D = Q.shape
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     dQ, dK, dV = np.zeros_like(Q), np.zeros_like(K), np.zeros_like(V)
-    rc = lib.oracle_attn_bwd_autograd(_d(Q), _d(K), _d(V), _d(dO), _d(dQ), _d(dK), _d(dV),
-                                      BH, S, D, float(scale), int(bool(causal)))
+    kl = None
+    if kv_len is not None:
+        kl = np.ascontiguousarray(kv_len, dtype=np.int32)
+        assert kl.shape == (BH // H,)
+    rc = lib.oracle_attn_bwd_autograd_ex(_d(Q), _d(K), _d(V), _d(dO), _d(dQ), _d(dK), _d(dV),
+                                         BH, int(H), S, D, float(scale), int(bool(causal)),
+                                         kl.ctypes.data_as(_ip) if kl is not None else None)
     if rc != 0:
         raise RuntimeError(f"oracle_attn_bwd_autograd failed: {rc}")
     return dQ, dK, dV

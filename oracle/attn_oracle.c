@@ -205,12 +205,15 @@ int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O
  * Given g = dL/dctx: walks the nodes in reverse topological order, summing
  * the two gradient contributions into e (Div numerator and SumAxis) and into
  * masked (Sub and MaxAxis scatter) as tensor/autograd.go:52-99 accumulates
- * them.
+ * them. kv_len: NULL, or per-batch valid key counts (length BH/H): the key
+ * padding mask ForwardMasked adds (nn/attention.go:261-272, :321-330), one
+ * more additive -1e30 term of `mask`.
  */
-int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V,
-                             const double* dO, double* dQ, double* dK, double* dV,
-                             int BH, int S, int D, double scale, int causal) {
-    if (BH <= 0 || S <= 0 || D <= 0) return -1;
+int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* V,
+                                const double* dO, double* dQ, double* dK, double* dV,
+                                int BH, int H, int S, int D, double scale, int causal,
+                                const int* kv_len) {
+    if (BH <= 0 || S <= 0 || D <= 0 || H <= 0 || BH % H != 0) return -1;
     const size_t SS = (size_t)S * S;
     double* KT = (double*)malloc(sizeof(double) * (size_t)D * S);
     double* msk = (double*)malloc(sizeof(double) * SS);  /* masked scores */
@@ -238,7 +241,12 @@ int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V,
         double* dVb = dV + (size_t)bh * S * D;
         /* forward, keeping the graph's tensors */
         transpose(Kb, KT, S, D);
-        scores_rows(Qb, KT, S, D, NULL, S, scale, causal, S, msk);
+        int len = S;
+        if (kv_len) {
+            len = kv_len[bh / H];
+            len = len < 0 ? 0 : (len > S ? S : len);
+        }
+        scores_rows(Qb, KT, S, D, NULL, S, scale, causal, len, msk);
         int* amax = (int*)malloc(sizeof(int) * S);
         double* se = (double*)malloc(sizeof(double) * S);
         double* g_se = (double*)malloc(sizeof(double) * S);
@@ -305,6 +313,13 @@ int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V,
     free(KT); free(msk); free(e); free(attn); free(g_attn); free(g_e); free(g_m);
     free(VT); free(AT); free(GT);
     return 0;
+}
+
+/* The reference backward's signature (no key padding). */
+int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V,
+                             const double* dO, double* dQ, double* dK, double* dV,
+                             int BH, int S, int D, double scale, int causal) {
+    return oracle_attn_bwd_autograd_ex(Q, K, V, dO, dQ, dK, dV, BH, 1, S, D, scale, causal, NULL);
 }
 
 /*

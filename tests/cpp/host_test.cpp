@@ -31,6 +31,9 @@ int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O
 int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V, const double* dO,
                              double* dQ, double* dK, double* dV, int BH, int S, int D,
                              double scale, int causal);
+int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* V,
+                                const double* dO, double* dQ, double* dK, double* dV, int BH,
+                                int H, int S, int D, double scale, int causal, const int* kv_len);
 int oracle_linear(const double* x, const double* W, const double* b, double* y, int N, int in,
                   int out);
 void oracle_heads(const double* in, double* out, int B, int T, int H, int D, int dir);
@@ -477,6 +480,31 @@ static void test_resident_gpu() {
     }
 }
 
+// fusedAttnDiff with key padding: the node's backward through
+// gonn_hip_flash_attn_f64_bwd_ex against the oracle's autograd chain.
+static void test_diff_key_padding_gpu() {
+    const int B = 2, H = 2, S = 70, D = 64, BH = B * H;
+    const size_t n = (size_t)BH * S * D;
+    Rng r(313);
+    Tensor q = Tensor::New(r.normals(n), {BH, S, D}), k = Tensor::New(r.normals(n), {BH, S, D}),
+           v = Tensor::New(r.normals(n), {BH, S, D}), g = Tensor::New(r.normals(n), {BH, S, D});
+    const std::vector<int> lens = {70, 23};
+    const double scale = 1.0 / std::sqrt((double)D);
+    gonn::hip::SetMode(0);
+    gonn::nn::DiffOut f = gonn::nn::fusedAttnDiff(q, k, v, BH, S, D, scale, true, lens, H);
+    std::vector<double> ro(n), rq(n), rk(n), rv(n);
+    oracle_attn_fwd(q.Data.data(), k.Data.data(), v.Data.data(), ro.data(), nullptr, BH, H, S, S,
+                    D, scale, 1, lens.data(), nullptr, 0);
+    oracle_attn_bwd_autograd_ex(q.Data.data(), k.Data.data(), v.Data.data(), g.Data.data(),
+                                rq.data(), rk.data(), rv.data(), BH, H, S, D, scale, 1,
+                                lens.data());
+    CHECK(close(f.Out.Data, ro, 1e-4, 0.0, "fusedAttnDiff key padding O"), "diff kv O");
+    const auto grads = f.Node.Backward(g);
+    CHECK(close(grads[0].Data, rq, 1e-4, 0.0, "fusedAttnDiff key padding dQ"), "diff kv dQ");
+    CHECK(close(grads[1].Data, rk, 1e-4, 0.0, "fusedAttnDiff key padding dK"), "diff kv dK");
+    CHECK(close(grads[2].Data, rv, 1e-4, 0.0, "fusedAttnDiff key padding dV"), "diff kv dV");
+}
+
 static void test_gpu() {
     CHECK(gonn::hip::Available(), "no gfx950 device");
     if (!gonn::hip::Available()) return;
@@ -639,6 +667,7 @@ static void test_gpu() {
     }
     test_backend_gpu();
     test_resident_gpu();
+    test_diff_key_padding_gpu();
 }
 
 int main(int argc, char** argv) {

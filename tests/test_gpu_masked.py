@@ -114,3 +114,78 @@ def test_mha_forward_masked_and_cross_attention(causal):
         mha.forward_masked(x, x, x, key_padding_mask=holes)
     with pytest.raises(ValueError):
         mha.forward_masked(x, x, x, attn_mask=np.zeros((Tk, Tk)))
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_bwd_kv_len_matches_oracle_autograd(mode, D, causal):
+    """Backward of ForwardMasked's key padding (kv_len) against GoNN's autograd
+    chain through the same additive masks (oracle.attn_bwd_autograd with
+    kv_len, pinned to torch fp64 autograd): padded keys get dK = dV = 0
+    exactly, a sequence with no key gets all-zero gradients."""
+    from gonn_amd import hip
+    B, H, S = 4, 2, 150
+    lens = np.array([150, 37, 0, 129], dtype=np.int32)
+    say(f"[masked] bwd mode={mode} D={D} causal={causal} S={S} lens={list(lens)}")
+    q, k, v, g = (randn((B * H, S, D), 820 + D + i) for i in range(4))
+    dev = [torch.from_numpy(x).cuda().reshape(B, H, S, D) for x in (q, k, v, g)]
+    kl = torch.from_numpy(lens).cuda()
+    o, l = hip.attn_fwd(*dev[:3], causal=causal, mode=mode, kv_len=kl)
+    dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=causal, mode=mode, kv_len=kl)
+    torch.cuda.synchronize()
+    dq, dk, dv = (t.reshape(B * H, S, D).cpu().numpy() for t in (dq, dk, dv))
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H)
+    live = np.repeat(lens > 0, H)
+    assert_close(dq[live], rq[live], mode, f"dQ kv_len {mode} D={D} causal={causal}")
+    assert_close(dk[live], rk[live], mode, f"dK kv_len {mode} D={D} causal={causal}")
+    assert_close(dv[live], rv[live], mode, f"dV kv_len {mode} D={D} causal={causal}")
+    for bh in range(B * H):
+        n = lens[bh // H]
+        assert np.all(dk[bh, n:] == 0.0) and np.all(dv[bh, n:] == 0.0), bh
+        if n == 0:
+            assert np.all(dq[bh] == 0.0)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_bwd_kv_len_full_equals_absent(mode):
+    """kv_len >= S for every sequence gives the same gradients as no kv_len,
+    bit for bit."""
+    from gonn_amd import hip
+    B, H, S, D = 2, 2, 200, 128
+    dev = [torch.from_numpy(randn((B, H, S, D), 840 + i)).cuda() for i in range(4)]
+    o, l = hip.attn_fwd(*dev[:3], causal=True, mode=mode)
+    g0 = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=True, mode=mode)
+    kl = torch.tensor([S, S + 5], dtype=torch.int32, device="cuda")
+    g1 = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=True, mode=mode, kv_len=kl)
+    torch.cuda.synchronize()
+    for a, b in zip(g0, g1):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_fused_attn_diff_with_key_padding(mode):
+    """nn.fused_attn_diff with kv_len: the fp64 entry points
+    (gonn_hip_flash_attn_f64_ex / _bwd_ex) give the forward and the node's
+    backward of ForwardMasked's key padding; against the oracle's forward and
+    autograd chain."""
+    from gonn_amd import hip, nn
+    prev = hip.AttnMode()
+    hip.SetAttnMode(mode)
+    try:
+        B, H, S, D = 3, 2, 90, 64
+        lens = np.array([90, 41, 7], dtype=np.int32)
+        q, k, v, g = (randn((B * H, S, D), 860 + i) for i in range(4))
+        O, node = nn.fused_attn_diff(q, k, v, B * H, S, D, 1 / math.sqrt(D), True,
+                                     kv_len=lens, H=H)
+        dq, dk, dv = (x.reshape(B * H, S, D) for x in node(g.ravel()))
+    finally:
+        hip.SetAttnMode(prev)
+    ro, _ = oracle.attn_fwd(q, k, v, 1 / math.sqrt(D), True, kv_len=lens, H=H)
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=True, kv_len=lens, H=H)
+    assert_close(O.reshape(B * H, S, D), ro, mode, f"fused_attn_diff O {mode}")
+    assert_close(dq, rq, mode, f"fused_attn_diff dQ {mode}")
+    assert_close(dk, rk, mode, f"fused_attn_diff dK {mode}")
+    assert_close(dv, rv, mode, f"fused_attn_diff dV {mode}")
+    for bh in range(B * H):
+        assert np.all(dk[bh, lens[bh // H]:] == 0.0)

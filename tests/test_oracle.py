@@ -206,6 +206,35 @@ def test_bwd_matches_torch_autograd(causal):
         np.testing.assert_allclose(got, t.grad.numpy(), atol=1e-12, rtol=0)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_bwd_key_padding_matches_torch_autograd(causal):
+    """ForwardMasked's key padding in the backward: torch fp64 autograd through
+    the same additive -1e30 masks (a library path), exact zeros on padded keys,
+    and kv_len = S equal to no padding bit for bit."""
+    rng = np.random.default_rng(23 + causal)
+    B, H, S, D = 3, 2, 40, 64
+    lens = [40, 17, 1]
+    q, k, v, g = (rng.standard_normal((B * H, S, D)) for _ in range(4))
+    dQ, dK, dV = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    s = (tq @ tk.transpose(1, 2)) / math.sqrt(D)
+    mask = torch.zeros(B * H, S, S, dtype=torch.float64)
+    if causal:
+        mask += torch.where(torch.arange(S)[None, :] > torch.arange(S)[:, None], -1e30, 0.0)
+    for bh in range(B * H):
+        mask[bh, :, lens[bh // H]:] += -1e30
+    (torch.softmax(s + mask, -1) @ tv).backward(torch.tensor(g))
+    for got, t in ((dQ, tq), (dK, tk), (dV, tv)):
+        np.testing.assert_allclose(got, t.grad.numpy(), atol=1e-12, rtol=0)
+    for bh in range(B * H):
+        n = lens[bh // H]
+        assert np.all(dK[bh, n:] == 0.0) and np.all(dV[bh, n:] == 0.0)
+    full = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=[S] * B, H=H)
+    plain = oracle.attn_bwd_autograd(q, k, v, g, causal=causal)
+    for a, b in zip(full, plain):
+        assert np.array_equal(a, b)
+
+
 def _fd_check(causal, fwd=oracle.attn_fwd, bwd=None):
     """benchmark/flashbwd/main.go:40-95: BH=2, S=6, D=64, loss = sum(O*dO),
     eps=1e-6, indices {0,1,64,130,200,n-1}, relErr <= 1e-4."""
