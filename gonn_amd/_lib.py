@@ -48,6 +48,7 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_unary_f64", "gonn_hip_binary_f64", "gonn_hip_unary_f64_dev", "gonn_hip_binary_f64_dev",
     "gonn_hip_mha_create", "gonn_hip_mha_free", "gonn_hip_mha_forward_f64",
     "gonn_hip_mha_workspace_bytes", "gonn_hip_mha_forward_dev", "gonn_hip_flash_attn_f64_bwd_ex",
+    "gonn_hip_flash_attn_f64_masked", "gonn_hip_flash_attn_f64_bwd_masked",
 )
 
 
@@ -68,7 +69,9 @@ class FwdArgs(ctypes.Structure):
     _fields_ = [("q", Buf), ("k", Buf), ("v", Buf), ("o", Buf), ("lse", Buf),
                 ("B", ctypes.c_int), ("H", ctypes.c_int), ("Sq", ctypes.c_int),
                 ("Sk", ctypes.c_int), ("D", ctypes.c_int), ("scale", ctypes.c_double),
-                ("causal", ctypes.c_int), ("mode", ctypes.c_int), ("kv_len", Buf)]
+                ("causal", ctypes.c_int), ("mode", ctypes.c_int), ("kv_len", Buf),
+                ("attn_mask", Buf), ("mask_stride_b", ctypes.c_int64),
+                ("mask_stride_h", ctypes.c_int64)]
 
 
 class BwdArgs(ctypes.Structure):
@@ -76,7 +79,9 @@ class BwdArgs(ctypes.Structure):
                 ("dq", Buf), ("dk", Buf), ("dv", Buf),
                 ("B", ctypes.c_int), ("H", ctypes.c_int), ("S", ctypes.c_int),
                 ("D", ctypes.c_int), ("scale", ctypes.c_double), ("causal", ctypes.c_int),
-                ("mode", ctypes.c_int), ("deterministic", ctypes.c_int), ("kv_len", Buf)]
+                ("mode", ctypes.c_int), ("deterministic", ctypes.c_int), ("kv_len", Buf),
+                ("attn_mask", Buf), ("mask_stride_b", ctypes.c_int64),
+                ("mask_stride_h", ctypes.c_int64)]
 
 
 class DecodeArgs(ctypes.Structure):
@@ -150,6 +155,11 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_binary_f64_dev.argtypes = [i, ctypes.POINTER(Buf), ctypes.POINTER(Buf),
                                             ctypes.POINTER(Buf), lg, vp]
     lib.gonn_hip_flash_attn_f64_bwd_ex.argtypes = [dp] * 9 + [i, i, i, i, ctypes.c_double, i, ip]
+    lg_ = ctypes.c_long
+    lib.gonn_hip_flash_attn_f64_masked.argtypes = [dp] * 5 + [i] * 5 + [ctypes.c_double, i, ip,
+                                                                        dp, lg_, lg_]
+    lib.gonn_hip_flash_attn_f64_bwd_masked.argtypes = [dp] * 9 + [i] * 4 + [ctypes.c_double, i,
+                                                                            ip, dp, lg_, lg_]
     lib.gonn_hip_mha_create.argtypes = [ctypes.POINTER(vp), i, i, i, i] + [dp] * 8
     lib.gonn_hip_mha_free.argtypes = [vp]
     lib.gonn_hip_mha_forward_f64.argtypes = [vp, dp, dp, dp, dp, i, i, i, i, ip]

@@ -100,6 +100,21 @@ bool head_dim_ok(int D) { return D == 64 || D == 128; }
 
 size_t round_up(size_t x, size_t m) { return (x + m - 1) / m * m; }
 
+// An additive mask buffer covers every element slices read: the last
+// sequence and head at their strides plus Sq x Sk rows.
+bool mask_ok(const gonn_buf& m, int64_t sb, int64_t sh, int B, int H, int Sq, int Sk) {
+    if (!m.ptr) return true;
+    if (sb < 0 || sh < 0) return false;
+    const double need = (double)(B - 1) * sb + (double)(H - 1) * sh + (double)Sq * Sk;
+    if (need >= 9.0e15) return false;
+    return buf_ok(m, (size_t)need, GONN_F32);
+}
+
+// The kernels a call runs: an additive mask is read by the fp32-MFMA kernels
+// only, in either mode.
+int fwd_mode(const gonn_attn_fwd_args* a) { return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode; }
+int bwd_mode(const gonn_attn_bwd_args* a) { return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode; }
+
 // ---- forward -----------------------------------------------------------
 
 int check_fwd(const gonn_attn_fwd_args* a) {
@@ -112,7 +127,9 @@ int check_fwd(const gonn_attn_fwd_args* a) {
     if ((double)BH * a->Sq * a->D >= 2147483647.0 * 8 || (double)BH * a->Sk * a->D >= 2147483647.0 * 8)
         return GONN_E_UNSUPPORTED;
     const size_t nq = BH * a->Sq * a->D, nk = BH * a->Sk * a->D;
-    if (a->mode == GONN_ATTN_FP32_MFMA) {
+    if (!mask_ok(a->attn_mask, a->mask_stride_b, a->mask_stride_h, a->B, a->H, a->Sq, a->Sk))
+        return GONN_E_INVALID;
+    if (fwd_mode(a) == GONN_ATTN_FP32_MFMA) {
         if (!buf_ok(a->q, nq, GONN_F32) || !buf_ok(a->k, nk, GONN_F32) || !buf_ok(a->v, nk, GONN_F32))
             return GONN_E_INVALID;
     } else {
@@ -127,7 +144,7 @@ int check_fwd(const gonn_attn_fwd_args* a) {
 }
 
 size_t fwd_ws(const gonn_attn_fwd_args* a) {
-    if (a->mode != GONN_ATTN_BF16_MFMA) return 0;
+    if (fwd_mode(a) != GONN_ATTN_BF16_MFMA) return 0;
     const size_t BH = (size_t)a->B * a->H;
     const size_t Skp = round_up((size_t)a->Sk, 64);
     return 2 * BH * Skp * a->D * sizeof(uint16_t) + 256;
@@ -177,6 +194,8 @@ int check_bwd(const gonn_attn_bwd_args* a) {
         if (!buf_ok(*b, n, GONN_F32)) return GONN_E_INVALID;
     if (!buf_ok(a->lse, BH * a->S, GONN_F32)) return GONN_E_INVALID;
     if (a->kv_len.ptr && !buf_ok(a->kv_len, (size_t)a->B, GONN_I32)) return GONN_E_INVALID;
+    if (!mask_ok(a->attn_mask, a->mask_stride_b, a->mask_stride_h, a->B, a->H, a->S, a->S))
+        return GONN_E_INVALID;
     return GONN_OK;
 }
 
@@ -206,7 +225,7 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int D) {
 }
 
 size_t bwd_ws(const gonn_attn_bwd_args* a) {
-    return bwd_layout(a->mode, (size_t)a->B * a->H, a->S, a->D).total + 256;
+    return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, a->D).total + 256;
 }
 
 // ---- helpers for the host shims ----------------------------------------
@@ -285,8 +304,12 @@ bool shim_args_ok(int BH, int S, int d) { return BH > 0 && S > 0 && d > 0 && d <
 // optional device kv_len[B].
 int run_fwd_f32_ex(DevMem& mem, const float* q, const float* k, const float* v, float* o,
                    float* lse, int B, int H, int Sq, int Sk, int dp, double scale, int causal,
-                   const int* kv_len) {
+                   const int* kv_len, const float* mask = nullptr, size_t mask_n = 0,
+                   int64_t mask_sb = 0, int64_t mask_sh = 0) {
     gonn_attn_fwd_args a{};
+    a.attn_mask = {(void*)mask, mask ? mask_n * 4 : 0, GONN_F32};
+    a.mask_stride_b = mask_sb;
+    a.mask_stride_h = mask_sh;
     const size_t BH = (size_t)B * H, nq = BH * Sq * dp, nk = BH * Sk * dp;
     a.q = {(void*)q, nq * 4, GONN_F32};
     a.k = {(void*)k, nk * 4, GONN_F32};
@@ -476,7 +499,14 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
     }
     p.scale_log2 = p.scale_abs * gonn::kLog2e;
     p.q = a->q.ptr;
-    if (a->mode == GONN_ATTN_BF16_MFMA) {
+    const int mode = fwd_mode(a);
+    if (a->attn_mask.ptr) {
+        p.mask = (const float*)a->attn_mask.ptr;
+        p.mask_sb = a->mask_stride_b;
+        p.mask_sh = a->mask_stride_h;
+        p.mask_mul = 1.f / p.scale_abs;
+    }
+    if (mode == GONN_ATTN_BF16_MFMA) {
         const int Skp = (int)round_up((size_t)a->Sk, 64);
         uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
         const size_t half = (size_t)BH * Skp * a->D * sizeof(uint16_t);
@@ -502,8 +532,8 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
         p.v = a->v.ptr;
         p.Skp = a->Sk;
     }
-    ProfScope ps(a->mode == GONN_ATTN_BF16_MFMA ? "fwd_bf16" : "fwd_f32", s);
-    return herr(gonn::launch_fwd(p, a->mode, a->D, a->causal, a->q.dtype == GONN_BF16, s));
+    ProfScope ps(mode == GONN_ATTN_BF16_MFMA ? "fwd_bf16" : "fwd_f32", s);
+    return herr(gonn::launch_fwd(p, mode, a->D, a->causal, a->q.dtype == GONN_BF16, s));
 }
 
 int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, void* stream) {
@@ -513,9 +543,15 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     hipStream_t s = (hipStream_t)stream;
     const int BH = a->B * a->H, S = a->S, D = a->D;
     const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
-    const BwdLayout L = bwd_layout(a->mode, (size_t)BH, S, D);
+    const int mode = bwd_mode(a);
+    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, D);
     uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
     gonn::BwdParams p{};
+    if (a->attn_mask.ptr) {
+        p.mask = (const float*)a->attn_mask.ptr;
+        p.mask_sb = a->mask_stride_b;
+        p.mask_sh = a->mask_stride_h;
+    }
     p.lse2 = (const float*)(w + L.lse2);
     p.delta = (const float*)(w + L.delta);
     p.dq = (float*)a->dq.ptr;
@@ -538,7 +574,7 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
                                    (const float*)a->lse.ptr, (float*)(w + L.lse2),
                                    (float*)(w + L.delta), BH, S, Sp, D, s));
     }
-    if (a->mode == GONN_ATTN_BF16_MFMA) {
+    if (mode == GONN_ATTN_BF16_MFMA) {
         void* Qb = w + L.packed[0];
         void* dOb = w + L.packed[1];
         void* Kb = w + L.packed[2];
@@ -584,10 +620,10 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     }
     {
         ProfScope ps("bwd_dkdv", s);
-        TRYH(gonn::launch_bwd_dkdv(p, a->mode, D, a->causal, s));
+        TRYH(gonn::launch_bwd_dkdv(p, mode, D, a->causal, s));
     }
     ProfScope ps("bwd_dq", s);
-    return herr(gonn::launch_bwd_dq(p, a->mode, D, a->causal, s));
+    return herr(gonn::launch_bwd_dq(p, mode, D, a->causal, s));
 }
 
 int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_bytes, void* stream) {
@@ -741,24 +777,43 @@ int gonn_hip_flash_attn_f64_fwd(const double* Q, const double* K, const double* 
 int gonn_hip_flash_attn_f64_ex(const double* Q, const double* K, const double* V, double* O,
                                double* L, int B, int H, int Sq, int Sk, int d, double scale,
                                int causal, const int* kv_len) {
+    return gonn_hip_flash_attn_f64_masked(Q, K, V, O, L, B, H, Sq, Sk, d, scale, causal, kv_len,
+                                          nullptr, 0, 0);
+}
+
+// Elements an additive mask with these strides spans (0: bad strides).
+static size_t mask_elems(int B, int H, int Sq, int Sk, long sb, long sh) {
+    if (sb < 0 || sh < 0) return 0;
+    const double n = (double)(B - 1) * sb + (double)(H - 1) * sh + (double)Sq * Sk;
+    return n < 9.0e15 ? (size_t)n : 0;
+}
+
+int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const double* V, double* O,
+                                   double* L, int B, int H, int Sq, int Sk, int d, double scale,
+                                   int causal, const int* kv_len, const double* mask,
+                                   long mask_sb, long mask_sh) {
     if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || d <= 0 || d > 128) return GONN_E_INVALID;
     if (!Q || !K || !V || !O || !std::isfinite(scale)) return GONN_E_INVALID;
+    const size_t mn = mask ? mask_elems(B, H, Sq, Sk, mask_sb, mask_sh) : 0;
+    if (mask && !mn) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
     DevMem mem;
     const int dp = pad_dim(d);
     const size_t rq = (size_t)B * H * Sq, rk = (size_t)B * H * Sk;
-    float *q, *k, *v, *o, *l = nullptr;
+    float *q, *k, *v, *o, *l = nullptr, *m = nullptr;
     int* kl = nullptr;
     TRY(upload_padded(mem, Q, rq, d, dp, &q));
     TRY(upload_padded(mem, K, rk, d, dp, &k));
     TRY(upload_padded(mem, V, rk, d, dp, &v));
+    if (mask) TRY(upload_padded(mem, mask, mn, 1, 1, &m));
     TRY(mem.alloc((void**)&o, rq * dp * 4));
     if (L) TRY(mem.alloc((void**)&l, rq * 4));
     if (kv_len) {
         TRY(mem.alloc((void**)&kl, (size_t)B * 4));
         TRYH(hipMemcpy(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice));
     }
-    TRY(run_fwd_f32_ex(mem, q, k, v, o, l, B, H, Sq, Sk, dp, scale, causal, kl));
+    TRY(run_fwd_f32_ex(mem, q, k, v, o, l, B, H, Sq, Sk, dp, scale, causal, kl, m, mn, mask_sb,
+                       mask_sh));
     TRY(download_padded(mem, o, rq, d, dp, O));
     if (L) TRY(download_padded(mem, l, rq, 1, 1, L));
     return herr(hipDeviceSynchronize());
@@ -775,9 +830,20 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
                                    const double* O, const double* L, const double* dO, double* dQ,
                                    double* dK, double* dV, int B, int H, int S, int d,
                                    double scale, int causal, const int* kv_len) {
+    return gonn_hip_flash_attn_f64_bwd_masked(Q, K, V, O, L, dO, dQ, dK, dV, B, H, S, d, scale,
+                                              causal, kv_len, nullptr, 0, 0);
+}
+
+int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const double* V,
+                                       const double* O, const double* L, const double* dO,
+                                       double* dQ, double* dK, double* dV, int B, int H, int S,
+                                       int d, double scale, int causal, const int* kv_len,
+                                       const double* mask, long mask_sb, long mask_sh) {
     if (B <= 0 || H <= 0 || !shim_args_ok(B * H, S, d) || !Q || !K || !V || !O || !L || !dO ||
         !dQ || !dK || !dV)
         return GONN_E_INVALID;
+    const size_t mn = mask ? mask_elems(B, H, S, S, mask_sb, mask_sh) : 0;
+    if (mask && !mn) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
     const int BH = B * H;
     DevMem mem;
@@ -794,6 +860,8 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
     TRY(mem.alloc((void**)&dk, n * 4));
     TRY(mem.alloc((void**)&dv, n * 4));
     int* kl = nullptr;
+    float* m = nullptr;
+    if (mask) TRY(upload_padded(mem, mask, mn, 1, 1, &m));
     if (kv_len) {
         TRY(mem.alloc((void**)&kl, (size_t)B * 4));
         TRYH(hipMemcpy(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice));
@@ -809,6 +877,9 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
     a.dk = {dk, n * 4, GONN_F32};
     a.dv = {dv, n * 4, GONN_F32};
     a.kv_len = {kl, kl ? (size_t)B * 4 : 0, GONN_I32};
+    a.attn_mask = {m, m ? mn * 4 : 0, GONN_F32};
+    a.mask_stride_b = mask_sb;
+    a.mask_stride_h = mask_sh;
     a.B = B;
     a.H = H;
     a.S = S;

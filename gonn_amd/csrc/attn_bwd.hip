@@ -469,6 +469,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
     const float* dOg = (const float*)p.dO + (size_t)bh * S * D;
     const float* lg = p.lse2 + (size_t)bh * Sp;
     const float* dg = p.delta + (size_t)bh * Sp;
+    // The additive mask's column of this lane's key (rows S apart), if any.
+    const float* mcol = p.mask ? p.mask + (size_t)(bh / p.H) * p.mask_sb +
+                                     (size_t)(bh % p.H) * p.mask_sh + (kj < S ? kj : S - 1)
+                               : nullptr;
 
     f32x4 rq[CH], rdo[CH];
     float rl = 0.f, rd = 0.f;
@@ -533,7 +537,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
             const bool need_mask = CAUSAL && (q0 < kw + 31);
             for (int r = 0; r < 16; r++) {
                 const int qr = 8 * (r >> 2) + 4 * g + (r & 3);
-                float pv = fast_exp2(__builtin_fmaf(sacc[r], c2, -s_lse[buf][qr]));
+                float off = -s_lse[buf][qr];
+                if (mcol) {  // mask[q][kj], clamped rows and keys are not used
+                    const int qq = q0 + qr < S ? q0 + qr : S - 1;
+                    off += mcol[(size_t)qq * S] * kLog2e;
+                }
+                float pv = fast_exp2(__builtin_fmaf(sacc[r], c2, off));
                 if (need_mask && kj > q0 + qr) pv = 0.f;
                 sacc[r] = pv;
                 dpacc[r] = pv * (dpacc[r] - s_del[buf][qr]);
@@ -617,6 +626,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
     const int ntiles = (kend + BN - 1) / BN;
     const float* Kg = (const float*)p.k + (size_t)bh * S * D;
     const float* Vg = (const float*)p.v + (size_t)bh * S * D;
+    // The additive mask's row of this lane's query, if any.
+    const float* mrow = p.mask ? p.mask + (size_t)(bh / p.H) * p.mask_sb +
+                                     (size_t)(bh % p.H) * p.mask_sh +
+                                     (size_t)(qi < S ? qi : S - 1) * S
+                               : nullptr;
 
     f32x4 rk[CH], rv[CH];
     auto gload = [&](int kt) {
@@ -666,7 +680,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
         const int kbase = kt * BN;
         const bool need_mask = (kbase + BN > Skv) || (CAUSAL && kbase + BN - 1 > q0 + wave * 32);
         for (int r = 0; r < 16; r++) {
-            float pv = fast_exp2(__builtin_fmaf(sacc[r], c2, -lq));
+            float off = -lq;  // log2 units: s scale log2e + m log2e - L log2e
+            if (mrow) {
+                const int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (key < Skv) off += mrow[key] * kLog2e;
+            }
+            float pv = fast_exp2(__builtin_fmaf(sacc[r], c2, off));
             if (need_mask) {
                 const int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (key >= Skv || (CAUSAL && key > qi)) pv = 0.f;

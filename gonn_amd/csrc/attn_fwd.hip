@@ -844,6 +844,11 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(FwdParams p) {
     const int ntiles = (kend + BN - 1) / BN;
     const float* Kg = (const float*)p.k + (size_t)bh * Ss * D;
     const float* Vg = (const float*)p.v + (size_t)bh * Ss * D;
+    // The additive mask's row of this lane's query (rows Ss apart).
+    const float* mrow = p.mask ? p.mask + (size_t)(bh / p.H) * p.mask_sb +
+                                     (size_t)(bh % p.H) * p.mask_sh +
+                                     (size_t)(qi < Sq ? qi : 0) * Ss
+                               : nullptr;
 
     f32x4 kreg[CH], vreg[CH];
     auto gload = [&](int kt) {
@@ -891,6 +896,12 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(FwdParams p) {
             sacc = mfma_f32(a[3], qf[i + 3], sacc);
         }
         const int kbase = kt * BN;
+        if (mrow) {  // scale * s + m = scale_abs * (sacc + m / scale_abs)
+            for (int r = 0; r < 16; r++) {
+                const int key = kbase + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (key < Sk) sacc[r] += mrow[key] * p.mask_mul;
+            }
+        }
         const bool need_mask = (kbase + BN > Sk) || (CAUSAL && kbase + BN - 1 > q0 + wave * 32);
         if (need_mask) {
             for (int r = 0; r < 16; r++) {

@@ -21,6 +21,12 @@ struct FwdParams {
     int hgroup;        // slices whose blocks are dispatched interleaved (map_block)
     const int* kv_len; // [BH / H] valid keys per sequence, or null (all Sk)
     int H;             // heads per sequence (slice bh belongs to sequence bh / H)
+    // Optional additive mask (WithAttnMask): slice bh = b*H + h adds
+    // mask[b*mask_sb + h*mask_sh + q*Sk + key] to the scaled scores; only the
+    // fp32 kernel reads it. mask_mul = 1 / scale_abs (raw score units).
+    const float* mask;
+    long long mask_sb, mask_sh;
+    float mask_mul;
 };
 
 struct DecodeParams {
@@ -75,6 +81,9 @@ struct BwdParams {
     // their dK, dV rows are zero and they add nothing to dQ.
     const int* kv_len;
     int H;
+    // Optional additive mask, as in FwdParams (fp32 kernels only).
+    const float* mask;
+    long long mask_sb, mask_sh;
 };
 
 // Keys of slice bh that take part in the backward: S, or the sequence's

@@ -133,8 +133,16 @@ def FlashAttnF64Bwd(Q, K, V, O, L, dO, BH: int, S: int, d: int, scale: float, ca
     return dQ, dK, dV
 
 
+def _host_mask(attn_mask, B, H, Sq, Sk):
+    if attn_mask is None:
+        return None, 0, 0
+    m = np.ascontiguousarray(attn_mask, dtype=np.float64)
+    sb, sh = mask_strides(m.shape, B, H, Sq, Sk)
+    return m, sb, sh
+
+
 def FlashAttnF64BwdEx(Q, K, V, O, L, dO, B: int, H: int, S: int, d: int, scale: float,
-                      causal: bool, kv_len=None):
+                      causal: bool, kv_len=None, attn_mask=None):
     """General backward on host fp64 (B*H,S,d) arrays with the forward's
     optional key padding kv_len[B] (new): returns (dQ, dK, dV). O and L come
     from FlashAttnF64Ex(..., kv_len, lse=True) with the same kv_len."""
@@ -147,20 +155,22 @@ def FlashAttnF64BwdEx(Q, K, V, O, L, dO, B: int, H: int, S: int, d: int, scale: 
         if kl.shape != (B,):
             raise ValueError(f"FlashAttnF64BwdEx: kv_len must have {B} entries")
     dQ, dK, dV = np.zeros(n), np.zeros(n), np.zeros(n)
-    check(_lib.load().gonn_hip_flash_attn_f64_bwd_ex(
+    m, sb, sh = _host_mask(attn_mask, B, H, S, S)
+    check(_lib.load().gonn_hip_flash_attn_f64_bwd_masked(
         _p(Q), _p(K), _p(V), _p(O), _p(L), _p(dO), _p(dQ), _p(dK), _p(dV), B, H, S, d,
         float(scale), int(bool(causal)),
-        kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None),
-        "FlashAttnF64BwdEx")
+        kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
+        _p(m) if m is not None else None, sb, sh), "FlashAttnF64BwdEx")
     return dQ, dK, dV
 
 
 def FlashAttnF64Ex(Q, K, V, B: int, H: int, Sq: int, Sk: int, d: int, scale: float,
-                   causal: bool, kv_len=None, lse: bool = False):
+                   causal: bool, kv_len=None, lse: bool = False, attn_mask=None):
     """General fused forward on host fp64 arrays (new; the reference seam is
     Tq == Tk only): Q (B*H,Sq,d), K/V (B*H,Sk,d), optional prefix key padding
-    kv_len[B] (keys t >= kv_len[b] masked, ForwardMasked semantics). Returns
-    O, or (O, L) when lse is set."""
+    kv_len[B] (keys t >= kv_len[b] masked, ForwardMasked semantics) and
+    additive mask attn_mask (WithAttnMask, one of mask_strides' shapes; runs
+    the fp32-MFMA kernel). Returns O, or (O, L) when lse is set."""
     Q = _f64(Q, B * H * Sq * d, "FlashAttnF64Ex Q")
     K = _f64(K, B * H * Sk * d, "FlashAttnF64Ex K")
     V = _f64(V, B * H * Sk * d, "FlashAttnF64Ex V")
@@ -171,11 +181,12 @@ def FlashAttnF64Ex(Q, K, V, B: int, H: int, Sq: int, Sk: int, d: int, scale: flo
         kl = np.ascontiguousarray(kv_len, dtype=np.int32)
         if kl.shape != (B,):
             raise ValueError(f"FlashAttnF64Ex: kv_len must have {B} entries")
-    check(_lib.load().gonn_hip_flash_attn_f64_ex(
+    m, sb, sh = _host_mask(attn_mask, B, H, Sq, Sk)
+    check(_lib.load().gonn_hip_flash_attn_f64_masked(
         _p(Q), _p(K), _p(V), _p(O), _p(L) if L is not None else None, B, H, Sq, Sk, d,
         float(scale), int(bool(causal)),
-        kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None),
-        "FlashAttnF64Ex")
+        kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
+        _p(m) if m is not None else None, sb, sh), "FlashAttnF64Ex")
     return (O, L) if lse else O
 
 
@@ -301,8 +312,24 @@ def _shape4(t, name):
     raise ValueError(f"{name}: expected (B,H,S,D) or (BH,S,D), got {tuple(t.shape)}")
 
 
+def mask_strides(shape, B: int, H: int, Sq: int, Sk: int):
+    """expandAttnMask (nn/attention.go:242-257): the (sequence, head) element
+    strides of an additive mask of shape (Sq,Sk), (B*H,Sq,Sk), (B,Sq,Sk) or
+    (B,H,Sq,Sk); rows are Sk apart. Other shapes raise ValueError."""
+    s = tuple(int(x) for x in shape)
+    if s == (Sq, Sk):
+        return 0, 0
+    if s == (B * H, Sq, Sk) or s == (B, H, Sq, Sk):
+        return H * Sq * Sk, Sq * Sk
+    if s == (B, Sq, Sk):
+        return Sq * Sk, 0
+    raise ValueError(f"MultiHeadAttention: attn mask shape {list(s)} incompatible with "
+                     f"(Tq,Tk)=({Sq},{Sk}), (B,Tq,Tk) B={B}, (B*H,Tq,Tk) B*H={B * H}, "
+                     f"or (B,H,Tq,Tk)")
+
+
 def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None,
-             lse=True, lse_out=None, kv_len=None, stream=None):
+             lse=True, lse_out=None, kv_len=None, stream=None, attn_mask=None):
     """O = softmax(scale QK^T + mask) V on device tensors.
 
     q (B,H,Sq,D) or (BH,Sq,D); k, v (.., Sk, D). fp32 mode needs float32
@@ -310,7 +337,9 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
     float32 like q and LSE float32 (B*H, Sq) in natural-log units (or None when
     lse is False). out / lse_out may supply preallocated outputs. kv_len: an
     optional int32 device tensor (B,) of valid keys per sequence (prefix key
-    padding; a 3-D q counts each slice as its own sequence).
+    padding; a 3-D q counts each slice as its own sequence). attn_mask: an
+    optional float32 device tensor, the additive mask of WithAttnMask in one
+    of mask_strides' shapes (runs the fp32-MFMA kernel in either mode).
     """
     torch = _torch()
     B, H, Sq, D = _shape4(q, "q")
@@ -322,8 +351,13 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
     l = lse_out
     if l is None and lse:
         l = torch.empty((B * H, Sq), dtype=torch.float32, device=q.device)
+    mb, sb, sh = Buf(), 0, 0
+    if attn_mask is not None:
+        sb, sh = mask_strides(attn_mask.shape, B, H, Sq, Sk)
+        mb = buf(attn_mask)
     a = FwdArgs(buf(q), buf(k), buf(v), buf(out), buf(l), B, H, Sq, Sk, D, float(scale),
-                int(bool(causal)), MODES[mode], buf(kv_len) if kv_len is not None else Buf())
+                int(bool(causal)), MODES[mode], buf(kv_len) if kv_len is not None else Buf(),
+                mb, sb, sh)
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_FWD, ctypes.byref(a))
@@ -334,10 +368,11 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
 
 
 def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp32",
-             out=None, stream=None, kv_len=None):
+             out=None, stream=None, kv_len=None, attn_mask=None):
     """dQ, dK, dV (float32) from the saved forward tensors (all float32).
     out may supply preallocated (dq, dk, dv). kv_len: optional int32 (B,)
-    device tensor, the key padding the forward was run with."""
+    device tensor, the key padding the forward was run with; attn_mask: its
+    additive mask."""
     torch = _torch()
     B, H, S, D = _shape4(q, "q")
     if scale is None:
@@ -347,9 +382,13 @@ def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp3
                       for _ in range(3))
     else:
         dq, dk, dv = out
+    mb, sb, sh = Buf(), 0, 0
+    if attn_mask is not None:
+        sb, sh = mask_strides(attn_mask.shape, B, H, S, S)
+        mb = buf(attn_mask)
     a = BwdArgs(buf(q), buf(k), buf(v), buf(o), buf(lse), buf(dO), buf(dq), buf(dk), buf(dv),
                 B, H, S, D, float(scale), int(bool(causal)), MODES[mode], 1,
-                buf(kv_len) if kv_len is not None else Buf(None, 0, GONN_I32))
+                buf(kv_len) if kv_len is not None else Buf(None, 0, GONN_I32), mb, sb, sh)
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
@@ -590,7 +629,7 @@ class DeviceMHA:
 
 __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "SelftestMFMA",
            "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex",
-           "FlashAttnF64BwdEx", "Gemm",
+           "FlashAttnF64BwdEx", "mask_strides", "Gemm",
            "Unary", "Binary",
            "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "DeviceMHA", "buf",
            "GonnHipError"]

@@ -90,6 +90,19 @@ std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vect
 FwdOut FlashAttnF64ExFwd(const std::vector<double>& Q, const std::vector<double>& K,
                          const std::vector<double>& V, int B, int H, int Sq, int Sk, int d,
                          double scale, bool causal, const std::vector<int>& kvLen = {});
+// New: forward and backward with an additive mask (WithAttnMask) as well:
+// mask is host fp64 read at b*maskSB + h*maskSH + i*Sk + j (rows S apart in
+// the backward); empty = none. They run the fp32-MFMA kernels.
+FwdOut FlashAttnF64Masked(const std::vector<double>& Q, const std::vector<double>& K,
+                          const std::vector<double>& V, int B, int H, int Sq, int Sk, int d,
+                          double scale, bool causal, const std::vector<int>& kvLen,
+                          const std::vector<double>& mask, long maskSB, long maskSH);
+BwdOut FlashAttnF64BwdMasked(const std::vector<double>& Q, const std::vector<double>& K,
+                             const std::vector<double>& V, const std::vector<double>& O,
+                             const std::vector<double>& L, const std::vector<double>& dO, int B,
+                             int H, int S, int d, double scale, bool causal,
+                             const std::vector<int>& kvLen, const std::vector<double>& mask,
+                             long maskSB, long maskSH);
 // New: the backward of a square (S x S) forward with key padding kvLen[B]
 // (empty = none); O and L from FlashAttnF64ExFwd with the same kvLen.
 BwdOut FlashAttnF64BwdEx(const std::vector<double>& Q, const std::vector<double>& K,
@@ -263,10 +276,18 @@ struct DiffOut {
     Tensor Out;
     FlashAttnNode Node;
 };
-// kvLen (new, BH / H entries or empty): the key padding of ForwardMasked, in
-// the forward and in the node's backward.
+// kvLen (new, BH / H entries or empty): the key padding of ForwardMasked;
+// attnMask (new, empty = none): its additive mask in one of expandAttnMask's
+// shapes for B = BH / H; both in the forward and in the node's backward.
 DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
-                      double scale, bool causal, const std::vector<int>& kvLen = {}, int H = 1);
+                      double scale, bool causal, const std::vector<int>& kvLen = {}, int H = 1,
+                      const Tensor& attnMask = Tensor{});
+
+// expandAttnMask (nn/attention.go:242-257): the (sequence, head) element
+// strides of an additive mask of shape (Tq,Tk), (B*H,Tq,Tk), (B,Tq,Tk) or
+// (B,H,Tq,Tk); throws std::invalid_argument with the reference's message
+// for any other shape.
+std::array<long, 2> maskStrides(const std::vector<int>& shape, int B, int H, int Tq, int Tk);
 
 // nn.MultiHeadAttention with the fused core (nn/attention.go:38-180).
 // Weights are given explicitly: GoNN draws them from Go's math/rand stream
@@ -285,12 +306,13 @@ class MultiHeadAttention {
     // takes Tq != Tk (cross-attention), which the reference's gate sends to
     // its CPU path.
     Tensor ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
-    // ForwardMasked (nn/attention.go:305-341) on the fused core with causal
-    // and a (B, Tk) key-padding mask (nonzero = ignore; the padded keys of a
-    // row must be a suffix). An empty keyPad means none. Inference; the
-    // differentiable form is fusedAttnDiff with kvLen.
+    // ForwardMasked (nn/attention.go:305-341) on the fused core with causal,
+    // a (B, Tk) key-padding mask (nonzero = ignore; the padded keys of a row
+    // must be a suffix) and an additive attnMask in any of expandAttnMask's
+    // shapes (runs the fp32-MFMA kernel). Empty tensors mean none. Inference;
+    // the differentiable form is fusedAttnDiff with kvLen and attnMask.
     Tensor ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
-                         const Tensor& keyPad);
+                         const Tensor& keyPad, const Tensor& attnMask = Tensor{});
 
     FlashAttnNode LastNode;
 
@@ -312,7 +334,7 @@ class MultiHeadAttention {
     void checkQKVDims(const Tensor& q, const Tensor& k, const Tensor& v) const;
     void requireFused(int D, int Tq, int Tk) const;
     Tensor fusedGeneral(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
-                        const std::vector<int>& kvLen);
+                        const std::vector<int>& kvLen, const Tensor& attnMask = Tensor{});
 };
 
 // MultiHeadAttention::Forward / ForwardMasked on a hip::DeviceMHA; the same

@@ -134,6 +134,67 @@ std::vector<double> FlashAttnF64Ex(const std::vector<double>& Q, const std::vect
     return FlashAttnF64ExFwd(Q, K, V, B, H, Sq, Sk, d, scale, causal, kvLen).O;
 }
 
+// Elements a mask with these strides spans.
+static size_t mask_span(int B, int H, int Sq, int Sk, long sb, long sh) {
+    if (sb < 0 || sh < 0) throw std::invalid_argument("hip: mask strides must be >= 0");
+    return (size_t)(B - 1) * sb + (size_t)(H - 1) * sh + (size_t)Sq * Sk;
+}
+
+FwdOut FlashAttnF64Masked(const std::vector<double>& Q, const std::vector<double>& K,
+                          const std::vector<double>& V, int B, int H, int Sq, int Sk, int d,
+                          double scale, bool causal, const std::vector<int>& kvLen,
+                          const std::vector<double>& mask, long maskSB, long maskSH) {
+    if (B <= 0 || H <= 0 || Sq <= 0 || Sk <= 0 || d <= 0)
+        throw std::invalid_argument("hip: FlashAttnF64Masked: B, H, Sq, Sk, d must be >= 1");
+    const size_t nq = (size_t)B * H * Sq * d, nk = (size_t)B * H * Sk * d;
+    need(Q, nq, "FlashAttnF64Masked Q");
+    need(K, nk, "FlashAttnF64Masked K");
+    need(V, nk, "FlashAttnF64Masked V");
+    if (!mask.empty()) need(mask, mask_span(B, H, Sq, Sk, maskSB, maskSH), "FlashAttnF64Masked mask");
+    if (!kvLen.empty() && (int)kvLen.size() != B)
+        throw std::invalid_argument("hip: FlashAttnF64Masked: kvLen needs B entries");
+    FwdOut r;
+    r.O.assign(nq, 0.0);
+    r.L.assign((size_t)B * H * Sq, 0.0);
+    check(gonn_hip_flash_attn_f64_masked(Q.data(), K.data(), V.data(), r.O.data(), r.L.data(), B,
+                                         H, Sq, Sk, d, scale, causal ? 1 : 0,
+                                         kvLen.empty() ? nullptr : kvLen.data(),
+                                         mask.empty() ? nullptr : mask.data(), maskSB, maskSH),
+          "FlashAttnF64Masked");
+    return r;
+}
+
+BwdOut FlashAttnF64BwdMasked(const std::vector<double>& Q, const std::vector<double>& K,
+                             const std::vector<double>& V, const std::vector<double>& O,
+                             const std::vector<double>& L, const std::vector<double>& dO, int B,
+                             int H, int S, int d, double scale, bool causal,
+                             const std::vector<int>& kvLen, const std::vector<double>& mask,
+                             long maskSB, long maskSH) {
+    if (B <= 0 || H <= 0) throw std::invalid_argument("hip: FlashAttnF64BwdMasked: B, H must be >= 1");
+    shape_ok(B * H, S, d, "FlashAttnF64BwdMasked");
+    const size_t n = (size_t)B * H * S * d;
+    need(Q, n, "FlashAttnF64BwdMasked Q");
+    need(K, n, "FlashAttnF64BwdMasked K");
+    need(V, n, "FlashAttnF64BwdMasked V");
+    need(O, n, "FlashAttnF64BwdMasked O");
+    need(L, (size_t)B * H * S, "FlashAttnF64BwdMasked L");
+    need(dO, n, "FlashAttnF64BwdMasked dO");
+    if (!mask.empty()) need(mask, mask_span(B, H, S, S, maskSB, maskSH), "FlashAttnF64BwdMasked mask");
+    if (!kvLen.empty() && (int)kvLen.size() != B)
+        throw std::invalid_argument("hip: FlashAttnF64BwdMasked: kvLen needs B entries");
+    BwdOut r;
+    r.dQ.assign(n, 0.0);
+    r.dK.assign(n, 0.0);
+    r.dV.assign(n, 0.0);
+    check(gonn_hip_flash_attn_f64_bwd_masked(Q.data(), K.data(), V.data(), O.data(), L.data(),
+                                             dO.data(), r.dQ.data(), r.dK.data(), r.dV.data(), B,
+                                             H, S, d, scale, causal ? 1 : 0,
+                                             kvLen.empty() ? nullptr : kvLen.data(),
+                                             mask.empty() ? nullptr : mask.data(), maskSB, maskSH),
+          "FlashAttnF64BwdMasked");
+    return r;
+}
+
 BwdOut FlashAttnF64BwdEx(const std::vector<double>& Q, const std::vector<double>& K,
                          const std::vector<double>& V, const std::vector<double>& O,
                          const std::vector<double>& L, const std::vector<double>& dO, int B,

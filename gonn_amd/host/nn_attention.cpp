@@ -99,9 +99,16 @@ std::vector<double> fusedAttnF64(const std::vector<double>& Q, const std::vector
 }
 
 DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
-                      double scale, bool causal, const std::vector<int>& kvLen, int H) {
+                      double scale, bool causal, const std::vector<int>& kvLen, int H,
+                      const Tensor& attnMask) {
     if (H <= 0 || BH % H != 0) throw std::invalid_argument("fusedAttnDiff: BH must be a multiple of H");
-    hip::FwdOut f = kvLen.empty()
+    const bool masked = !attnMask.Data.empty();
+    std::array<long, 2> st{0, 0};
+    if (masked) st = maskStrides(attnMask.Shape, BH / H, H, S, S);
+    auto mask = std::make_shared<std::vector<double>>(attnMask.Data);
+    hip::FwdOut f = masked ? hip::FlashAttnF64Masked(qp.Data, kp.Data, vp.Data, BH / H, H, S, S,
+                                                     D, scale, causal, kvLen, *mask, st[0], st[1])
+                    : kvLen.empty()
                         ? hip::FlashAttnF64Fwd(qp.Data, kp.Data, vp.Data, BH, S, D, scale, causal)
                         : hip::FlashAttnF64ExFwd(qp.Data, kp.Data, vp.Data, BH / H, H, S, S, D,
                                                  scale, causal, kvLen);
@@ -112,10 +119,13 @@ DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int 
     auto saved = std::make_shared<std::array<Tensor, 3>>(std::array<Tensor, 3>{qp, kp, vp});
     auto O = std::make_shared<std::vector<double>>(std::move(f.O));
     auto L = std::make_shared<std::vector<double>>(std::move(f.L));
-    r.Node.Backward = [saved, O, L, BH, S, D, scale, causal, kvLen, H](const Tensor& grad) {
+    r.Node.Backward = [saved, O, L, BH, S, D, scale, causal, kvLen, H, masked, mask,
+                       st](const Tensor& grad) {
         const Tensor &q = (*saved)[0], &k = (*saved)[1], &v = (*saved)[2];
         hip::BwdOut b =
-            kvLen.empty()
+            masked ? hip::FlashAttnF64BwdMasked(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH / H,
+                                                H, S, D, scale, causal, kvLen, *mask, st[0], st[1])
+            : kvLen.empty()
                 ? hip::FlashAttnF64Bwd(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH, S, D, scale,
                                        causal)
                 : hip::FlashAttnF64BwdEx(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH / H, H, S,
@@ -185,8 +195,22 @@ Tensor MultiHeadAttention::Forward(const Tensor& q, const Tensor& k, const Tenso
     return OutProj.Forward(ctx);                                         // :132
 }
 
+std::array<long, 2> maskStrides(const std::vector<int>& s, int B, int H, int Tq, int Tk) {
+    const long qk = (long)Tq * Tk;
+    if (s.size() == 2 && s[0] == Tq && s[1] == Tk) return {0, 0};
+    if (s.size() == 3 && s[0] == B * H && s[1] == Tq && s[2] == Tk) return {H * qk, qk};
+    if (s.size() == 3 && s[0] == B && s[1] == Tq && s[2] == Tk) return {qk, 0};
+    if (s.size() == 4 && s[0] == B && s[1] == H && s[2] == Tq && s[3] == Tk) return {H * qk, qk};
+    throw std::invalid_argument("MultiHeadAttention: attn mask shape " + shape_str(s) +
+                                " incompatible with (Tq,Tk)=(" + std::to_string(Tq) + "," +
+                                std::to_string(Tk) + "), (B,Tq,Tk) B=" + std::to_string(B) +
+                                ", (B*H,Tq,Tk) B*H=" + std::to_string(B * H) +
+                                ", or (B,H,Tq,Tk)");
+}
+
 Tensor MultiHeadAttention::fusedGeneral(const Tensor& q, const Tensor& k, const Tensor& v,
-                                        bool causal, const std::vector<int>& kvLen) {
+                                        bool causal, const std::vector<int>& kvLen,
+                                        const Tensor& attnMask) {
     const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1], H = NumHeads, D = HeadDim;
     if (!fusedAttnAvailable())
         throw hip::Error(-5, "nn: fused attention needs libgonn_hip.so and a gfx950 device");
@@ -197,8 +221,15 @@ Tensor MultiHeadAttention::fusedGeneral(const Tensor& q, const Tensor& k, const 
     const Tensor kp = KProj.Forward(k).Reshape({B, Tk, H, D}).Permute0213();
     const Tensor vp = VProj.Forward(v).Reshape({B, Tk, H, D}).Permute0213();
     const double scale = 1.0 / std::sqrt((double)D);
-    std::vector<double> O =
-        hip::FlashAttnF64Ex(qp.Data, kp.Data, vp.Data, B, H, Tq, Tk, D, scale, causal, kvLen);
+    std::vector<double> O;
+    if (attnMask.Data.empty()) {
+        O = hip::FlashAttnF64Ex(qp.Data, kp.Data, vp.Data, B, H, Tq, Tk, D, scale, causal, kvLen);
+    } else {
+        const auto st = maskStrides(attnMask.Shape, B, H, Tq, Tk);
+        O = hip::FlashAttnF64Masked(qp.Data, kp.Data, vp.Data, B, H, Tq, Tk, D, scale, causal,
+                                    kvLen, attnMask.Data, st[0], st[1])
+                .O;
+    }
     const Tensor ctx = Tensor::New(std::move(O), {B, H, Tq, D}).Permute0213().Reshape({B, Tq, EmbedDim});
     return OutProj.Forward(ctx);
 }
@@ -233,11 +264,13 @@ static std::vector<int> kv_len_from_mask(const Tensor& keyPad, int B, int Tk) {
 }
 
 Tensor MultiHeadAttention::ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v,
-                                         bool causal, const Tensor& keyPad) {
+                                         bool causal, const Tensor& keyPad,
+                                         const Tensor& attnMask) {
     checkQKVDims(q, k, v);
     const int B = q.Shape[0], Tk = k.Shape[1];
     const std::vector<int> kvLen = kv_len_from_mask(keyPad, B, Tk);
-    return fusedGeneral(q, k, v, causal, kvLen);
+    if (!attnMask.Data.empty()) maskStrides(attnMask.Shape, B, NumHeads, q.Shape[1], Tk);
+    return fusedGeneral(q, k, v, causal, kvLen, attnMask);
 }
 
 Tensor MultiHeadAttention::ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v,

@@ -46,36 +46,38 @@ class FusedAttnNode:
     nn/flashattn_cuda.go:29-37): holds what the backward needs and runs the
     device backward when called with the upstream gradient."""
 
-    def __init__(self, Q, K, V, O, L, BH, S, D, scale, causal, kv_len=None, H=1):
+    def __init__(self, Q, K, V, O, L, BH, S, D, scale, causal, kv_len=None, H=1, attn_mask=None):
         self.saved = (Q, K, V, O, L)
         self.shape = (BH, S, D)
         self.scale = scale
         self.causal = causal
-        self.kv_len, self.H = kv_len, H
+        self.kv_len, self.H, self.attn_mask = kv_len, H, attn_mask
 
     def __call__(self, grad):
         Q, K, V, O, L = self.saved
         BH, S, D = self.shape
-        if self.kv_len is None:
+        if self.kv_len is None and self.attn_mask is None:
             return hip.FlashAttnF64Bwd(Q, K, V, O, L, grad, BH, S, D, self.scale, self.causal)
         return hip.FlashAttnF64BwdEx(Q, K, V, O, L, grad, BH // self.H, self.H, S, D,
-                                     self.scale, self.causal, kv_len=self.kv_len)
+                                     self.scale, self.causal, kv_len=self.kv_len,
+                                     attn_mask=self.attn_mask)
 
 
 def fused_attn_diff(qp, kp, vp, BH: int, S: int, D: int, scale: float, causal: bool,
-                    kv_len=None, H: int = 1):
+                    kv_len=None, H: int = 1, attn_mask=None):
     """Differentiable core: returns (O, node) where node(dO) -> (dQ, dK, dV).
     kv_len (new): optional per-sequence key counts (BH / H entries), the key
-    padding of ForwardMasked, in the forward and the backward."""
-    if kv_len is None:
+    padding of ForwardMasked; attn_mask (new): its additive mask; both in the
+    forward and the backward."""
+    if kv_len is None and attn_mask is None:
         O, L = hip.FlashAttnF64Fwd(qp, kp, vp, BH, S, D, scale, causal)
     else:
         O, L = hip.FlashAttnF64Ex(qp, kp, vp, BH // H, H, S, S, D, scale, causal,
-                                  kv_len=kv_len, lse=True)
+                                  kv_len=kv_len, lse=True, attn_mask=attn_mask)
     return O, FusedAttnNode(np.ascontiguousarray(qp, dtype=np.float64).ravel(),
                             np.ascontiguousarray(kp, dtype=np.float64).ravel(),
                             np.ascontiguousarray(vp, dtype=np.float64).ravel(), O, L, BH, S, D,
-                            scale, causal, kv_len, H)
+                            scale, causal, kv_len, H, attn_mask)
 
 
 class Linear:
@@ -165,7 +167,7 @@ class MultiHeadAttention:
 
     forward = forward_fused
 
-    def _fused(self, q, k, v, causal, kv_len):
+    def _fused(self, q, k, v, causal, kv_len, attn_mask=None):
         B, Tq, _ = q.shape
         Tk = k.shape[1]
         H, D = self.NumHeads, self.HeadDim
@@ -173,30 +175,36 @@ class MultiHeadAttention:
         kp = self._split(self.KProj.forward(k))
         vp = self._split(self.VProj.forward(v))
         scale = 1.0 / math.sqrt(D)
-        if Tq == Tk and kv_len is None:
+        if Tq == Tk and kv_len is None and attn_mask is None:
             O = fused_attn_f64(qp, kp, vp, B * H, Tq, D, scale, causal)
         else:
-            # the wider gate: cross-attention and / or prefix key padding
-            O = hip.FlashAttnF64Ex(qp, kp, vp, B, H, Tq, Tk, D, scale, causal, kv_len=kv_len)
+            # the wider gate: cross-attention, prefix key padding, additive mask
+            O = hip.FlashAttnF64Ex(qp, kp, vp, B, H, Tq, Tk, D, scale, causal, kv_len=kv_len,
+                                   attn_mask=attn_mask)
         ctx = O.reshape(B, H, Tq, D).transpose(0, 2, 1, 3).reshape(B, Tq, self.EmbedDim)
         return self.OutProj.forward(ctx)
 
     def forward_masked(self, q, k, v, causal: bool = False, key_padding_mask=None,
                        attn_mask=None, dropout: float = 0.0):
-        """ForwardMasked (nn/attention.go:305-341) on the fused core: causal
-        and a (B, Tk) key-padding mask (nonzero = ignore the key) whose padded
-        keys form a suffix of each row, which is how padded batches look. An
-        additive attn_mask, attention dropout or a padding mask with holes are
-        not fused (the reference always runs ForwardMasked on its CPU path;
-        this library has none) and raise ValueError."""
-        if attn_mask is not None or dropout:
-            raise ValueError("nn: the fused core takes no additive attn mask or dropout")
+        """ForwardMasked (nn/attention.go:305-341) on the fused core: causal,
+        an additive attn_mask in any of expandAttnMask's shapes (runs the
+        fp32-MFMA kernel), and a (B, Tk) key-padding mask (nonzero = ignore
+        the key) whose padded keys form a suffix of each row, which is how
+        padded batches look. Attention dropout (Go's math/rand stream) and a
+        padding mask with holes are not fused (the reference always runs
+        ForwardMasked on its CPU path; this library has none) and raise
+        ValueError."""
+        if dropout:
+            raise ValueError("nn: the fused core takes no attention dropout")
         q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
         self._check(q, k, v)
         if not fused_attn_available():
             raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
         kv_len = _kv_len_from_mask(key_padding_mask, q.shape[0], k.shape[1])
-        return self._fused(q, k, v, causal, kv_len)
+        if attn_mask is not None:
+            hip.mask_strides(np.shape(attn_mask), q.shape[0], self.NumHeads, q.shape[1],
+                             k.shape[1])  # expandAttnMask's shape check
+        return self._fused(q, k, v, causal, kv_len, attn_mask)
 
     # ---- device-resident forward (new: weights and intermediates in HBM) ----
     def to_device(self) -> "ResidentMultiHeadAttention":
@@ -278,7 +286,8 @@ class ResidentMultiHeadAttention:
     def forward_masked(self, q, k, v, causal: bool = False, key_padding_mask=None,
                        attn_mask=None, dropout: float = 0.0):
         if attn_mask is not None or dropout:
-            raise ValueError("nn: the fused core takes no additive attn mask or dropout")
+            raise ValueError("nn: the resident layer takes no additive attn mask or dropout "
+                             "(MultiHeadAttention.forward_masked takes the mask)")
         same_k, same_v = k is q, v is k
         q = np.asarray(q, dtype=np.float64)
         k = q if same_k else np.asarray(k, dtype=np.float64)

@@ -91,6 +91,16 @@ typedef struct {
     int causal;
     int mode; /* gonn_attn_mode */
     gonn_buf kv_len;
+    /* Optional additive mask (WithAttnMask, nn/attention.go:212-257):
+     * GONN_F32 device data, ptr NULL = none. Slice b*H + h adds
+     * attn_mask[b*mask_stride_b + h*mask_stride_h + i*Sk + j] to the scaled
+     * score of query i and key j, after the causal mask and before the key
+     * padding, as ForwardMasked orders them. Strides (elements, >= 0) of 0
+     * broadcast: (Sq,Sk) -> 0, 0; (B,Sq,Sk) -> Sq*Sk, 0; (B*H,Sq,Sk) and
+     * (B,H,Sq,Sk) -> H*Sq*Sk, Sq*Sk. A masked call runs the fp32-MFMA
+     * kernels in either mode and needs GONN_F32 q, k, v.                    */
+    gonn_buf attn_mask;
+    int64_t mask_stride_b, mask_stride_h;
 } gonn_attn_fwd_args;
 
 /* Backward from the saved forward tensors: dQ, dK, dV (all GONN_F32).
@@ -111,6 +121,10 @@ typedef struct {
     int mode;
     int deterministic;
     gonn_buf kv_len;
+    /* The forward's additive mask (layout as in gonn_attn_fwd_args with
+     * Sq = Sk = S); a masked call runs the fp32-MFMA kernels.              */
+    gonn_buf attn_mask;
+    int64_t mask_stride_b, mask_stride_h;
 } gonn_attn_bwd_args;
 
 /* KV-cache decode, one query per (b, h): o[b,h] = attention of q[b,h] over
@@ -319,6 +333,20 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
                                    const double* O, const double* L, const double* dO, double* dQ,
                                    double* dK, double* dV, int B, int H, int S, int d,
                                    double scale, int causal, const int* kv_len);
+
+/* Additive-mask forms of the two general fp64 entries (new): mask is host
+ * fp64 data read as in gonn_attn_fwd_args.attn_mask with element strides
+ * mask_sb (sequence) and mask_sh (head) and rows Sk apart (S for the
+ * backward); NULL = none. They run the fp32-MFMA kernels in either mode.  */
+int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const double* V, double* O,
+                                   double* L, int B, int H, int Sq, int Sk, int d, double scale,
+                                   int causal, const int* kv_len, const double* mask,
+                                   long mask_sb, long mask_sh);
+int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const double* V,
+                                       const double* O, const double* L, const double* dO,
+                                       double* dQ, double* dK, double* dV, int B, int H, int S,
+                                       int d, double scale, int causal, const int* kv_len,
+                                       const double* mask, long mask_sb, long mask_sh);
 /* New (the reference's fused seam is Tq == Tk, causal-or-not only): the
  * general forward on host fp64 arrays for the wider fused gate, i.e.
  * cross-attention (Sq != Sk, top-left causal mask when causal) and

@@ -15,7 +15,9 @@ Pinning (each check lives in tests/test_oracle.py):
   attn_bwd_autograd torch fp64 autograd, central finite differences with the
                     flashbwd protocol (benchmark/flashbwd/main.go:32-95); with
                     kv_len, torch fp64 autograd through an explicit key mask
-                    and exact zeros on the padded keys' dK, dV.
+                    and exact zeros on the padded keys' dK, dV; with an
+                    additive attn_mask, torch fp64 autograd through the same
+                    mask in all four of expandAttnMask's shapes.
   attn_bwd_rows     equal to attn_bwd_autograd on every row (1e-12).
   linear / mha_fwd  torch fp64 F.linear / the composed reference sequence.
 Planted-mistake tests show each of these checks fails on a plausible bug.
@@ -50,7 +52,11 @@ def _load():
     lib.oracle_attn_bwd_autograd.argtypes = [_dp] * 7 + [ctypes.c_int] * 3 + [
         ctypes.c_double, ctypes.c_int]
     lib.oracle_attn_bwd_autograd_ex.argtypes = [_dp] * 7 + [ctypes.c_int] * 4 + [
-        ctypes.c_double, ctypes.c_int, _ip]
+        ctypes.c_double, ctypes.c_int, _ip, _dp, ctypes.c_long, ctypes.c_long]
+    lib.oracle_attn_fwd_ex.argtypes = [_dp, _dp, _dp, _dp, _dp, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_double, ctypes.c_int, _ip, _dp, ctypes.c_long,
+                                       ctypes.c_long, _ip, ctypes.c_int]
     lib.oracle_attn_bwd_rows.argtypes = [_dp] * 9 + [ctypes.c_int] * 3 + [
         ctypes.c_double, ctypes.c_int, _ip, ctypes.c_int, _ip, ctypes.c_int]
     lib.oracle_linear.argtypes = [_dp, _dp, _dp, _dp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
@@ -87,11 +93,29 @@ def get_threads() -> int:
     return int(_load().oracle_get_threads())
 
 
-def attn_fwd(Q, K, V, scale=None, causal=False, kv_len=None, H=1, rows=None):
+def mask_layout(mask, B, H, Sq, Sk):
+    """expandAttnMask (nn/attention.go:242-257): an additive mask of shape
+    (Sq,Sk), (B*H,Sq,Sk), (B,Sq,Sk) or (B,H,Sq,Sk) as (flat fp64 data, batch
+    stride, head stride) in elements; rows are Sk apart."""
+    m = _c64(mask)
+    s = m.shape
+    if s == (Sq, Sk):
+        return m.ravel(), 0, 0
+    if s == (B * H, Sq, Sk):
+        return m.ravel(), H * Sq * Sk, Sq * Sk
+    if s == (B, Sq, Sk):
+        return m.ravel(), Sq * Sk, 0
+    if s == (B, H, Sq, Sk):
+        return m.ravel(), H * Sq * Sk, Sq * Sk
+    raise ValueError(f"attn mask shape {s} incompatible with (Tq,Tk)=({Sq},{Sk})")
+
+
+def attn_fwd(Q, K, V, scale=None, causal=False, kv_len=None, H=1, rows=None, attn_mask=None):
     """Forward core. Q (BH,Sq,D), K/V (BH,Sk,D) -> (O (BH,Sq,D), LSE (BH,Sq)).
 
     kv_len: per-batch valid key counts (length BH/H) or None.
     rows: optional query rows to compute; other rows of O/LSE are NaN.
+    attn_mask: optional additive mask in one of mask_layout's shapes.
     """
     lib = _load()
     Q, K, V = _c64(Q), _c64(K), _c64(V)
@@ -110,19 +134,23 @@ def attn_fwd(Q, K, V, scale=None, causal=False, kv_len=None, H=1, rows=None):
     if rows is not None:
         r = np.ascontiguousarray(rows, dtype=np.int32)
         nr = int(r.shape[0])
-    rc = lib.oracle_attn_fwd(_d(Q), _d(K), _d(V), _d(O), _d(L), BH, H, Sq, Sk, D,
-                             float(scale), int(bool(causal)),
-                             kl.ctypes.data_as(_ip) if kl is not None else None,
-                             r.ctypes.data_as(_ip) if r is not None else None, nr)
+    am, sb, sh = (None, 0, 0)
+    if attn_mask is not None:
+        am, sb, sh = mask_layout(attn_mask, BH // H, H, Sq, Sk)
+    rc = lib.oracle_attn_fwd_ex(_d(Q), _d(K), _d(V), _d(O), _d(L), BH, H, Sq, Sk, D,
+                                float(scale), int(bool(causal)),
+                                kl.ctypes.data_as(_ip) if kl is not None else None,
+                                _d(am) if am is not None else None, sb, sh,
+                                r.ctypes.data_as(_ip) if r is not None else None, nr)
     if rc != 0:
         raise RuntimeError(f"oracle_attn_fwd failed: {rc}")
     return O, L
 
 
-def attn_bwd_autograd(Q, K, V, dO, scale=None, causal=False, kv_len=None, H=1):
+def attn_bwd_autograd(Q, K, V, dO, scale=None, causal=False, kv_len=None, H=1, attn_mask=None):
     """Backward through the reference's autograd chain -> (dQ, dK, dV).
     kv_len: optional per-batch valid key counts (BH/H entries), the key
-    padding mask of ForwardMasked."""
+    padding mask of ForwardMasked; attn_mask: its additive mask."""
     lib = _load()
     Q, K, V, dO = _c64(Q), _c64(K), _c64(V), _c64(dO)
     BH, S, D = Q.shape
@@ -133,9 +161,13 @@ def attn_bwd_autograd(Q, K, V, dO, scale=None, causal=False, kv_len=None, H=1):
     if kv_len is not None:
         kl = np.ascontiguousarray(kv_len, dtype=np.int32)
         assert kl.shape == (BH // H,)
+    am, sb, sh = (None, 0, 0)
+    if attn_mask is not None:
+        am, sb, sh = mask_layout(attn_mask, BH // H, H, S, S)
     rc = lib.oracle_attn_bwd_autograd_ex(_d(Q), _d(K), _d(V), _d(dO), _d(dQ), _d(dK), _d(dV),
                                          BH, int(H), S, D, float(scale), int(bool(causal)),
-                                         kl.ctypes.data_as(_ip) if kl is not None else None)
+                                         kl.ctypes.data_as(_ip) if kl is not None else None,
+                                         _d(am) if am is not None else None, sb, sh)
     if rc != 0:
         raise RuntimeError(f"oracle_attn_bwd_autograd failed: {rc}")
     return dQ, dK, dV
@@ -191,7 +223,7 @@ def merge_heads(x, B, H):
     return out
 
 
-def mha_fwd(q, k, v, params, H, causal=False, key_pad=None):
+def mha_fwd(q, k, v, params, H, causal=False, key_pad=None, attn_mask=None):
     """MultiHeadAttention.Forward (nn/attention.go:107-148) / ForwardMasked with
     WithKeyPaddingMask (nn/attention.go:305-341) in fp64.
 
@@ -212,7 +244,8 @@ def mha_fwd(q, k, v, params, H, causal=False, key_pad=None):
             ln = int(nz[0]) if nz.size else kp_arr.shape[1]
             assert np.all(kp_arr[b, ln:] != 0), "only prefix padding masks are supported"
             kv_len.append(ln)
-    O, _ = attn_fwd(qp, kp, vp, 1.0 / math.sqrt(E // H), causal, kv_len=kv_len, H=H)
+    O, _ = attn_fwd(qp, kp, vp, 1.0 / math.sqrt(E // H), causal, kv_len=kv_len, H=H,
+                    attn_mask=attn_mask)
     ctx = merge_heads(O, B, H)
     return linear(ctx, params["Wo"], params["bo"])
 

@@ -112,11 +112,13 @@ static inline int masked(int i, int j, int causal, int len) {
 /*
  * Scores of one (b,h) slice for the listed query rows, after scale and masks:
  * out (nrows, Sk). rows == NULL means rows 0..Sq-1. The additive masks are
- * added exactly like the reference (x + (-1e30)), not by assignment.
+ * added exactly like the reference (x + (-1e30)), not by assignment, in the
+ * reference's order (nn/attention.go:321-330): causal, the user's additive
+ * mask amask (this slice's (Sq, Sk) rows, or NULL), key padding.
  */
 static void scores_rows(const double* Qb, const double* KTb, int Sk, int D,
                         const int* rows, int nrows, double scale, int causal,
-                        int len, double* out) {
+                        const double* amask, int len, double* out) {
     const double sc = (g_mutation == MUT_NO_SCALE) ? 1.0 : scale;
     #pragma omp parallel for schedule(static)
     for (int r = 0; r < nrows; r++) {
@@ -131,6 +133,8 @@ static void scores_rows(const double* Qb, const double* KTb, int Sk, int D,
         for (int j = 0; j < Sk; j++) s[j] = s[j] * sc;
         if (causal)
             for (int j = 0; j < Sk; j++) s[j] = s[j] + (masked(i, j, 1, Sk) ? MASK_NEG : 0.0);
+        if (amask)  /* WithAttnMask: the user's additive mask, row i */
+            for (int j = 0; j < Sk; j++) s[j] = s[j] + amask[(size_t)i * Sk + j];
         if (len < Sk)
             for (int j = 0; j < Sk; j++) s[j] = s[j] + (j >= len ? MASK_NEG : 0.0);
     }
@@ -141,13 +145,17 @@ static void scores_rows(const double* Qb, const double* KTb, int Sk, int D,
  *   Q (BH,Sq,D), K/V (BH,Sk,D), O (BH,Sq,D), LSE (BH,Sq) or NULL.
  *   kv_len: NULL, or per-batch valid key counts (length BH/H), applied as the
  *   key padding mask of every head of that batch.
+ *   amask: NULL, or the additive mask of WithAttnMask (nn/attention.go:212-
+ *   257): slice bh = b*H + h reads (Sq, Sk) rows at amask + b*mask_sb +
+ *   h*mask_sh (strides 0 broadcast, as expandAttnMask's shapes do).
  *   rows/nrows: NULL/0 for all query rows, else only these rows are computed
  *   (and only those rows of O/LSE are written); each row's arithmetic is the
  *   same as in the full computation.
  */
-int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O,
-                    double* LSE, int BH, int H, int Sq, int Sk, int D, double scale,
-                    int causal, const int* kv_len, const int* rows, int nrows) {
+int oracle_attn_fwd_ex(const double* Q, const double* K, const double* V, double* O,
+                       double* LSE, int BH, int H, int Sq, int Sk, int D, double scale,
+                       int causal, const int* kv_len, const double* amask, long mask_sb,
+                       long mask_sh, const int* rows, int nrows) {
     if (BH <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || H <= 0 || BH % H) return -1;
     const int nr = rows ? nrows : Sq;
     double* KT = (double*)malloc(sizeof(double) * (size_t)D * Sk);
@@ -160,7 +168,9 @@ int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O
         const double* Vb = V + (size_t)bh * Sk * D;
         const int len = kv_len ? kv_len[bh / H] : Sk;
         transpose(Kb, KT, Sk, D);
-        scores_rows(Qb, KT, Sk, D, rows, nr, scale, causal, len, P);
+        const double* am = amask ? amask + (size_t)(bh / H) * mask_sb + (size_t)(bh % H) * mask_sh
+                                 : NULL;
+        scores_rows(Qb, KT, Sk, D, rows, nr, scale, causal, am, len, P);
         double* mx = (double*)malloc(sizeof(double) * nr);
         double* sm = (double*)malloc(sizeof(double) * nr);
         #pragma omp parallel for schedule(static)
@@ -196,6 +206,13 @@ int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O
     return 0;
 }
 
+int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O,
+                    double* LSE, int BH, int H, int Sq, int Sk, int D, double scale,
+                    int causal, const int* kv_len, const int* rows, int nrows) {
+    return oracle_attn_fwd_ex(Q, K, V, O, LSE, BH, H, Sq, Sk, D, scale, causal, kv_len, NULL, 0,
+                              0, rows, nrows);
+}
+
 /*
  * Backward of the core by the reference's autograd chain, one (b,h) slice at a
  * time, materialising every intermediate the Go graph holds:
@@ -207,12 +224,15 @@ int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O
  * masked (Sub and MaxAxis scatter) as tensor/autograd.go:52-99 accumulates
  * them. kv_len: NULL, or per-batch valid key counts (length BH/H): the key
  * padding mask ForwardMasked adds (nn/attention.go:261-272, :321-330), one
- * more additive -1e30 term of `mask`.
+ * more additive -1e30 term of `mask`; amask / mask_sb / mask_sh: the user's
+ * additive mask as in oracle_attn_fwd_ex (a constant: its gradient is not
+ * needed, the chain passes through the addition unchanged).
  */
 int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* V,
                                 const double* dO, double* dQ, double* dK, double* dV,
                                 int BH, int H, int S, int D, double scale, int causal,
-                                const int* kv_len) {
+                                const int* kv_len, const double* amask, long mask_sb,
+                                long mask_sh) {
     if (BH <= 0 || S <= 0 || D <= 0 || H <= 0 || BH % H != 0) return -1;
     const size_t SS = (size_t)S * S;
     double* KT = (double*)malloc(sizeof(double) * (size_t)D * S);
@@ -246,7 +266,9 @@ int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* 
             len = kv_len[bh / H];
             len = len < 0 ? 0 : (len > S ? S : len);
         }
-        scores_rows(Qb, KT, S, D, NULL, S, scale, causal, len, msk);
+        const double* am = amask ? amask + (size_t)(bh / H) * mask_sb + (size_t)(bh % H) * mask_sh
+                                 : NULL;
+        scores_rows(Qb, KT, S, D, NULL, S, scale, causal, am, len, msk);
         int* amax = (int*)malloc(sizeof(int) * S);
         double* se = (double*)malloc(sizeof(double) * S);
         double* g_se = (double*)malloc(sizeof(double) * S);
@@ -319,7 +341,8 @@ int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* 
 int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V,
                              const double* dO, double* dQ, double* dK, double* dV,
                              int BH, int S, int D, double scale, int causal) {
-    return oracle_attn_bwd_autograd_ex(Q, K, V, dO, dQ, dK, dV, BH, 1, S, D, scale, causal, NULL);
+    return oracle_attn_bwd_autograd_ex(Q, K, V, dO, dQ, dK, dV, BH, 1, S, D, scale, causal, NULL,
+                                       NULL, 0, 0);
 }
 
 /*

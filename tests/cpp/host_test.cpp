@@ -31,9 +31,14 @@ int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O
 int oracle_attn_bwd_autograd(const double* Q, const double* K, const double* V, const double* dO,
                              double* dQ, double* dK, double* dV, int BH, int S, int D,
                              double scale, int causal);
+int oracle_attn_fwd_ex(const double* Q, const double* K, const double* V, double* O,
+                       double* LSE, int BH, int H, int Sq, int Sk, int D, double scale,
+                       int causal, const int* kv_len, const double* amask, long mask_sb,
+                       long mask_sh, const int* rows, int nrows);
 int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* V,
                                 const double* dO, double* dQ, double* dK, double* dV, int BH,
-                                int H, int S, int D, double scale, int causal, const int* kv_len);
+                                int H, int S, int D, double scale, int causal, const int* kv_len,
+                                const double* amask, long mask_sb, long mask_sh);
 int oracle_linear(const double* x, const double* W, const double* b, double* y, int N, int in,
                   int out);
 void oracle_heads(const double* in, double* out, int B, int T, int H, int D, int dir);
@@ -289,6 +294,14 @@ static void test_cpu() {
     CHECK(y.Shape == std::vector<int>({3, 7, 24}), "Linear shape");
     CHECK(close(y.Data, yref, 1e-12, 0.0, "Linear vs oracle"), "Linear vs oracle");
     test_backend_cpu(r);
+    {
+        using gonn::nn::maskStrides;
+        CHECK((maskStrides({5, 7}, 2, 3, 5, 7) == std::array<long, 2>{0, 0}), "mask (Tq,Tk)");
+        CHECK((maskStrides({2, 5, 7}, 2, 3, 5, 7) == std::array<long, 2>{35, 0}), "mask (B,Tq,Tk)");
+        CHECK((maskStrides({6, 5, 7}, 2, 3, 5, 7) == std::array<long, 2>{105, 35}), "mask (B*H,Tq,Tk)");
+        CHECK((maskStrides({2, 3, 5, 7}, 2, 3, 5, 7) == std::array<long, 2>{105, 35}), "mask 4-D");
+        CHECK(throws_invalid([&] { maskStrides({5, 8}, 2, 3, 5, 7); }), "mask bad shape");
+    }
 
     // MultiHeadAttention construction and checkQKVDims (nn/attention.go:45-103).
     CHECK(throws_invalid([&] {
@@ -497,12 +510,41 @@ static void test_diff_key_padding_gpu() {
                     D, scale, 1, lens.data(), nullptr, 0);
     oracle_attn_bwd_autograd_ex(q.Data.data(), k.Data.data(), v.Data.data(), g.Data.data(),
                                 rq.data(), rk.data(), rv.data(), BH, H, S, D, scale, 1,
-                                lens.data());
+                                lens.data(), nullptr, 0, 0);
     CHECK(close(f.Out.Data, ro, 1e-4, 0.0, "fusedAttnDiff key padding O"), "diff kv O");
     const auto grads = f.Node.Backward(g);
     CHECK(close(grads[0].Data, rq, 1e-4, 0.0, "fusedAttnDiff key padding dQ"), "diff kv dQ");
     CHECK(close(grads[1].Data, rk, 1e-4, 0.0, "fusedAttnDiff key padding dK"), "diff kv dK");
     CHECK(close(grads[2].Data, rv, 1e-4, 0.0, "fusedAttnDiff key padding dV"), "diff kv dV");
+}
+
+// Additive masks (WithAttnMask): fusedAttnDiff with a (B, S, S) mask and key
+// padding against the oracle's chain; maskStrides' shape rules.
+static void test_attn_mask_gpu() {
+    const int B = 2, H = 2, S = 60, D = 64, BH = B * H;
+    const size_t n = (size_t)BH * S * D;
+    Rng r(414);
+    Tensor q = Tensor::New(r.normals(n), {BH, S, D}), k = Tensor::New(r.normals(n), {BH, S, D}),
+           v = Tensor::New(r.normals(n), {BH, S, D}), g = Tensor::New(r.normals(n), {BH, S, D});
+    Tensor m = Tensor::New(r.normals((size_t)B * S * S, 1.5), {B, S, S});
+    for (int b = 0; b < B; b++)
+        for (int i = 0; i < S; i++) m.Data[((size_t)b * S + i) * S + 7] = -1e30;  // blocked key
+    const std::vector<int> lens = {60, 41};
+    const double scale = 1.0 / std::sqrt((double)D);
+    gonn::hip::SetMode(1);  // a masked call runs the fp32 kernels in either mode
+    gonn::nn::DiffOut f = gonn::nn::fusedAttnDiff(q, k, v, BH, S, D, scale, true, lens, H, m);
+    std::vector<double> ro(n), rq(n), rk(n), rv(n);
+    oracle_attn_fwd_ex(q.Data.data(), k.Data.data(), v.Data.data(), ro.data(), nullptr, BH, H, S,
+                       S, D, scale, 1, lens.data(), m.Data.data(), (long)S * S, 0, nullptr, 0);
+    oracle_attn_bwd_autograd_ex(q.Data.data(), k.Data.data(), v.Data.data(), g.Data.data(),
+                                rq.data(), rk.data(), rv.data(), BH, H, S, D, scale, 1,
+                                lens.data(), m.Data.data(), (long)S * S, 0);
+    CHECK(close(f.Out.Data, ro, 1e-4, 0.0, "fusedAttnDiff attn mask O"), "mask O");
+    const auto grads = f.Node.Backward(g);
+    CHECK(close(grads[0].Data, rq, 1e-4, 0.0, "fusedAttnDiff attn mask dQ"), "mask dQ");
+    CHECK(close(grads[1].Data, rk, 1e-4, 0.0, "fusedAttnDiff attn mask dK"), "mask dK");
+    CHECK(close(grads[2].Data, rv, 1e-4, 0.0, "fusedAttnDiff attn mask dV"), "mask dV");
+    gonn::hip::SetMode(0);
 }
 
 static void test_gpu() {
@@ -668,6 +710,7 @@ static void test_gpu() {
     test_backend_gpu();
     test_resident_gpu();
     test_diff_key_padding_gpu();
+    test_attn_mask_gpu();
 }
 
 int main(int argc, char** argv) {

@@ -113,7 +113,9 @@ def test_mha_forward_masked_and_cross_attention(causal):
     with pytest.raises(ValueError):
         mha.forward_masked(x, x, x, key_padding_mask=holes)
     with pytest.raises(ValueError):
-        mha.forward_masked(x, x, x, attn_mask=np.zeros((Tk, Tk)))
+        mha.forward_masked(x, x, x, dropout=0.1)
+    with pytest.raises(ValueError):
+        mha.forward_masked(x, x, x, attn_mask=np.zeros((Tk, Tk + 1)))
 
 
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
@@ -189,3 +191,91 @@ def test_fused_attn_diff_with_key_padding(mode):
     assert_close(dv, rv, mode, f"fused_attn_diff dV {mode}")
     for bh in range(B * H):
         assert np.all(dk[bh, lens[bh // H]:] == 0.0)
+
+
+def _mask_of(kind, B, H, Sq, Sk, seed):
+    """An additive mask in one of expandAttnMask's shapes, with a blocked
+    (-1e30) key column and a band of blocked scores, plus its dense
+    (B*H, Sq, Sk) expansion."""
+    rng = np.random.default_rng(seed)
+    full = rng.standard_normal((B, H, Sq, Sk)) * 1.5
+    full[..., 3] = -1e30
+    for i in range(Sq):
+        full[:, :, i, max(0, i - 40):max(0, i - 30)] = -1e30  # a blocked band
+    if kind == "TqTk":
+        full[:] = full[0, 0]
+        m = full[0, 0]
+    elif kind == "BTqTk":
+        full[:] = full[:, :1]
+        m = full[:, 0]
+    elif kind == "BHTqTk3":
+        m = full.reshape(B * H, Sq, Sk)
+    else:
+        m = full
+    return np.ascontiguousarray(m), full.reshape(B * H, Sq, Sk)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("kind", ["TqTk", "BTqTk", "BHTqTk3", "BHTqTk4"])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attn_mask_fwd_bwd_matches_oracle(mode, kind, causal):
+    """WithAttnMask on the fused path (device API): forward and backward
+    against the oracle's reference chain with the same additive mask, key
+    padding and causal mask. A masked call runs the fp32-MFMA kernels in
+    either mode, so both are held to the fp32 bar."""
+    from gonn_amd import hip
+    B, H, S, D = 2, 2, 100, 64
+    lens = np.array([100, 71], dtype=np.int32)
+    say(f"[masked] attn_mask {kind} mode={mode} causal={causal}")
+    m, _ = _mask_of(kind, B, H, S, S, 870)
+    q, k, v, g = (randn((B * H, S, D), 880 + i) for i in range(4))
+    dev = [torch.from_numpy(x).cuda().reshape(B, H, S, D) for x in (q, k, v, g)]
+    kl = torch.from_numpy(lens).cuda()
+    md = torch.from_numpy(m.astype(np.float32)).cuda()
+    o, l = hip.attn_fwd(*dev[:3], causal=causal, mode=mode, kv_len=kl, attn_mask=md)
+    dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=causal, mode=mode, kv_len=kl,
+                              attn_mask=md)
+    torch.cuda.synchronize()
+    ro, rl = oracle.attn_fwd(q, k, v, 1 / math.sqrt(D), causal, kv_len=lens, H=H, attn_mask=m)
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H,
+                                          attn_mask=m)
+    o = o.reshape(B * H, S, D).cpu().numpy()
+    assert_close(o, ro, "fp32", f"O mask {kind}")
+    assert_close(l.cpu().numpy(), rl, "fp32", f"LSE mask {kind}")
+    for got, ref, n in ((dq, rq, "dQ"), (dk, rk, "dK"), (dv, rv, "dV")):
+        assert_close(got.reshape(B * H, S, D).cpu().numpy(), ref, "fp32", f"{n} mask {kind}")
+
+
+def test_attn_mask_cross_attention_and_nn(mode="fp32"):
+    """nn.MultiHeadAttention.forward_masked with an additive (B, Tq, Tk) mask
+    on cross-attention, and fused_attn_diff with a (Tq, Tk) mask, against the
+    oracle."""
+    from gonn_amd import nn
+    E, H, B, Tq, Tk = 256, 4, 2, 60, 130
+    s = 1.0 / math.sqrt(E)
+    p = {}
+    for i, n in enumerate("qkvo"):
+        p["W" + n] = randn((E, E), 890 + 2 * i).astype(np.float64) * s
+        p["b" + n] = randn((E,), 891 + 2 * i).astype(np.float64) * 0.1
+    mha = nn.MultiHeadAttention(E, H, p["Wq"], p["bq"], p["Wk"], p["bk"], p["Wv"], p["bv"],
+                                p["Wo"], p["bo"])
+    q = randn((B, Tq, E), 899).astype(np.float64)
+    mem = randn((B, Tk, E), 900).astype(np.float64)
+    m, _ = _mask_of("BTqTk", B, 1, Tq, Tk, 901)
+    pad = np.zeros((B, Tk))
+    pad[1, 90:] = 1
+    got = mha.forward_masked(q, mem, mem, causal=True, key_padding_mask=pad, attn_mask=m)
+    ref = oracle.mha_fwd(q, mem, mem, p, H, causal=True, key_pad=pad, attn_mask=m)
+    assert_close(got, ref, "fp32", "forward_masked cross + attn_mask")
+
+    S, D, BH = 80, 64, 4
+    q2, k2, v2, g2 = (randn((BH, S, D), 910 + i) for i in range(4))
+    m2, _ = _mask_of("TqTk", 1, 1, S, S, 915)
+    O, node = nn.fused_attn_diff(q2, k2, v2, BH, S, D, 1 / math.sqrt(D), False, H=BH,
+                                 attn_mask=m2)
+    ro, _ = oracle.attn_fwd(q2, k2, v2, 1 / math.sqrt(D), False, H=BH, attn_mask=m2)
+    assert_close(O.reshape(BH, S, D), ro, "fp32", "fused_attn_diff O attn_mask")
+    grads = node(g2.ravel())
+    ref = oracle.attn_bwd_autograd(q2, k2, v2, g2, causal=False, H=BH, attn_mask=m2)
+    for got, r, n in zip(grads, ref, ("dQ", "dK", "dV")):
+        assert_close(got.reshape(BH, S, D), r, "fp32", f"fused_attn_diff {n} attn_mask")

@@ -359,3 +359,39 @@ def test_planted_mistakes_are_caught(mutation):
         full = oracle.attn_bwd_autograd(q, k, v, g, causal=True)
         caught = caught or not all(np.allclose(a, b, atol=1e-9) for a, b in zip(part, full))
     assert caught, f"planted mistake {mutation} went unnoticed"
+
+
+@pytest.mark.parametrize("shape_kind", ["TqTk", "BTqTk", "BHTqTk3", "BHTqTk4"])
+def test_additive_attn_mask_matches_torch(shape_kind):
+    """WithAttnMask (nn/attention.go:212-257) in the forward and the autograd
+    chain: torch fp64 through scores*scale + causal + mask + key padding, for
+    each of expandAttnMask's accepted shapes."""
+    rng = np.random.default_rng(31)
+    B, H, S, D = 2, 3, 24, 64
+    q, k, v, g = (rng.standard_normal((B * H, S, D)) for _ in range(4))
+    full = rng.standard_normal((B, H, S, S)) * 2.0
+    full[..., 5] = -1e30  # a blocked key column, as the reference suggests
+    m = {"TqTk": full[0, 0], "BTqTk": full[:, 0], "BHTqTk3": full.reshape(B * H, S, S),
+         "BHTqTk4": full}[shape_kind]
+    dense = np.broadcast_to(m.reshape((1, 1, S, S)) if m.ndim == 2 else
+                            (m.reshape(B, 1, S, S) if shape_kind == "BTqTk" else m.reshape(B, H, S, S)),
+                            (B, H, S, S)).reshape(B * H, S, S)
+    lens = [S, 17]
+    O, L = oracle.attn_fwd(q, k, v, causal=True, kv_len=lens, H=H, attn_mask=m)
+    dq, dk, dv = oracle.attn_bwd_autograd(q, k, v, g, causal=True, kv_len=lens, H=H, attn_mask=m)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    s = (tq @ tk.transpose(1, 2)) / math.sqrt(D)
+    s = s + torch.where(torch.arange(S)[None, :] > torch.arange(S)[:, None], -1e30, 0.0)
+    s = s + torch.from_numpy(np.array(dense))
+    pad = torch.zeros(B * H, 1, S, dtype=torch.float64)
+    for bh in range(B * H):
+        pad[bh, :, lens[bh // H]:] = -1e30
+    s = s + pad
+    out = torch.softmax(s, -1) @ tv
+    np.testing.assert_allclose(O, out.detach().numpy(), atol=1e-12, rtol=0)
+    np.testing.assert_allclose(L, torch.logsumexp(s, -1).detach().numpy(), atol=1e-9, rtol=0)
+    out.backward(torch.tensor(g))
+    for got, t in ((dq, tq), (dk, tk), (dv, tv)):
+        np.testing.assert_allclose(got, t.grad.numpy(), atol=1e-12, rtol=0)
+    with pytest.raises(ValueError):
+        oracle.attn_fwd(q, k, v, attn_mask=np.zeros((S, S + 1)), H=H)
