@@ -81,7 +81,7 @@ class BwdArgs(ctypes.Structure):
                 ("D", ctypes.c_int), ("scale", ctypes.c_double), ("causal", ctypes.c_int),
                 ("mode", ctypes.c_int), ("deterministic", ctypes.c_int), ("kv_len", Buf),
                 ("attn_mask", Buf), ("mask_stride_b", ctypes.c_int64),
-                ("mask_stride_h", ctypes.c_int64)]
+                ("mask_stride_h", ctypes.c_int64), ("Sk", ctypes.c_int)]
 
 
 class DecodeArgs(ctypes.Structure):
@@ -158,7 +158,7 @@ def load() -> ctypes.CDLL:
     lg_ = ctypes.c_long
     lib.gonn_hip_flash_attn_f64_masked.argtypes = [dp] * 5 + [i] * 5 + [ctypes.c_double, i, ip,
                                                                         dp, lg_, lg_]
-    lib.gonn_hip_flash_attn_f64_bwd_masked.argtypes = [dp] * 9 + [i] * 4 + [ctypes.c_double, i,
+    lib.gonn_hip_flash_attn_f64_bwd_masked.argtypes = [dp] * 9 + [i] * 5 + [ctypes.c_double, i,
                                                                             ip, dp, lg_, lg_]
     lib.gonn_hip_mha_create.argtypes = [ctypes.POINTER(vp), i, i, i, i] + [dp] * 8
     lib.gonn_hip_mha_free.argtypes = [vp]

@@ -113,7 +113,10 @@ bool mask_ok(const gonn_buf& m, int64_t sb, int64_t sh, int B, int H, int Sq, in
 // The kernels a call runs: an additive mask is read by the fp32-MFMA kernels
 // only, in either mode.
 int fwd_mode(const gonn_attn_fwd_args* a) { return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode; }
-int bwd_mode(const gonn_attn_bwd_args* a) { return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode; }
+int bwd_keys_of(const gonn_attn_bwd_args* a) { return a->Sk > 0 ? a->Sk : a->S; }
+int bwd_mode(const gonn_attn_bwd_args* a) {
+    return a->attn_mask.ptr || bwd_keys_of(a) != a->S ? GONN_ATTN_FP32_MFMA : a->mode;
+}
 
 // ---- forward -----------------------------------------------------------
 
@@ -183,18 +186,22 @@ size_t decode_ws(const gonn_attn_decode_args* a) {
 
 int check_bwd(const gonn_attn_bwd_args* a) {
     if (!a) return GONN_E_INVALID;
-    if (a->B <= 0 || a->H <= 0 || a->S <= 0 || a->D <= 0) return GONN_E_INVALID;
+    if (a->B <= 0 || a->H <= 0 || a->S <= 0 || a->D <= 0 || a->Sk < 0) return GONN_E_INVALID;
     if (a->mode != GONN_ATTN_FP32_MFMA && a->mode != GONN_ATTN_BF16_MFMA) return GONN_E_INVALID;
     if (!std::isfinite(a->scale)) return GONN_E_INVALID;
     if (!head_dim_ok(a->D)) return GONN_E_UNSUPPORTED;
-    const size_t BH = (size_t)a->B * a->H, n = BH * a->S * a->D;
-    if ((double)n >= 2147483647.0 * 8) return GONN_E_UNSUPPORTED;
-    const gonn_buf* in[] = {&a->q, &a->k, &a->v, &a->o, &a->dO, &a->dq, &a->dk, &a->dv};
-    for (const gonn_buf* b : in)
+    const int Sk = bwd_keys_of(a);
+    const size_t BH = (size_t)a->B * a->H, n = BH * a->S * a->D, nk = BH * Sk * a->D;
+    if ((double)n >= 2147483647.0 * 8 || (double)nk >= 2147483647.0 * 8) return GONN_E_UNSUPPORTED;
+    const gonn_buf* qs[] = {&a->q, &a->o, &a->dO, &a->dq};
+    for (const gonn_buf* b : qs)
         if (!buf_ok(*b, n, GONN_F32)) return GONN_E_INVALID;
+    const gonn_buf* ks[] = {&a->k, &a->v, &a->dk, &a->dv};
+    for (const gonn_buf* b : ks)
+        if (!buf_ok(*b, nk, GONN_F32)) return GONN_E_INVALID;
     if (!buf_ok(a->lse, BH * a->S, GONN_F32)) return GONN_E_INVALID;
     if (a->kv_len.ptr && !buf_ok(a->kv_len, (size_t)a->B, GONN_I32)) return GONN_E_INVALID;
-    if (!mask_ok(a->attn_mask, a->mask_stride_b, a->mask_stride_h, a->B, a->H, a->S, a->S))
+    if (!mask_ok(a->attn_mask, a->mask_stride_b, a->mask_stride_h, a->B, a->H, a->S, Sk))
         return GONN_E_INVALID;
     return GONN_OK;
 }
@@ -560,6 +567,8 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     p.BH = BH;
     p.S = S;
     p.Sp = Sp;
+    p.Sk = bwd_keys_of(a);
+    p.Skp = (int)round_up((size_t)p.Sk, gonn::kBwdPad);
     p.scale = (float)a->scale;
     p.scale_log2 = (float)(a->scale * (double)gonn::kLog2e);
     const float qsign = a->scale > 0 ? 1.f : (a->scale < 0 ? -1.f : 0.f);
@@ -830,35 +839,36 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
                                    const double* O, const double* L, const double* dO, double* dQ,
                                    double* dK, double* dV, int B, int H, int S, int d,
                                    double scale, int causal, const int* kv_len) {
-    return gonn_hip_flash_attn_f64_bwd_masked(Q, K, V, O, L, dO, dQ, dK, dV, B, H, S, d, scale,
+    return gonn_hip_flash_attn_f64_bwd_masked(Q, K, V, O, L, dO, dQ, dK, dV, B, H, S, S, d, scale,
                                               causal, kv_len, nullptr, 0, 0);
 }
 
 int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const double* V,
                                        const double* O, const double* L, const double* dO,
-                                       double* dQ, double* dK, double* dV, int B, int H, int S,
-                                       int d, double scale, int causal, const int* kv_len,
-                                       const double* mask, long mask_sb, long mask_sh) {
-    if (B <= 0 || H <= 0 || !shim_args_ok(B * H, S, d) || !Q || !K || !V || !O || !L || !dO ||
-        !dQ || !dK || !dV)
+                                       double* dQ, double* dK, double* dV, int B, int H, int Sq,
+                                       int Sk, int d, double scale, int causal,
+                                       const int* kv_len, const double* mask, long mask_sb,
+                                       long mask_sh) {
+    if (B <= 0 || H <= 0 || !shim_args_ok(B * H, Sq, d) || !shim_args_ok(B * H, Sk, d) || !Q ||
+        !K || !V || !O || !L || !dO || !dQ || !dK || !dV)
         return GONN_E_INVALID;
-    const size_t mn = mask ? mask_elems(B, H, S, S, mask_sb, mask_sh) : 0;
+    const size_t mn = mask ? mask_elems(B, H, Sq, Sk, mask_sb, mask_sh) : 0;
     if (mask && !mn) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
     const int BH = B * H;
     DevMem mem;
     const int dp = pad_dim(d);
-    const size_t rows = (size_t)BH * S, n = rows * dp;
+    const size_t rq = (size_t)BH * Sq, rk = (size_t)BH * Sk, nq = rq * dp, nk = rk * dp;
     float *q, *k, *v, *o, *l, *g, *dq, *dk, *dv;
-    TRY(upload_padded(mem, Q, rows, d, dp, &q));
-    TRY(upload_padded(mem, K, rows, d, dp, &k));
-    TRY(upload_padded(mem, V, rows, d, dp, &v));
-    TRY(upload_padded(mem, O, rows, d, dp, &o));
-    TRY(upload_padded(mem, L, rows, 1, 1, &l));
-    TRY(upload_padded(mem, dO, rows, d, dp, &g));
-    TRY(mem.alloc((void**)&dq, n * 4));
-    TRY(mem.alloc((void**)&dk, n * 4));
-    TRY(mem.alloc((void**)&dv, n * 4));
+    TRY(upload_padded(mem, Q, rq, d, dp, &q));
+    TRY(upload_padded(mem, K, rk, d, dp, &k));
+    TRY(upload_padded(mem, V, rk, d, dp, &v));
+    TRY(upload_padded(mem, O, rq, d, dp, &o));
+    TRY(upload_padded(mem, L, rq, 1, 1, &l));
+    TRY(upload_padded(mem, dO, rq, d, dp, &g));
+    TRY(mem.alloc((void**)&dq, nq * 4));
+    TRY(mem.alloc((void**)&dk, nk * 4));
+    TRY(mem.alloc((void**)&dv, nk * 4));
     int* kl = nullptr;
     float* m = nullptr;
     if (mask) TRY(upload_padded(mem, mask, mn, 1, 1, &m));
@@ -867,22 +877,23 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
         TRYH(hipMemcpy(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice));
     }
     gonn_attn_bwd_args a{};
-    a.q = {q, n * 4, GONN_F32};
-    a.k = {k, n * 4, GONN_F32};
-    a.v = {v, n * 4, GONN_F32};
-    a.o = {o, n * 4, GONN_F32};
-    a.lse = {l, rows * 4, GONN_F32};
-    a.dO = {g, n * 4, GONN_F32};
-    a.dq = {dq, n * 4, GONN_F32};
-    a.dk = {dk, n * 4, GONN_F32};
-    a.dv = {dv, n * 4, GONN_F32};
+    a.q = {q, nq * 4, GONN_F32};
+    a.k = {k, nk * 4, GONN_F32};
+    a.v = {v, nk * 4, GONN_F32};
+    a.o = {o, nq * 4, GONN_F32};
+    a.lse = {l, rq * 4, GONN_F32};
+    a.dO = {g, nq * 4, GONN_F32};
+    a.dq = {dq, nq * 4, GONN_F32};
+    a.dk = {dk, nk * 4, GONN_F32};
+    a.dv = {dv, nk * 4, GONN_F32};
     a.kv_len = {kl, kl ? (size_t)B * 4 : 0, GONN_I32};
     a.attn_mask = {m, m ? mn * 4 : 0, GONN_F32};
     a.mask_stride_b = mask_sb;
     a.mask_stride_h = mask_sh;
     a.B = B;
     a.H = H;
-    a.S = S;
+    a.S = Sq;
+    a.Sk = Sk;
     a.D = dp;
     a.scale = scale;
     a.causal = causal;
@@ -892,9 +903,9 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
     void* ws = nullptr;
     if (wsb) TRY(mem.alloc(&ws, wsb));
     TRY(gonn_hip_attn_bwd(&a, ws, wsb, nullptr));
-    TRY(download_padded(mem, dq, rows, d, dp, dQ));
-    TRY(download_padded(mem, dk, rows, d, dp, dK));
-    TRY(download_padded(mem, dv, rows, d, dp, dV));
+    TRY(download_padded(mem, dq, rq, d, dp, dQ));
+    TRY(download_padded(mem, dk, rk, d, dp, dK));
+    TRY(download_padded(mem, dv, rk, d, dp, dV));
     return herr(hipDeviceSynchronize());
 }
 

@@ -440,23 +440,23 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, ln = lane & 31;
-    const int S = p.S, Sp = p.Sp;
+    const int S = p.S, Sp = p.Sp, Sk = p.Sk;  // S queries, Sk keys
     int bh, kb;
-    map_block(blockIdx.x, Sp / BN, p.BH, false, bh, kb);
+    map_block(blockIdx.x, p.Skp / BN, p.BH, false, bh, kb);
     const int kw = kb * BN + wave * 32;
     const int kj = kw + ln;
     const int Skv = bwd_keys(p, bh);  // keys >= Skv are padded: dK = dV = 0
     if (kb * BN >= Skv) {
-        bwd_zero_rows<D>(p.dk, S, bh, kb * BN, BN);
-        bwd_zero_rows<D>(p.dv, S, bh, kb * BN, BN);
+        bwd_zero_rows<D>(p.dk, Sk, bh, kb * BN, BN);
+        bwd_zero_rows<D>(p.dv, Sk, bh, kb * BN, BN);
         return;
     }
 
     float kf[HD], vf[HD];
     {
-        const int kr = kj < S ? kj : S - 1;  // pad keys are computed, never written
-        const float* kp = (const float*)p.k + ((size_t)bh * S + kr) * D + g * HD;
-        const float* vp = (const float*)p.v + ((size_t)bh * S + kr) * D + g * HD;
+        const int kr = kj < Sk ? kj : Sk - 1;  // pad keys are computed, never written
+        const float* kp = (const float*)p.k + ((size_t)bh * Sk + kr) * D + g * HD;
+        const float* vp = (const float*)p.v + ((size_t)bh * Sk + kr) * D + g * HD;
         for (int i = 0; i < HD; i += 4) {
             const f32x4 a = *(const f32x4*)(kp + i), b = *(const f32x4*)(vp + i);
             for (int j = 0; j < 4; j++) {
@@ -471,7 +471,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
     const float* dg = p.delta + (size_t)bh * Sp;
     // The additive mask's column of this lane's key (rows S apart), if any.
     const float* mcol = p.mask ? p.mask + (size_t)(bh / p.H) * p.mask_sb +
-                                     (size_t)(bh % p.H) * p.mask_sh + (kj < S ? kj : S - 1)
+                                     (size_t)(bh % p.H) * p.mask_sh + (kj < Sk ? kj : Sk - 1)
                                : nullptr;
 
     f32x4 rq[CH], rdo[CH];
@@ -540,7 +540,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
                 float off = -s_lse[buf][qr];
                 if (mcol) {  // mask[q][kj], clamped rows and keys are not used
                     const int qq = q0 + qr < S ? q0 + qr : S - 1;
-                    off += mcol[(size_t)qq * S] * kLog2e;
+                    off += mcol[(size_t)qq * Sk] * kLog2e;
                 }
                 float pv = fast_exp2(__builtin_fmaf(sacc[r], c2, off));
                 if (need_mask && kj > q0 + qr) pv = 0.f;
@@ -561,11 +561,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_f32_kernel(BwdParams p) {
         __syncthreads();
     }
 
-    if (kj < S) {
+    if (kj < Sk) {
         const float sc = p.scale;
         const bool live = kj < Skv;
-        float* dkr = p.dk + ((size_t)bh * S + kj) * D;
-        float* dvr = p.dv + ((size_t)bh * S + kj) * D;
+        float* dkr = p.dk + ((size_t)bh * Sk + kj) * D;
+        float* dvr = p.dv + ((size_t)bh * Sk + kj) * D;
         for (int t = 0; t < NDT; t++)
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 f32x4 a, b;
@@ -594,7 +594,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 5, ln = lane & 31;
-    const int S = p.S, Sp = p.Sp;
+    const int S = p.S, Sp = p.Sp, Sk = p.Sk;  // S queries, Sk keys
     int bh, qb;
     map_block(blockIdx.x, Sp / BM, p.BH, CAUSAL, bh, qb);
     const int q0 = qb * BM;
@@ -624,12 +624,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
     int kend = Skv;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
     const int ntiles = (kend + BN - 1) / BN;
-    const float* Kg = (const float*)p.k + (size_t)bh * S * D;
-    const float* Vg = (const float*)p.v + (size_t)bh * S * D;
+    const float* Kg = (const float*)p.k + (size_t)bh * Sk * D;
+    const float* Vg = (const float*)p.v + (size_t)bh * Sk * D;
     // The additive mask's row of this lane's query, if any.
     const float* mrow = p.mask ? p.mask + (size_t)(bh / p.H) * p.mask_sb +
                                      (size_t)(bh % p.H) * p.mask_sh +
-                                     (size_t)(qi < S ? qi : S - 1) * S
+                                     (size_t)(qi < S ? qi : S - 1) * Sk
                                : nullptr;
 
     f32x4 rk[CH], rv[CH];
@@ -638,7 +638,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
             const int c = tid + i * 256;
             const int row = c / (D / 4), col = (c % (D / 4)) * 4;
             int key = kt * BN + row;
-            key = key < S ? key : S - 1;  // clamped rows are masked
+            key = key < Sk ? key : Sk - 1;  // clamped rows are masked
             rk[i] = *(const f32x4*)(Kg + (size_t)key * D + col);
             rv[i] = *(const f32x4*)(Vg + (size_t)key * D + col);
         }
@@ -743,8 +743,9 @@ hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, fl
     } while (0)
 
 hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipStream_t s) {
-    if (p.Sp % kBwdPad != 0) return hipErrorInvalidValue;
-    const dim3 grid((p.Sp / 128) * p.BH);
+    if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0) return hipErrorInvalidValue;
+    if (mode == 1 && (p.Sk != p.S || p.Skp != p.Sp)) return hipErrorInvalidValue;
+    const dim3 grid((p.Skp / 128) * p.BH);
     if (mode == 1) GONN_BWD_LAUNCH(bwd_dkdv_bf16_kernel);
     else GONN_BWD_LAUNCH(bwd_dkdv_f32_kernel);
     return hipGetLastError();
@@ -752,6 +753,7 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipS
 
 hipError_t launch_bwd_dq(const BwdParams& p, int mode, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0) return hipErrorInvalidValue;
+    if (mode == 1 && p.Sk != p.S) return hipErrorInvalidValue;
     const dim3 grid((p.Sp / 128) * p.BH);
     if (mode == 1) return launch_bwd_dq_bf16(p, D, causal, s);
     GONN_BWD_LAUNCH(bwd_dq_f32_kernel);

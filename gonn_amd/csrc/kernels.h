@@ -67,9 +67,11 @@ struct BwdParams {
     const float* lse2;   // (BH,Sp) LSE * log2(e); +inf on pad rows
     const float* delta;  // (BH,Sp) rowsum(dO * O); 0 on pad rows
     float* dq;           // (BH,S,D)
-    float* dk;
+    float* dk;           // (BH,Sk,D)
     float* dv;
-    int BH, S, Sp;
+    int BH, S, Sp;       // S: query rows, Sp: S padded (lse2 / delta rows)
+    int Sk, Skp;         // key rows and padded (equal to S, Sp except in the
+                         // fp32 kernels' cross-attention backward)
     float scale;       // signed scale (fp32 kernels)
     float scale_log2;  // scale * log2(e) (fp32 kernels)
     // bf16 kernels: Q is packed times sign(scale) (0 for a zero scale), so
@@ -86,12 +88,12 @@ struct BwdParams {
     long long mask_sb, mask_sh;
 };
 
-// Keys of slice bh that take part in the backward: S, or the sequence's
-// kv_len clamped to [0, S]. Wave-uniform.
+// Keys of slice bh that take part in the backward: Sk, or the sequence's
+// kv_len clamped to [0, Sk]. Wave-uniform.
 GONN_DEV int bwd_keys(const BwdParams& p, int bh) {
-    if (!p.kv_len) return p.S;
+    if (!p.kv_len) return p.Sk;
     int l = p.kv_len[bh / p.H];
-    l = l < 0 ? 0 : (l > p.S ? p.S : l);
+    l = l < 0 ? 0 : (l > p.Sk ? p.Sk : l);
     return __builtin_amdgcn_readfirstlane(l);
 }
 

@@ -142,22 +142,26 @@ def _host_mask(attn_mask, B, H, Sq, Sk):
 
 
 def FlashAttnF64BwdEx(Q, K, V, O, L, dO, B: int, H: int, S: int, d: int, scale: float,
-                      causal: bool, kv_len=None, attn_mask=None):
-    """General backward on host fp64 (B*H,S,d) arrays with the forward's
-    optional key padding kv_len[B] (new): returns (dQ, dK, dV). O and L come
-    from FlashAttnF64Ex(..., kv_len, lse=True) with the same kv_len."""
-    n = B * H * S * d
-    Q, K, V, O, dO = (_f64(x, n, "FlashAttnF64BwdEx") for x in (Q, K, V, O, dO))
+                      causal: bool, kv_len=None, attn_mask=None, Sk=None):
+    """General backward on host fp64 arrays (new): Q, O, dO (B*H,S,d), K, V
+    (B*H,Sk,d) with Sk = S unless given (cross-attention), the forward's
+    optional key padding kv_len[B] and additive attn_mask; returns
+    (dQ, dK, dV). O and L come from FlashAttnF64Ex(..., lse=True) with the
+    same options."""
+    Sk = S if Sk is None else int(Sk)
+    n, nk = B * H * S * d, B * H * Sk * d
+    Q, O, dO = (_f64(x, n, "FlashAttnF64BwdEx") for x in (Q, O, dO))
+    K, V = (_f64(x, nk, "FlashAttnF64BwdEx K/V") for x in (K, V))
     L = _f64(L, B * H * S, "FlashAttnF64BwdEx L")
     kl = None
     if kv_len is not None:
         kl = np.ascontiguousarray(kv_len, dtype=np.int32)
         if kl.shape != (B,):
             raise ValueError(f"FlashAttnF64BwdEx: kv_len must have {B} entries")
-    dQ, dK, dV = np.zeros(n), np.zeros(n), np.zeros(n)
-    m, sb, sh = _host_mask(attn_mask, B, H, S, S)
+    dQ, dK, dV = np.zeros(n), np.zeros(nk), np.zeros(nk)
+    m, sb, sh = _host_mask(attn_mask, B, H, S, Sk)
     check(_lib.load().gonn_hip_flash_attn_f64_bwd_masked(
-        _p(Q), _p(K), _p(V), _p(O), _p(L), _p(dO), _p(dQ), _p(dK), _p(dV), B, H, S, d,
+        _p(Q), _p(K), _p(V), _p(O), _p(L), _p(dO), _p(dQ), _p(dK), _p(dV), B, H, S, Sk, d,
         float(scale), int(bool(causal)),
         kl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)) if kl is not None else None,
         _p(m) if m is not None else None, sb, sh), "FlashAttnF64BwdEx")
@@ -375,20 +379,22 @@ def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp3
     additive mask."""
     torch = _torch()
     B, H, S, D = _shape4(q, "q")
+    Sk = k.shape[-2]  # key rows: != S for cross-attention (fp32-MFMA kernels)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     if out is None:
-        dq, dk, dv = (torch.empty(q.shape, dtype=torch.float32, device=q.device)
-                      for _ in range(3))
+        dq = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+        dk, dv = (torch.empty(k.shape, dtype=torch.float32, device=q.device) for _ in range(2))
     else:
         dq, dk, dv = out
     mb, sb, sh = Buf(), 0, 0
     if attn_mask is not None:
-        sb, sh = mask_strides(attn_mask.shape, B, H, S, S)
+        sb, sh = mask_strides(attn_mask.shape, B, H, S, Sk)
         mb = buf(attn_mask)
     a = BwdArgs(buf(q), buf(k), buf(v), buf(o), buf(lse), buf(dO), buf(dq), buf(dk), buf(dv),
                 B, H, S, D, float(scale), int(bool(causal)), MODES[mode], 1,
-                buf(kv_len) if kv_len is not None else Buf(None, 0, GONN_I32), mb, sb, sh)
+                buf(kv_len) if kv_len is not None else Buf(None, 0, GONN_I32), mb, sb, sh,
+                0 if Sk == S else Sk)
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))

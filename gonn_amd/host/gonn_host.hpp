@@ -97,10 +97,11 @@ FwdOut FlashAttnF64Masked(const std::vector<double>& Q, const std::vector<double
                           const std::vector<double>& V, int B, int H, int Sq, int Sk, int d,
                           double scale, bool causal, const std::vector<int>& kvLen,
                           const std::vector<double>& mask, long maskSB, long maskSH);
+// The backward also takes cross-attention: K, V, dK, dV are (B*H,Sk,d).
 BwdOut FlashAttnF64BwdMasked(const std::vector<double>& Q, const std::vector<double>& K,
                              const std::vector<double>& V, const std::vector<double>& O,
                              const std::vector<double>& L, const std::vector<double>& dO, int B,
-                             int H, int S, int d, double scale, bool causal,
+                             int H, int Sq, int Sk, int d, double scale, bool causal,
                              const std::vector<int>& kvLen, const std::vector<double>& mask,
                              long maskSB, long maskSH);
 // New: the backward of a square (S x S) forward with key padding kvLen[B]

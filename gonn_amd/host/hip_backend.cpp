@@ -167,28 +167,29 @@ FwdOut FlashAttnF64Masked(const std::vector<double>& Q, const std::vector<double
 BwdOut FlashAttnF64BwdMasked(const std::vector<double>& Q, const std::vector<double>& K,
                              const std::vector<double>& V, const std::vector<double>& O,
                              const std::vector<double>& L, const std::vector<double>& dO, int B,
-                             int H, int S, int d, double scale, bool causal,
+                             int H, int Sq, int Sk, int d, double scale, bool causal,
                              const std::vector<int>& kvLen, const std::vector<double>& mask,
                              long maskSB, long maskSH) {
     if (B <= 0 || H <= 0) throw std::invalid_argument("hip: FlashAttnF64BwdMasked: B, H must be >= 1");
-    shape_ok(B * H, S, d, "FlashAttnF64BwdMasked");
-    const size_t n = (size_t)B * H * S * d;
-    need(Q, n, "FlashAttnF64BwdMasked Q");
-    need(K, n, "FlashAttnF64BwdMasked K");
-    need(V, n, "FlashAttnF64BwdMasked V");
-    need(O, n, "FlashAttnF64BwdMasked O");
-    need(L, (size_t)B * H * S, "FlashAttnF64BwdMasked L");
-    need(dO, n, "FlashAttnF64BwdMasked dO");
-    if (!mask.empty()) need(mask, mask_span(B, H, S, S, maskSB, maskSH), "FlashAttnF64BwdMasked mask");
+    shape_ok(B * H, Sq, d, "FlashAttnF64BwdMasked");
+    shape_ok(B * H, Sk, d, "FlashAttnF64BwdMasked");
+    const size_t nq = (size_t)B * H * Sq * d, nk = (size_t)B * H * Sk * d;
+    need(Q, nq, "FlashAttnF64BwdMasked Q");
+    need(K, nk, "FlashAttnF64BwdMasked K");
+    need(V, nk, "FlashAttnF64BwdMasked V");
+    need(O, nq, "FlashAttnF64BwdMasked O");
+    need(L, (size_t)B * H * Sq, "FlashAttnF64BwdMasked L");
+    need(dO, nq, "FlashAttnF64BwdMasked dO");
+    if (!mask.empty()) need(mask, mask_span(B, H, Sq, Sk, maskSB, maskSH), "FlashAttnF64BwdMasked mask");
     if (!kvLen.empty() && (int)kvLen.size() != B)
         throw std::invalid_argument("hip: FlashAttnF64BwdMasked: kvLen needs B entries");
     BwdOut r;
-    r.dQ.assign(n, 0.0);
-    r.dK.assign(n, 0.0);
-    r.dV.assign(n, 0.0);
+    r.dQ.assign(nq, 0.0);
+    r.dK.assign(nk, 0.0);
+    r.dV.assign(nk, 0.0);
     check(gonn_hip_flash_attn_f64_bwd_masked(Q.data(), K.data(), V.data(), O.data(), L.data(),
                                              dO.data(), r.dQ.data(), r.dK.data(), r.dV.data(), B,
-                                             H, S, d, scale, causal ? 1 : 0,
+                                             H, Sq, Sk, d, scale, causal ? 1 : 0,
                                              kvLen.empty() ? nullptr : kvLen.data(),
                                              mask.empty() ? nullptr : mask.data(), maskSB, maskSH),
           "FlashAttnF64BwdMasked");

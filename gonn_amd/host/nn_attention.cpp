@@ -124,7 +124,8 @@ DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int 
         const Tensor &q = (*saved)[0], &k = (*saved)[1], &v = (*saved)[2];
         hip::BwdOut b =
             masked ? hip::FlashAttnF64BwdMasked(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH / H,
-                                                H, S, D, scale, causal, kvLen, *mask, st[0], st[1])
+                                                H, S, S, D, scale, causal, kvLen, *mask, st[0],
+                                                st[1])
             : kvLen.empty()
                 ? hip::FlashAttnF64Bwd(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH, S, D, scale,
                                        causal)

@@ -105,7 +105,7 @@ typedef struct {
 
 /* Backward from the saved forward tensors: dQ, dK, dV (all GONN_F32).
  * q, k, v, o, dO: GONN_F32; lse: GONN_F32 from gonn_hip_attn_fwd.
- * Sq == Sk is required (the reference backward's contract).
+ * S is the query (and, unless Sk is set, key) count.
  * deterministic: accepted for API completeness; every mode of this library
  * is deterministic (no floating-point atomics), so 0 and 1 give
  * bit-identical results.
@@ -122,9 +122,13 @@ typedef struct {
     int deterministic;
     gonn_buf kv_len;
     /* The forward's additive mask (layout as in gonn_attn_fwd_args with
-     * Sq = Sk = S); a masked call runs the fp32-MFMA kernels.              */
+     * Sq = S); a masked call runs the fp32-MFMA kernels.                   */
     gonn_buf attn_mask;
     int64_t mask_stride_b, mask_stride_h;
+    /* Key rows when they differ from the S query rows (cross-attention with
+     * the forward's top-left causal mask): k, v, dk, dv are (B*H, Sk, D).
+     * 0 means Sk = S. A cross-attention call runs the fp32-MFMA kernels.   */
+    int Sk;
 } gonn_attn_bwd_args;
 
 /* KV-cache decode, one query per (b, h): o[b,h] = attention of q[b,h] over
@@ -336,17 +340,20 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
 
 /* Additive-mask forms of the two general fp64 entries (new): mask is host
  * fp64 data read as in gonn_attn_fwd_args.attn_mask with element strides
- * mask_sb (sequence) and mask_sh (head) and rows Sk apart (S for the
- * backward); NULL = none. They run the fp32-MFMA kernels in either mode.  */
+ * mask_sb (sequence) and mask_sh (head) and rows Sk apart; NULL = none. The
+ * backward also takes cross-attention (Sq != Sk: K, V, dK, dV are
+ * (B*H, Sk, d)). Masked or cross-attention calls run the fp32-MFMA kernels
+ * in either mode.                                                          */
 int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const double* V, double* O,
                                    double* L, int B, int H, int Sq, int Sk, int d, double scale,
                                    int causal, const int* kv_len, const double* mask,
                                    long mask_sb, long mask_sh);
 int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const double* V,
                                        const double* O, const double* L, const double* dO,
-                                       double* dQ, double* dK, double* dV, int B, int H, int S,
-                                       int d, double scale, int causal, const int* kv_len,
-                                       const double* mask, long mask_sb, long mask_sh);
+                                       double* dQ, double* dK, double* dV, int B, int H, int Sq,
+                                       int Sk, int d, double scale, int causal,
+                                       const int* kv_len, const double* mask, long mask_sb,
+                                       long mask_sh);
 /* New (the reference's fused seam is Tq == Tk, causal-or-not only): the
  * general forward on host fp64 arrays for the wider fused gate, i.e.
  * cross-attention (Sq != Sk, top-left causal mask when causal) and

@@ -53,6 +53,8 @@ def _load():
         ctypes.c_double, ctypes.c_int]
     lib.oracle_attn_bwd_autograd_ex.argtypes = [_dp] * 7 + [ctypes.c_int] * 4 + [
         ctypes.c_double, ctypes.c_int, _ip, _dp, ctypes.c_long, ctypes.c_long]
+    lib.oracle_attn_bwd_autograd_x.argtypes = [_dp] * 7 + [ctypes.c_int] * 5 + [
+        ctypes.c_double, ctypes.c_int, _ip, _dp, ctypes.c_long, ctypes.c_long]
     lib.oracle_attn_fwd_ex.argtypes = [_dp, _dp, _dp, _dp, _dp, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                        ctypes.c_double, ctypes.c_int, _ip, _dp, ctypes.c_long,
@@ -154,6 +156,7 @@ def attn_bwd_autograd(Q, K, V, dO, scale=None, causal=False, kv_len=None, H=1, a
     lib = _load()
     Q, K, V, dO = _c64(Q), _c64(K), _c64(V), _c64(dO)
     BH, S, D = Q.shape
+    Sk = K.shape[1]  # != S for cross-attention (top-left causal)
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     dQ, dK, dV = np.zeros_like(Q), np.zeros_like(K), np.zeros_like(V)
@@ -163,11 +166,11 @@ def attn_bwd_autograd(Q, K, V, dO, scale=None, causal=False, kv_len=None, H=1, a
         assert kl.shape == (BH // H,)
     am, sb, sh = (None, 0, 0)
     if attn_mask is not None:
-        am, sb, sh = mask_layout(attn_mask, BH // H, H, S, S)
-    rc = lib.oracle_attn_bwd_autograd_ex(_d(Q), _d(K), _d(V), _d(dO), _d(dQ), _d(dK), _d(dV),
-                                         BH, int(H), S, D, float(scale), int(bool(causal)),
-                                         kl.ctypes.data_as(_ip) if kl is not None else None,
-                                         _d(am) if am is not None else None, sb, sh)
+        am, sb, sh = mask_layout(attn_mask, BH // H, H, S, Sk)
+    rc = lib.oracle_attn_bwd_autograd_x(_d(Q), _d(K), _d(V), _d(dO), _d(dQ), _d(dK), _d(dV),
+                                        BH, int(H), S, Sk, D, float(scale), int(bool(causal)),
+                                        kl.ctypes.data_as(_ip) if kl is not None else None,
+                                        _d(am) if am is not None else None, sb, sh)
     if rc != 0:
         raise RuntimeError(f"oracle_attn_bwd_autograd failed: {rc}")
     return dQ, dK, dV

@@ -222,29 +222,31 @@ int oracle_attn_fwd(const double* Q, const double* K, const double* V, double* O
  * Given g = dL/dctx: walks the nodes in reverse topological order, summing
  * the two gradient contributions into e (Div numerator and SumAxis) and into
  * masked (Sub and MaxAxis scatter) as tensor/autograd.go:52-99 accumulates
- * them. kv_len: NULL, or per-batch valid key counts (length BH/H): the key
+ * them. Q, dO, dQ are (BH,Sq,D), K, V, dK, dV (BH,Sk,D) (Sq != Sk for
+ * cross-attention, top-left causal). kv_len: NULL, or per-batch valid key
+ * counts (length BH/H): the key
  * padding mask ForwardMasked adds (nn/attention.go:261-272, :321-330), one
  * more additive -1e30 term of `mask`; amask / mask_sb / mask_sh: the user's
  * additive mask as in oracle_attn_fwd_ex (a constant: its gradient is not
  * needed, the chain passes through the addition unchanged).
  */
-int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* V,
-                                const double* dO, double* dQ, double* dK, double* dV,
-                                int BH, int H, int S, int D, double scale, int causal,
-                                const int* kv_len, const double* amask, long mask_sb,
-                                long mask_sh) {
-    if (BH <= 0 || S <= 0 || D <= 0 || H <= 0 || BH % H != 0) return -1;
-    const size_t SS = (size_t)S * S;
-    double* KT = (double*)malloc(sizeof(double) * (size_t)D * S);
-    double* msk = (double*)malloc(sizeof(double) * SS);  /* masked scores */
-    double* e = (double*)malloc(sizeof(double) * SS);
-    double* attn = (double*)malloc(sizeof(double) * SS);
-    double* g_attn = (double*)malloc(sizeof(double) * SS);
-    double* g_e = (double*)malloc(sizeof(double) * SS);
-    double* g_m = (double*)malloc(sizeof(double) * SS);
-    double* VT = (double*)malloc(sizeof(double) * (size_t)D * S);
-    double* AT = (double*)malloc(sizeof(double) * SS);
-    double* GT = (double*)malloc(sizeof(double) * SS);
+int oracle_attn_bwd_autograd_x(const double* Q, const double* K, const double* V,
+                               const double* dO, double* dQ, double* dK, double* dV, int BH,
+                               int H, int Sq, int Sk, int D, double scale, int causal,
+                               const int* kv_len, const double* amask, long mask_sb,
+                               long mask_sh) {
+    if (BH <= 0 || Sq <= 0 || Sk <= 0 || D <= 0 || H <= 0 || BH % H != 0) return -1;
+    const size_t QK = (size_t)Sq * Sk;
+    double* KT = (double*)malloc(sizeof(double) * (size_t)D * Sk);
+    double* msk = (double*)malloc(sizeof(double) * QK);  /* masked scores */
+    double* e = (double*)malloc(sizeof(double) * QK);
+    double* attn = (double*)malloc(sizeof(double) * QK);
+    double* g_attn = (double*)malloc(sizeof(double) * QK);
+    double* g_e = (double*)malloc(sizeof(double) * QK);
+    double* g_m = (double*)malloc(sizeof(double) * QK);
+    double* VT = (double*)malloc(sizeof(double) * (size_t)D * Sk);
+    double* AT = (double*)malloc(sizeof(double) * QK);
+    double* GT = (double*)malloc(sizeof(double) * QK);
     if (!KT || !msk || !e || !attn || !g_attn || !g_e || !g_m || !VT || !AT || !GT) {
         free(KT); free(msk); free(e); free(attn); free(g_attn); free(g_e); free(g_m);
         free(VT); free(AT); free(GT);
@@ -252,89 +254,99 @@ int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* 
     }
     const double sc = (g_mutation == MUT_NO_SCALE) ? 1.0 : scale;
     for (int bh = 0; bh < BH; bh++) {
-        const double* Qb = Q + (size_t)bh * S * D;
-        const double* Kb = K + (size_t)bh * S * D;
-        const double* Vb = V + (size_t)bh * S * D;
-        const double* G = dO + (size_t)bh * S * D;
-        double* dQb = dQ + (size_t)bh * S * D;
-        double* dKb = dK + (size_t)bh * S * D;
-        double* dVb = dV + (size_t)bh * S * D;
+        const double* Qb = Q + (size_t)bh * Sq * D;
+        const double* Kb = K + (size_t)bh * Sk * D;
+        const double* Vb = V + (size_t)bh * Sk * D;
+        const double* G = dO + (size_t)bh * Sq * D;
+        double* dQb = dQ + (size_t)bh * Sq * D;
+        double* dKb = dK + (size_t)bh * Sk * D;
+        double* dVb = dV + (size_t)bh * Sk * D;
         /* forward, keeping the graph's tensors */
-        transpose(Kb, KT, S, D);
-        int len = S;
+        transpose(Kb, KT, Sk, D);
+        int len = Sk;
         if (kv_len) {
             len = kv_len[bh / H];
-            len = len < 0 ? 0 : (len > S ? S : len);
+            len = len < 0 ? 0 : (len > Sk ? Sk : len);
         }
         const double* am = amask ? amask + (size_t)(bh / H) * mask_sb + (size_t)(bh % H) * mask_sh
                                  : NULL;
-        scores_rows(Qb, KT, S, D, NULL, S, scale, causal, am, len, msk);
-        int* amax = (int*)malloc(sizeof(int) * S);
-        double* se = (double*)malloc(sizeof(double) * S);
-        double* g_se = (double*)malloc(sizeof(double) * S);
-        double* g_mx = (double*)malloc(sizeof(double) * S);
+        scores_rows(Qb, KT, Sk, D, NULL, Sq, scale, causal, am, len, msk);
+        int* amax = (int*)malloc(sizeof(int) * Sq);
+        double* se = (double*)malloc(sizeof(double) * Sq);
+        double* g_se = (double*)malloc(sizeof(double) * Sq);
+        double* g_mx = (double*)malloc(sizeof(double) * Sq);
         #pragma omp parallel for schedule(static)
-        for (int i = 0; i < S; i++) {
-            const double* x = msk + (size_t)i * S;
+        for (int i = 0; i < Sq; i++) {
+            const double* x = msk + (size_t)i * Sk;
             double best = -INFINITY;
             int bi = 0;
-            for (int j = 0; j < S; j++)
+            for (int j = 0; j < Sk; j++)
                 if (x[j] > best) { best = x[j]; bi = j; }
             amax[i] = bi;
             double s = 0.0;
-            for (int j = 0; j < S; j++) {
-                e[(size_t)i * S + j] = exp(x[j] - best);
-                s += e[(size_t)i * S + j];
+            for (int j = 0; j < Sk; j++) {
+                e[(size_t)i * Sk + j] = exp(x[j] - best);
+                s += e[(size_t)i * Sk + j];
             }
             se[i] = s;
-            for (int j = 0; j < S; j++) attn[(size_t)i * S + j] = e[(size_t)i * S + j] / s;
+            for (int j = 0; j < Sk; j++) attn[(size_t)i * Sk + j] = e[(size_t)i * Sk + j] / s;
         }
         /* ctx = attn @ V: dattn = g @ V^T, dV = attn^T @ g */
-        transpose(Vb, VT, S, D);
-        gemm_nn(G, VT, g_attn, S, D, S);
-        transpose(attn, AT, S, S);
-        gemm_nn(AT, G, dVb, S, S, D);
+        transpose(Vb, VT, Sk, D);
+        gemm_nn(G, VT, g_attn, Sq, D, Sk);
+        transpose(attn, AT, Sq, Sk);
+        gemm_nn(AT, G, dVb, Sk, Sq, D);
         /* attn = e / se (broadcast): ga = g / se, gb = -g * e / se^2 summed */
         #pragma omp parallel for schedule(static)
-        for (int i = 0; i < S; i++) {
+        for (int i = 0; i < Sq; i++) {
             double acc = 0.0;
-            for (int j = 0; j < S; j++) {
-                const double g = g_attn[(size_t)i * S + j];
-                g_e[(size_t)i * S + j] = g / se[i];
-                acc += -g * e[(size_t)i * S + j] / (se[i] * se[i]);
+            for (int j = 0; j < Sk; j++) {
+                const double g = g_attn[(size_t)i * Sk + j];
+                g_e[(size_t)i * Sk + j] = g / se[i];
+                acc += -g * e[(size_t)i * Sk + j] / (se[i] * se[i]);
             }
             g_se[i] = acc;
         }
         /* se = SumAxis(e): broadcast back and accumulate into g_e */
         #pragma omp parallel for schedule(static)
-        for (int i = 0; i < S; i++)
-            for (int j = 0; j < S; j++) g_e[(size_t)i * S + j] += g_se[i];
+        for (int i = 0; i < Sq; i++)
+            for (int j = 0; j < Sk; j++) g_e[(size_t)i * Sk + j] += g_se[i];
         /* e = Exp(sh): g_sh = g_e * e; sh = masked - mx */
         #pragma omp parallel for schedule(static)
-        for (int i = 0; i < S; i++) {
+        for (int i = 0; i < Sq; i++) {
             double acc = 0.0;
-            for (int j = 0; j < S; j++) {
-                const double gs = g_e[(size_t)i * S + j] * e[(size_t)i * S + j];
-                g_m[(size_t)i * S + j] = gs;
+            for (int j = 0; j < Sk; j++) {
+                const double gs = g_e[(size_t)i * Sk + j] * e[(size_t)i * Sk + j];
+                g_m[(size_t)i * Sk + j] = gs;
                 acc += -gs;
             }
             g_mx[i] = acc;
         }
         /* mx = MaxAxis(masked): scatter to the argmax */
-        for (int i = 0; i < S; i++) g_m[(size_t)i * S + amax[i]] += g_mx[i];
+        for (int i = 0; i < Sq; i++) g_m[(size_t)i * Sk + amax[i]] += g_mx[i];
         /* masked = scaled + mask: identity; scaled = raw * scale */
         #pragma omp parallel for schedule(static)
-        for (int i = 0; i < S; i++)
-            for (int j = 0; j < S; j++) g_m[(size_t)i * S + j] = g_m[(size_t)i * S + j] * sc;
+        for (int i = 0; i < Sq; i++)
+            for (int j = 0; j < Sk; j++) g_m[(size_t)i * Sk + j] = g_m[(size_t)i * Sk + j] * sc;
         /* raw = Q @ K^T: dQ = g_raw @ K, d(K^T) = Q^T @ g_raw -> dK = g_raw^T @ Q */
-        gemm_nn(g_m, Kb, dQb, S, S, D);
-        transpose(g_m, GT, S, S);
-        gemm_nn(GT, Qb, dKb, S, S, D);
+        gemm_nn(g_m, Kb, dQb, Sq, Sk, D);
+        transpose(g_m, GT, Sq, Sk);
+        gemm_nn(GT, Qb, dKb, Sk, Sq, D);
         free(amax); free(se); free(g_se); free(g_mx);
     }
     free(KT); free(msk); free(e); free(attn); free(g_attn); free(g_e); free(g_m);
     free(VT); free(AT); free(GT);
     return 0;
+}
+
+/* The square form (S x S) of oracle_attn_bwd_autograd_x. */
+int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* V,
+                                const double* dO, double* dQ, double* dK, double* dV,
+                                int BH, int H, int S, int D, double scale, int causal,
+                                const int* kv_len, const double* amask, long mask_sb,
+                                long mask_sh) {
+    return oracle_attn_bwd_autograd_x(Q, K, V, dO, dQ, dK, dV, BH, H, S, S, D, scale, causal,
+                                      kv_len, amask, mask_sb, mask_sh);
 }
 
 /* The reference backward's signature (no key padding). */

@@ -175,6 +175,22 @@ def test_bwd_argument_errors():
     a.lse.bytes = B * H * S * 4
     a.dq.dtype = GONN_BF16
     assert lib.gonn_hip_attn_bwd(ctypes.byref(a), None, 0, None) == GONN_E_INVALID
+    a.dq.dtype = GONN_F32
+    # Cross-attention: k, v, dk, dv must hold (B*H, Sk, D); a negative Sk is invalid.
+    a.Sk = -1
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), None, 0, None) == GONN_E_INVALID
+    a.Sk = 2 * S
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), None, 0, None) == GONN_E_INVALID
+    for name in ("k", "v", "dk", "dv"):
+        getattr(a, name).bytes = 2 * n
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), None, 0, None) == GONN_E_WORKSPACE
+    # An additive mask must cover (B-1)*sb + (H-1)*sh + S*Sk f32 elements.
+    a.attn_mask = Buf(P, 4 * S * 2 * S - 4, GONN_F32)
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), None, 0, None) == GONN_E_INVALID
+    a.attn_mask.bytes = 4 * S * 2 * S
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), None, 0, None) == GONN_E_WORKSPACE
+    a.mask_stride_h = -1
+    assert lib.gonn_hip_attn_bwd(ctypes.byref(a), None, 0, None) == GONN_E_INVALID
     assert lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, None) == 0
 
 

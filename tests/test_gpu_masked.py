@@ -279,3 +279,49 @@ def test_attn_mask_cross_attention_and_nn(mode="fp32"):
     ref = oracle.attn_bwd_autograd(q2, k2, v2, g2, causal=False, H=BH, attn_mask=m2)
     for got, r, n in zip(grads, ref, ("dQ", "dK", "dV")):
         assert_close(got.reshape(BH, S, D), r, "fp32", f"fused_attn_diff {n} attn_mask")
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("sq_sk", [(70, 150), (150, 70)], ids=lambda t: f"{t[0]}x{t[1]}")
+def test_cross_attention_backward_matches_oracle(mode, D, causal, sq_sk):
+    """Cross-attention backward (Sq != Sk, top-left causal, key padding):
+    dQ (B*H,Sq,D), dK, dV (B*H,Sk,D) against the oracle's autograd chain.
+    The backward runs the fp32-MFMA kernels in either mode; O and LSE come
+    from the forward of the stated mode, whose bar applies."""
+    from gonn_amd import hip
+    Sq, Sk = sq_sk
+    B, H = 2, 2
+    lens = np.array([Sk, Sk // 2 + 3], dtype=np.int32)
+    say(f"[masked] cross bwd mode={mode} D={D} causal={causal} Sq={Sq} Sk={Sk}")
+    q, g = (randn((B * H, Sq, D), 930 + i) for i in range(2))
+    k, v = (randn((B * H, Sk, D), 932 + i) for i in range(2))
+    dq_, dg_ = (torch.from_numpy(x).cuda().reshape(B, H, Sq, D) for x in (q, g))
+    dk_, dv_ = (torch.from_numpy(x).cuda().reshape(B, H, Sk, D) for x in (k, v))
+    kl = torch.from_numpy(lens).cuda()
+    o, l = hip.attn_fwd(dq_, dk_, dv_, causal=causal, mode=mode, kv_len=kl)
+    dq, dk, dv = hip.attn_bwd(dq_, dk_, dv_, o, l, dg_, causal=causal, mode=mode, kv_len=kl)
+    torch.cuda.synchronize()
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H)
+    assert dk.shape == dk_.shape and dq.shape == dq_.shape
+    assert_close(dq.reshape(B * H, Sq, D).cpu().numpy(), rq, mode, "cross dQ")
+    assert_close(dk.reshape(B * H, Sk, D).cpu().numpy(), rk, mode, "cross dK")
+    assert_close(dv.reshape(B * H, Sk, D).cpu().numpy(), rv, mode, "cross dV")
+
+
+def test_cross_attention_backward_f64_entry():
+    """gonn_hip_flash_attn_f64_bwd_masked with Sq != Sk through
+    FlashAttnF64BwdEx, with an additive (Sq, Sk) mask."""
+    from gonn_amd import hip
+    B, H, Sq, Sk, D = 2, 1, 40, 90, 64
+    q, g = (randn((B * H, Sq, D), 940 + i) for i in range(2))
+    k, v = (randn((B * H, Sk, D), 942 + i) for i in range(2))
+    m, _ = _mask_of("TqTk", 1, 1, Sq, Sk, 944)
+    sc = 1 / math.sqrt(D)
+    O, L = hip.FlashAttnF64Ex(q, k, v, B, H, Sq, Sk, D, sc, True, lse=True, attn_mask=m)
+    dq, dk, dv = hip.FlashAttnF64BwdEx(q, k, v, O, L, g, B, H, Sq, D, sc, True, attn_mask=m, Sk=Sk)
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=True, H=H, attn_mask=m)
+    assert_close(dq.reshape(B * H, Sq, D), rq, "fp32", "f64 cross dQ")
+    assert_close(dk.reshape(B * H, Sk, D), rk, "fp32", "f64 cross dK")
+    assert_close(dv.reshape(B * H, Sk, D), rv, "fp32", "f64 cross dV")

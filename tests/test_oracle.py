@@ -395,3 +395,26 @@ def test_additive_attn_mask_matches_torch(shape_kind):
         np.testing.assert_allclose(got, t.grad.numpy(), atol=1e-12, rtol=0)
     with pytest.raises(ValueError):
         oracle.attn_fwd(q, k, v, attn_mask=np.zeros((S, S + 1)), H=H)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_cross_attention_backward_matches_torch(causal):
+    """Cross-attention (Sq != Sk, top-left causal as causalMaskAdd builds it,
+    nn/attention.go:185-196) through the autograd chain, with key padding:
+    torch fp64 autograd through the same masks."""
+    rng = np.random.default_rng(37 + causal)
+    B, H, Sq, Sk, D = 2, 2, 21, 53, 64
+    q, g = (rng.standard_normal((B * H, Sq, D)) for _ in range(2))
+    k, v = (rng.standard_normal((B * H, Sk, D)) for _ in range(2))
+    lens = [53, 30]
+    dq, dk, dv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H)
+    tq, tk, tv = (torch.tensor(x, requires_grad=True) for x in (q, k, v))
+    s = (tq @ tk.transpose(1, 2)) / math.sqrt(D)
+    if causal:
+        s = s + torch.where(torch.arange(Sk)[None, :] > torch.arange(Sq)[:, None], -1e30, 0.0)
+    pad = torch.zeros(B * H, 1, Sk, dtype=torch.float64)
+    for bh in range(B * H):
+        pad[bh, :, lens[bh // H]:] = -1e30
+    (torch.softmax(s + pad, -1) @ tv).backward(torch.tensor(g))
+    for got, t in ((dq, tq), (dk, tk), (dv, tv)):
+        np.testing.assert_allclose(got, t.grad.numpy(), atol=1e-12, rtol=0)
