@@ -113,8 +113,8 @@ def bench_prefill(torch, hip, steps, warmup):
     kt, kn = hip.profile_read("fwd_bf16")
     pt, pn = hip.profile_read("pack_kv")
     hip.profile_reset()
-    # The library splits a large forward into head chunks (one pack and one
-    # attention launch each): per-launch time and FLOP, launches per step.
+    # Per-launch time of each stage and the launches per step (one pack and
+    # one attention kernel per gonn_hip_attn_fwd call).
     return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, median_ms=med, wall_s=wall,
                 kernel_ms=kt / max(kn, 1), pack_ms=pt / max(pn, 1),
                 launches=max(kn, 1) / steps, q=q, k=k, v=v)
