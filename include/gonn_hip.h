@@ -98,7 +98,10 @@ typedef struct {
      * padding, as ForwardMasked orders them. Strides (elements, >= 0) of 0
      * broadcast: (Sq,Sk) -> 0, 0; (B,Sq,Sk) -> Sq*Sk, 0; (B*H,Sq,Sk) and
      * (B,H,Sq,Sk) -> H*Sq*Sk, Sq*Sk. A masked call runs the fp32-MFMA
-     * kernels in either mode and needs GONN_F32 q, k, v.                    */
+     * kernels in either mode and needs GONN_F32 q, k, v. A row whose every
+     * key carries a -1e30-scale term (the mask's, or the mask's plus the
+     * causal one) has no finite LSE in fp32: such rows are outside this
+     * library's definition, as fully padded ones are.                      */
     gonn_buf attn_mask;
     int64_t mask_stride_b, mask_stride_h;
 } gonn_attn_fwd_args;
