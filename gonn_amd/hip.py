@@ -277,11 +277,12 @@ def buf(t) -> Buf:
     return Buf(t.data_ptr(), t.numel() * t.element_size(), _dtype_code(t))
 
 
+def _torch_stream(stream):
+    return _torch().cuda.current_stream() if stream is None else stream
+
+
 def _stream(stream):
-    torch = _torch()
-    if stream is None:
-        stream = torch.cuda.current_stream()
-    return ctypes.c_void_p(stream.cuda_stream)
+    return ctypes.c_void_p(_torch_stream(stream).cuda_stream)
 
 
 class _Workspace:
@@ -293,14 +294,22 @@ class _Workspace:
         self._mu = threading.Lock()
 
     def get(self, nbytes: int, device, stream):
+        """stream: the torch stream the call runs on. A new buffer is
+        allocated on that stream, and a replaced one is marked as used there,
+        so torch's caching allocator cannot hand it out while queued kernels
+        still read it."""
         if nbytes == 0:
             return None
         torch = _torch()
-        key = (str(device), stream.value)
+        stream = _torch_stream(stream)
+        key = (str(device), stream.cuda_stream)
         with self._mu:
             t = self._bufs.get(key)
             if t is None or t.numel() < nbytes:
-                t = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
+                if t is not None:
+                    t.record_stream(stream)
+                with torch.cuda.stream(stream):
+                    t = torch.empty(int(nbytes), dtype=torch.uint8, device=device)
                 self._bufs[key] = t
             return t
 
@@ -365,7 +374,7 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_FWD, ctypes.byref(a))
-    ws = _WS.get(nb, q.device, st)
+    ws = _WS.get(nb, q.device, stream)
     check(lib.gonn_hip_attn_fwd(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
                                 nb, st), "attn_fwd")
     return out, l
@@ -398,7 +407,7 @@ def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp3
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
-    ws = _WS.get(nb, q.device, st)
+    ws = _WS.get(nb, q.device, stream)
     check(lib.gonn_hip_attn_bwd(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
                                 nb, st), "attn_bwd")
     return dq, dk, dv
@@ -419,7 +428,7 @@ def attn_decode(q, kcache, vcache, kv_len, *, scale=None, split_keys: int = 0, o
     lib = _lib.load()
     st = _stream(stream)
     nb = lib.gonn_hip_attn_workspace_bytes(GONN_OP_DECODE, ctypes.byref(a))
-    ws = _WS.get(nb, q.device, st)
+    ws = _WS.get(nb, q.device, stream)
     check(lib.gonn_hip_attn_decode(ctypes.byref(a), ws.data_ptr() if ws is not None else None,
                                    nb, st), "attn_decode")
     return out

@@ -82,3 +82,52 @@ def test_random_case(i):
         assert_close(got[live], ref[live], fmode, f"{n} case {i}")
         assert np.all(got[~live] == 0.0), f"{n} case {i}: a sequence with no key"
     assert np.all(o[~live] == 0.0)
+
+
+def test_concurrent_calls_on_separate_streams():
+    """The entry points are reentrant (gonn_hip.h): threads running forward +
+    backward on their own streams at once give exactly what each call gives
+    alone (the reference's contract allows concurrent Backward calls,
+    tensor/autograd.go:10-32)."""
+    import threading
+    from gonn_amd import hip
+    cases = []
+    for t in range(4):
+        r = np.random.default_rng(7000 + t)
+        B, H, S, D = 2, 2, 96 + 37 * t, (64, 128)[t % 2]
+        mode = ("fp32", "bf16")[t // 2]
+        x = [torch.from_numpy(r.standard_normal((B, H, S, D)).astype(np.float32)).cuda()
+             for _ in range(4)]
+        cases.append((x, mode))
+    torch.cuda.synchronize()
+
+    def run(x, mode):
+        o, l = hip.attn_fwd(x[0], x[1], x[2], causal=True, mode=mode)
+        g = hip.attn_bwd(x[0], x[1], x[2], o, l, x[3], causal=True, mode=mode)
+        return [o, l, *g]
+
+    ref = [run(*c) for c in cases]
+    torch.cuda.synchronize()
+    got = [None] * len(cases)
+    errs = []
+
+    def worker(i):
+        try:
+            s = torch.cuda.Stream()
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    got[i] = run(*cases[i])
+            s.synchronize()
+        except Exception as e:  # surfaced below
+            errs.append(repr(e))
+
+    ts = [threading.Thread(target=worker, args=(i,)) for i in range(len(cases))]
+    for t in ts:
+        t.start()
+    for t in ts:
+        t.join(timeout=120)
+    torch.cuda.synchronize()
+    assert not errs, errs
+    for i in range(len(cases)):
+        for a, b in zip(got[i], ref[i]):
+            assert torch.equal(a, b), f"thread {i}"
