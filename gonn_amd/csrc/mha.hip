@@ -10,7 +10,9 @@
 // device buffers, a caller workspace and a stream, and allocates nothing.
 //
 // Per forward, on one stream:
-//   Y_p = x_p W_p^T            rocBLAS fp64 (gonn_hip_gemm_f64_dev), p = q, k, v
+//   Y_p = x_p W_p^T            rocBLAS fp64 (gonn_hip_gemm_f64_dev), p = q, k, v;
+//                              one GEMM against the stacked (3E, E) weights for
+//                              self-attention with kdim = vdim = E
 //   heads_p = split(Y_p + b_p)  fp32 (B, H, T, dp), zero-padded to dp = 64 | 128
 //   O = attention core          gonn_hip_attn_fwd (current MFMA mode)
 //   ctx = merge(O)              fp64 (B, Tq, E)
@@ -41,12 +43,12 @@ unsigned grid_for(size_t n) {
     return (unsigned)(want < 4096 ? (want ? want : 1) : 4096);
 }
 
-// heads[b][h][t][d] = Y[b][t][h D + d] + bias[h D + d] for d < D, 0 for D <= d < dp.
+// heads[b][h][t][d] = Y[b][t][h D + d] + bias[h D + d] for d < D, 0 for D <= d < dp;
+// rows of Y are ldy apart (E, or 3E for the fused q/k/v projection).
 __global__ __launch_bounds__(256) void split_heads_kernel(const double* __restrict__ Y,
                                                           const double* __restrict__ bias,
                                                           float* __restrict__ heads, int T, int H,
-                                                          int D, int dp, size_t total) {
-    const size_t E = (size_t)H * D;
+                                                          int D, int dp, size_t ldy, size_t total) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
          i += (size_t)gridDim.x * blockDim.x) {
         const int d = (int)(i % dp);
@@ -58,7 +60,7 @@ __global__ __launch_bounds__(256) void split_heads_kernel(const double* __restri
         float v = 0.f;
         if (d < D) {
             const size_t e = (size_t)h * D + d;
-            v = (float)(Y[(b * T + t) * E + e] + bias[e]);
+            v = (float)(Y[(b * T + t) * ldy + e] + bias[e]);
         }
         heads[i] = v;
     }
@@ -95,8 +97,11 @@ gonn_buf f64buf(const void* p, size_t n) { return gonn_buf{(void*)p, n * sizeof(
 // The handle of the C ABI (opaque to callers).
 struct gonn_mha {
     int E = 0, H = 0, D = 0, dp = 0, kdim = 0, vdim = 0;
-    double* W[4] = {nullptr, nullptr, nullptr, nullptr};  // q, k, v, out: (E, in)
-    double* b[4] = {nullptr, nullptr, nullptr, nullptr};  // (E)
+    // q, k, v, out weights (E, in), one allocation in that order, so that for
+    // kdim = vdim = E the first three form one (3E, E) matrix: a
+    // self-attention forward projects q, k and v with a single GEMM.
+    double* W[4] = {nullptr, nullptr, nullptr, nullptr};
+    double* b[4] = {nullptr, nullptr, nullptr, nullptr};  // (E) each, one allocation
     std::mutex mu;       // guards the host entry's workspace
     void* ws = nullptr;  // grow-only workspace of gonn_hip_mha_forward_f64
     size_t ws_bytes = 0;
@@ -105,10 +110,8 @@ struct gonn_mha {
 namespace {
 
 void mha_release(gonn_mha* m) {
-    for (int i = 0; i < 4; i++) {
-        if (m->W[i]) (void)hipFree(m->W[i]);
-        if (m->b[i]) (void)hipFree(m->b[i]);
-    }
+    if (m->W[0]) (void)hipFree(m->W[0]);
+    if (m->b[0]) (void)hipFree(m->b[0]);
     if (m->ws) (void)hipFree(m->ws);
 }
 
@@ -173,13 +176,27 @@ int run_forward(gonn_mha* m, const double* xq, const double* xk, const double* x
     const int in[3] = {E, m->kdim, m->vdim};
     const size_t rows[3] = {nq, nk, nk};
     const int T[3] = {Tq, Tk, Tk};
+    // Self-attention with square projections: one GEMM against the stacked
+    // (3E, E) weights writes [Q | K | V] rows of 3E into Yq's slot, which the
+    // layout follows with Yk's and Yv's (room for 3 nq E values).
+    const bool fused = xq == xk && xk == xv && Tq == Tk && m->kdim == E && m->vdim == E;
+    if (fused) {
+        const gonn_buf A = f64buf(xq, nq * E), Wb = f64buf(m->W[0], (size_t)3 * E * E);
+        gonn_buf C = f64buf(Y[0], nq * 3 * E);
+        TRY(gonn_hip_gemm_f64_dev(&A, &Wb, &C, 1, (int)nq, E, 3 * E, 0, 1, s));
+    }
     for (int p = 0; p < 3; p++) {
-        const gonn_buf A = f64buf(x[p], rows[p] * in[p]), Wb = f64buf(m->W[p], (size_t)E * in[p]);
-        gonn_buf C = f64buf(Y[p], rows[p] * E);
-        TRY(gonn_hip_gemm_f64_dev(&A, &Wb, &C, 1, (int)rows[p], in[p], E, 0, 1, s));
+        if (!fused) {
+            const gonn_buf A = f64buf(x[p], rows[p] * in[p]),
+                           Wb = f64buf(m->W[p], (size_t)E * in[p]);
+            gonn_buf C = f64buf(Y[p], rows[p] * E);
+            TRY(gonn_hip_gemm_f64_dev(&A, &Wb, &C, 1, (int)rows[p], in[p], E, 0, 1, s));
+        }
+        const double* src = fused ? Y[0] + (size_t)p * E : Y[p];
+        const size_t ldy = fused ? (size_t)3 * E : (size_t)E;
         const size_t tot = rows[p] * H * dp;
-        hipLaunchKernelGGL(split_heads_kernel, dim3(grid_for(tot)), dim3(256), 0, s, Y[p], m->b[p],
-                           hd[p], T[p], H, D, dp, tot);
+        hipLaunchKernelGGL(split_heads_kernel, dim3(grid_for(tot)), dim3(256), 0, s, src, m->b[p],
+                           hd[p], T[p], H, D, dp, ldy, tot);
         TRY(herr(hipGetLastError()));
     }
     gonn_attn_fwd_args a{};
@@ -237,14 +254,19 @@ int gonn_hip_mha_create(gonn_mha** out, int E, int H, int kdim, int vdim, const 
     const double* W[4] = {Wq, Wk, Wv, Wo};
     const double* b[4] = {bq, bk, bv, bo};
     const int in[4] = {E, kdim, vdim, E};
+    const size_t wall = (size_t)E * (2 * (size_t)E + kdim + vdim);
+    if (hipMalloc(&m->W[0], wall * 8) != hipSuccess || hipMalloc(&m->b[0], (size_t)4 * E * 8) != hipSuccess) {
+        (void)hipGetLastError();
+        mha_release(m);
+        delete m;
+        return GONN_E_NOMEM;
+    }
+    for (int i = 1; i < 4; i++) {
+        m->W[i] = m->W[i - 1] + (size_t)E * in[i - 1];
+        m->b[i] = m->b[i - 1] + E;
+    }
     for (int i = 0; i < 4; i++) {
         const size_t wn = (size_t)E * in[i];
-        if (hipMalloc(&m->W[i], wn * 8) != hipSuccess || hipMalloc(&m->b[i], (size_t)E * 8) != hipSuccess) {
-            (void)hipGetLastError();
-            mha_release(m);
-            delete m;
-            return GONN_E_NOMEM;
-        }
         int rc = herr(hipMemcpy(m->W[i], W[i], wn * 8, hipMemcpyHostToDevice));
         // A missing bias is zero (nn.Linear without bias).
         if (!rc) rc = b[i] ? herr(hipMemcpy(m->b[i], b[i], (size_t)E * 8, hipMemcpyHostToDevice))
