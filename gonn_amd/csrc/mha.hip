@@ -66,6 +66,35 @@ __global__ __launch_bounds__(256) void split_heads_kernel(const double* __restri
     }
 }
 
+// The three splits of a fused projection in one launch: Y rows hold
+// [Q | K | V] (3E apart); tensor p of heads3[p] (each `per` values) takes
+// columns p E .. p E + E - 1 and bias3 + p E.
+__global__ __launch_bounds__(256) void split_heads3_kernel(const double* __restrict__ Y,
+                                                           const double* __restrict__ bias3,
+                                                           float* __restrict__ h0,
+                                                           float* __restrict__ h1,
+                                                           float* __restrict__ h2, int T, int H,
+                                                           int D, int dp, size_t per) {
+    const size_t E = (size_t)H * D;
+    for (size_t j = (size_t)blockIdx.x * blockDim.x + threadIdx.x; j < 3 * per;
+         j += (size_t)gridDim.x * blockDim.x) {
+        const int p = (int)(j / per);
+        const size_t i = j - (size_t)p * per;
+        const int d = (int)(i % dp);
+        const size_t r = i / dp;
+        const int t = (int)(r % T);
+        const size_t bh = r / T;
+        const int h = (int)(bh % H);
+        const size_t b = bh / H;
+        float v = 0.f;
+        if (d < D) {
+            const size_t e = (size_t)h * D + d;
+            v = (float)(Y[(b * T + t) * 3 * E + p * E + e] + bias3[p * E + e]);
+        }
+        (p == 0 ? h0 : p == 1 ? h1 : h2)[i] = v;
+    }
+}
+
 // ctx[b][t][h D + d] = O[b][h][t][d].
 __global__ __launch_bounds__(256) void merge_heads_kernel(const float* __restrict__ O,
                                                           double* __restrict__ ctx, int T, int H,
@@ -184,20 +213,21 @@ int run_forward(gonn_mha* m, const double* xq, const double* xk, const double* x
         const gonn_buf A = f64buf(xq, nq * E), Wb = f64buf(m->W[0], (size_t)3 * E * E);
         gonn_buf C = f64buf(Y[0], nq * 3 * E);
         TRY(gonn_hip_gemm_f64_dev(&A, &Wb, &C, 1, (int)nq, E, 3 * E, 0, 1, s));
-    }
-    for (int p = 0; p < 3; p++) {
-        if (!fused) {
+        const size_t per = nq * H * dp;
+        hipLaunchKernelGGL(split_heads3_kernel, dim3(grid_for(3 * per)), dim3(256), 0, s, Y[0],
+                           m->b[0], hd[0], hd[1], hd[2], Tq, H, D, dp, per);
+        TRY(herr(hipGetLastError()));
+    } else {
+        for (int p = 0; p < 3; p++) {
             const gonn_buf A = f64buf(x[p], rows[p] * in[p]),
                            Wb = f64buf(m->W[p], (size_t)E * in[p]);
             gonn_buf C = f64buf(Y[p], rows[p] * E);
             TRY(gonn_hip_gemm_f64_dev(&A, &Wb, &C, 1, (int)rows[p], in[p], E, 0, 1, s));
+            const size_t tot = rows[p] * H * dp;
+            hipLaunchKernelGGL(split_heads_kernel, dim3(grid_for(tot)), dim3(256), 0, s, Y[p],
+                               m->b[p], hd[p], T[p], H, D, dp, (size_t)E, tot);
+            TRY(herr(hipGetLastError()));
         }
-        const double* src = fused ? Y[0] + (size_t)p * E : Y[p];
-        const size_t ldy = fused ? (size_t)3 * E : (size_t)E;
-        const size_t tot = rows[p] * H * dp;
-        hipLaunchKernelGGL(split_heads_kernel, dim3(grid_for(tot)), dim3(256), 0, s, src, m->b[p],
-                           hd[p], T[p], H, D, dp, ldy, tot);
-        TRY(herr(hipGetLastError()));
     }
     gonn_attn_fwd_args a{};
     const size_t hq = nq * H * dp, hk = nk * H * dp;
