@@ -181,3 +181,50 @@ def test_elementwise_entry_checks():
     if not hip.Available():
         assert lib.gonn_hip_unary_f64(0, p, p, 8) == GONN_E_NODEVICE
         assert lib.gonn_hip_binary_f64(0, p, p, p, 8) == GONN_E_NODEVICE
+
+
+def test_mask_strides_follow_expand_attn_mask():
+    # nn/attention.go:242-257: the four accepted shapes and the panic otherwise.
+    B, H, Sq, Sk = 2, 3, 5, 7
+    assert hip.mask_strides((Sq, Sk), B, H, Sq, Sk) == (0, 0)
+    assert hip.mask_strides((B, Sq, Sk), B, H, Sq, Sk) == (Sq * Sk, 0)
+    assert hip.mask_strides((B * H, Sq, Sk), B, H, Sq, Sk) == (H * Sq * Sk, Sq * Sk)
+    assert hip.mask_strides((B, H, Sq, Sk), B, H, Sq, Sk) == (H * Sq * Sk, Sq * Sk)
+    for bad in ((Sk, Sq), (B, Sq, Sk + 1), (B * H + 1, Sq, Sk), (1, B, H, Sq, Sk)):
+        with pytest.raises(ValueError, match="attn mask shape"):
+            hip.mask_strides(bad, B, H, Sq, Sk)
+
+
+def test_key_padding_mask_to_kv_len():
+    # keyPaddingMaskAdd (nn/attention.go:261-272): nonzero = ignore; the fused
+    # path takes masks whose padded keys are a suffix of each row.
+    from gonn_amd import nn
+    m = np.zeros((4, 6))
+    m[1, 4:] = 1
+    m[2, :] = 1          # every key padded: kv_len 0
+    m[3, 5] = 2.5        # any nonzero value pads
+    assert list(nn._kv_len_from_mask(m, 4, 6)) == [6, 4, 0, 5]
+    assert nn._kv_len_from_mask(None, 4, 6) is None
+    holes = m.copy()
+    holes[0, 2] = 1      # a padded key before valid ones
+    with pytest.raises(ValueError, match="suffix"):
+        nn._kv_len_from_mask(holes, 4, 6)
+    with pytest.raises(ValueError, match="key padding mask shape"):
+        nn._kv_len_from_mask(np.zeros((4, 5)), 4, 6)
+
+
+def test_resident_layer_and_cache_need_a_device():
+    # No CPU fallback: without a gfx950 device the device-resident objects
+    # refuse to construct (gonn_hip_*_create returns GONN_E_NODEVICE).
+    from gonn_amd import nn
+    if hip.Available():
+        pytest.skip("a device is present")
+    E = 64
+    w = np.eye(E)
+    mha = nn.MultiHeadAttention(E, 4, w, None, w, None, w, None, w, None)
+    with pytest.raises(Exception):
+        mha.to_device()
+    with pytest.raises(hip.GonnHipError):
+        hip.DeviceMHA(E, 4, w, None, w, None, w, None, w, None)
+    with pytest.raises(hip.GonnHipError):
+        hip.KVCache(1, 1, 16, 64)
