@@ -984,8 +984,8 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
     // The bf16 D = 128 causal kernel pairs q-blocks (nqb-1-j, j) per workgroup.
     const bool paired = mode == 1 && D == 128 && causal && kFwdPairBlocks;
     dim3 grid((paired ? (p.nqb + 1) / 2 : p.nqb) * p.BH);
-    // Causal dispatch groups: about one XCD's worth of workgroup slots
-    // (CUs / 8 XCDs x 2 resident workgroups) of q-blocks per group.
+    // Causal dispatch groups: about two XCDs' worth of workgroup slots
+    // (2 x CUs / 8 XCDs x 2 resident workgroups) of q-blocks per group.
     p.hgroup = 1;
     if (causal && mode == 1 && D == 128 && !paired) {
         static int cus = 0;
@@ -995,8 +995,10 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
                 hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
                 cus = 256;
         }
+        // Two XCDs' worth measured 1% faster on C3 than one (interleaved
+        // runs), and the same on C5.
         const int slots = cus / 8 * (8 / kFwdWaves);
-        p.hgroup = slots / p.nqb > 1 ? slots / p.nqb : 1;
+        p.hgroup = 2 * slots / p.nqb > 1 ? 2 * slots / p.nqb : 1;
     }
     if (mode == 1) {
         if (D == 64) {
