@@ -49,7 +49,12 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_mha_create", "gonn_hip_mha_free", "gonn_hip_mha_forward_f64",
     "gonn_hip_mha_workspace_bytes", "gonn_hip_mha_forward_dev", "gonn_hip_flash_attn_f64_bwd_ex",
     "gonn_hip_flash_attn_f64_masked", "gonn_hip_flash_attn_f64_bwd_masked",
+    "gonn_hip_attn_decode_noalloc",
 )
+
+# Size of the library-owned scratch array of gonn_hip_attn_decode_noalloc
+# (GONN_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 
 class GonnHipError(RuntimeError):
@@ -118,6 +123,7 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_attn_fwd.argtypes = [ctypes.POINTER(FwdArgs), vp, sz, vp]
     lib.gonn_hip_attn_bwd.argtypes = [ctypes.POINTER(BwdArgs), vp, sz, vp]
     lib.gonn_hip_attn_decode.argtypes = [ctypes.POINTER(DecodeArgs), vp, sz, vp]
+    lib.gonn_hip_attn_decode_noalloc.argtypes = [ctypes.POINTER(DecodeArgs), vp]
     lib.gonn_hip_alloc.argtypes = [ctypes.POINTER(Buf), sz, i]
     lib.gonn_hip_free.argtypes = [ctypes.POINTER(Buf)]
     lib.gonn_hip_upload_from_f64.argtypes = [ctypes.POINTER(Buf), dp, sz, vp]

@@ -42,7 +42,7 @@ struct ProfScope {
     const char* name;
     hipStream_t s;
     ProfScope(const char* n, hipStream_t st) : name(n), s(st) {
-        if (!g_prof_on.load()) return;
+        if (!n || !g_prof_on.load()) return;
         if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) {
             a = b = nullptr;
             return;
@@ -338,6 +338,73 @@ int run_fwd_f32_ex(DevMem& mem, const float* q, const float* k, const float* v, 
     return gonn_hip_attn_fwd(&a, ws, wsb, nullptr);
 }
 
+// Split-KV decode on a checked call with a workspace of at least
+// decode_ws(a) bytes. `profile`: bracket the stages with profiler events
+// (event creation allocates, so the no-allocation entry passes false).
+int run_decode(const gonn_attn_decode_args* a, void* ws, hipStream_t s, bool profile) {
+    gonn::DecodeParams p{};
+    const int sk = decode_split(a);
+    p.q = a->q.ptr;
+    p.kc = a->kcache.ptr;
+    p.vc = a->vcache.ptr;
+    p.kv_len = (const int*)a->kv_len.ptr;
+    p.o = (float*)a->o.ptr;
+    p.B = a->B;
+    p.H = a->H;
+    p.Lmax = a->Lmax;
+    p.split_keys = sk;
+    p.nsplit = (a->Lmax + sk - 1) / sk;
+    float* w = (float*)round_up((size_t)ws, 256);
+    p.part_ml = w;
+    p.part_o = w + round_up((size_t)a->B * a->H * p.nsplit * 2, 64);
+    p.scale_log2 = (float)a->scale * gonn::kLog2e;
+    {
+        ProfScope ps(profile ? "decode_split" : nullptr, s);
+        TRYH(gonn::launch_decode_split(p, a->D, a->q.dtype == GONN_BF16, s));
+    }
+    ProfScope ps(profile ? "decode_combine" : nullptr, s);
+    return herr(gonn::launch_decode_combine(p, a->D, s));
+}
+
+// ---- no-allocation scratch ----------------------------------------------
+// One library-owned device array per GPU for callers that cannot allocate
+// (gonn_hip_attn_decode_noalloc). In host code `scratch` names a host-side
+// stand-in, not the device array: its device address is looked up once per
+// device with hipGetSymbolAddress (on the first call on that device, with
+// the device current) and only that address is ever handed to kernels. The
+// array keeps the last call's contents; the decode kernels write every
+// partial they later read, so nothing needs clearing between calls.
+constexpr size_t kNoAllocScratchBytes = GONN_NOALLOC_SCRATCH_BYTES;  // 32 MiB per device
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+    std::once_flag once;
+    void* ptr = nullptr;
+    int rc = GONN_OK;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+
+int noalloc_scratch(void** out) {
+    int dev = 0;
+    TRYH(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return GONN_E_UNSUPPORTED;
+    ScratchSlot& slot = g_scratch[dev];
+    std::call_once(slot.once, [&slot] {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        slot.rc = herr(e);
+        slot.ptr = e == hipSuccess ? p : nullptr;
+    });
+    if (slot.rc != GONN_OK) return slot.rc;
+    if (!slot.ptr) return GONN_E_NODEVICE;
+    *out = slot.ptr;
+    return GONN_OK;
+}
 }  // namespace
 
 // The KV-cache handle of the C ABI (opaque to callers).
@@ -639,30 +706,17 @@ int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_byt
     TRY(check_decode(a));
     const size_t need = decode_ws(a);
     if (!ws || ws_bytes < need) return GONN_E_WORKSPACE;
-    gonn::DecodeParams p{};
-    const int sk = decode_split(a);
-    p.q = a->q.ptr;
-    p.kc = a->kcache.ptr;
-    p.vc = a->vcache.ptr;
-    p.kv_len = (const int*)a->kv_len.ptr;
-    p.o = (float*)a->o.ptr;
-    p.B = a->B;
-    p.H = a->H;
-    p.Lmax = a->Lmax;
-    p.split_keys = sk;
-    p.nsplit = (a->Lmax + sk - 1) / sk;
-    float* w = (float*)round_up((size_t)ws, 256);
-    p.part_ml = w;
-    p.part_o = w + round_up((size_t)a->B * a->H * p.nsplit * 2, 64);
-    p.scale_log2 = (float)a->scale * gonn::kLog2e;
-    hipStream_t s = (hipStream_t)stream;
-    {
-        ProfScope ps("decode_split", s);
-        TRYH(gonn::launch_decode_split(p, a->D, a->q.dtype == GONN_BF16, s));
-    }
-    ProfScope ps("decode_combine", s);
-    return herr(gonn::launch_decode_combine(p, a->D, s));
+    return run_decode(a, ws, (hipStream_t)stream, true);
 }
+
+int gonn_hip_attn_decode_noalloc(const gonn_attn_decode_args* a, void* stream) {
+    TRY(check_decode(a));
+    if (decode_ws(a) > kNoAllocScratchBytes) return GONN_E_WORKSPACE;
+    void* ws = nullptr;
+    TRY(noalloc_scratch(&ws));
+    return run_decode(a, ws, (hipStream_t)stream, false);
+}
+
 
 int gonn_hip_alloc(gonn_buf* b, size_t n_elems, int dtype) {
     if (!b || dtype_size(dtype) == 0) return GONN_E_INVALID;

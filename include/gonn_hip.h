@@ -192,6 +192,20 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
  * :261-272) on the post-projection core with pad[b][t] = (t >= kv_len[b]).  */
 int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_bytes, void* stream);
 
+/* No-allocation split-KV decode. No counterpart in the reference: for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). The same kernels and
+ * result as gonn_hip_attn_decode, with the split partials kept in a
+ * library-owned device array of GONN_NOALLOC_SCRATCH_BYTES per GPU (held
+ * until the process ends) instead of a caller workspace; calls no
+ * hipMalloc/hipFree. A call whose partials need more than that
+ * (gonn_hip_attn_workspace_bytes(GONN_OP_DECODE) > GONN_NOALLOC_SCRATCH_BYTES)
+ * returns GONN_E_WORKSPACE before any GPU work is queued. Every call on one
+ * GPU shares that array: calls that overlap on one GPU (different streams or
+ * threads) race and must be serialised by the caller.                     */
+#define GONN_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int gonn_hip_attn_decode_noalloc(const gonn_attn_decode_args* a, void* stream);
+
 /* ---- KV cache for incremental decoding ----------------------------------
  * New: the reference has no KV cache (its decoder recomputes attention over
  * the whole prefix through MultiHeadAttention.Forward). A handle owns one

@@ -159,6 +159,33 @@ def test_decode_argument_errors():
     assert lib.gonn_hip_attn_decode(ctypes.byref(a), P, nb, None) == GONN_E_UNSUPPORTED
 
 
+def test_decode_noalloc_argument_errors():
+    """The no-allocation decode checks its arguments like the workspace entry
+    and rejects a call whose partials exceed the library's scratch array, all
+    before any device access."""
+    lib = _lib.load()
+    B, H, L, D = 2, 2, 256, 128
+    mk = lambda: DecodeArgs(Buf(P, B * H * D * 2, GONN_BF16),  # noqa: E731
+                            Buf(P, B * H * L * D * 2, GONN_BF16),
+                            Buf(P, B * H * L * D * 2, GONN_BF16), Buf(P, B * 4, GONN_I32),
+                            Buf(P, B * H * D * 4, GONN_F32), B, H, L, D, 0.088, 0)
+    assert lib.gonn_hip_attn_decode_noalloc(None, None) == GONN_E_INVALID
+    a = mk()
+    a.split_keys = 100
+    assert lib.gonn_hip_attn_decode_noalloc(ctypes.byref(a), None) == GONN_E_INVALID
+    a = mk()
+    a.D = 80
+    assert lib.gonn_hip_attn_decode_noalloc(ctypes.byref(a), None) == GONN_E_UNSUPPORTED
+    # 2048 x 256 (b,h) slices of 16 splits at D=128 need 2048*256*16*130*4 B > 32 MiB.
+    Bb, Hb, Lb = 2048, 256, 8192
+    big = DecodeArgs(Buf(P, Bb * Hb * D * 2, GONN_BF16), Buf(P, Bb * Hb * Lb * D * 2, GONN_BF16),
+                     Buf(P, Bb * Hb * Lb * D * 2, GONN_BF16), Buf(P, Bb * 4, GONN_I32),
+                     Buf(P, Bb * Hb * D * 4, GONN_F32), Bb, Hb, Lb, D, 0.088, 0)
+    need = lib.gonn_hip_attn_workspace_bytes(GONN_OP_DECODE, ctypes.byref(big))
+    assert need > _lib.NOALLOC_SCRATCH_BYTES
+    assert lib.gonn_hip_attn_decode_noalloc(ctypes.byref(big), None) == GONN_E_WORKSPACE
+
+
 def test_bwd_argument_errors():
     lib = _lib.load()
     B, H, S, D = 1, 2, 64, 64
