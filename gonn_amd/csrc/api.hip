@@ -118,6 +118,22 @@ int bwd_mode(const gonn_attn_bwd_args* a) {
     return a->attn_mask.ptr || bwd_keys_of(a) != a->S ? GONN_ATTN_FP32_MFMA : a->mode;
 }
 
+// The bf16-MFMA kernels take Q as bf16(q * (sign(scale) * c2)) with
+// c2 = |scale| log2(e) (log2(e) and sign 0 for a zero scale), so Q K^T is
+// the exp2 argument of the softmax. The forward (which packs Q itself) and the
+// backward's pack round the same fp32 products, so the backward recomputes
+// exactly the scores whose row sums the forward's LSE normalises.
+struct QFold {
+    float sign, sabs, c2;
+};
+QFold q_fold(double scale) {
+    QFold f;
+    f.sign = scale > 0 ? 1.f : (scale < 0 ? -1.f : 0.f);
+    f.sabs = scale == 0.0 ? 1.f : (float)std::fabs(scale);
+    f.c2 = f.sabs * gonn::kLog2e;
+    return f;
+}
+
 // ---- forward -----------------------------------------------------------
 
 int check_fwd(const gonn_attn_fwd_args* a) {
@@ -564,14 +580,10 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
     p.Sk = a->Sk;
     p.H = a->H;
     p.kv_len = a->kv_len.ptr ? (const int*)a->kv_len.ptr : nullptr;
-    if (a->scale == 0.0) {  // all scores 0: uniform weights; Q is zeroed
-        p.qsign = 0.f;
-        p.scale_abs = 1.f;
-    } else {
-        p.qsign = a->scale < 0 ? -1.f : 1.f;
-        p.scale_abs = (float)std::fabs(a->scale);
-    }
-    p.scale_log2 = p.scale_abs * gonn::kLog2e;
+    const QFold qf = q_fold(a->scale);
+    p.qsign = qf.sign;
+    p.scale_abs = qf.sabs;
+    p.scale_log2 = qf.c2;
     p.q = a->q.ptr;
     const int mode = fwd_mode(a);
     if (a->attn_mask.ptr) {
@@ -638,17 +650,21 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     p.Skp = (int)round_up((size_t)p.Sk, gonn::kBwdPad);
     p.scale = (float)a->scale;
     p.scale_log2 = (float)(a->scale * (double)gonn::kLog2e);
-    const float qsign = a->scale > 0 ? 1.f : (a->scale < 0 ? -1.f : 0.f);
-    p.c2b = (float)((a->scale == 0.0 ? 1.0 : std::fabs(a->scale)) * (double)gonn::kLog2e);
+    // bf16 kernels: Q packed exactly as the bf16 forward packs it (see
+    // q_fold), so S = Q K^T is already the exp2 argument's scale and
+    // dK = |scale| / c2 * (dS^T Q).
+    const QFold qf = q_fold(a->scale);
+    p.c2b = 1.f;
     p.dqs = (float)a->scale;
-    p.dks = (float)std::fabs(a->scale);
+    p.dks = (float)(std::fabs(a->scale) / (double)qf.c2);
     p.kv_len = a->kv_len.ptr ? (const int*)a->kv_len.ptr : nullptr;
     p.H = a->H;
     {
         ProfScope ps("bwd_prep", s);
         TRYH(gonn::launch_bwd_prep((const float*)a->o.ptr, (const float*)a->dO.ptr,
                                    (const float*)a->lse.ptr, (float*)(w + L.lse2),
-                                   (float*)(w + L.delta), BH, S, Sp, D, s));
+                                   (float*)(w + L.delta), BH, S, Sp, D,
+                                   mode == GONN_ATTN_BF16_MFMA, s));
     }
     if (mode == GONN_ATTN_BF16_MFMA) {
         void* Qb = w + L.packed[0];
@@ -666,7 +682,7 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p1.src[1] = a->dO.ptr;
         p1.row[1] = dOb;
         p1.tr[1] = dOt;
-        p1.mul[0] = qsign;
+        p1.mul[0] = qf.sign * qf.c2;
         p1.mul[1] = 1.f;
         p1.S = S;
         p1.Sp = Sp;

@@ -39,6 +39,9 @@ namespace gonn {
 
 // ---------------------------------------------------------------------------
 // prep: grid ceil(BH*Sp/16), 256 threads (16 lanes per query row).
+// delta = rowsum(dO * O). With round_do (bf16 mode) dO is rounded to bf16
+// first, the operand the dP = dO V^T product sees, so that dS = P (dP - delta)
+// loses the dO rounding in both terms alike and its rows still sum to ~0.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__ O,
@@ -46,7 +49,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
                                                        const float* __restrict__ lse,
                                                        float* __restrict__ lse2,
                                                        float* __restrict__ delta, int BH, int S,
-                                                       int Sp) {
+                                                       int Sp, int round_do) {
     constexpr int EPL = D / 16;
     const int tid = threadIdx.x, c = tid & 15;
     const size_t row = (size_t)blockIdx.x * 16 + (tid >> 4);
@@ -59,7 +62,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
         for (int e = 0; e < EPL; e += 4) {
             const f32x4 o = *(const f32x4*)(O + off + e);
             const f32x4 g = *(const f32x4*)(dO + off + e);
-            for (int j = 0; j < 4; j++) acc = __builtin_fmaf(o[j], g[j], acc);
+            for (int j = 0; j < 4; j++)
+                acc = __builtin_fmaf(o[j], round_do ? (float)to_bf16(g[j]) : g[j], acc);
         }
     }
     acc = row_sum16(acc);
@@ -717,13 +721,14 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_f32_kernel(BwdParams p) {
 // Launchers.
 // ---------------------------------------------------------------------------
 hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, float* lse2,
-                           float* delta, int BH, int S, int Sp, int D, hipStream_t s) {
+                           float* delta, int BH, int S, int Sp, int D, int round_do,
+                           hipStream_t s) {
     const size_t rows = (size_t)BH * Sp;
     const unsigned grid = (unsigned)((rows + 15) / 16);
     if (D == 64)
-        bwd_prep_kernel<64><<<grid, 256, 0, s>>>(O, dO, lse, lse2, delta, BH, S, Sp);
+        bwd_prep_kernel<64><<<grid, 256, 0, s>>>(O, dO, lse, lse2, delta, BH, S, Sp, round_do);
     else if (D == 128)
-        bwd_prep_kernel<128><<<grid, 256, 0, s>>>(O, dO, lse, lse2, delta, BH, S, Sp);
+        bwd_prep_kernel<128><<<grid, 256, 0, s>>>(O, dO, lse, lse2, delta, BH, S, Sp, round_do);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -121,7 +121,9 @@ __global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
     bf16x8 qf[NKS];
     {
         const QT* qrow = (const QT*)p.q + ((size_t)bh * Sq + (qi < Sq ? qi : 0)) * D;
-        const float sg = qi < Sq ? p.qsign : 0.f;
+        // Q carries sign(scale) * c2 (c2 = |scale| log2 e), as the bf16
+        // backward packs it: scores come out in log2 units.
+        const float sg = qi < Sq ? p.qsign * p.scale_log2 : 0.f;
         for (int ks = 0; ks < NKS; ks++) {
             const int d0 = ks * 16 + g * 8;
             float v[8];
@@ -192,7 +194,7 @@ __global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
     f32x16 oacc[NDT];
     for (int t = 0; t < NDT; t++) oacc[t] = f32x16{};
     float m = -INFINITY, l = 0.f;
-    const float c2 = p.scale_log2;
+    const float c2 = 1.f;  // the exponent scale, folded into Q
 
     // Causal (key > query) and key-end (key >= Sk) masks of tile kt.
     auto mask = [&](int kt, f32x16* s) {
@@ -346,80 +348,106 @@ __global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
                 for (int i = 0; i < 4; i++) v[i] = oacc[t][rq * 4 + i] * inv;
                 *(f32x4*)(orow + t * 32 + rq * 8 + g * 4) = v;
             }
-        if (p.lse && g == 0) p.lse[(size_t)bh * Sq + qi] = m * p.scale_abs + fast_log2(lt) * kLn2;
+        if (p.lse && g == 0) p.lse[(size_t)bh * Sq + qi] = (m + fast_log2(lt)) * kLn2;
     }
 }
 
 // ---------------------------------------------------------------------------
-// bf16-MFMA forward for D = 128, NW waves (32 query rows each) per workgroup:
-// NW = 4 runs two workgroups per CU, NW = 8 one.
+// bf16-MFMA forward for D = 128: 4 wave64s (32 query rows each) per
+// workgroup, two workgroups per CU (two waves per SIMD).
 //
 // Three-stage software pipeline. Step t issues, with no dependency between
 // them inside the step:
 //   MFMA  O^T += V(t)^T P(t)            (P(t) packed by step t-1)
-//   MFMA  S^T(t+2) = K(t+2) Q^T          (K(t+2) landed by the end of step t-1)
-//   VALU  P(t+1) = exp2(S^T(t+1) c - mc) packed to bf16, row sums
+//   MFMA  S^T(t+2) = K(t+2) Q^T - mc     (K(t+2) landed by the end of step t-1)
+//   VALU  P(t+1) = exp2(S^T(t+1)) packed to bf16, row sums
 // so the MFMA stream never waits on the softmax of the tile it is computing.
 //
-// The softmax VALU work is the binding cost next to the MFMAs on gfx950 (an
-// exp2 occupies the SIMD ~13 cycles, a plain VALU op ~2.5, an MFMA 32), so
-// the common path is one FMA, one exp2, half a bf16 pack and half a v_dot2 per
-// score, and no per-tile row max: P = exp2(s c - mc) is exact for any offset
-// mc, which only has to keep P bounded. A tile whose row sum exceeds 2^14 (or
-// is not finite) takes a rare, wave-uniform branch that computes the tile max,
-// moves mc to it, recomputes the tile's P and rescales l and O by
-// alpha = 2^(old - new). Otherwise every score is below mc + 14, so P, l and O
-// stay far inside fp32 range, and their relative precision does not depend
-// on mc. The first tile (prologue) uses its exact max.
+// The step is issue-bound (each wave issues its own MFMAs, their LDS operand
+// reads and waits, the softmax VALU and the tile loads), so the per-score work
+// is cut to one exp2, half a bf16 pack and half a v_dot2:
+//  * |scale| log2(e) is folded into the packed Q and the first MFMA of each
+//    S^T tile accumulates onto a register block holding -mc, so the MFMA
+//    result already is the exp2 argument s c - mc (no per-score FMA);
+//  * no per-tile row max: P = exp2(s c - mc) is exact for any offset mc,
+//    which only has to keep P bounded. A tile whose row sum exceeds 2^14 (or
+//    is not finite) takes a rare, wave-uniform branch that computes the tile
+//    max, moves mc to it, recomputes the tile's P, shifts the S^T tile already
+//    accumulated against the old offset and rescales l and O by
+//    alpha = 2^(old - new). Otherwise every score is below mc + 14, so P, l
+//    and O stay far inside fp32 range, and their relative precision does not
+//    depend on mc. The first tile (prologue) uses its exact max.
 //
-// LDS: rings of K tiles (64 keys x D) and Vt tiles (D x 64 keys) filled
-// straight from HBM/L2 by buffer_load ... lds, one barrier per step. Rows
-// keep one spare 16-byte chunk (conflict-free MFMA operand reads with one
-// address register per ring); lanes that land on a spare chunk load a dummy.
-//  NW = 8: 4-slot rings; step t loads K(t+4) and V(t+2), two steps ahead.
-//  NW = 4: 2-slot rings (two workgroups share the CU's LDS); step t loads
-//          K(t+3) and V(t+1), one step ahead.
-// In steady state the loads are spread over the MFMA stream so the texture
-// unit drains them in the background.
+// LDS: two-slot rings of K tiles (64 keys x D) and Vt tiles (D x 64 keys)
+// filled straight from HBM/L2 by buffer_load ... lds, one barrier per step;
+// step t loads K(t+3) and V(t+1), one step ahead, spread over the first half
+// of the MFMA stream. Rows keep one spare 16-byte chunk (conflict-free MFMA
+// operand reads with one address register per ring); lanes that land on a
+// spare chunk load a dummy. Each load's M0 (its LDS base) is written one slot
+// ahead, so the M0 -> LDS-DMA wait state is filled by an MFMA, not a nop.
+//
+// Every step has the same form: the last two steps compute S^T of tiles past
+// the end and the last one their softmax; those keys lie past the key end
+// (or the causal diagonal), so the mask sets the whole tile to -inf and
+// P = 0 adds nothing to l or O. One step form keeps the register allocation
+// the same in every step (tail variants spilled), for two masked S^T tiles
+// per q-block.
 // ---------------------------------------------------------------------------
 constexpr float kSumBound = 16384.f;  // 2^14: row-sum bound of one 64-key tile
-// Causal: pair q-blocks (nqb-1-j, j) in one workgroup.
-constexpr bool kFwdPairBlocks = false;
 // Wave issue priority (s_setprio) during a step's MFMA stream.
 constexpr int kFwdStreamPrio = 1;
+// Waves per workgroup of the D = 128 bf16 forward.
+constexpr int kFwdWaves = 4;
 
-template <int NW, bool CAUSAL, typename QT>
-__global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParams p) {
-    constexpr int D = 128, BM = NW * 32, BN = 64, NT = NW * 64;
+template <bool CAUSAL, typename QT>
+__global__ __launch_bounds__(256, 2) void fwd_bf16_d128_kernel(FwdParams p) {
+    constexpr int NW = kFwdWaves, D = 128, BM = NW * 32, BN = 64, NT = NW * 64;
     constexpr int NKS = D / 16, NDT = D / 32;
     constexpr int KST = D + 8, VST = BN + 8;          // padded row strides (bf16)
     constexpr uint32_t KTB = BN * KST * 2, VTB = D * VST * 2;  // slot bytes
-    constexpr int NSLOT = NW == 8 ? 4 : 2;
-    constexpr int KLEAD = NW == 8 ? 4 : 3, VLEAD = NW == 8 ? 2 : 1;  // load distance (tiles)
+    constexpr int NSLOT = 2;
+    constexpr int KLEAD = 3, VLEAD = 1;  // load distance (tiles)
     __shared__ __attribute__((aligned(16))) bf16 sKb[NSLOT * BN * KST];
     __shared__ __attribute__((aligned(16))) bf16 sVb[NSLOT * D * VST];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, ln = lane & 31;
-    // Causal: workgroup j of a head runs q-block nqb-1-j, then q-block j, so
-    // every workgroup covers 2 nqb + 2 key tiles (one pass for the middle
-    // block of an odd nqb) and the grid has no long tail; both blocks share
-    // the head's K/V in the XCD's L2. Non-causal: one q-block each.
-    constexpr bool PAIR = CAUSAL && kFwdPairBlocks;
-    const int nwg = PAIR ? (p.nqb + 1) / 2 : p.nqb;
-    int bh, pj;
-    map_block(blockIdx.x, nwg, p.BH, CAUSAL && !PAIR, bh, pj, CAUSAL && !PAIR ? p.hgroup : 1);
+    int bh, qb;
+    map_block(blockIdx.x, p.nqb, p.BH, CAUSAL, bh, qb, CAUSAL ? p.hgroup : 1);
     const int Sq = p.Sq, Sk = fwd_keys(p, bh), Skp = p.Skp;
     if (Sk == 0) {  // uniform: the whole slice is padded
-        fwd_empty_rows<D>(p, bh, (PAIR ? p.nqb - 1 - pj : pj) * BM, BM);
-        if (PAIR && p.nqb - 1 - pj != pj) fwd_empty_rows<D>(p, bh, pj * BM, BM);
+        fwd_empty_rows<D>(p, bh, qb * BM, BM);
         return;
     }
-    // Per q-block state (set by each pass): first query row of the block and
-    // of this wave, this lane's query row, number of 64-key tiles.
-    int q0 = 0, qw = 0, qi = 0, ntiles = 0;
-    bf16x8 qf[NKS];  // Q[qi][16ks + 8g .. +7] * sign(scale), in bf16
+    const int q0 = qb * BM, qw = q0 + wave * 32, qi = qw + ln;
+    const float c2 = p.scale_log2;
+    int ntiles;
+    {
+        int kend = Sk;
+        if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
+        ntiles = (kend + BN - 1) / BN;
+    }
+
+    // Q fragment: qf[ks] = Q[qi][16ks + 8g .. +7] * sign(scale) * c2, in bf16.
+    bf16x8 qf[NKS];
+    {
+        const QT* qrow = (const QT*)p.q + ((size_t)bh * Sq + (qi < Sq ? qi : 0)) * D;
+        const float sg = qi < Sq ? p.qsign * c2 : 0.f;
+        for (int ks = 0; ks < NKS; ks++) {
+            const int d0 = ks * 16 + g * 8;
+            float v[8];
+            if constexpr (sizeof(QT) == 4) {
+                const f32x4 a = *(const f32x4*)(qrow + d0), b = *(const f32x4*)(qrow + d0 + 4);
+                for (int i = 0; i < 4; i++) { v[i] = a[i]; v[4 + i] = b[i]; }
+            } else {
+                const u16x8 a = *(const u16x8*)(qrow + d0);
+                for (int i = 0; i < 8; i++) v[i] = bf16_to_f32(a[i]);
+            }
+            qf[ks] = pack8(v[0] * sg, v[1] * sg, v[2] * sg, v[3] * sg, v[4] * sg, v[5] * sg,
+                           v[6] * sg, v[7] * sg);
+        }
+    }
 
     // ---- tile loads: instruction i of thread tid fills 16-byte chunk
     // position i*NT + tid of a padded tile (K: 64 x 17 positions, Vt:
@@ -444,7 +472,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     const brsrc krs = make_rsrc(Kg, (uint32_t)Skp * D * 2);
     const brsrc vrs = make_rsrc(Vg, (uint32_t)Skp * D * 2);
     const uint32_t kl = lds_addr(sKb) + wave * 1024, vl = lds_addr(sVb) + wave * 1024;
-    // Load i of K / Vt tile kt into ring slot `slot`.
+    // Load i of K / Vt tile kt into ring slot `slot` (M0 written by the call).
     auto dma_ki = [&](int kt, int slot, int i) {
         if (i < NKI - 1) dma16(krs, kl + slot * KTB + i * NT * 16, koff[i], kt * BN * D * 2);
         else dma16_if(krs, kl + slot * KTB + i * NT * 16, koff[i], kt * BN * D * 2, klast);
@@ -459,10 +487,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     auto dma_v = [&](int kt, int slot) {
         for (int i = 0; i < NVI; i++) dma_vi(kt, slot, i);
     };
-    // Waits count loads conservatively (NKI - 1 per tile): a wave with the
-    // extra load keeps fewer of its newest loads in flight than it could,
-    // which only waits longer, and the count stays a compile-time immediate.
-    constexpr int NL = NKI - 1;
 
     // ---- MFMA operand reads: K row mt*32 + ln, Vt row dt*32 + ln; chunk
     // 2ks + g (bytes from a slot's start) ----
@@ -477,9 +501,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     };
 
     f32x16 oacc[NDT];
-    // mc: this lane's running offset (log2 units); l: row sum relative to it.
+    for (int dt = 0; dt < NDT; dt++) oacc[dt] = f32x16{};
+    // mc: this lane's running offset (log2 units); l: row sum relative to it;
+    // nmc: -mc in every element, the first S^T accumulator of each tile.
     float mc = 0.f, l = 0.f, alpha = 1.f;
-    const float c2 = p.scale_log2;
+    f32x16 nmc;
 
     auto mask = [&](int kt, f32x16* s) {
         const int kb = kt * BN + 4 * g;
@@ -505,73 +531,51 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
     };
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     const bf16x2 one2 = {(__bf16)1.0f, (__bf16)1.0f};
-    // P = exp2(s c - mc) of score pair k (0..15) of a tile: the packed bf16
-    // word; the row sum of the packed values is added into part[k & 3].
-    auto p_pair = [&](const f32x16* s, int k, float* part) {
-        const int mt = k >> 3, r = (k & 7) * 2;
-        const float e0 = fast_exp2(__builtin_fmaf(s[mt][r], c2, -mc));
-        const float e1 = fast_exp2(__builtin_fmaf(s[mt][r + 1], c2, -mc));
-        const bf16x2 pr = {to_bf16(e0), to_bf16(e1)};
-        part[k & 3] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, part[k & 3], false);
-        return __builtin_bit_cast(uint32_t, pr);
-    };
-    // Whole-tile P and row sum (prologue and the rare rescale branch).
-    auto p_tile = [&](const f32x16* s, u32x4* pk) {
+    // Whole-tile P = exp2(s + off) as packed bf16 pairs, and its row sum
+    // (prologue and the rare rescale branch).
+    auto p_tile = [&](const f32x16* s, u32x4* pk, float off) {
         float part[4] = {0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < 16; k++) pk[k >> 2][k & 3] = p_pair(s, k, part);
+        for (int k = 0; k < 16; k++) {
+            const int mt = k >> 3, r = (k & 7) * 2;
+            const bf16x2 pr = {to_bf16(fast_exp2(s[mt][r] + off)),
+                               to_bf16(fast_exp2(s[mt][r + 1] + off))};
+            part[k & 3] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, part[k & 3], false);
+            pk[k >> 2][k & 3] = __builtin_bit_cast(uint32_t, pr);
+        }
         return (part[0] + part[1]) + (part[2] + part[3]);
     };
     u32x4 pp[4];  // P of the tile PV consumes next, bf16 pairs per 32-bit word
 
-    // One pipeline step (see the header). sA <- S^T(t+2), sB = S^T(t+1);
+    // One pipeline step (see the header). sA <- S^T(t+2) - mc, sB = S^T(t+1) - mc;
     // pp holds P(t) and is overwritten with P(t+1) 16 keys at a time, each
     // part after the PV MFMAs that read it were issued.
     //
     // The step is scheduled by hand: slot e issues the LDS read of MFMA e+3,
-    // MFMA e, possibly one tile load and the softmax micro-op mapped to it,
-    // and a sched_barrier keeps the compiler from regrouping slots (left to
-    // itself it serialises the S^T chains behind their LDS reads). MFMA order
-    // per 16-key PV k-step j: PV(j, dt = 0..3), then S^T k-steps 2j and 2j+1
-    // (mt = 0, 1), so six accumulator chains interleave.
-    //
-    // SS (steady state: both tile loads of the step are needed) spreads the
-    // loads over the first half of the stream; otherwise the needed ones are
-    // issued up front.
-    //
-    // GB (NW = 8, waves 4-7): the wave group runs half a step behind waves
-    // 0-3: its barrier (and the wait for its loads) sits in the middle of its
-    // MFMA stream instead of at the end, so on every SIMD one wave's barrier,
-    // tile-load wait and step start overlap the other wave's MFMAs. Both
-    // groups still meet once per step at the same barrier instance k (group
-    // A at the end of step k, group B halfway through step k): tiles for step
-    // k are waited for by every wave before instance k-1, and a ring slot is
-    // refilled in step j only after instance j-1, by which both groups are
-    // done with the tile of step j-2 it held.
-    const bool gB = NW == 8 && wave >= 4;  // wave-uniform
-    auto step = [&](auto ha_tag, auto hb_tag, auto ss_tag, int t, f32x16* sA,
-                    f32x16* sB) __attribute__((always_inline)) {
-        constexpr bool HA = decltype(ha_tag)::value;
-        constexpr bool HB = decltype(hb_tag)::value;
-        constexpr bool SS = decltype(ss_tag)::value;
+    // MFMA e, possibly one tile load (or the M0 write of the next slot's
+    // load) and the softmax micro-op mapped to it, and a sched_barrier keeps
+    // the compiler from regrouping slots (left to itself it serialises the
+    // S^T chains behind their LDS reads). MFMA order per 16-key PV k-step j:
+    // PV(j, dt = 0..3), then S^T k-steps 2j and 2j+1 (mt = 0, 1), so six
+    // accumulator chains interleave.
+    auto step = [&](int t, f32x16* sA, f32x16* sB) __attribute__((always_inline)) {
         const int kslot = (t + KLEAD) & (NSLOT - 1), vslot = (t + VLEAD) & (NSLOT - 1);
-        const bool dk = SS || t + KLEAD < ntiles, dv = SS || t + VLEAD < ntiles;
-        if constexpr (!SS) {
-            if (dk) dma_k(t + KLEAD, kslot);
-            if (dv) dma_v(t + VLEAD, vslot);
-        }
+        // Tiles past the last one are clamped to it: such a load refills a
+        // slot no later step reads as real data (its S^T tile is masked).
+        const int kload = t + KLEAD < ntiles ? t + KLEAD : ntiles - 1;
+        const int vload = t + VLEAD < ntiles ? t + VLEAD : ntiles - 1;
         // Diagonal / key-end tiles only (a wave-uniform branch ahead of the
         // step's MFMA stream).
-        if constexpr (HB)
-            if (needs_mask(t + 1)) mask(t + 1, sB);
+        if (needs_mask(t + 1)) mask(t + 1, sB);
         const uint32_t vb = (uint32_t)(t & (NSLOT - 1)) * VTB;
         const uint32_t kb = (uint32_t)((t + 2) & (NSLOT - 1)) * KTB;
 
-        constexpr int GW = HA ? 8 : 4;     // MFMAs per PV k-step group
+        constexpr int GW = 8;              // MFMAs per PV k-step group
         constexpr int NM = 4 * GW;         // MFMAs in the step
-        constexpr int MID = NM / 2;        // group B's barrier: before slot MID
-        constexpr int NU = HB ? 16 : 0;    // softmax micro-ops (one score pair each)
+        constexpr int NU = 16;             // softmax micro-ops (one score pair each)
         constexpr int LA = 3;              // LDS read lead (MFMAs)
-        constexpr int NDMA = 2 * NKI;      // tile loads of a steady-state step
+        constexpr int NDMA = 2 * NKI;      // tile loads of a step
+        constexpr int DS = NM / NDMA;      // slots between tile loads
+        static_assert(DS >= 2, "an M0 write needs the slot before its load");
         bf16x8 opr[4];
         auto fetch = [&](auto E) {
             constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
@@ -584,28 +588,44 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
                 oacc[w] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pp[j]), oacc[w]);
             } else {
                 constexpr int kk = 2 * j + ((w - 4) >> 1), mt = (w - 4) & 1;
-                sA[mt] = mfma_bf16(opr[e & 3], qf[kk], kk == 0 ? f32x16{} : sA[mt]);
+                sA[mt] = mfma_bf16(opr[e & 3], qf[kk], kk == 0 ? nmc : sA[mt]);
+            }
+        };
+        // Tile load d (0 .. NDMA-1) at slot 1 + d*DS, alternating K and V;
+        // its M0 is written at the slot before.
+        auto dma_slot = [&](auto E) {
+            constexpr int e = decltype(E)::value;
+            if constexpr (e + 1 >= 1 && e % DS == 0 && e / DS < NDMA) {
+                constexpr int d = e / DS, i = d / 2;
+                const uint32_t lds = d % 2 == 0 ? kl + kslot * KTB + i * NT * 16
+                                                : vl + vslot * VTB + i * NT * 16;
+                dma_set_m0(lds);
+            }
+            if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
+                constexpr int d = (e - 1) / DS, i = d / 2;
+                if constexpr (d % 2 == 0) {
+                    if constexpr (i < NKI - 1) dma16_m0(krs, koff[i], kload * BN * D * 2);
+                    else dma16_m0_if(krs, koff[i], kload * BN * D * 2, klast);
+                } else {
+                    if constexpr (i < NVI - 1) dma16_m0(vrs, voff[i], vload * BN * 2);
+                    else dma16_m0_if(vrs, voff[i], vload * BN * 2, vlast);
+                }
             }
         };
         float part[4] = {0.f, 0.f, 0.f, 0.f};
-        // Score pair k (16 keys j = k / 4 of P(t+1)) in three micro-ops two
-        // slots apart so no slot waits on a dependent VALU result: (0) the
-        // FMA s c - mc, (1) exp2, (2) bf16 pack into pp and row sum. Stage 2
-        // lands in slot uslot(k), after the PV MFMAs of k-step j read pp[j];
-        // micro-ops past the stream's end run after it.
+        // Score pair k (16 keys j = k / 4 of P(t+1)) in two micro-ops two
+        // slots apart so no slot waits on a dependent VALU result: (0) exp2,
+        // (1) bf16 pack into pp and row sum. Stage 1 lands in slot uslot(k),
+        // after the PV MFMAs of k-step j read pp[j]; micro-ops past the
+        // stream's end run after it.
         auto uslot = [](int k) { return (k >> 2) * GW + 4 + (k & 3); };
-        float ua[16][2], ub[16][2];
+        float ub[16][2];
         auto uop = [&](auto U, auto S) {
             constexpr int k = decltype(U)::value, stage = decltype(S)::value;
             constexpr int mt = k >> 3, r = (k & 7) * 2;
             if constexpr (stage == 0) {
-                ua[k][0] = __builtin_fmaf(sB[mt][r], c2, -mc);
-                ua[k][1] = __builtin_fmaf(sB[mt][r + 1], c2, -mc);
-                pin(ua[k][0]);
-                pin(ua[k][1]);
-            } else if constexpr (stage == 1) {
-                ub[k][0] = fast_exp2(ua[k][0]);
-                ub[k][1] = fast_exp2(ua[k][1]);
+                ub[k][0] = fast_exp2(sB[mt][r]);
+                ub[k][1] = fast_exp2(sB[mt][r + 1]);
                 pin(ub[k][0]);
                 pin(ub[k][1]);
             } else {
@@ -617,12 +637,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
             }
         };
         // Run the micro-ops of slot e (stage st of pair k sits at slot
-        // uslot(k) - 2 + st); e = NM runs everything past the stream's end.
+        // uslot(k) - 2 + 2 st); e = NM runs everything past the stream's end.
         auto uops_at = [&](auto E) {
             constexpr int e = decltype(E)::value;
-            static_for<3>([&](auto S) {
+            static_for<2>([&](auto S) {
                 static_for<NU>([&](auto U) {
-                    constexpr int at = uslot(decltype(U)::value) - 2 + decltype(S)::value;
+                    constexpr int at = uslot(decltype(U)::value) - 2 + 2 * decltype(S)::value;
                     if constexpr (e < NM ? at == e : at >= NM) uop(U, S);
                 });
             });
@@ -632,34 +652,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
         // then fill the gaps of this stream rather than delay it.
         __builtin_amdgcn_s_setprio(kFwdStreamPrio);
         static_for<LA>([&](auto E) { fetch(E); });
-        auto wait_loads = [&] {
-            if constexpr (NW == 8) {
-                if (dk) GONN_VMCNT(2 * NL);
-                else if (dv) GONN_VMCNT(NL);
-                else GONN_VMCNT(0);
-            } else {
-                GONN_VMCNT(0);
-            }
-        };
         static_for<NM>([&](auto E) {
             constexpr int e = decltype(E)::value;
-            if constexpr (NW == 8 && e == MID) {
-                if (gB) {
-                    wait_loads();
-                    __syncthreads();
-                }
-            }
             if constexpr (e + LA < NM) fetch(std::integral_constant<int, e + LA>{});
             issue(E);
-            // Tile loads at slots 1, 1 + DS, ..., alternating K and V; with
-            // NW = 8 all before slot MID (group B waits for them there).
-            constexpr int DSPAN = NW == 8 ? MID : NM;
-            constexpr int DS = DSPAN / NDMA > 0 ? DSPAN / NDMA : 1;
-            if constexpr (SS && e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
-                constexpr int d = (e - 1) / DS;
-                if constexpr (d % 2 == 0) dma_ki(t + KLEAD, kslot, d / 2);
-                else dma_vi(t + VLEAD, vslot, d / 2);
-            }
+            dma_slot(E);
             // Softmax micro-ops; their results are pinned (an empty asm) so
             // IR passes cannot sink the work out of its slot.
             uops_at(E);
@@ -667,126 +664,62 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
         });
         uops_at(std::integral_constant<int, NM>{});
         __builtin_amdgcn_s_setprio(0);
-        if constexpr (HB) {
-            float ts = (part[0] + part[1]) + (part[2] + part[3]);
-            alpha = 1.f;
-            // Rare: the tile's P is not bounded by the current offset (or is
-            // not finite). Move the offset to the tile max and redo the tile.
-            if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound))) {
-                const float mx = tile_max(sB) * c2;
-                const float mnew = mx > mc + kLazyLog2 ? mx : mc;
-                alpha = fast_exp2(mc - mnew);
-                mc = mnew;
-                ts = p_tile(sB, pp);
-            }
-            l = l * alpha + ts;
+        float ts = (part[0] + part[1]) + (part[2] + part[3]);
+        alpha = 1.f;
+        // Rare: the tile's P is not bounded by the current offset (or is not
+        // finite). Move the offset to the tile max (log2 units), redo the
+        // tile, and shift S^T(t+2), accumulated against the old offset.
+        if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound))) {
+            const float mx = tile_max(sB);  // relative to mc
+            const float dlt = mx > kLazyLog2 ? -mx : 0.f;
+            alpha = fast_exp2(dlt);
+            mc -= dlt;
+            ts = p_tile(sB, pp, dlt);
+            for (int mt = 0; mt < 2; mt++) sA[mt] += dlt;
+            nmc = f32x16{} - mc;
         }
+        l = l * alpha + ts;
 
-        if (!gB) {
-            wait_loads();
-            __syncthreads();
-        }
-        if constexpr (HB) {
-            if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
-                for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
-        }
+        GONN_VMCNT(0);
+        __syncthreads();
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
+            for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
     };
-    using Yes = std::integral_constant<bool, true>;
-    using No = std::integral_constant<bool, false>;
-
-    f32x16 s0[2], s1[2];
-    for (int pass = 0; pass < (PAIR ? 2 : 1); pass++) {
-    const int qb = !PAIR ? pj : (pass == 0 ? p.nqb - 1 - pj : pj);
-    if (pass == 1 && qb == p.nqb - 1 - pj) break;
-    q0 = qb * BM;
-    qw = q0 + wave * 32;
-    qi = qw + ln;
-    {
-        const QT* qrow = (const QT*)p.q + ((size_t)bh * Sq + (qi < Sq ? qi : 0)) * D;
-        const float sg = qi < Sq ? p.qsign : 0.f;
-        for (int ks = 0; ks < NKS; ks++) {
-            const int d0 = ks * 16 + g * 8;
-            float v[8];
-            if constexpr (sizeof(QT) == 4) {
-                const f32x4 a = *(const f32x4*)(qrow + d0), b = *(const f32x4*)(qrow + d0 + 4);
-                for (int i = 0; i < 4; i++) { v[i] = a[i]; v[4 + i] = b[i]; }
-            } else {
-                const u16x8 a = *(const u16x8*)(qrow + d0);
-                for (int i = 0; i < 8; i++) v[i] = bf16_to_f32(a[i]);
-            }
-            qf[ks] = pack8(v[0] * sg, v[1] * sg, v[2] * sg, v[3] * sg, v[4] * sg, v[5] * sg,
-                           v[6] * sg, v[7] * sg);
-        }
-    }
-    {
-        int kend = Sk;
-        if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
-        ntiles = (kend + BN - 1) / BN;
-    }
-    for (int dt = 0; dt < NDT; dt++) oacc[dt] = f32x16{};
-    alpha = 1.f;
 
     // ---- prologue: S^T(0) -> P(0), S^T(1); the rings hold what step 0 needs ----
-    auto qk_slot = [&](int slot, f32x16* s) {
-        s[0] = f32x16{};
-        s[1] = f32x16{};
+    f32x16 s0[2], s1[2];
+    auto qk_slot = [&](int slot, f32x16* s, f32x16 c) {
+        s[0] = c;
+        s[1] = c;
         for (int ks = 0; ks < NKS; ks++)
             for (int mt = 0; mt < 2; mt++) s[mt] = mfma_bf16(kfrag(slot * KTB, ks, mt), qf[ks], s[mt]);
     };
     auto last = [&](int kt) { return kt < ntiles ? kt : ntiles - 1; };
-    if constexpr (NW == 8) {
-        dma_k(0, 0);
-        dma_k(last(1), 1);
-        dma_v(0, 0);
-        dma_k(last(2), 2);
-        dma_k(last(3), 3);
-        dma_v(last(1), 1);
-        GONN_VMCNT(3 * NL);  // Q, K(0), K(1), V(0) landed
-        __syncthreads();
-        qk_slot(0, s0);
-        if (ntiles > 1) qk_slot(1, s1);
-    } else {
-        dma_k(0, 0);
-        dma_k(last(1), 1);
-        dma_v(0, 0);
-        GONN_VMCNT(0);
-        __syncthreads();
-        qk_slot(0, s0);
-        if (ntiles > 1) qk_slot(1, s1);
-        __syncthreads();  // K(0) read by every wave: its slot takes K(2)
-        dma_k(last(2), 0);
-    }
+    dma_k(0, 0);
+    dma_k(last(1), 1);
+    dma_v(0, 0);
+    GONN_VMCNT(0);
+    __syncthreads();
+    qk_slot(0, s0, f32x16{});
     // First tile: exact offset (its max; key 0 is never masked, so it is
     // finite).
     if (needs_mask(0)) mask(0, s0);
-    mc = tile_max(s0) * c2;
-    l = p_tile(s0, pp);
-    if constexpr (NW == 8) GONN_VMCNT(2 * NL);  // K(2) landed (K(3), V(1) may be in flight)
-    else GONN_VMCNT(0);
+    mc = tile_max(s0);
+    nmc = f32x16{} - mc;
+    l = p_tile(s0, pp, -mc);
+    qk_slot(1, s1, nmc);  // K(1), or for a one-tile block a masked copy of K(0)
+    __syncthreads();      // K(0) read by every wave: its slot takes K(2)
+    dma_k(last(2), 0);
+    GONN_VMCNT(0);
     __syncthreads();
 
-    // Steady state while both loads of a step are needed: t + KLEAD < ntiles.
     {
         int t = 0;
-        for (; t + KLEAD + 1 < ntiles; t += 2) {
-            step(Yes{}, Yes{}, Yes{}, t, s0, s1);
-            step(Yes{}, Yes{}, Yes{}, t + 1, s1, s0);
+        for (; t + 1 < ntiles; t += 2) {
+            step(t, s0, s1);
+            step(t + 1, s1, s0);
         }
-        for (; t + 3 < ntiles; t += 2) {
-            step(Yes{}, Yes{}, No{}, t, s0, s1);
-            step(Yes{}, Yes{}, No{}, t + 1, s1, s0);
-        }
-        const int rem = ntiles - t;
-        if (rem == 3) {
-            step(Yes{}, Yes{}, No{}, t, s0, s1);
-            step(No{}, Yes{}, No{}, t + 1, s1, s0);
-            step(No{}, No{}, No{}, t + 2, s0, s1);
-        } else if (rem == 2) {
-            step(No{}, Yes{}, No{}, t, s0, s1);
-            step(No{}, No{}, No{}, t + 1, s1, s0);
-        } else {
-            step(No{}, No{}, No{}, t, s0, s1);
-        }
+        if (t < ntiles) step(t, s0, s1);
     }
 
     const float lt = pair_sum32(l);
@@ -802,7 +735,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void fwd_bf16_d128_kernel(FwdParam
         // LSE = (mc + log2 l) * ln 2, natural-log units of the scaled scores.
         if (p.lse && g == 0) p.lse[(size_t)bh * Sq + qi] = (mc + fast_log2(lt)) * kLn2;
     }
-    }  // pass
 }
 
 // ---------------------------------------------------------------------------
@@ -963,16 +895,12 @@ static void launch_bf16_d(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t
         fwd_bf16_kernel<D, C, float><<<grid, 256, 0, s>>>(p);
 }
 
-// Waves per workgroup of the D = 128 bf16 forward (4: two workgroups per CU;
-// 8: one).
-constexpr int kFwdWaves = 4;
-
 template <bool C>
 static void launch_bf16_d128(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t s) {
     if (q_bf16)
-        fwd_bf16_d128_kernel<kFwdWaves, C, bf16><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        fwd_bf16_d128_kernel<C, bf16><<<grid, kFwdWaves * 64, 0, s>>>(p);
     else
-        fwd_bf16_d128_kernel<kFwdWaves, C, float><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        fwd_bf16_d128_kernel<C, float><<<grid, kFwdWaves * 64, 0, s>>>(p);
 }
 
 hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_bf16,
@@ -981,13 +909,11 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
     // Query rows per workgroup.
     const int bm = (mode == 1 && D == 128) ? kFwdWaves * 32 : 128;
     p.nqb = (p.Sq + bm - 1) / bm;
-    // The bf16 D = 128 causal kernel pairs q-blocks (nqb-1-j, j) per workgroup.
-    const bool paired = mode == 1 && D == 128 && causal && kFwdPairBlocks;
-    dim3 grid((paired ? (p.nqb + 1) / 2 : p.nqb) * p.BH);
+    dim3 grid(p.nqb * p.BH);
     // Causal dispatch groups: about two XCDs' worth of workgroup slots
     // (2 x CUs / 8 XCDs x 2 resident workgroups) of q-blocks per group.
     p.hgroup = 1;
-    if (causal && mode == 1 && D == 128 && !paired) {
+    if (causal && mode == 1 && D == 128) {
         static int cus = 0;
         if (!cus) {
             int dev = 0;

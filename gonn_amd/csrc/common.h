@@ -173,6 +173,23 @@ GONN_DEV void dma16_if(brsrc r, uint32_t lds, uint32_t voff, uint32_t soff, uint
            "s"(__builtin_amdgcn_readfirstlane(on))
         : "memory", "scc");
 }
+// dma16 split in two, so the M0 write can sit one instruction slot ahead of
+// its load (an M0 write needs one wait state before an LDS-DMA load; another
+// instruction in between fills it instead of an s_nop). The kernels that use
+// these make no M0 use of their own between the two statements.
+GONN_DEV void dma_set_m0(uint32_t lds) {
+    asm volatile("s_mov_b32 m0, %0" ::"s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+GONN_DEV void dma16_m0(brsrc r, uint32_t voff, uint32_t soff) {
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
+GONN_DEV void dma16_m0_if(brsrc r, uint32_t voff, uint32_t soff, uint32_t on) {
+    asm volatile(
+        "s_cmp_eq_u32 %3, 0\n\ts_cbranch_scc1 1f\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds\n1:"
+        ::"v"(voff), "s"(r), "s"(soff), "s"(__builtin_amdgcn_readfirstlane(on))
+        : "memory", "scc");
+}
 // LDS byte address of a __shared__ object (apply to the array itself, so the
 // address-space cast folds to a constant).
 GONN_DEV uint32_t lds_addr(const void* p) {

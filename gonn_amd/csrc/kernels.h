@@ -15,9 +15,9 @@ struct FwdParams {
     float* o;       // (BH,Sq,D)
     float* lse;     // (BH,Sq) or null
     int BH, Sq, Sk, Skp, nqb;
-    float scale_log2;  // |scale| * log2(e)
-    float scale_abs;   // |scale|
-    float qsign;       // sign(scale) (Q is negated for a negative scale)
+    float scale_log2;  // c2 = |scale| * log2(e) (log2(e) for a zero scale)
+    float scale_abs;   // |scale| (1 for a zero scale)
+    float qsign;       // sign(scale) (Q is negated for a negative scale; 0 for 0)
     int hgroup;        // slices whose blocks are dispatched interleaved (map_block)
     const int* kv_len; // [BH / H] valid keys per sequence, or null (all Sk)
     int H;             // heads per sequence (slice bh belongs to sequence bh / H)
@@ -74,9 +74,10 @@ struct BwdParams {
                          // fp32 kernels' cross-attention backward)
     float scale;       // signed scale (fp32 kernels)
     float scale_log2;  // scale * log2(e) (fp32 kernels)
-    // bf16 kernels: Q is packed times sign(scale) (0 for a zero scale), so
-    // the exponent scale is positive: c2b = (scale ? |scale| : 1) * log2(e);
-    // outputs dQ = dqs * acc, dK = dks * acc with dqs = scale, dks = |scale|.
+    // bf16 kernels: Q is packed times sign(scale) * c2 with
+    // c2 = (scale ? |scale| : 1) * log2(e) (sign 0 for a zero scale), as the
+    // bf16 forward packs it, so the exponent scale is c2b = 1; outputs
+    // dQ = dqs * acc, dK = dks * acc with dqs = scale, dks = |scale| / c2.
     float c2b, dqs, dks;
     // Optional per-sequence key counts (device int32[BH / H]): keys
     // t >= kv_len[bh / H] of slice bh are padded (ForwardMasked key padding);
@@ -121,7 +122,8 @@ hipError_t launch_kv_append(const void* ks, const void* vs, int src_bf16, void* 
 // Backward stages: prep (lse2, delta), then dK/dV (one workgroup per key
 // block) and dQ (one workgroup per query block), both deterministic.
 hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, float* lse2,
-                           float* delta, int BH, int S, int Sp, int D, hipStream_t s);
+                           float* delta, int BH, int S, int Sp, int D, int round_do,
+                           hipStream_t s);
 hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipStream_t s);
 hipError_t launch_bwd_dq(const BwdParams& p, int mode, int D, int causal, hipStream_t s);
 // bf16 dQ (attn_bwd_dq.hip); launch_bwd_dq dispatches mode 1 here.
