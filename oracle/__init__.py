@@ -63,6 +63,8 @@ def _load():
         ctypes.c_double, ctypes.c_int, _ip, ctypes.c_int, _ip, ctypes.c_int]
     lib.oracle_linear.argtypes = [_dp, _dp, _dp, _dp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.oracle_heads.argtypes = [_dp, _dp] + [ctypes.c_int] * 5
+    lib.oracle_attn_fwd_goflow.argtypes = [_dp, _dp, _dp, _dp, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_int, ctypes.c_double, ctypes.c_int]
     lib.oracle_set_mutation.argtypes = [ctypes.c_int]
     lib.oracle_set_threads.argtypes = [ctypes.c_int]
     lib.oracle_get_threads.restype = ctypes.c_int
@@ -281,4 +283,22 @@ def ref_attn(Q, K, V, scale, causal):
                 for j in range(jmax):
                     acc += scores[j] * V[bh, j, t]
                 O[bh, i, t] = acc / tot
+    return O
+
+
+def attn_fwd_goflow(Q, K, V, scale=None, causal=False):
+    """GoNN's CPU forward core with GoNN's pass structure (every op a whole-
+    tensor pass into a new buffer, broadcasts materialised, elementwise loops
+    on one thread, GEMMs threaded): the timed CPU baseline. Q, K, V (BH,S,D)
+    -> O (BH,S,D), equal to attn_fwd's O. Needs ~6 fp64 copies of the
+    (BH,S,S) scores in memory."""
+    Q, K, V = _c64(Q), _c64(K), _c64(V)
+    BH, S, D = Q.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+    O = np.empty_like(Q)
+    rc = _load().oracle_attn_fwd_goflow(_d(Q), _d(K), _d(V), _d(O), BH, S, D, float(scale),
+                                        int(bool(causal)))
+    if rc:
+        raise MemoryError(f"oracle_attn_fwd_goflow: {rc}")
     return O

@@ -460,6 +460,96 @@ void oracle_heads(const double* in, double* out, int B, int T, int H, int D, int
                 }
 }
 
+/*
+ * GoNN's CPU forward core with GoNN's own pass structure and threading, for
+ * the cpu_baseline leg of bench.py (timing only; O equals oracle_attn_fwd's
+ * bit for bit, which tests/test_oracle.py checks). Each tensor op of
+ * nn/attention.go:135-146 is one pass over the whole (BH, S, S) score tensor
+ * into a freshly allocated result, as the tensor package does:
+ *   MatMul            one GEMM per slice in sequence (backend/cpu.go:38-45),
+ *                     the GEMM itself threaded, as gonum's Dgemm is; the K^T
+ *                     operand a Permute copy (tensor/ops_shape.go:53-107)
+ *   MulScalar(scale)  Scalar(scale) broadcast to the full shape by expandTo
+ *                     (tensor/broadcast.go:35-80, a copy), then the binary loop
+ *                     (tensor/ops_binary.go:32-56)
+ *   Add(causal mask)  causalMaskAdd (1,1,S,S) built (nn/attention.go:185-196),
+ *                     expanded to (BH,S,S), then the binary loop
+ *   Softmax(3)        MaxAxis; Sub with the max expanded; Exp; SumAxis; Div
+ *                     with the sum expanded (tensor/ops_activation.go:455-461)
+ *   MatMul with V     as above.
+ * The elementwise loops and reductions run on one thread: the CPU backend has
+ * no Elementwiser (backend/cpu.go:9-11), so they are plain Go loops.
+ */
+static double* g_alloc(size_t n) { return (double*)malloc(n * sizeof(double)); }
+int oracle_attn_fwd_goflow(const double* Q, const double* K, const double* V, double* O,
+                           int BH, int S, int D, double scale, int causal) {
+    const size_t SS = (size_t)S * S, N = (size_t)BH * SS;
+    double* KT = g_alloc((size_t)BH * D * S);
+    double* sc = g_alloc(N);
+    if (!KT || !sc) { free(KT); free(sc); return -2; }
+    for (int bh = 0; bh < BH; bh++)  /* Permute copy (single-threaded loop) */
+        for (int j = 0; j < D; j++)
+            for (int i = 0; i < S; i++)
+                KT[((size_t)bh * D + j) * S + i] = K[((size_t)bh * S + i) * D + j];
+    for (int bh = 0; bh < BH; bh++)
+        gemm_nn(Q + (size_t)bh * S * D, KT + (size_t)bh * D * S, sc + (size_t)bh * SS, S, D, S);
+    free(KT);
+    /* MulScalar */
+    double* ex = g_alloc(N);
+    double* t1 = g_alloc(N);
+    if (!ex || !t1) { free(ex); free(t1); free(sc); return -2; }
+    for (size_t i = 0; i < N; i++) ex[i] = scale;
+    for (size_t i = 0; i < N; i++) t1[i] = sc[i] * ex[i];
+    free(sc);
+    double* t2 = t1;
+    if (causal) {
+        double* m = g_alloc(SS);
+        t2 = g_alloc(N);
+        if (!m || !t2) { free(m); free(t2); free(ex); free(t1); return -2; }
+        for (int i = 0; i < S; i++)
+            for (int j = 0; j < S; j++) m[(size_t)i * S + j] = j > i ? MASK_NEG : 0.0;
+        for (size_t i = 0; i < N; i++) ex[i] = m[i % SS];
+        for (size_t i = 0; i < N; i++) t2[i] = t1[i] + ex[i];
+        free(m);
+        free(t1);
+    }
+    /* Softmax(3) */
+    const size_t R = (size_t)BH * S;
+    double* mx = g_alloc(R);
+    double* sm = g_alloc(R);
+    double* t3 = g_alloc(N);
+    if (!mx || !sm || !t3) { free(mx); free(sm); free(t3); free(ex); free(t2); return -2; }
+    for (size_t r = 0; r < R; r++) {
+        double v = -INFINITY;
+        for (int j = 0; j < S; j++) if (t2[r * S + j] > v) v = t2[r * S + j];
+        mx[r] = v;
+    }
+    for (size_t i = 0; i < N; i++) ex[i] = mx[i / S];
+    for (size_t i = 0; i < N; i++) t3[i] = t2[i] - ex[i];
+    free(t2);
+    double* t4 = g_alloc(N);
+    if (!t4) { free(mx); free(sm); free(t3); free(ex); return -2; }
+    for (size_t i = 0; i < N; i++) t4[i] = exp(t3[i]);
+    free(t3);
+    for (size_t r = 0; r < R; r++) {
+        double v = 0.0;
+        for (int j = 0; j < S; j++) v += t4[r * S + j];
+        sm[r] = v;
+    }
+    double* at = g_alloc(N);
+    if (!at) { free(mx); free(sm); free(t4); free(ex); return -2; }
+    for (size_t i = 0; i < N; i++) ex[i] = sm[i / S];
+    for (size_t i = 0; i < N; i++) at[i] = t4[i] / ex[i];
+    free(t4);
+    free(ex);
+    free(mx);
+    free(sm);
+    for (int bh = 0; bh < BH; bh++)
+        gemm_nn(at + (size_t)bh * SS, V + (size_t)bh * S * D, O + (size_t)bh * S * D, S, S, D);
+    free(at);
+    return 0;
+}
+
 /* Timing helper for the CPU baseline: the forward core over `nslices` (b,h)
  * slices with OpenMP threads `threads` (0 = runtime default). */
 #ifdef _OPENMP

@@ -177,6 +177,18 @@ def test_fwd_rows_subset_is_identical():
     assert np.array_equal(O[:, rows], Or[:, rows]) and np.array_equal(L[:, rows], Lr[:, rows])
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_goflow_baseline_equals_oracle(causal):
+    """The timed CPU baseline (GoNN's pass structure: whole-tensor passes,
+    materialised broadcasts) computes the same fp64 numbers as the oracle:
+    the same op order per element, so bit for bit."""
+    rng = np.random.default_rng(18)
+    q, k, v = (rng.standard_normal((3, 70, 32)) for _ in range(3))
+    O = oracle.attn_fwd_goflow(q, k, v, scale=0.3, causal=causal)
+    Or, _ = oracle.attn_fwd(q, k, v, scale=0.3, causal=causal)
+    assert np.array_equal(O, Or)
+
+
 # ---------------------------------------------------------------------------
 # backward
 # ---------------------------------------------------------------------------
