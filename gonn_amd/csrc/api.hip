@@ -253,15 +253,50 @@ size_t bwd_ws(const gonn_attn_bwd_args* a) {
 
 // ---- helpers for the host shims ----------------------------------------
 
+#define TRYH_EARLY(x)                                        \
+    do {                                                     \
+        const hipError_t _e = (x);                           \
+        if (_e != hipSuccess) return (int)_e;                \
+    } while (0)
+
+// The host (fp64) entry points run on a stream of the calling thread, not on
+// the legacy null stream, and wait for that stream only: GoNN runs Backward
+// calls concurrently (tensor/autograd.go:10-32), and such callers must not
+// serialise on each other's device work. One non-blocking stream (default
+// priority) per thread and device, created on first use and kept for the
+// thread's life.
+constexpr int kMaxDevices = 64;
+int host_stream(hipStream_t* out) {
+    thread_local hipStream_t streams[kMaxDevices] = {};
+    int dev = 0;
+    TRYH_EARLY(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return GONN_E_UNSUPPORTED;
+    if (!streams[dev]) TRYH_EARLY(hipStreamCreateWithFlags(&streams[dev], hipStreamNonBlocking));
+    *out = streams[dev];
+    return GONN_OK;
+}
+
+// Waits for a host call's stream on every exit path, so no copy from or to
+// the caller's host arrays is still queued when the call returns.
+struct StreamSync {
+    hipStream_t s;
+    ~StreamSync() { (void)hipStreamSynchronize(s); }
+};
+
+// Scratch device memory of one host call, stream-ordered on that call's
+// stream (hipMallocAsync / hipFreeAsync): no device-wide synchronisation.
 struct DevMem {
+    hipStream_t s;
     std::vector<void*> ptrs;
+    explicit DevMem(hipStream_t st) : s(st) {}
     ~DevMem() {
-        for (void* p : ptrs) (void)hipFree(p);
+        for (void* p : ptrs) (void)hipFreeAsync(p, s);
     }
     int alloc(void** p, size_t bytes) {
         if (fail_alloc_injected()) return GONN_E_INJECTED;
         if (bytes == 0) bytes = 16;
-        if (hipMalloc(p, bytes) != hipSuccess) {
+        if (hipMallocAsync(p, bytes, s) != hipSuccess) {
+            (void)hipGetLastError();
             *p = nullptr;
             return GONN_E_NOMEM;
         }
@@ -285,8 +320,8 @@ int upload_padded(DevMem& mem, const double* host, size_t rows, int d, int dp, f
     void* dst = nullptr;
     TRY(mem.alloc(&stage, rows * d * sizeof(double)));
     TRY(mem.alloc(&dst, rows * dp * sizeof(float)));
-    TRYH(hipMemcpy(stage, host, rows * d * sizeof(double), hipMemcpyHostToDevice));
-    TRYH(gonn::launch_convert_from_f64((const double*)stage, dst, 0, rows, d, dp, nullptr));
+    TRYH(hipMemcpyAsync(stage, host, rows * d * sizeof(double), hipMemcpyHostToDevice, mem.s));
+    TRYH(gonn::launch_convert_from_f64((const double*)stage, dst, 0, rows, d, dp, mem.s));
     *out = (float*)dst;
     return GONN_OK;
 }
@@ -294,8 +329,8 @@ int upload_padded(DevMem& mem, const double* host, size_t rows, int d, int dp, f
 int download_padded(DevMem& mem, const float* dev, size_t rows, int d, int dp, double* host) {
     void* stage = nullptr;
     TRY(mem.alloc(&stage, rows * d * sizeof(double)));
-    TRYH(gonn::launch_convert_to_f64(dev, 0, (double*)stage, rows, d, dp, nullptr));
-    TRYH(hipMemcpy(host, stage, rows * d * sizeof(double), hipMemcpyDeviceToHost));
+    TRYH(gonn::launch_convert_to_f64(dev, 0, (double*)stage, rows, d, dp, mem.s));
+    TRYH(hipMemcpyAsync(host, stage, rows * d * sizeof(double), hipMemcpyDeviceToHost, mem.s));
     return GONN_OK;
 }
 
@@ -318,7 +353,7 @@ int run_fwd_f32(DevMem& mem, const float* q, const float* k, const float* v, flo
     const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_FWD, &a);
     void* ws = nullptr;
     if (wsb) TRY(mem.alloc(&ws, wsb));
-    return gonn_hip_attn_fwd(&a, ws, wsb, nullptr);
+    return gonn_hip_attn_fwd(&a, ws, wsb, mem.s);
 }
 
 bool shim_args_ok(int BH, int S, int d) { return BH > 0 && S > 0 && d > 0 && d <= 128; }
@@ -351,7 +386,7 @@ int run_fwd_f32_ex(DevMem& mem, const float* q, const float* k, const float* v, 
     const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_FWD, &a);
     void* ws = nullptr;
     if (wsb) TRY(mem.alloc(&ws, wsb));
-    return gonn_hip_attn_fwd(&a, ws, wsb, nullptr);
+    return gonn_hip_attn_fwd(&a, ws, wsb, mem.s);
 }
 
 // Split-KV decode on a checked call with a workspace of at least
@@ -391,7 +426,6 @@ int run_decode(const gonn_attn_decode_args* a, void* ws, hipStream_t s, bool pro
 // array keeps the last call's contents; the decode kernels write every
 // partial they later read, so nothing needs clearing between calls.
 constexpr size_t kNoAllocScratchBytes = GONN_NOALLOC_SCRATCH_BYTES;  // 32 MiB per device
-constexpr int kMaxDevices = 64;
 struct ScratchSlot {
     std::once_flag once;
     void* ptr = nullptr;
@@ -483,10 +517,16 @@ int kv_append_dev(gonn_kvcache* c, const void* k, const void* v, int src_bf16, i
                         hipMemcpyHostToDevice, s));
     TRYH(gonn::launch_kv_append(k, v, src_bf16, c->k, c->v, c->d_pc, c->d_pc + c->B, c->B, c->H,
                                 T, c->Lmax, c->D, s));
-    for (int b = 0; b < c->B; b++) c->h_len[b] += c->h_pc[c->B + b];
-    TRYH(hipMemcpyAsync(c->d_len, c->h_len.data(), (size_t)c->B * sizeof(int),
-                        hipMemcpyHostToDevice, s));
-    return herr(hipStreamSynchronize(s));
+    // The new lengths become the handle's only once the append and their
+    // upload have completed, so a failed call leaves host and device
+    // lengths as they were.
+    std::vector<int> len(c->h_len);
+    for (int b = 0; b < c->B; b++) len[b] += c->h_pc[c->B + b];
+    TRYH(hipMemcpyAsync(c->d_len, len.data(), (size_t)c->B * sizeof(int), hipMemcpyHostToDevice,
+                        s));
+    TRYH(hipStreamSynchronize(s));
+    c->h_len.swap(len);
+    return GONN_OK;
 }
 
 }  // namespace
@@ -773,7 +813,7 @@ int gonn_hip_upload_from_f64(gonn_buf* dst, const double* src, size_t n, void* s
         TRYH(hipMemcpyAsync(dst->ptr, src, n * 8, hipMemcpyHostToDevice, s));
         return herr(hipStreamSynchronize(s));
     }
-    DevMem mem;
+    DevMem mem(s);
     void* stage = nullptr;
     TRY(mem.alloc(&stage, n * 8));
     TRYH(hipMemcpyAsync(stage, src, n * 8, hipMemcpyHostToDevice, s));
@@ -793,7 +833,7 @@ int gonn_hip_download_to_f64(double* dst, const gonn_buf* src, size_t n, void* s
         TRYH(hipMemcpyAsync(dst, src->ptr, n * 8, hipMemcpyDeviceToHost, s));
         return herr(hipStreamSynchronize(s));
     }
-    DevMem mem;
+    DevMem mem(s);
     void* stage = nullptr;
     TRY(mem.alloc(&stage, n * 8));
     TRYH(gonn::launch_convert_to_f64(src->ptr, src->dtype == GONN_BF16, (double*)stage, n, 1, 1, s));
@@ -821,7 +861,10 @@ int gonn_hip_flash_attn_f64(const double* Q, const double* K, const double* V, d
                             int S, int d, double scale, int causal) {
     if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
-    DevMem mem;
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
     const int dp = pad_dim(d);
     const size_t rows = (size_t)BH * S;
     float *q, *k, *v, *o;
@@ -831,14 +874,17 @@ int gonn_hip_flash_attn_f64(const double* Q, const double* K, const double* V, d
     TRY(mem.alloc((void**)&o, rows * dp * 4));
     TRY(run_fwd_f32(mem, q, k, v, o, nullptr, BH, S, dp, scale, causal));
     TRY(download_padded(mem, o, rows, d, dp, O));
-    return herr(hipDeviceSynchronize());
+    return herr(hipStreamSynchronize(hs));
 }
 
 int gonn_hip_flash_attn_f64_fwd(const double* Q, const double* K, const double* V, double* O,
                                 double* L, int BH, int S, int d, double scale, int causal) {
     if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O || !L) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
-    DevMem mem;
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
     const int dp = pad_dim(d);
     const size_t rows = (size_t)BH * S;
     float *q, *k, *v, *o, *l;
@@ -850,7 +896,7 @@ int gonn_hip_flash_attn_f64_fwd(const double* Q, const double* K, const double* 
     TRY(run_fwd_f32(mem, q, k, v, o, l, BH, S, dp, scale, causal));
     TRY(download_padded(mem, o, rows, d, dp, O));
     TRY(download_padded(mem, l, rows, 1, 1, L));
-    return herr(hipDeviceSynchronize());
+    return herr(hipStreamSynchronize(hs));
 }
 
 int gonn_hip_flash_attn_f64_ex(const double* Q, const double* K, const double* V, double* O,
@@ -876,7 +922,10 @@ int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const doubl
     const size_t mn = mask ? mask_elems(B, H, Sq, Sk, mask_sb, mask_sh) : 0;
     if (mask && !mn) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
-    DevMem mem;
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
     const int dp = pad_dim(d);
     const size_t rq = (size_t)B * H * Sq, rk = (size_t)B * H * Sk;
     float *q, *k, *v, *o, *l = nullptr, *m = nullptr;
@@ -889,13 +938,13 @@ int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const doubl
     if (L) TRY(mem.alloc((void**)&l, rq * 4));
     if (kv_len) {
         TRY(mem.alloc((void**)&kl, (size_t)B * 4));
-        TRYH(hipMemcpy(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice));
+        TRYH(hipMemcpyAsync(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice, mem.s));
     }
     TRY(run_fwd_f32_ex(mem, q, k, v, o, l, B, H, Sq, Sk, dp, scale, causal, kl, m, mn, mask_sb,
                        mask_sh));
     TRY(download_padded(mem, o, rq, d, dp, O));
     if (L) TRY(download_padded(mem, l, rq, 1, 1, L));
-    return herr(hipDeviceSynchronize());
+    return herr(hipStreamSynchronize(hs));
 }
 
 int gonn_hip_flash_attn_f64_bwd(const double* Q, const double* K, const double* V, const double* O,
@@ -926,7 +975,10 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
     if (mask && !mn) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
     const int BH = B * H;
-    DevMem mem;
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
     const int dp = pad_dim(d);
     const size_t rq = (size_t)BH * Sq, rk = (size_t)BH * Sk, nq = rq * dp, nk = rk * dp;
     float *q, *k, *v, *o, *l, *g, *dq, *dk, *dv;
@@ -944,7 +996,7 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
     if (mask) TRY(upload_padded(mem, mask, mn, 1, 1, &m));
     if (kv_len) {
         TRY(mem.alloc((void**)&kl, (size_t)B * 4));
-        TRYH(hipMemcpy(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice));
+        TRYH(hipMemcpyAsync(kl, kv_len, (size_t)B * 4, hipMemcpyHostToDevice, mem.s));
     }
     gonn_attn_bwd_args a{};
     a.q = {q, nq * 4, GONN_F32};
@@ -972,17 +1024,17 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
     const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_BWD, &a);
     void* ws = nullptr;
     if (wsb) TRY(mem.alloc(&ws, wsb));
-    TRY(gonn_hip_attn_bwd(&a, ws, wsb, nullptr));
+    TRY(gonn_hip_attn_bwd(&a, ws, wsb, mem.s));
     TRY(download_padded(mem, dq, rq, d, dp, dQ));
     TRY(download_padded(mem, dk, rk, d, dp, dK));
     TRY(download_padded(mem, dv, rk, d, dp, dV));
-    return herr(hipDeviceSynchronize());
+    return herr(hipStreamSynchronize(hs));
 }
 
 double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal) {
     if (!shim_args_ok(BH, S, d) || iters <= 0) return (double)GONN_E_INVALID;
     if (!gonn_hip_available()) return (double)GONN_E_NODEVICE;
-    DevMem mem;
+    DevMem mem(nullptr);
     const int dp = pad_dim(d);
     const size_t n = (size_t)BH * S * dp;
     float *q, *k, *v, *o;
@@ -1141,11 +1193,14 @@ int gonn_hip_kvcache_append_f64(gonn_kvcache* c, const double* k, const double* 
     if (!c || !k || !v) return GONN_E_INVALID;
     TRY(kv_check_append(c, T, counts));
     const size_t rows = (size_t)c->B * c->H * T;
-    DevMem mem;
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
     float *kd = nullptr, *vd = nullptr;
     TRY(upload_padded(mem, k, rows, c->D, c->D, &kd));
     TRY(upload_padded(mem, v, rows, c->D, c->D, &vd));
-    return kv_append_dev(c, kd, vd, 0, T, nullptr);
+    return kv_append_dev(c, kd, vd, 0, T, hs);
 }
 
 int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, double scale,
@@ -1161,14 +1216,18 @@ int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, dou
 int gonn_hip_kvcache_attend_f64(gonn_kvcache* c, const double* q, double* o, double scale) {
     if (!c || !q || !o) return GONN_E_INVALID;
     const size_t rows = (size_t)c->B * c->H;
-    DevMem mem;
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
     float* qd = nullptr;
     void* od = nullptr;
     TRY(upload_padded(mem, q, rows, c->D, c->D, &qd));
     TRY(mem.alloc(&od, rows * c->D * sizeof(float)));
     gonn_buf qb{qd, rows * c->D * 4, GONN_F32}, ob{od, rows * c->D * 4, GONN_F32};
-    TRY(gonn_hip_kvcache_attend(c, &qb, &ob, scale, nullptr));
-    return download_padded(mem, (const float*)od, rows, c->D, c->D, o);
+    TRY(gonn_hip_kvcache_attend(c, &qb, &ob, scale, hs));
+    TRY(download_padded(mem, (const float*)od, rows, c->D, c->D, o));
+    return herr(hipStreamSynchronize(hs));
 }
 
 }  // extern "C"
