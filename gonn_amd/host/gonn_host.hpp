@@ -279,10 +279,12 @@ struct DiffOut {
 };
 // kvLen (new, BH / H entries or empty): the key padding of ForwardMasked;
 // attnMask (new, empty = none): its additive mask in one of expandAttnMask's
-// shapes for B = BH / H; both in the forward and in the node's backward.
+// shapes for B = BH / H; Sk (new, 0 = S): key rows of kp and vp for
+// cross-attention (top-left causal mask); all in the forward and in the
+// node's backward.
 DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
                       double scale, bool causal, const std::vector<int>& kvLen = {}, int H = 1,
-                      const Tensor& attnMask = Tensor{});
+                      const Tensor& attnMask = Tensor{}, int Sk = 0);
 
 // expandAttnMask (nn/attention.go:242-257): the (sequence, head) element
 // strides of an additive mask of shape (Tq,Tk), (B*H,Tq,Tk), (B,Tq,Tk) or
@@ -300,8 +302,9 @@ class MultiHeadAttention {
 
     MultiHeadAttention(int embedDim, int numHeads, Linear q, Linear k, Linear v, Linear out);
 
-    // Forward (nn/attention.go:107-148) through the differentiable fused core;
-    // the node of the last call is kept in LastNode for a backward pass.
+    // Forward (nn/attention.go:107-148) through the differentiable fused core,
+    // Tq != Tk included (cross-attention); the node of the last call is kept
+    // in LastNode for a backward pass.
     Tensor Forward(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
     // ForwardFused (nn/attention.go:159-180): inference core, no node. Also
     // takes Tq != Tk (cross-attention), which the reference's gate sends to

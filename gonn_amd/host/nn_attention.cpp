@@ -100,18 +100,19 @@ std::vector<double> fusedAttnF64(const std::vector<double>& Q, const std::vector
 
 DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int BH, int S, int D,
                       double scale, bool causal, const std::vector<int>& kvLen, int H,
-                      const Tensor& attnMask) {
+                      const Tensor& attnMask, int Sk) {
     if (H <= 0 || BH % H != 0) throw std::invalid_argument("fusedAttnDiff: BH must be a multiple of H");
+    if (Sk <= 0) Sk = S;
     const bool masked = !attnMask.Data.empty();
+    // The reference seam's entry points (square, no mask, no padding), else
+    // the general ones of the wider gate.
+    const bool plain = !masked && kvLen.empty() && Sk == S;
     std::array<long, 2> st{0, 0};
-    if (masked) st = maskStrides(attnMask.Shape, BH / H, H, S, S);
+    if (masked) st = maskStrides(attnMask.Shape, BH / H, H, S, Sk);
     auto mask = std::make_shared<std::vector<double>>(attnMask.Data);
-    hip::FwdOut f = masked ? hip::FlashAttnF64Masked(qp.Data, kp.Data, vp.Data, BH / H, H, S, S,
-                                                     D, scale, causal, kvLen, *mask, st[0], st[1])
-                    : kvLen.empty()
-                        ? hip::FlashAttnF64Fwd(qp.Data, kp.Data, vp.Data, BH, S, D, scale, causal)
-                        : hip::FlashAttnF64ExFwd(qp.Data, kp.Data, vp.Data, BH / H, H, S, S, D,
-                                                 scale, causal, kvLen);
+    hip::FwdOut f = plain ? hip::FlashAttnF64Fwd(qp.Data, kp.Data, vp.Data, BH, S, D, scale, causal)
+                          : hip::FlashAttnF64Masked(qp.Data, kp.Data, vp.Data, BH / H, H, S, Sk, D,
+                                                    scale, causal, kvLen, *mask, st[0], st[1]);
     DiffOut r;
     r.Out = Tensor::New(f.O, qp.Shape);
     // The node's closure holds the inputs and the saved O and L, as the Go
@@ -119,18 +120,14 @@ DiffOut fusedAttnDiff(const Tensor& qp, const Tensor& kp, const Tensor& vp, int 
     auto saved = std::make_shared<std::array<Tensor, 3>>(std::array<Tensor, 3>{qp, kp, vp});
     auto O = std::make_shared<std::vector<double>>(std::move(f.O));
     auto L = std::make_shared<std::vector<double>>(std::move(f.L));
-    r.Node.Backward = [saved, O, L, BH, S, D, scale, causal, kvLen, H, masked, mask,
+    r.Node.Backward = [saved, O, L, BH, S, Sk, D, scale, causal, kvLen, H, plain, mask,
                        st](const Tensor& grad) {
         const Tensor &q = (*saved)[0], &k = (*saved)[1], &v = (*saved)[2];
         hip::BwdOut b =
-            masked ? hip::FlashAttnF64BwdMasked(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH / H,
-                                                H, S, S, D, scale, causal, kvLen, *mask, st[0],
-                                                st[1])
-            : kvLen.empty()
-                ? hip::FlashAttnF64Bwd(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH, S, D, scale,
-                                       causal)
-                : hip::FlashAttnF64BwdEx(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH / H, H, S,
-                                         D, scale, causal, kvLen);
+            plain ? hip::FlashAttnF64Bwd(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH, S, D, scale,
+                                         causal)
+                  : hip::FlashAttnF64BwdMasked(q.Data, k.Data, v.Data, *O, *L, grad.Data, BH / H, H,
+                                               S, Sk, D, scale, causal, kvLen, *mask, st[0], st[1]);
         return std::array<Tensor, 3>{Tensor::New(std::move(b.dQ), q.Shape),
                                      Tensor::New(std::move(b.dK), k.Shape),
                                      Tensor::New(std::move(b.dV), v.Shape)};
@@ -174,8 +171,8 @@ void MultiHeadAttention::checkQKVDims(const Tensor& q, const Tensor& k, const Te
 void MultiHeadAttention::requireFused(int D, int Tq, int Tk) const {
     if (!fusedAttnAvailable())
         throw hip::Error(-5, "nn: fused attention needs libgonn_hip.so and a gfx950 device");
-    if (!fusedAttnSupports(D, Tq, Tk) || Tq != Tk)
-        throw std::invalid_argument("nn: the fused core needs D in {64, 128} and Tq == Tk, got D=" +
+    if (!fusedAttnSupports(D, Tq, Tk))
+        throw std::invalid_argument("nn: the fused core needs D in {64, 128}, got D=" +
                                     std::to_string(D) + " Tq=" + std::to_string(Tq) +
                                     " Tk=" + std::to_string(Tk));
 }
@@ -190,7 +187,10 @@ Tensor MultiHeadAttention::Forward(const Tensor& q, const Tensor& k, const Tenso
     const Tensor kp = KProj.Forward(k).Reshape({B, Tk, H, D}).Permute0213();
     const Tensor vp = VProj.Forward(v).Reshape({B, Tk, H, D}).Permute0213();
     const double scale = 1.0 / std::sqrt((double)D);
-    DiffOut f = fusedAttnDiff(qp, kp, vp, B * H, Tq, D, scale, causal);
+    // Cross-attention (Tq != Tk, TransformerDecoderLayer's Forward(x, memory,
+    // memory, false), nn/transformer.go:234) takes the same differentiable
+    // node with Tk key rows.
+    DiffOut f = fusedAttnDiff(qp, kp, vp, B * H, Tq, D, scale, causal, {}, H, Tensor{}, Tk);
     LastNode = f.Node;
     const Tensor ctx = f.Out.Permute0213().Reshape({B, Tq, EmbedDim});  // :130-131
     return OutProj.Forward(ctx);                                         // :132

@@ -46,38 +46,49 @@ class FusedAttnNode:
     nn/flashattn_cuda.go:29-37): holds what the backward needs and runs the
     device backward when called with the upstream gradient."""
 
-    def __init__(self, Q, K, V, O, L, BH, S, D, scale, causal, kv_len=None, H=1, attn_mask=None):
+    def __init__(self, Q, K, V, O, L, BH, S, D, scale, causal, kv_len=None, H=1, attn_mask=None,
+                 Sk=None):
         self.saved = (Q, K, V, O, L)
         self.shape = (BH, S, D)
+        self.Sk = S if Sk is None else int(Sk)
         self.scale = scale
         self.causal = causal
         self.kv_len, self.H, self.attn_mask = kv_len, H, attn_mask
 
+    def plain(self) -> bool:
+        """The reference seam's own case: square, no padding, no mask."""
+        return self.kv_len is None and self.attn_mask is None and self.Sk == self.shape[1]
+
     def __call__(self, grad):
         Q, K, V, O, L = self.saved
         BH, S, D = self.shape
-        if self.kv_len is None and self.attn_mask is None:
+        if self.plain():
             return hip.FlashAttnF64Bwd(Q, K, V, O, L, grad, BH, S, D, self.scale, self.causal)
         return hip.FlashAttnF64BwdEx(Q, K, V, O, L, grad, BH // self.H, self.H, S, D,
                                      self.scale, self.causal, kv_len=self.kv_len,
-                                     attn_mask=self.attn_mask)
+                                     attn_mask=self.attn_mask, Sk=self.Sk)
 
 
 def fused_attn_diff(qp, kp, vp, BH: int, S: int, D: int, scale: float, causal: bool,
-                    kv_len=None, H: int = 1, attn_mask=None):
+                    kv_len=None, H: int = 1, attn_mask=None, Sk=None):
     """Differentiable core: returns (O, node) where node(dO) -> (dQ, dK, dV).
     kv_len (new): optional per-sequence key counts (BH / H entries), the key
-    padding of ForwardMasked; attn_mask (new): its additive mask; both in the
-    forward and the backward."""
-    if kv_len is None and attn_mask is None:
-        O, L = hip.FlashAttnF64Fwd(qp, kp, vp, BH, S, D, scale, causal)
+    padding of ForwardMasked; attn_mask (new): its additive mask; Sk (new):
+    the key rows of kp and vp when they differ from S (cross-attention, top-
+    left causal mask); all in the forward and the backward."""
+    Sk = S if Sk is None else int(Sk)
+    node = FusedAttnNode(np.ascontiguousarray(qp, dtype=np.float64).ravel(),
+                         np.ascontiguousarray(kp, dtype=np.float64).ravel(),
+                         np.ascontiguousarray(vp, dtype=np.float64).ravel(), None, None, BH, S, D,
+                         scale, causal, kv_len, H, attn_mask, Sk)
+    Q, K, V = node.saved[:3]
+    if node.plain():
+        O, L = hip.FlashAttnF64Fwd(Q, K, V, BH, S, D, scale, causal)
     else:
-        O, L = hip.FlashAttnF64Ex(qp, kp, vp, BH // H, H, S, S, D, scale, causal,
+        O, L = hip.FlashAttnF64Ex(Q, K, V, BH // H, H, S, Sk, D, scale, causal,
                                   kv_len=kv_len, lse=True, attn_mask=attn_mask)
-    return O, FusedAttnNode(np.ascontiguousarray(qp, dtype=np.float64).ravel(),
-                            np.ascontiguousarray(kp, dtype=np.float64).ravel(),
-                            np.ascontiguousarray(vp, dtype=np.float64).ravel(), O, L, BH, S, D,
-                            scale, causal, kv_len, H, attn_mask)
+    node.saved = (Q, K, V, O, L)
+    return O, node
 
 
 class Linear:
@@ -158,14 +169,32 @@ class MultiHeadAttention:
         """ForwardFused: projections, fused core, output projection."""
         q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
         self._check(q, k, v)
-        B, Tq, _ = q.shape
-        Tk = k.shape[1]
-        H, D = self.NumHeads, self.HeadDim
         if not fused_attn_available():
             raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
         return self._fused(q, k, v, causal, None)
 
-    forward = forward_fused
+    def forward(self, q, k, v, causal: bool):
+        """Forward (nn/attention.go:107-148) with the differentiable fused
+        core (fusedAttnDiff, :129-133), Tq != Tk included: the encoder's
+        Forward(x, x, x, false), the decoder's causal self-attention
+        Forward(t, t, t, true) and its cross-attention Forward(x, memory,
+        memory, false) (nn/transformer.go:124-136, :224-238). The node of the
+        call is kept in last_node: last_node(g) maps the gradient g of the
+        core output (B*H, Tq, D) to the gradients of the projected heads."""
+        q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
+        self._check(q, k, v)
+        if not fused_attn_available():
+            raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
+        B, Tq, _ = q.shape
+        Tk = k.shape[1]
+        H, D = self.NumHeads, self.HeadDim
+        qp = self._split(self.QProj.forward(q))
+        kp = self._split(self.KProj.forward(k))
+        vp = self._split(self.VProj.forward(v))
+        O, self.last_node = fused_attn_diff(qp, kp, vp, B * H, Tq, D, 1.0 / math.sqrt(D), causal,
+                                            H=H, Sk=Tk)
+        ctx = O.reshape(B, H, Tq, D).transpose(0, 2, 1, 3).reshape(B, Tq, self.EmbedDim)
+        return self.OutProj.forward(ctx)
 
     def _fused(self, q, k, v, causal, kv_len, attn_mask=None):
         B, Tq, _ = q.shape

@@ -39,6 +39,11 @@ int oracle_attn_bwd_autograd_ex(const double* Q, const double* K, const double* 
                                 const double* dO, double* dQ, double* dK, double* dV, int BH,
                                 int H, int S, int D, double scale, int causal, const int* kv_len,
                                 const double* amask, long mask_sb, long mask_sh);
+int oracle_attn_bwd_autograd_x(const double* Q, const double* K, const double* V,
+                               const double* dO, double* dQ, double* dK, double* dV, int BH,
+                               int H, int Sq, int Sk, int D, double scale, int causal,
+                               const int* kv_len, const double* amask, long mask_sb,
+                               long mask_sh);
 int oracle_linear(const double* x, const double* W, const double* b, double* y, int N, int in,
                   int out);
 void oracle_heads(const double* in, double* out, int B, int T, int H, int D, int dir);
@@ -618,16 +623,49 @@ static void test_gpu() {
         }
     }
     gonn::hip::SetMode(0);
-    // The fused gate: Tq != Tk is outside the seam's contract.
-    {
-        Rng r(5);
-        Linear l;
-        l.W = Tensor::New(r.normals(64 * 64, 0.125), {64, 64});
-        MultiHeadAttention m(64, 1, l, l, l, l);
-        Tensor q = Tensor::New(r.normals(1 * 8 * 64), {1, 8, 64});
-        Tensor k = Tensor::New(r.normals(1 * 9 * 64), {1, 9, 64});
-        CHECK(throws_invalid([&] { m.Forward(q, k, k, false); }), "Tq != Tk rejected");
+    // TransformerDecoderLayer's cross-attention Forward(x, memory, memory,
+    // false) (nn/transformer.go:234), Tq != Tk, through Forward and its
+    // LastNode: output vs the oracle's MHA, the node's gradients vs the
+    // oracle's rectangular autograd chain on the projected heads.
+    for (int D : {64, 128}) {
+        const int B = 2, Tq = 45, Tk = 70, H = 2, E = H * D;
+        Rng r(4000 + D);
+        const double ws = 1.0 / std::sqrt((double)E);
+        auto lin = [&] {
+            Linear l;
+            l.W = Tensor::New(r.normals((size_t)E * E, ws), {E, E});
+            l.B = r.normals(E, 0.1);
+            return l;
+        };
+        MultiHeadAttention m(E, H, lin(), lin(), lin(), lin());
+        Tensor x = Tensor::New(r.normals((size_t)B * Tq * E, ws), {B, Tq, E});
+        Tensor mem = Tensor::New(r.normals((size_t)B * Tk * E, ws), {B, Tk, E});
+        const std::vector<double> ref = oracle_mha(m, x, mem, mem, false);
+        // projected heads for the gradient reference
+        auto heads = [&](const Linear& l, const Tensor& t, int T) {
+            Tensor y = l.Forward(t).Reshape({B, T, H, D}).Permute0213();
+            return y;
+        };
+        const Tensor qh = heads(m.QProj, x, Tq), kh = heads(m.KProj, mem, Tk),
+                     vh = heads(m.VProj, mem, Tk);
+        Tensor g = Tensor::New(r.normals((size_t)B * H * Tq * D), {B, H, Tq, D});
+        std::vector<double> rq(qh.Numel()), rk(kh.Numel()), rv(vh.Numel());
+        oracle_attn_bwd_autograd_x(qh.Data.data(), kh.Data.data(), vh.Data.data(), g.Data.data(),
+                                   rq.data(), rk.data(), rv.data(), B * H, H, Tq, Tk, D,
+                                   1.0 / std::sqrt((double)D), 0, nullptr, nullptr, 0, 0);
+        for (int mode = 0; mode < 2; mode++) {
+            gonn::hip::SetMode(mode);
+            const double atol = mode ? 2e-2 : 1e-4, rtol = mode ? 1e-2 : 0.0;
+            const std::string tag = "cross Forward D=" + std::to_string(D) + (mode ? " bf16" : " fp32");
+            Tensor out = m.Forward(x, mem, mem, false);
+            CHECK(close(out.Data, ref, atol, rtol, (tag + " out").c_str()), "%s out", tag.c_str());
+            auto grads = m.LastNode.Backward(g);
+            CHECK(close(grads[0].Data, rq, atol, rtol, (tag + " dQ").c_str()), "%s dQ", tag.c_str());
+            CHECK(close(grads[1].Data, rk, atol, rtol, (tag + " dK").c_str()), "%s dK", tag.c_str());
+            CHECK(close(grads[2].Data, rv, atol, rtol, (tag + " dV").c_str()), "%s dV", tag.c_str());
+        }
     }
+    gonn::hip::SetMode(0);
     // The wider gate: cross-attention (Tq != Tk) through ForwardFused and a
     // suffix key-padding mask through ForwardMasked, against the oracle.
     for (bool causal : {false, true}) {
