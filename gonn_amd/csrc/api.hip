@@ -115,7 +115,7 @@ bool mask_ok(const gonn_buf& m, int64_t sb, int64_t sh, int B, int H, int Sq, in
 int fwd_mode(const gonn_attn_fwd_args* a) { return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode; }
 int bwd_keys_of(const gonn_attn_bwd_args* a) { return a->Sk > 0 ? a->Sk : a->S; }
 int bwd_mode(const gonn_attn_bwd_args* a) {
-    return a->attn_mask.ptr || bwd_keys_of(a) != a->S ? GONN_ATTN_FP32_MFMA : a->mode;
+    return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode;
 }
 
 // The bf16-MFMA kernels take Q as bf16(q * (sign(scale) * c2)) with
@@ -223,24 +223,26 @@ int check_bwd(const gonn_attn_bwd_args* a) {
 }
 
 // Backward workspace: lse2 and delta (BH,Sp) f32, then in bf16 mode the
-// packed operands Qb, dOb, Kb, Vb (BH,Sp,D) and Qt, dOt, Kt (BH,D,Sp) bf16,
-// each region 256-byte aligned.
+// packed operands Qb, dOb (BH,Sp,D), Kb, Vb (BH,Skp,D), Qt, dOt (BH,D,Sp)
+// and Kt (BH,D,Skp) bf16, each region 256-byte aligned (Sp, Skp: the query
+// and key counts rounded up to kBwdPad).
 struct BwdLayout {
     size_t lse2, delta, packed[7], total;
 };
 
-BwdLayout bwd_layout(int mode, size_t BH, int S, int D) {
+BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D) {
     BwdLayout L{};
-    const size_t Sp = round_up((size_t)S, gonn::kBwdPad);
+    const size_t Sp = round_up((size_t)S, gonn::kBwdPad), Skp = round_up((size_t)Sk, gonn::kBwdPad);
     size_t off = 0;
     L.lse2 = off;
     off = round_up(off + BH * Sp * 4, 256);
     L.delta = off;
     off = round_up(off + BH * Sp * 4, 256);
     if (mode == GONN_ATTN_BF16_MFMA) {
+        const bool keyside[7] = {false, false, true, true, false, false, true};
         for (int i = 0; i < 7; i++) {
             L.packed[i] = off;
-            off = round_up(off + BH * Sp * D * 2, 256);
+            off = round_up(off + BH * (keyside[i] ? Skp : Sp) * D * 2, 256);
         }
     }
     L.total = off;
@@ -248,7 +250,7 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int D) {
 }
 
 size_t bwd_ws(const gonn_attn_bwd_args* a) {
-    return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, a->D).total + 256;
+    return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->D).total + 256;
 }
 
 // ---- helpers for the host shims ----------------------------------------
@@ -670,7 +672,7 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     const int BH = a->B * a->H, S = a->S, D = a->D;
     const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
     const int mode = bwd_mode(a);
-    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, D);
+    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, bwd_keys_of(a), D);
     uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
     gonn::BwdParams p{};
     if (a->attn_mask.ptr) {
@@ -734,8 +736,8 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p2.src[1] = a->v.ptr;
         p2.row[1] = Vb;
         p2.mul[0] = p2.mul[1] = 1.f;
-        p2.S = S;
-        p2.Sp = Sp;
+        p2.S = p.Sk;
+        p2.Sp = p.Skp;
         TRYH(gonn::launch_pack(p2, 2, 0, BH, D, s));
         p.q = Qb;
         p.dO = dOb;

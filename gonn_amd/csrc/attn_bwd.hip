@@ -126,24 +126,29 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, ln = lane & 31;
-    const int S = p.S, Sp = p.Sp;
+    const int S = p.S, Sp = p.Sp;  // query rows (Q, dO, L, D padded to Sp)
+    const int Sk = p.Sk, Skp = p.Skp;  // key rows (K, V padded to Skp)
     int bh, kb;
-    map_block(blockIdx.x, Sp / BN, p.BH, false, bh, kb);
+    map_block(blockIdx.x, Skp / BN, p.BH, false, bh, kb);
     const int kw = kb * BN + wave * 32;  // first key of this wave
     const int kj = kw + ln;              // this lane's key
     // Keys >= Skv are padded: zero probability for every query, so their dK
     // and dV rows are 0, and the other keys' gradients do not involve them.
     const int Skv = bwd_keys(p, bh);
-    if (kb * BN >= Skv) {
-        bwd_zero_rows<D>(p.dk, S, bh, kb * BN, BN);
-        bwd_zero_rows<D>(p.dv, S, bh, kb * BN, BN);
+    // Top-left causal: key j is seen by queries i >= j only, so a block past
+    // the last query has no gradient either (cross-attention, Sq < Sk).
+    const int qb0 = CAUSAL ? (kb * BN) / BM : 0;  // earlier queries see none of these keys
+    const int nq = (S + BM - 1) / BM - qb0;
+    if (kb * BN >= Skv || nq <= 0) {
+        bwd_zero_rows<D>(p.dk, Sk, bh, kb * BN, BN);
+        bwd_zero_rows<D>(p.dv, Sk, bh, kb * BN, BN);
         return;
     }
 
     bf16x8 kf[NKS], vf[NKS];
     {
-        const bf16* kr = (const bf16*)p.k + ((size_t)bh * Sp + kj) * D + g * 8;
-        const bf16* vr = (const bf16*)p.v + ((size_t)bh * Sp + kj) * D + g * 8;
+        const bf16* kr = (const bf16*)p.k + ((size_t)bh * Skp + kj) * D + g * 8;
+        const bf16* vr = (const bf16*)p.v + ((size_t)bh * Skp + kj) * D + g * 8;
         for (int ks = 0; ks < NKS; ks++) {
             kf[ks] = *(const bf16x8*)(kr + ks * 16);
             vf[ks] = *(const bf16x8*)(vr + ks * 16);
@@ -212,8 +217,6 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     f32x16 dvacc[NDT], dkacc[NDT];
     for (int t = 0; t < NDT; t++) dvacc[t] = dkacc[t] = f32x16{};
     const float c2 = p.c2b;
-    const int qb0 = CAUSAL ? (kb * BN) / BM : 0;  // earlier queries see none of these keys
-    const int nq = (S + BM - 1) / BM - qb0;       // >= 1
     u32x4 pp[4], pd[4];  // P and dS of the tile dV/dK consume next, bf16 pairs per word
 
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -408,11 +411,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         }
     }
 
-    if (kj < S) {
+    if (kj < Sk) {
         const float sc = p.dks;
         const bool live = kj < Skv;  // a padded key of a partial block: zeros
-        float* dkr = p.dk + ((size_t)bh * S + kj) * D;
-        float* dvr = p.dv + ((size_t)bh * S + kj) * D;
+        float* dkr = p.dk + ((size_t)bh * Sk + kj) * D;
+        float* dvr = p.dv + ((size_t)bh * Sk + kj) * D;
         for (int t = 0; t < NDT; t++)
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 f32x4 a, b;
@@ -749,7 +752,6 @@ hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, fl
 
 hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0) return hipErrorInvalidValue;
-    if (mode == 1 && (p.Sk != p.S || p.Skp != p.Sp)) return hipErrorInvalidValue;
     const dim3 grid((p.Skp / 128) * p.BH);
     if (mode == 1) GONN_BWD_LAUNCH(bwd_dkdv_bf16_kernel);
     else GONN_BWD_LAUNCH(bwd_dkdv_f32_kernel);
@@ -758,7 +760,6 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipS
 
 hipError_t launch_bwd_dq(const BwdParams& p, int mode, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0) return hipErrorInvalidValue;
-    if (mode == 1 && p.Sk != p.S) return hipErrorInvalidValue;
     const dim3 grid((p.Sp / 128) * p.BH);
     if (mode == 1) return launch_bwd_dq_bf16(p, D, causal, s);
     GONN_BWD_LAUNCH(bwd_dq_f32_kernel);

@@ -108,9 +108,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     int kend = Skv;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
     const int nt = (kend + BN - 1) / BN;
-    const bf16* Kg = (const bf16*)p.k + (size_t)bh * Sp * D;
-    const bf16* Vg = (const bf16*)p.v + (size_t)bh * Sp * D;
-    const bf16* Ktg = (const bf16*)p.kt + (size_t)bh * D * Sp;
+    // K, V and K^T hold Sk key rows padded to Skp (Sk != S for
+    // cross-attention).
+    const int Skp = p.Skp;
+    const bf16* Kg = (const bf16*)p.k + (size_t)bh * Skp * D;
+    const bf16* Vg = (const bf16*)p.v + (size_t)bh * Skp * D;
+    const bf16* Ktg = (const bf16*)p.kt + (size_t)bh * D * Skp;
 
     uint32_t roff[NRI], toff[NTI];
     for (int i = 0; i < NRI; i++) {
@@ -119,10 +122,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     }
     for (int i = 0; i < NTI; i++) {
         const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
-        toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
+        toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Skp + (ch < TCD ? ch : 0) * 8) * 2);
     }
     const uint32_t rlast = wave * 64 < RLAST, tlast = wave * 64 < TLAST;  // wave-uniform
-    const uint32_t slice = (uint32_t)Sp * D * 2;  // bytes of one (b,h) slice
+    const uint32_t slice = (uint32_t)Skp * D * 2;  // bytes of one (b,h) slice of K, V, K^T
     const brsrc rk = make_rsrc(Kg, slice), rv = make_rsrc(Vg, slice), rkt = make_rsrc(Ktg, slice);
     const uint32_t lk = lds_addr(sK) + wave * 1024, lv = lds_addr(sV) + wave * 1024;
     const uint32_t lkt = lds_addr(sKt) + wave * 1024;
@@ -329,7 +332,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
 }
 
 hipError_t launch_bwd_dq_bf16(const BwdParams& p, int D, int causal, hipStream_t s) {
-    if (p.Sp % kBwdPad != 0) return hipErrorInvalidValue;
+    if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0) return hipErrorInvalidValue;
     const dim3 grid((p.Sp / 128) * p.BH);
     if (D == 64) {
         if (causal) bwd_dq_bf16_kernel<64, true><<<grid, 256, 0, s>>>(p);

@@ -130,7 +130,7 @@ typedef struct {
     int64_t mask_stride_b, mask_stride_h;
     /* Key rows when they differ from the S query rows (cross-attention with
      * the forward's top-left causal mask): k, v, dk, dv are (B*H, Sk, D).
-     * 0 means Sk = S. A cross-attention call runs the fp32-MFMA kernels.   */
+     * 0 means Sk = S. Cross-attention runs in the requested mode.          */
     int Sk;
 } gonn_attn_bwd_args;
 
@@ -359,7 +359,7 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
  * fp64 data read as in gonn_attn_fwd_args.attn_mask with element strides
  * mask_sb (sequence) and mask_sh (head) and rows Sk apart; NULL = none. The
  * backward also takes cross-attention (Sq != Sk: K, V, dK, dV are
- * (B*H, Sk, d)). Masked or cross-attention calls run the fp32-MFMA kernels
+ * (B*H, Sk, d)). Masked calls run the fp32-MFMA kernels
  * in either mode.                                                          */
 int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const double* V, double* O,
                                    double* L, int B, int H, int Sq, int Sk, int d, double scale,

@@ -287,9 +287,9 @@ def test_attn_mask_cross_attention_and_nn(mode="fp32"):
 @pytest.mark.parametrize("sq_sk", [(70, 150), (150, 70)], ids=lambda t: f"{t[0]}x{t[1]}")
 def test_cross_attention_backward_matches_oracle(mode, D, causal, sq_sk):
     """Cross-attention backward (Sq != Sk, top-left causal, key padding):
-    dQ (B*H,Sq,D), dK, dV (B*H,Sk,D) against the oracle's autograd chain.
-    The backward runs the fp32-MFMA kernels in either mode; O and LSE come
-    from the forward of the stated mode, whose bar applies."""
+    dQ (B*H,Sq,D), dK, dV (B*H,Sk,D) against the oracle's autograd chain,
+    in the stated mode (the bf16 backward packs K and V with their own key
+    padding) at that mode's bar."""
     from gonn_amd import hip
     Sq, Sk = sq_sk
     B, H = 2, 2
