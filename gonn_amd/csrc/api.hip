@@ -110,9 +110,10 @@ bool mask_ok(const gonn_buf& m, int64_t sb, int64_t sh, int B, int H, int Sq, in
     return buf_ok(m, (size_t)need, GONN_F32);
 }
 
-// The kernels a call runs: an additive mask is read by the fp32-MFMA kernels
-// only, in either mode.
-int fwd_mode(const gonn_attn_fwd_args* a) { return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode; }
+// The kernels a call runs: the forward runs every call in the requested mode
+// (the bf16 kernels have masked variants); the backward reads an additive
+// mask in the fp32-MFMA kernels only, in either mode.
+int fwd_mode(const gonn_attn_fwd_args* a) { return a->mode; }
 int bwd_keys_of(const gonn_attn_bwd_args* a) { return a->Sk > 0 ? a->Sk : a->S; }
 int bwd_mode(const gonn_attn_bwd_args* a) {
     return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode;
@@ -148,6 +149,10 @@ int check_fwd(const gonn_attn_fwd_args* a) {
     const size_t nq = BH * a->Sq * a->D, nk = BH * a->Sk * a->D;
     if (!mask_ok(a->attn_mask, a->mask_stride_b, a->mask_stride_h, a->B, a->H, a->Sq, a->Sk))
         return GONN_E_INVALID;
+    // The bf16 kernels address one slice's mask rows with 32-bit byte offsets.
+    if (a->attn_mask.ptr && fwd_mode(a) == GONN_ATTN_BF16_MFMA &&
+        (double)a->Sq * a->Sk * 4 >= 4294967295.0)
+        return GONN_E_UNSUPPORTED;
     if (fwd_mode(a) == GONN_ATTN_FP32_MFMA) {
         if (!buf_ok(a->q, nq, GONN_F32) || !buf_ok(a->k, nk, GONN_F32) || !buf_ok(a->v, nk, GONN_F32))
             return GONN_E_INVALID;

@@ -89,12 +89,44 @@ GONN_DEV void fwd_empty_rows(const FwdParams& p, int bh, int q0, int rows) {
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgVALU = 0x002, kSgMFMA = 0x008, kSgDSR = 0x100;
 
+// Additive mask (WithAttnMask) for the bf16 kernels: one lane's row of one
+// (b,h) slice, read 4 consecutive keys at a time through a raw buffer
+// resource (a read past the slice returns 0; keys past the key end read
+// whatever follows and are set to -inf by the key-end mask afterwards).
+// Values are added to S^T tiles in log2 units (m log2 e), the units of the
+// bf16 kernels' scores, after the tile is complete and before its masks.
+struct FwdMaskRow {
+    brsrc rs;
+    uint32_t row;  // byte offset of this lane's row
+    GONN_DEV void init(const FwdParams& p, int bh, int qi) {
+        const float* base = p.mask + (size_t)(bh / p.H) * p.mask_sb + (size_t)(bh % p.H) * p.mask_sh;
+        rs = make_rsrc(base, (uint32_t)((size_t)p.Sq * p.Sk * 4));
+        row = (uint32_t)((qi < p.Sq ? qi : p.Sq - 1) * p.Sk) * 4u;
+    }
+    // The 32 mask values of this lane's scores in a 64-key tile kt: register
+    // 4j + e of S^T block mt holds key kt*64 + mt*32 + 8j + 4g + e.
+    GONN_DEV void load(int kt, int g, f32x4* m) const {
+        for (int mt = 0; mt < 2; mt++)
+            for (int j = 0; j < 4; j++) {
+                const uint32_t key0 = (uint32_t)(kt * 64 + mt * 32 + 8 * j + 4 * g);
+                m[mt * 4 + j] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, row + key0 * 4u, 0, 0));
+            }
+    }
+    GONN_DEV static void add(const f32x4* m, f32x16* s) {
+        for (int mt = 0; mt < 2; mt++)
+            for (int j = 0; j < 4; j++)
+                for (int e = 0; e < 4; e++)
+                    s[mt][4 * j + e] = __builtin_fmaf(m[mt * 4 + j][e], kLog2e, s[mt][4 * j + e]);
+    }
+};
+
 
 // Three workgroups per CU (168 VGPRs, a few spilled outside the key loop):
 // measured 7% faster than two on the C2 encoder grid (768 workgroups fit one
 // round of the 256 CUs instead of 1.5).
-template <int D, bool CAUSAL, typename QT>
-__global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
+template <int D, bool CAUSAL, typename QT, bool MASK>
+__global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p) {
     constexpr int BM = 128, BN = 64;
     constexpr int KST = D + 8;   // K tile row stride (bf16)
     constexpr int VST = BN + 8;  // Vt tile row stride (bf16)
@@ -142,6 +174,9 @@ __global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
     int kend = Sk;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
     const int ntiles = (kend + BN - 1) / BN;
+    FwdMaskRow mrow{};
+    f32x4 mreg[8];  // mask values of the S^T tile in flight (MASK only)
+    if constexpr (MASK) mrow.init(p, bh, qi);
 
     const bf16* Kg = (const bf16*)p.k + (size_t)bh * Skp * D;
     const bf16* Vg = (const bf16*)p.v + (size_t)bh * D * Skp;
@@ -235,6 +270,7 @@ __global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
             // clamped: the load is redundant and its buffer is not read again.
             dma_k(kt + 2 < ntiles ? kt + 2 : ntiles - 1, buf);
             dma_v(kt + 1, buf ^ 1);
+            if constexpr (MASK) mrow.load(kt + 1, g, mreg);  // lands with the tiles
         }
         // Lazy rescale (wave-uniform branch, rare after the first tile).
         if (__builtin_amdgcn_ballot_w64(grow)) {
@@ -301,6 +337,10 @@ __global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
         }
         __builtin_amdgcn_s_setprio(0);
         if constexpr (NEXT) {
+            if constexpr (MASK) {
+                dma_wait();
+                FwdMaskRow::add(mreg, nxt);
+            }
             if (needs_mask(kt + 1)) mask(kt + 1, nxt);
             mxc = tile_max(nxt);
             grow = (mxc - m) * c2 > kLazyLog2;
@@ -319,6 +359,10 @@ __global__ __launch_bounds__(256, 3) void fwd_bf16_kernel(FwdParams p) {
     __syncthreads();
     f32x16 s0[2], s1[2];
     qk(0, s0);
+    if constexpr (MASK) {
+        mrow.load(0, g, mreg);
+        FwdMaskRow::add(mreg, s0);
+    }
     if (needs_mask(0)) mask(0, s0);
     mxc = tile_max(s0);
     grow = (mxc - m) * c2 > kLazyLog2;
@@ -399,8 +443,8 @@ constexpr int kFwdStreamPrio = 1;
 // Waves per workgroup of the D = 128 bf16 forward.
 constexpr int kFwdWaves = 4;
 
-template <bool CAUSAL, typename QT>
-__global__ __launch_bounds__(256, 2) void fwd_bf16_d128_kernel(FwdParams p) {
+template <bool CAUSAL, typename QT, bool MASK>
+__global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdParams p) {
     constexpr int NW = kFwdWaves, D = 128, BM = NW * 32, BN = 64, NT = NW * 64;
     constexpr int NKS = D / 16, NDT = D / 32;
     constexpr int KST = D + 8, VST = BN + 8;          // padded row strides (bf16)
@@ -428,6 +472,12 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_d128_kernel(FwdParams p) {
         if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
         ntiles = (kend + BN - 1) / BN;
     }
+    // Additive mask (MASK variant, one workgroup per CU for the registers):
+    // the values of S^T(t+2) are loaded at the start of step t and added when
+    // that tile is complete, at the step's end.
+    FwdMaskRow mrow{};
+    f32x4 mreg[8];
+    if constexpr (MASK) mrow.init(p, bh, qi);
 
     // Q fragment: qf[ks] = Q[qi][16ks + 8g .. +7] * sign(scale) * c2, in bf16.
     bf16x8 qf[NKS];
@@ -566,6 +616,7 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_d128_kernel(FwdParams p) {
         // Diagonal / key-end tiles only (a wave-uniform branch ahead of the
         // step's MFMA stream).
         if (needs_mask(t + 1)) mask(t + 1, sB);
+        if constexpr (MASK) mrow.load(t + 2 < ntiles ? t + 2 : ntiles - 1, g, mreg);
         const uint32_t vb = (uint32_t)(t & (NSLOT - 1)) * VTB;
         const uint32_t kb = (uint32_t)((t + 2) & (NSLOT - 1)) * KTB;
 
@@ -682,6 +733,7 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_d128_kernel(FwdParams p) {
 
         GONN_VMCNT(0);
         __syncthreads();
+        if constexpr (MASK) FwdMaskRow::add(mreg, sA);
         if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
             for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
     };
@@ -701,13 +753,22 @@ __global__ __launch_bounds__(256, 2) void fwd_bf16_d128_kernel(FwdParams p) {
     GONN_VMCNT(0);
     __syncthreads();
     qk_slot(0, s0, f32x16{});
-    // First tile: exact offset (its max; key 0 is never masked, so it is
-    // finite).
+    if constexpr (MASK) {
+        mrow.load(0, g, mreg);
+        FwdMaskRow::add(mreg, s0);
+    }
+    // First tile: exact offset (its max; key 0 is never masked by the
+    // causal or key-end mask, so it is finite unless the additive mask
+    // makes it -inf).
     if (needs_mask(0)) mask(0, s0);
     mc = tile_max(s0);
     nmc = f32x16{} - mc;
     l = p_tile(s0, pp, -mc);
     qk_slot(1, s1, nmc);  // K(1), or for a one-tile block a masked copy of K(0)
+    if constexpr (MASK) {
+        mrow.load(last(1), g, mreg);
+        FwdMaskRow::add(mreg, s1);
+    }
     __syncthreads();      // K(0) read by every wave: its slot takes K(2)
     dma_k(last(2), 0);
     GONN_VMCNT(0);
@@ -889,18 +950,24 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(FwdParams p) {
 // ---------------------------------------------------------------------------
 template <int D, bool C>
 static void launch_bf16_d(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t s) {
-    if (q_bf16)
-        fwd_bf16_kernel<D, C, bf16><<<grid, 256, 0, s>>>(p);
-    else
-        fwd_bf16_kernel<D, C, float><<<grid, 256, 0, s>>>(p);
+    if (p.mask) {
+        if (q_bf16) fwd_bf16_kernel<D, C, bf16, true><<<grid, 256, 0, s>>>(p);
+        else fwd_bf16_kernel<D, C, float, true><<<grid, 256, 0, s>>>(p);
+    } else {
+        if (q_bf16) fwd_bf16_kernel<D, C, bf16, false><<<grid, 256, 0, s>>>(p);
+        else fwd_bf16_kernel<D, C, float, false><<<grid, 256, 0, s>>>(p);
+    }
 }
 
 template <bool C>
 static void launch_bf16_d128(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t s) {
-    if (q_bf16)
-        fwd_bf16_d128_kernel<C, bf16><<<grid, kFwdWaves * 64, 0, s>>>(p);
-    else
-        fwd_bf16_d128_kernel<C, float><<<grid, kFwdWaves * 64, 0, s>>>(p);
+    if (p.mask) {
+        if (q_bf16) fwd_bf16_d128_kernel<C, bf16, true><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        else fwd_bf16_d128_kernel<C, float, true><<<grid, kFwdWaves * 64, 0, s>>>(p);
+    } else {
+        if (q_bf16) fwd_bf16_d128_kernel<C, bf16, false><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        else fwd_bf16_d128_kernel<C, float, false><<<grid, kFwdWaves * 64, 0, s>>>(p);
+    }
 }
 
 hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_bf16,

@@ -97,8 +97,9 @@ typedef struct {
      * score of query i and key j, after the causal mask and before the key
      * padding, as ForwardMasked orders them. Strides (elements, >= 0) of 0
      * broadcast: (Sq,Sk) -> 0, 0; (B,Sq,Sk) -> Sq*Sk, 0; (B*H,Sq,Sk) and
-     * (B,H,Sq,Sk) -> H*Sq*Sk, Sq*Sk. A masked call runs the fp32-MFMA
-     * kernels in either mode and needs GONN_F32 q, k, v. A row whose every
+     * (B,H,Sq,Sk) -> H*Sq*Sk, Sq*Sk. A masked forward runs in the
+     * requested mode (bf16 mode: Sq*Sk*4 bytes must stay below 4 GiB, else
+     * GONN_E_UNSUPPORTED); the fp32 mode needs GONN_F32 q, k, v. A row whose every
      * key carries a -1e30-scale term (the mask's, or the mask's plus the
      * causal one) has no finite LSE in fp32: such rows are outside this
      * library's definition, as fully padded ones are.                      */

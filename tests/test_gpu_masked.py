@@ -218,13 +218,16 @@ def _mask_of(kind, B, H, Sq, Sk, seed):
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
 @pytest.mark.parametrize("kind", ["TqTk", "BTqTk", "BHTqTk3", "BHTqTk4"])
 @pytest.mark.parametrize("causal", [False, True])
-def test_attn_mask_fwd_bwd_matches_oracle(mode, kind, causal):
+@pytest.mark.parametrize("D", [64, 128])
+def test_attn_mask_fwd_bwd_matches_oracle(mode, kind, causal, D):
     """WithAttnMask on the fused path (device API): forward and backward
     against the oracle's reference chain with the same additive mask, key
-    padding and causal mask. A masked call runs the fp32-MFMA kernels in
-    either mode, so both are held to the fp32 bar."""
+    padding and causal mask. The forward runs the stated mode's kernels (the
+    bf16 ones add the mask in log2 units to each completed S^T tile); the
+    backward reads the mask in the fp32-MFMA kernels, from the forward's O
+    and LSE, so everything is held to the stated mode's bar."""
     from gonn_amd import hip
-    B, H, S, D = 2, 2, 100, 64
+    B, H, S = 2, 2, 100
     lens = np.array([100, 71], dtype=np.int32)
     say(f"[masked] attn_mask {kind} mode={mode} causal={causal}")
     m, _ = _mask_of(kind, B, H, S, S, 870)
@@ -240,10 +243,10 @@ def test_attn_mask_fwd_bwd_matches_oracle(mode, kind, causal):
     rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H,
                                           attn_mask=m)
     o = o.reshape(B * H, S, D).cpu().numpy()
-    assert_close(o, ro, "fp32", f"O mask {kind}")
-    assert_close(l.cpu().numpy(), rl, "fp32", f"LSE mask {kind}")
+    assert_close(o, ro, mode, f"O mask {kind}")
+    assert_close(l.cpu().numpy(), rl, mode, f"LSE mask {kind}")
     for got, ref, n in ((dq, rq, "dQ"), (dk, rk, "dK"), (dv, rv, "dV")):
-        assert_close(got.reshape(B * H, S, D).cpu().numpy(), ref, "fp32", f"{n} mask {kind}")
+        assert_close(got.reshape(B * H, S, D).cpu().numpy(), ref, mode, f"{n} mask {kind}")
 
 
 def test_attn_mask_cross_attention_and_nn(mode="fp32"):

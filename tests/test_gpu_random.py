@@ -70,9 +70,9 @@ def test_random_case(i):
     ro, rl = oracle.attn_fwd(q, k, v, sc, c["causal"], kv_len=c["kv"], H=H, attn_mask=m)
     rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, sc, c["causal"], kv_len=c["kv"], H=H,
                                           attn_mask=m)
-    # A masked or cross-attention backward runs the fp32 kernels, but O and
-    # LSE come from the forward of the stated mode; a masked forward is fp32.
-    fmode = "fp32" if m is not None else c["mode"]
+    # Every call runs in the stated mode (a masked backward reads the mask in
+    # the fp32 kernels, from the stated mode's O and LSE): that mode's bar.
+    fmode = c["mode"]
     live = np.ones(B * H, bool) if c["kv"] is None else np.repeat(c["kv"] > 0, H)
     o = o.reshape(B * H, Sq, D).cpu().numpy()
     assert_close(o[live], ro[live], fmode, f"O case {i}")
