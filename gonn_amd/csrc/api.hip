@@ -110,14 +110,11 @@ bool mask_ok(const gonn_buf& m, int64_t sb, int64_t sh, int B, int H, int Sq, in
     return buf_ok(m, (size_t)need, GONN_F32);
 }
 
-// The kernels a call runs: the forward runs every call in the requested mode
-// (the bf16 kernels have masked variants); the backward reads an additive
-// mask in the fp32-MFMA kernels only, in either mode.
+// The kernels a call runs: every call runs in the requested mode (the bf16
+// kernels have masked and cross-attention variants).
 int fwd_mode(const gonn_attn_fwd_args* a) { return a->mode; }
 int bwd_keys_of(const gonn_attn_bwd_args* a) { return a->Sk > 0 ? a->Sk : a->S; }
-int bwd_mode(const gonn_attn_bwd_args* a) {
-    return a->attn_mask.ptr ? GONN_ATTN_FP32_MFMA : a->mode;
-}
+int bwd_mode(const gonn_attn_bwd_args* a) { return a->mode; }
 
 // The bf16-MFMA kernels take Q as bf16(q * (sign(scale) * c2)) with
 // c2 = |scale| log2(e) (log2(e) and sign 0 for a zero scale), so Q K^T is
@@ -224,6 +221,10 @@ int check_bwd(const gonn_attn_bwd_args* a) {
     if (a->kv_len.ptr && !buf_ok(a->kv_len, (size_t)a->B, GONN_I32)) return GONN_E_INVALID;
     if (!mask_ok(a->attn_mask, a->mask_stride_b, a->mask_stride_h, a->B, a->H, a->S, Sk))
         return GONN_E_INVALID;
+    // The bf16 kernels address one slice's mask rows with 32-bit byte offsets.
+    if (a->attn_mask.ptr && bwd_mode(a) == GONN_ATTN_BF16_MFMA &&
+        (double)a->S * Sk * 4 >= 4294967295.0)
+        return GONN_E_UNSUPPORTED;
     return GONN_OK;
 }
 

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 constexpr int kDkdvLookahead = 3;
 constexpr int kDkdvDmaSpan = 40;  // slots over which a step's tile loads are spread (0: all)
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     constexpr int BN = 128;      // keys per workgroup
     constexpr int BM = 64;       // queries per tile
@@ -217,6 +217,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     f32x16 dvacc[NDT], dkacc[NDT];
     for (int t = 0; t < NDT; t++) dvacc[t] = dkacc[t] = f32x16{};
     const float c2 = p.c2b;
+    // Additive mask (MASK variant): this lane's key column; the values of
+    // S(i+1) are loaded at the start of step i and added at its end, when
+    // that tile is complete.
+    MaskCol mcol{};
+    f32x4 mreg[8];
+    if constexpr (MASK) mcol.init(p.mask, p.mask_sb, p.mask_sh, p.H, S, Sk, bh, kj);
     u32x4 pp[4], pd[4];  // P and dS of the tile dV/dK consume next, bf16 pairs per word
 
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -228,6 +234,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         constexpr bool HC = decltype(hc_tag)::value;  // dV/dK of tile i-1
         constexpr bool MK = decltype(mk_tag)::value;  // tile i may need the causal mask
         const int qb = qb0 + i;
+        if constexpr (MASK && HA) mcol.load(qb + 1, g, mreg);
         // Loads for the next step: row tile i+2, transposed tile i, L/D i+1.
         const uint32_t dr = HA && i + 2 < nq, dt = HB;
         const bool dl = HA;
@@ -361,6 +368,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         uops_at(std::integral_constant<int, NM>{});
         GONN_VMCNT(0);
         __syncthreads();
+        if constexpr (MASK && HA) MaskRow::add(mreg, sA);
     };
     using Yes = std::integral_constant<bool, true>;
     using No = std::integral_constant<bool, false>;
@@ -378,6 +386,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             sX[mt] = mfma_bf16(*(const bf16x8*)(cQ + rq0 + (mt * 32 * RST + kk * 16) * 2), kf[kk], sX[mt]);
             dX[mt] = mfma_bf16(*(const bf16x8*)(cdO + rq0 + (mt * 32 * RST + kk * 16) * 2), vf[kk], dX[mt]);
         }
+    if constexpr (MASK) {
+        mcol.load(qb0, g, mreg);
+        MaskRow::add(mreg, sX);
+    }
     __syncthreads();  // row slot 0 is reloaded by step 0
 
     // Steps 0 .. nq: step i has S/dP(i+1) while i+1 < nq, P/dS(i) while
@@ -750,11 +762,28 @@ hipError_t launch_bwd_prep(const float* O, const float* dO, const float* lse, fl
         }                                                                            \
     } while (0)
 
+template <int D, bool C>
+static void launch_dkdv_bf16(const BwdParams& p, dim3 grid, hipStream_t s) {
+    if (p.mask) bwd_dkdv_bf16_kernel<D, C, true><<<grid, 256, 0, s>>>(p);
+    else bwd_dkdv_bf16_kernel<D, C, false><<<grid, 256, 0, s>>>(p);
+}
+
 hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0) return hipErrorInvalidValue;
     const dim3 grid((p.Skp / 128) * p.BH);
-    if (mode == 1) GONN_BWD_LAUNCH(bwd_dkdv_bf16_kernel);
-    else GONN_BWD_LAUNCH(bwd_dkdv_f32_kernel);
+    if (mode == 1) {
+        if (D == 64) {
+            if (causal) launch_dkdv_bf16<64, true>(p, grid, s);
+            else launch_dkdv_bf16<64, false>(p, grid, s);
+        } else if (D == 128) {
+            if (causal) launch_dkdv_bf16<128, true>(p, grid, s);
+            else launch_dkdv_bf16<128, false>(p, grid, s);
+        } else {
+            return hipErrorInvalidValue;
+        }
+        return hipGetLastError();
+    }
+    GONN_BWD_LAUNCH(bwd_dkdv_f32_kernel);
     return hipGetLastError();
 }
 

@@ -53,7 +53,7 @@ constexpr int kDqDmaSpan = 24;     // slots over which the step's tile loads are
 constexpr int kDqLookahead = 3;    // LDS operand lead (deeper measured no faster)
 constexpr bool kDqFragsInAgpr = true;
 
-template <int D, bool CAUSAL>
+template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     constexpr int BM = 128, BN = 64;
     constexpr int KST = D + 8;   // K / V tile row stride (bf16)
@@ -171,6 +171,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
     f32x16 dqacc[NDT];
     for (int t = 0; t < NDT; t++) dqacc[t] = f32x16{};
     const float c2 = p.c2b;
+    // Additive mask (MASK variant): this lane's query row; the values of
+    // S^T(t+1) are loaded at the start of step t and added at its end, when
+    // that tile is complete.
+    MaskRow mrow{};
+    f32x4 mreg[8];
+    if constexpr (MASK) mrow.init(p.mask, p.mask_sb, p.mask_sh, p.H, S, p.Sk, bh, qi);
     u32x4 pd[4];  // dS of the tile dQ consumes next, bf16 pairs per word
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -183,6 +189,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
         const uint32_t dr = HA && t + 2 < nt, dt = HB;
         if constexpr (HB)
             if (needs_mask(t)) mask(t, sB);
+        if constexpr (MASK && HA) mrow.load(t + 1, g, mreg);
         const uint32_t rsl = (uint32_t)((t + 1) & 1) * RTB;  // K, V of tile t+1
         const uint32_t tsl = (uint32_t)((t + 1) & 1) * TTB;  // K^T of tile t-1
 
@@ -278,6 +285,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
         uops_at(std::integral_constant<int, NM>{});
         GONN_VMCNT(0);
         __syncthreads();
+        if constexpr (MASK && HA) MaskRow::add(mreg, sA);
     };
     using Yes = std::integral_constant<bool, true>;
     using No = std::integral_constant<bool, false>;
@@ -297,6 +305,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
             sX[mt] = mfma_bf16(*(const bf16x8*)(cK + rq0 + (mt * 32 * KST + kk * 16) * 2), qf[kk], sX[mt]);
             dX[mt] = mfma_bf16(*(const bf16x8*)(cV + rq0 + (mt * 32 * KST + kk * 16) * 2), df[kk], dX[mt]);
         }
+    if constexpr (MASK) {
+        mrow.load(0, g, mreg);
+        MaskRow::add(mreg, sX);
+    }
     __syncthreads();  // row slot 0 is reloaded by step 0
 
     if (nt == 1) {
@@ -334,12 +346,17 @@ __global__ __launch_bounds__(256, 1) void bwd_dq_bf16_kernel(BwdParams p) {
 hipError_t launch_bwd_dq_bf16(const BwdParams& p, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0) return hipErrorInvalidValue;
     const dim3 grid((p.Sp / 128) * p.BH);
+    const bool m = p.mask != nullptr;
     if (D == 64) {
-        if (causal) bwd_dq_bf16_kernel<64, true><<<grid, 256, 0, s>>>(p);
-        else bwd_dq_bf16_kernel<64, false><<<grid, 256, 0, s>>>(p);
+        if (causal) m ? bwd_dq_bf16_kernel<64, true, true><<<grid, 256, 0, s>>>(p)
+                      : bwd_dq_bf16_kernel<64, true, false><<<grid, 256, 0, s>>>(p);
+        else m ? bwd_dq_bf16_kernel<64, false, true><<<grid, 256, 0, s>>>(p)
+               : bwd_dq_bf16_kernel<64, false, false><<<grid, 256, 0, s>>>(p);
     } else if (D == 128) {
-        if (causal) bwd_dq_bf16_kernel<128, true><<<grid, 256, 0, s>>>(p);
-        else bwd_dq_bf16_kernel<128, false><<<grid, 256, 0, s>>>(p);
+        if (causal) m ? bwd_dq_bf16_kernel<128, true, true><<<grid, 256, 0, s>>>(p)
+                      : bwd_dq_bf16_kernel<128, true, false><<<grid, 256, 0, s>>>(p);
+        else m ? bwd_dq_bf16_kernel<128, false, true><<<grid, 256, 0, s>>>(p)
+               : bwd_dq_bf16_kernel<128, false, false><<<grid, 256, 0, s>>>(p);
     } else {
         return hipErrorInvalidValue;
     }

@@ -89,42 +89,6 @@ GONN_DEV void fwd_empty_rows(const FwdParams& p, int bh, int q0, int rows) {
 // Scheduling-group masks of __builtin_amdgcn_sched_group_barrier.
 constexpr int kSgVALU = 0x002, kSgMFMA = 0x008, kSgDSR = 0x100;
 
-// Additive mask (WithAttnMask) for the bf16 kernels: one lane's row of one
-// (b,h) slice, read 4 consecutive keys at a time through a raw buffer
-// resource (a read past the slice returns 0; keys past the key end read
-// whatever follows and are set to -inf by the key-end mask afterwards).
-// Values are added to S^T tiles in log2 units (m log2 e), the units of the
-// bf16 kernels' scores, after the tile is complete and before its masks.
-struct FwdMaskRow {
-    brsrc rs;
-    uint32_t row;  // byte offset of this lane's row
-    GONN_DEV void init(const FwdParams& p, int bh, int qi) {
-        const float* base = p.mask + (size_t)(bh / p.H) * p.mask_sb + (size_t)(bh % p.H) * p.mask_sh;
-        rs = make_rsrc(base, (uint32_t)((size_t)p.Sq * p.Sk * 4));
-        row = (uint32_t)((qi < p.Sq ? qi : p.Sq - 1) * p.Sk) * 4u;
-    }
-    // The 32 mask values of this lane's scores in a 64-key tile kt: register
-    // 4j + e of S^T block mt holds key kt*64 + mt*32 + 8j + 4g + e.
-    GONN_DEV void load(int kt, int g, f32x4* m) const {
-        for (int mt = 0; mt < 2; mt++)
-            for (int j = 0; j < 4; j++) {
-                const uint32_t key0 = (uint32_t)(kt * 64 + mt * 32 + 8 * j + 4 * g);
-                m[mt * 4 + j] = __builtin_bit_cast(
-                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, row + key0 * 4u, 0, 0));
-            }
-    }
-    GONN_DEV static void add(const f32x4* m, f32x16* s) {
-        for (int mt = 0; mt < 2; mt++)
-            for (int j = 0; j < 4; j++)
-                for (int e = 0; e < 4; e++)
-                    s[mt][4 * j + e] = __builtin_fmaf(m[mt * 4 + j][e], kLog2e, s[mt][4 * j + e]);
-    }
-};
-
-
-// Three workgroups per CU (168 VGPRs, a few spilled outside the key loop):
-// measured 7% faster than two on the C2 encoder grid (768 workgroups fit one
-// round of the 256 CUs instead of 1.5).
 template <int D, bool CAUSAL, typename QT, bool MASK>
 __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p) {
     constexpr int BM = 128, BN = 64;
@@ -174,9 +138,9 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
     int kend = Sk;
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
     const int ntiles = (kend + BN - 1) / BN;
-    FwdMaskRow mrow{};
+    MaskRow mrow{};
     f32x4 mreg[8];  // mask values of the S^T tile in flight (MASK only)
-    if constexpr (MASK) mrow.init(p, bh, qi);
+    if constexpr (MASK) mrow.init(p.mask, p.mask_sb, p.mask_sh, p.H, p.Sq, p.Sk, bh, qi);
 
     const bf16* Kg = (const bf16*)p.k + (size_t)bh * Skp * D;
     const bf16* Vg = (const bf16*)p.v + (size_t)bh * D * Skp;
@@ -339,7 +303,7 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
         if constexpr (NEXT) {
             if constexpr (MASK) {
                 dma_wait();
-                FwdMaskRow::add(mreg, nxt);
+                MaskRow::add(mreg, nxt);
             }
             if (needs_mask(kt + 1)) mask(kt + 1, nxt);
             mxc = tile_max(nxt);
@@ -361,7 +325,7 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
     qk(0, s0);
     if constexpr (MASK) {
         mrow.load(0, g, mreg);
-        FwdMaskRow::add(mreg, s0);
+        MaskRow::add(mreg, s0);
     }
     if (needs_mask(0)) mask(0, s0);
     mxc = tile_max(s0);
@@ -475,9 +439,9 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
     // Additive mask (MASK variant, one workgroup per CU for the registers):
     // the values of S^T(t+2) are loaded at the start of step t and added when
     // that tile is complete, at the step's end.
-    FwdMaskRow mrow{};
+    MaskRow mrow{};
     f32x4 mreg[8];
-    if constexpr (MASK) mrow.init(p, bh, qi);
+    if constexpr (MASK) mrow.init(p.mask, p.mask_sb, p.mask_sh, p.H, p.Sq, p.Sk, bh, qi);
 
     // Q fragment: qf[ks] = Q[qi][16ks + 8g .. +7] * sign(scale) * c2, in bf16.
     bf16x8 qf[NKS];
@@ -733,7 +697,7 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
 
         GONN_VMCNT(0);
         __syncthreads();
-        if constexpr (MASK) FwdMaskRow::add(mreg, sA);
+        if constexpr (MASK) MaskRow::add(mreg, sA);
         if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
             for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
     };
@@ -755,7 +719,7 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
     qk_slot(0, s0, f32x16{});
     if constexpr (MASK) {
         mrow.load(0, g, mreg);
-        FwdMaskRow::add(mreg, s0);
+        MaskRow::add(mreg, s0);
     }
     // First tile: exact offset (its max; key 0 is never masked by the
     // causal or key-end mask, so it is finite unless the additive mask
@@ -767,7 +731,7 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
     qk_slot(1, s1, nmc);  // K(1), or for a one-tile block a masked copy of K(0)
     if constexpr (MASK) {
         mrow.load(last(1), g, mreg);
-        FwdMaskRow::add(mreg, s1);
+        MaskRow::add(mreg, s1);
     }
     __syncthreads();      // K(0) read by every wave: its slot takes K(2)
     dma_k(last(2), 0);

@@ -89,6 +89,66 @@ struct BwdParams {
     long long mask_sb, mask_sh;
 };
 
+// Additive mask (WithAttnMask) in the bf16 kernels whose lanes each own one
+// query and whose S^T tiles hold 64 keys (the forwards and the dQ
+// backward): one lane's row of one (b,h) slice, read 4 consecutive keys at a
+// time through a raw buffer resource (a read past the slice returns 0; keys
+// past the key end read whatever follows and are set to -inf by the key-end
+// mask afterwards). Values are added to completed S^T tiles in log2 units
+// (m log2 e), the units of the bf16 kernels' scores, before their masks.
+struct MaskRow {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t row;  // byte offset of this lane's row
+    GONN_DEV void init(const float* mask, long long sb, long long sh, int H, int Sq, int Sk, int bh,
+                       int qi) {
+        const float* base = mask + (size_t)(bh / H) * sb + (size_t)(bh % H) * sh;
+        rs = make_rsrc(base, (uint32_t)((size_t)Sq * Sk * 4));
+        row = (uint32_t)((qi < Sq ? qi : Sq - 1) * Sk) * 4u;
+    }
+    // The 32 mask values of this lane's scores in 64-key tile kt: register
+    // 4j + e of S^T block mt holds key kt*64 + mt*32 + 8j + 4g + e.
+    GONN_DEV void load(int kt, int g, f32x4* m) const {
+        for (int mt = 0; mt < 2; mt++)
+            for (int j = 0; j < 4; j++) {
+                const uint32_t key0 = (uint32_t)(kt * 64 + mt * 32 + 8 * j + 4 * g);
+                m[mt * 4 + j] = __builtin_bit_cast(
+                    f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, row + key0 * 4u, 0, 0));
+            }
+    }
+    GONN_DEV static void add(const f32x4* m, f32x16* s) {
+        for (int mt = 0; mt < 2; mt++)
+            for (int j = 0; j < 4; j++)
+                for (int e = 0; e < 4; e++)
+                    s[mt][4 * j + e] = __builtin_fmaf(m[mt * 4 + j][e], kLog2e, s[mt][4 * j + e]);
+    }
+};
+
+// The same mask for the bf16 dK/dV backward, whose lanes each own one key and
+// whose S tiles hold 64 queries: register 4j + e of S block mt of query tile
+// qb is query qb*64 + mt*32 + 8j + 4g + e. One 4-byte read per score (a read
+// past the slice returns 0; rows past the last query have P = 0).
+struct MaskCol {
+    __amdgpu_buffer_rsrc_t rs;
+    uint32_t col;  // byte offset of this lane's key in row 0
+    uint32_t rowb;  // bytes per row
+    GONN_DEV void init(const float* mask, long long sb, long long sh, int H, int Sq, int Sk, int bh,
+                       int kj) {
+        const float* base = mask + (size_t)(bh / H) * sb + (size_t)(bh % H) * sh;
+        rs = make_rsrc(base, (uint32_t)((size_t)Sq * Sk * 4));
+        col = (uint32_t)(kj < Sk ? kj : Sk - 1) * 4u;
+        rowb = (uint32_t)Sk * 4u;
+    }
+    GONN_DEV void load(int qb, int g, f32x4* m) const {
+        for (int mt = 0; mt < 2; mt++)
+            for (int j = 0; j < 4; j++)
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t q = (uint32_t)(qb * 64 + mt * 32 + 8 * j + 4 * g + e);
+                    m[mt * 4 + j][e] = __builtin_bit_cast(
+                        float, __builtin_amdgcn_raw_buffer_load_b32(rs, col + q * rowb, 0, 0));
+                }
+    }
+};
+
 // Keys of slice bh that take part in the backward: Sk, or the sequence's
 // kv_len clamped to [0, Sk]. Wave-uniform.
 GONN_DEV int bwd_keys(const BwdParams& p, int bh) {

@@ -126,7 +126,8 @@ typedef struct {
     int deterministic;
     gonn_buf kv_len;
     /* The forward's additive mask (layout as in gonn_attn_fwd_args with
-     * Sq = S); a masked call runs the fp32-MFMA kernels.                   */
+     * Sq = S), read in the requested mode's kernels (bf16 mode: S*Sk*4
+     * bytes must stay below 4 GiB, else GONN_E_UNSUPPORTED).               */
     gonn_buf attn_mask;
     int64_t mask_stride_b, mask_stride_h;
     /* Key rows when they differ from the S query rows (cross-attention with
@@ -360,8 +361,7 @@ int gonn_hip_flash_attn_f64_bwd_ex(const double* Q, const double* K, const doubl
  * fp64 data read as in gonn_attn_fwd_args.attn_mask with element strides
  * mask_sb (sequence) and mask_sh (head) and rows Sk apart; NULL = none. The
  * backward also takes cross-attention (Sq != Sk: K, V, dK, dV are
- * (B*H, Sk, d)). Masked calls run the fp32-MFMA kernels
- * in either mode.                                                          */
+ * (B*H, Sk, d)). Both run in the current mode.                           */
 int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const double* V, double* O,
                                    double* L, int B, int H, int Sq, int Sk, int d, double scale,
                                    int causal, const int* kv_len, const double* mask,

@@ -542,9 +542,8 @@ static void test_attn_mask_gpu() {
     oracle_attn_bwd_autograd_ex(q.Data.data(), k.Data.data(), v.Data.data(), g.Data.data(),
                                 rq.data(), rk.data(), rv.data(), BH, H, S, D, scale, 1,
                                 lens.data(), m.Data.data(), (long)S * S, 0);
-    // Both modes: the forward runs the mode's kernels (the bf16 ones have a
-    // masked variant); the backward reads the mask in the fp32 kernels from
-    // that forward's O and L, so the mode's bar applies throughout.
+    // Both modes: forward and backward run the mode's kernels (the bf16 ones
+    // have masked variants), at the mode's bar.
     for (int mode = 0; mode < 2; mode++) {
         gonn::hip::SetMode(mode);
         const double atol = mode ? 2e-2 : 1e-4, rtol = mode ? 1e-2 : 0.0;

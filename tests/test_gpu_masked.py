@@ -223,9 +223,8 @@ def test_attn_mask_fwd_bwd_matches_oracle(mode, kind, causal, D):
     """WithAttnMask on the fused path (device API): forward and backward
     against the oracle's reference chain with the same additive mask, key
     padding and causal mask. The forward runs the stated mode's kernels (the
-    bf16 ones add the mask in log2 units to each completed S^T tile); the
-    backward reads the mask in the fp32-MFMA kernels, from the forward's O
-    and LSE, so everything is held to the stated mode's bar."""
+    bf16 ones add the mask in log2 units to each completed S^T tile), and so
+    does the backward; everything is held to the stated mode's bar."""
     from gonn_amd import hip
     B, H, S = 2, 2, 100
     lens = np.array([100, 71], dtype=np.int32)

@@ -70,8 +70,7 @@ def test_random_case(i):
     ro, rl = oracle.attn_fwd(q, k, v, sc, c["causal"], kv_len=c["kv"], H=H, attn_mask=m)
     rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, sc, c["causal"], kv_len=c["kv"], H=H,
                                           attn_mask=m)
-    # Every call runs in the stated mode (a masked backward reads the mask in
-    # the fp32 kernels, from the stated mode's O and LSE): that mode's bar.
+    # Every call runs in the stated mode: that mode's bar.
     fmode = c["mode"]
     live = np.ones(B * H, bool) if c["kv"] is None else np.repeat(c["kv"] > 0, H)
     o = o.reshape(B * H, Sq, D).cpu().numpy()
