@@ -211,6 +211,50 @@ def bench_encoder(torch, hip, steps, warmup, mode):
                 pack_ms=per["pack_kv"], launches=nl[kname])
 
 
+def bench_wide_gate(torch, hip, steps, warmup, kind):
+    """The wider fused gate in bf16-MFMA mode, forward + backward:
+    masked: C2's shape (B=8 H=12 S=1024 D=64, non-causal) with an additive
+            (B, S, S) mask (WithAttnMask; N(0,1) bias, a blocked key band of
+            -1e30), forward and backward read it;
+    cross:  decoder cross-attention Forward(x, memory, memory, false),
+            B=4 H=16 Sq=1024 Sk=4096 D=128."""
+    if kind == "masked":
+        B, H, Sq, Sk, D = 8, 12, 1024, 1024, 64
+    else:
+        B, H, Sq, Sk, D = 4, 16, 1024, 4096, 128
+    fwd_flop = 4.0 * B * H * Sq * Sk * D
+    g = torch.Generator(device="cuda")
+    g.manual_seed(6)
+    q, do = (torch.randn((B, H, Sq, D), generator=g, device="cuda") for _ in range(2))
+    k, v = (torch.randn((B, H, Sk, D), generator=g, device="cuda") for _ in range(2))
+    m = None
+    if kind == "masked":
+        m = torch.randn((B, Sq, Sk), generator=g, device="cuda")
+        m[:, :, 100:140] = -1e30
+    o, lse = hip.attn_fwd(q, k, v, mode="bf16", attn_mask=m)
+    grads = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v))
+
+    def run():
+        hip.attn_fwd(q, k, v, mode="bf16", out=o, lse_out=lse, attn_mask=m)
+        hip.attn_bwd(q, k, v, o, lse, do, mode="bf16", out=grads, attn_mask=m)
+    (ms, med), per, nl = _timed(torch, hip, run, steps, warmup,
+                                ("pack_kv", "fwd_bf16", "bwd_prep", "bwd_pack", "bwd_dkdv",
+                                 "bwd_dq"))
+    per = {k: v * nl[k] for k, v in per.items()}
+    tot = 3.5 * fwd_flop
+    return {"metric": "fwd+bwd TFLOP/s", "value": round(tot / (ms * 1e-3) / 1e12, 3),
+            "unit": "TFLOP/s", "ms_per_step": round(ms, 4), "median_ms_per_step": round(med, 4),
+            "config": {"workload": f"{kind}: " + ("C2 shape + (B,S,S) additive mask"
+                                                  if kind == "masked" else
+                                                  "decoder cross-attention, Sq != Sk"),
+                       "B": B, "H": H, "Sq": Sq, "Sk": Sk, "D": D, "causal": False,
+                       "mode": "bf16", "fwd_flop": fwd_flop, "bwd_flop": 2.5 * fwd_flop},
+            "fwd_TFLOPs": round(fwd_flop / (per["fwd_bf16"] * 1e-3) / 1e12, 3),
+            "bwd_TFLOPs": round(2.5 * fwd_flop / ((per["bwd_dkdv"] + per["bwd_dq"]) * 1e-3)
+                                / 1e12, 3),
+            "stage_ms": {k: round(v, 5) for k, v in per.items()}}
+
+
 def bench_mha(torch, hip, steps, warmup):
     """C1: MHA forward, three routes, ms per forward."""
     import numpy as np
@@ -318,6 +362,7 @@ def main():
     ap.add_argument("--no-bwd", action="store_true")
     ap.add_argument("--no-encoder", action="store_true")
     ap.add_argument("--no-mha", action="store_true")
+    ap.add_argument("--no-wide", action="store_true", help="skip the masked / cross legs")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the headline leg (profiling runs of the other legs only)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -357,6 +402,11 @@ def main():
             for mode in ("bf16", "fp32"):
                 log(f"[bench] encoder C2 {mode}")
                 bench_encoder(torch, hip, args.steps, args.warmup, mode)
+        if not args.no_wide:
+            for kind in ("masked", "cross"):
+                log(f"[bench] wide gate {kind}")
+                bench_wide_gate(torch, hip, max(args.steps // 5, 3), max(args.warmup // 2, 1),
+                                kind)
         return
     log("[bench] prefill C3")
     pre = bench_prefill(torch, hip, args.steps, args.warmup)
@@ -445,6 +495,12 @@ def main():
                              "kernel_ms": round(en["kernel_ms"], 5),
                              "launches_per_step": en["launches"],
                              "pack_kv_ms": round(en["pack_ms"], 5)}}
+    if not args.no_wide:
+        line["wide_gate"] = {}
+        for kind in ("masked", "cross"):
+            log(f"[bench] wide gate {kind}")
+            line["wide_gate"][kind] = bench_wide_gate(torch, hip, max(args.steps // 5, 3),
+                                                      max(args.warmup // 2, 1), kind)
     if not args.no_mha:
         log("[bench] MHA C1")
         line["mha"] = bench_mha(torch, hip, args.steps, args.warmup)
