@@ -518,8 +518,12 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
     for (int dt = 0; dt < NDT; dt++) oacc[dt] = f32x16{};
     // mc: this lane's running offset (log2 units); l: row sum relative to it;
     // nmc: -mc in every element, the first S^T accumulator of each tile.
+    // MASK variant: S^T tiles stay absolute (nmc = 0) and P = exp2(s - mc).
+    // An additive mask can make a whole tile huge and negative (-1e30 blocks
+    // keys); an offset taken from such a tile would absorb every later score
+    // if it were folded into the accumulator, so the offset stays out of it.
     float mc = 0.f, l = 0.f, alpha = 1.f;
-    f32x16 nmc;
+    f32x16 nmc = f32x16{};
 
     auto mask = [&](int kt, f32x16* s) {
         const int kb = kt * BN + 4 * g;
@@ -639,8 +643,13 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
             constexpr int k = decltype(U)::value, stage = decltype(S)::value;
             constexpr int mt = k >> 3, r = (k & 7) * 2;
             if constexpr (stage == 0) {
-                ub[k][0] = fast_exp2(sB[mt][r]);
-                ub[k][1] = fast_exp2(sB[mt][r + 1]);
+                if constexpr (MASK) {
+                    ub[k][0] = fast_exp2(sB[mt][r] - mc);
+                    ub[k][1] = fast_exp2(sB[mt][r + 1] - mc);
+                } else {
+                    ub[k][0] = fast_exp2(sB[mt][r]);
+                    ub[k][1] = fast_exp2(sB[mt][r + 1]);
+                }
                 pin(ub[k][0]);
                 pin(ub[k][1]);
             } else {
@@ -684,7 +693,21 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
         // Rare: the tile's P is not bounded by the current offset (or is not
         // finite). Move the offset to the tile max (log2 units), redo the
         // tile, and shift S^T(t+2), accumulated against the old offset.
-        if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound))) {
+        if constexpr (MASK) {
+            // Absolute tiles. Also taken while the row holds nothing (l = 0:
+            // every earlier key blocked or -inf), so the offset follows the
+            // first tile with a finite score instead of staying at a level
+            // below which the tile's P would underflow.
+            if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound) || l == 0.f)) {
+                const float mx = tile_max(sB);
+                const bool empty = pair_sum32(l) == 0.f;
+                const float mn =
+                    mx > -INFINITY && (empty || mx - mc > kLazyLog2) ? mx : mc;
+                alpha = empty ? 0.f : fast_exp2(mc - mn);
+                mc = mn;
+                ts = p_tile(sB, pp, -mc);
+            }
+        } else if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound))) {
             const float mx = tile_max(sB);  // relative to mc
             const float dlt = mx > kLazyLog2 ? -mx : 0.f;
             alpha = fast_exp2(dlt);
@@ -726,7 +749,11 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
     // makes it -inf).
     if (needs_mask(0)) mask(0, s0);
     mc = tile_max(s0);
-    nmc = f32x16{} - mc;
+    if constexpr (MASK) {
+        if (!(mc > -INFINITY)) mc = 0.f;  // a first tile of -inf: no offset yet
+    } else {
+        nmc = f32x16{} - mc;
+    }
     l = p_tile(s0, pp, -mc);
     qk_slot(1, s1, nmc);  // K(1), or for a one-tile block a masked copy of K(0)
     if constexpr (MASK) {
@@ -874,10 +901,13 @@ __global__ __launch_bounds__(256, 2) void fwd_f32_kernel(FwdParams p) {
         mx = pair_max32(mx);
         const float mnew = fmaxf(m, mx);
         const float alpha = (m == -INFINITY) ? 0.f : fast_exp2((m - mnew) * c2);
-        const float mc = mnew * c2;
+        // exp2((s - max) c2): the difference is formed before the scaling, so
+        // scores equal to the max give exactly 1 at any magnitude (an additive
+        // -1e30 mask on every key of a tile gives ties, as in fp64).
+        const float mref = (mnew == -INFINITY) ? 0.f : mnew;
         float rs = 0.f;
         for (int r = 0; r < 16; r++) {
-            const float e = fast_exp2(__builtin_fmaf(sacc[r], c2, -mc));
+            const float e = fast_exp2((sacc[r] - mref) * c2);
             sacc[r] = e;
             rs += e;
         }

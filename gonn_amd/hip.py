@@ -173,8 +173,8 @@ def FlashAttnF64Ex(Q, K, V, B: int, H: int, Sq: int, Sk: int, d: int, scale: flo
     """General fused forward on host fp64 arrays (new; the reference seam is
     Tq == Tk only): Q (B*H,Sq,d), K/V (B*H,Sk,d), optional prefix key padding
     kv_len[B] (keys t >= kv_len[b] masked, ForwardMasked semantics) and
-    additive mask attn_mask (WithAttnMask, one of mask_strides' shapes; runs
-    the fp32-MFMA kernel). Returns O, or (O, L) when lse is set."""
+    additive mask attn_mask (WithAttnMask, one of mask_strides' shapes), in the
+    current mode. Returns O, or (O, L) when lse is set."""
     Q = _f64(Q, B * H * Sq * d, "FlashAttnF64Ex Q")
     K = _f64(K, B * H * Sk * d, "FlashAttnF64Ex K")
     V = _f64(V, B * H * Sk * d, "FlashAttnF64Ex V")
@@ -352,7 +352,7 @@ def attn_fwd(q, k, v, *, causal: bool = False, scale=None, mode="fp32", out=None
     optional int32 device tensor (B,) of valid keys per sequence (prefix key
     padding; a 3-D q counts each slice as its own sequence). attn_mask: an
     optional float32 device tensor, the additive mask of WithAttnMask in one
-    of mask_strides' shapes (runs the fp32-MFMA kernel in either mode).
+    of mask_strides' shapes, added to the scores in the stated mode.
     """
     torch = _torch()
     B, H, Sq, D = _shape4(q, "q")
@@ -388,7 +388,7 @@ def attn_bwd(q, k, v, o, lse, dO, *, causal: bool = False, scale=None, mode="fp3
     additive mask."""
     torch = _torch()
     B, H, S, D = _shape4(q, "q")
-    Sk = k.shape[-2]  # key rows: != S for cross-attention (fp32-MFMA kernels)
+    Sk = k.shape[-2]  # key rows: != S for cross-attention
     if scale is None:
         scale = 1.0 / math.sqrt(D)
     if out is None:

@@ -92,7 +92,7 @@ FwdOut FlashAttnF64ExFwd(const std::vector<double>& Q, const std::vector<double>
                          double scale, bool causal, const std::vector<int>& kvLen = {});
 // New: forward and backward with an additive mask (WithAttnMask) as well:
 // mask is host fp64 read at b*maskSB + h*maskSH + i*Sk + j (rows S apart in
-// the backward); empty = none. They run the fp32-MFMA kernels.
+// the backward); empty = none. They run in the current mode.
 FwdOut FlashAttnF64Masked(const std::vector<double>& Q, const std::vector<double>& K,
                           const std::vector<double>& V, int B, int H, int Sq, int Sk, int d,
                           double scale, bool causal, const std::vector<int>& kvLen,
@@ -311,10 +311,13 @@ class MultiHeadAttention {
     // its CPU path.
     Tensor ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v, bool causal);
     // ForwardMasked (nn/attention.go:305-341) on the fused core with causal,
-    // a (B, Tk) key-padding mask (nonzero = ignore; the padded keys of a row
-    // must be a suffix) and an additive attnMask in any of expandAttnMask's
-    // shapes (runs the fp32-MFMA kernel). Empty tensors mean none. Inference;
-    // the differentiable form is fusedAttnDiff with kvLen and attnMask.
+    // a (B, Tk) key-padding mask (nonzero = ignore; suffix-form masks run as
+    // per-sequence key counts, others are added as -1e30) and an additive
+    // attnMask in any of expandAttnMask's shapes, in the current mode. Empty
+    // tensors mean none. A query row with no unblocked key throws
+    // std::invalid_argument (GoNN gives it a uniform average; the fused core
+    // does not define it). Inference; the differentiable form is
+    // fusedAttnDiff with kvLen and attnMask.
     Tensor ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
                          const Tensor& keyPad, const Tensor& attnMask = Tensor{});
 

@@ -1,6 +1,7 @@
 // nn_attention.cpp -- gonn::nn: the fused attention seam and the fused branch
 // of MultiHeadAttention, mirroring nn/flashattn_cuda.go:13-38 and
 // nn/attention.go:83-180 over gonn::hip.
+#include <algorithm>
 #include <cmath>
 #include <memory>
 #include <string>
@@ -235,33 +236,112 @@ Tensor MultiHeadAttention::fusedGeneral(const Tensor& q, const Tensor& k, const 
     return OutProj.Forward(ctx);
 }
 
-// kvLen[b] of a (B, Tk) key-padding mask (nonzero = ignore the key) whose
-// padded keys are a suffix of each row; empty for no mask.
-static std::vector<int> kv_len_from_mask(const Tensor& keyPad, int B, int Tk) {
-    std::vector<int> kvLen;
-    if (keyPad.Data.empty()) return kvLen;
-    // keyPaddingMaskAdd's shape check, nn/attention.go:262-264
+// A query row whose best in-window additive mask value is at or below this
+// has no unblocked key. GoNN then returns a uniform average (every score is
+// absorbed into the -1e30 constants, nn/attention.go:185-196, :261-272); the
+// fused core does not define such rows and refuses them.
+constexpr double kNoKeyLevel = -1e15;
+static const char* kNoKeyMsg =
+    "nn: a query row has no unblocked key (every key it may attend is padded or masked); "
+    "the fused core does not define such rows";
+
+// keyPaddingMaskAdd's shape check (nn/attention.go:262-264) and the mask's
+// form: kvLen (B entries) when every row's padded keys (nonzero = ignore) are
+// a suffix that leaves a key, else kpAdd, the (B, Tk) 0 / -1e30 values
+// GoNN adds. Both empty for no mask.
+static void key_padding(const Tensor& keyPad, int B, int Tk, std::vector<int>& kvLen,
+                        std::vector<double>& kpAdd) {
+    kvLen.clear();
+    kpAdd.clear();
+    if (keyPad.Data.empty()) return;
     if (keyPad.Shape.size() != 2 || keyPad.Shape[0] != B || keyPad.Shape[1] != Tk)
         throw std::invalid_argument("MultiHeadAttention: key padding mask shape " +
                                     shape_str(keyPad.Shape) + ", want (B, Tk) = (" +
                                     std::to_string(B) + ", " + std::to_string(Tk) + ")");
+    bool suffix = true;
     kvLen.assign(B, Tk);
-    for (int b = 0; b < B; b++) {
+    for (int b = 0; b < B && suffix; b++) {
         const double* row = &keyPad.Data[(size_t)b * Tk];
-        int n = Tk;
-        for (int t = 0; t < Tk; t++)
-            if (row[t] != 0) {
-                n = t;
-                break;
-            }
+        int n = 0;
+        while (n < Tk && row[n] == 0) n++;
         for (int t = n; t < Tk; t++)
-            if (row[t] == 0)
-                throw std::invalid_argument(
-                    "nn: the fused core takes key padding masks whose padded keys are a "
-                    "suffix of the row");
+            if (row[t] == 0) suffix = false;
+        if (n == 0) suffix = false;
         kvLen[b] = n;
     }
+    if (suffix) return;
+    kvLen.clear();
+    kpAdd.assign(keyPad.Data.size(), 0.0);
+    for (size_t i = 0; i < kpAdd.size(); i++)
+        if (keyPad.Data[i] != 0) kpAdd[i] = -1e30;
+}
+
+// kvLen of a suffix-form key-padding mask whose rows keep a key (the
+// resident layer takes no other).
+static std::vector<int> kv_len_from_mask(const Tensor& keyPad, int B, int Tk) {
+    std::vector<int> kvLen;
+    std::vector<double> kpAdd;
+    key_padding(keyPad, B, Tk, kvLen, kpAdd);
+    if (!kpAdd.empty()) {
+        for (int b = 0; b < B; b++) {
+            bool any = false;
+            for (int t = 0; t < Tk; t++) any |= keyPad.Data[(size_t)b * Tk + t] == 0;
+            if (!any) throw std::invalid_argument(kNoKeyMsg);
+        }
+        throw std::invalid_argument(
+            "nn: this path takes key padding masks whose padded keys are a suffix of the row");
+    }
     return kvLen;
+}
+
+// ForwardMasked's masks (nn/attention.go:318-330) in the form the fused core
+// takes them. A suffix-form padding mask becomes kvLen (the kernels skip the
+// padded keys); any other is added as keyPaddingMaskAdd's -1e30. Each row of
+// the additive mask is shifted by its maximum over the keys the row attends
+// (causal window, kvLen): softmax is unchanged, and the fp32 scores the
+// kernels form keep full precision under a large common offset. A row with
+// no unblocked key throws.
+static void core_masks(const Tensor& keyPad, const Tensor& attnMask, int B, int H, int Tq,
+                       int Tk, bool causal, std::vector<int>& kvLen, Tensor& mask) {
+    std::vector<double> kpAdd;
+    key_padding(keyPad, B, Tk, kvLen, kpAdd);
+    mask = Tensor{};
+    if (attnMask.Data.empty() && kpAdd.empty()) return;
+    int Bu = 1, Hu = 1;
+    if (!attnMask.Data.empty()) {
+        const auto st = maskStrides(attnMask.Shape, B, H, Tq, Tk);  // expandAttnMask's check
+        Bu = st[0] ? B : 1;
+        Hu = st[1] ? H : 1;
+    }
+    const size_t QK = (size_t)Tq * Tk;
+    std::vector<double> full((size_t)B * Hu * QK);
+    bool shifted = !kpAdd.empty();
+    for (int b = 0; b < B; b++)
+        for (int h = 0; h < Hu; h++)
+            for (int i = 0; i < Tq; i++) {
+                const double* src =
+                    attnMask.Data.empty()
+                        ? nullptr
+                        : &attnMask.Data[((size_t)(b % Bu) * Hu + h) * QK + (size_t)i * Tk];
+                double* dst = &full[((size_t)b * Hu + h) * QK + (size_t)i * Tk];
+                for (int j = 0; j < Tk; j++)
+                    dst[j] = (src ? src[j] : 0.0) + (kpAdd.empty() ? 0.0 : kpAdd[(size_t)b * Tk + j]);
+                int n = kvLen.empty() ? Tk : kvLen[b];
+                if (causal && i + 1 < n) n = i + 1;
+                double mx = -INFINITY;
+                for (int j = 0; j < n; j++) mx = std::max(mx, dst[j]);
+                if (!(mx > kNoKeyLevel)) throw std::invalid_argument(kNoKeyMsg);
+                if (mx != 0) {
+                    shifted = true;
+                    for (int j = 0; j < Tk; j++) dst[j] -= mx;
+                }
+            }
+    if (!shifted) {
+        mask = attnMask;
+        return;
+    }
+    mask = Hu == 1 ? Tensor::New(std::move(full), {B, Tq, Tk})
+                   : Tensor::New(std::move(full), {B, H, Tq, Tk});
 }
 
 Tensor MultiHeadAttention::ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v,
@@ -269,9 +349,10 @@ Tensor MultiHeadAttention::ForwardMasked(const Tensor& q, const Tensor& k, const
                                          const Tensor& attnMask) {
     checkQKVDims(q, k, v);
     const int B = q.Shape[0], Tk = k.Shape[1];
-    const std::vector<int> kvLen = kv_len_from_mask(keyPad, B, Tk);
-    if (!attnMask.Data.empty()) maskStrides(attnMask.Shape, B, NumHeads, q.Shape[1], Tk);
-    return fusedGeneral(q, k, v, causal, kvLen, attnMask);
+    std::vector<int> kvLen;
+    Tensor mask;
+    core_masks(keyPad, attnMask, B, NumHeads, q.Shape[1], Tk, causal, kvLen, mask);
+    return fusedGeneral(q, k, v, causal, kvLen, mask);
 }
 
 Tensor MultiHeadAttention::ForwardFused(const Tensor& q, const Tensor& k, const Tensor& v,

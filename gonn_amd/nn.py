@@ -111,25 +111,81 @@ class Linear:
         return y.reshape(*x.shape[:-1], out)
 
 
+# A row of the core whose best in-window additive mask value is at or below
+# this has no unblocked key. The reference then returns a uniform average
+# (every score absorbed into the -1e30 constants, nn/attention.go:185-196,
+# :261-272), which the fused core does not define; such calls are refused.
+NO_KEY_LEVEL = -1e15
+_NO_KEY_MSG = ("nn: a query row has no unblocked key (every key it may attend is padded or "
+               "masked); the fused core does not define such rows")
+
+
 def _kv_len_from_mask(key_padding_mask, B: int, Tk: int):
     """kv_len[b] of a (B, Tk) key-padding mask (nonzero = ignore the key,
     keyPaddingMaskAdd, nn/attention.go:261-272) whose padded keys are a
-    suffix of each row; None for no mask."""
+    suffix of each row, leaving at least one key; None for no mask. Any
+    other mask raises ValueError."""
+    kv_len, kp_add = _key_padding(key_padding_mask, B, Tk)
+    if kp_add is not None:
+        if (kp_add != 0).all(axis=1).any():
+            raise ValueError(_NO_KEY_MSG)
+        raise ValueError("nn: this path takes key padding masks whose padded keys are a "
+                         "suffix of the row")
+    return kv_len
+
+
+def _key_padding(key_padding_mask, B: int, Tk: int):
+    """(kv_len, None) for a suffix-form padding mask whose rows keep a key,
+    (None, additive (B, Tk) 0 / -1e30 mask) for any other, (None, None) for
+    none."""
     if key_padding_mask is None:
-        return None
+        return None, None
     m = np.asarray(key_padding_mask)
-    if m.shape != (B, Tk):
+    if m.shape != (B, Tk):  # keyPaddingMaskAdd's shape check, nn/attention.go:262-264
         raise ValueError(f"MultiHeadAttention: key padding mask shape {m.shape}, "
                          f"want (B, Tk) = ({B}, {Tk})")
-    kv_len = np.empty(B, dtype=np.int32)
-    for b in range(B):
-        nz = np.nonzero(m[b])[0]
-        n = int(nz[0]) if nz.size else Tk
-        if np.any(m[b, n:] == 0):
-            raise ValueError("nn: the fused core takes key padding masks whose padded "
-                             "keys are a suffix of the row")
-        kv_len[b] = n
-    return kv_len
+    pad = m != 0
+    n = np.where(pad.any(axis=1), pad.argmax(axis=1), Tk)
+    if all(pad[b, n[b]:].all() for b in range(B)) and n.all():
+        return n.astype(np.int32), None
+    return None, np.where(pad, -1e30, 0.0)
+
+
+def _core_masks(key_padding_mask, attn_mask, B: int, H: int, Tq: int, Tk: int, causal: bool):
+    """ForwardMasked's masks (nn/attention.go:318-330) in the form the fused
+    core takes them: (kv_len or None, additive mask or None).
+
+    A suffix-form padding mask becomes kv_len (the kernels skip the padded
+    keys); any other is added as keyPaddingMaskAdd's 0 / -1e30 values. Each
+    row of the additive mask is shifted by its maximum over the keys the row
+    attends (causal window, kv_len): softmax is unchanged, and the fp32
+    scores the kernels form keep full precision under a large common offset.
+    A row with no unblocked key (that maximum at or below NO_KEY_LEVEL, or no
+    key at all) raises ValueError."""
+    kv_len, kp_add = _key_padding(key_padding_mask, B, Tk)
+    if attn_mask is None and kp_add is None:
+        return kv_len, None
+    if attn_mask is not None:
+        sb, sh = hip.mask_strides(np.shape(attn_mask), B, H, Tq, Tk)  # expandAttnMask's check
+        Hu = H if sh else 1
+        full = np.asarray(attn_mask, dtype=np.float64).reshape(B if sb else 1, Hu, Tq, Tk)
+        full = np.broadcast_to(full, (B, Hu, Tq, Tk))
+    else:
+        full = np.zeros((B, 1, Tq, Tk))
+    if kp_add is not None:
+        full = full + kp_add[:, None, None, :]
+    win = np.ones((B, 1, Tq, Tk), dtype=bool)
+    if kv_len is not None:
+        win &= (np.arange(Tk)[None, :] < kv_len[:, None])[:, None, None, :]
+    if causal:
+        win &= (np.arange(Tk)[None, :] <= np.arange(Tq)[:, None])[None, None]
+    wmax = np.where(win, full, -np.inf).max(axis=-1)
+    if not (wmax > NO_KEY_LEVEL).all():
+        raise ValueError(_NO_KEY_MSG)
+    if kp_add is None and not wmax.any():
+        return kv_len, attn_mask
+    out = np.ascontiguousarray(full - wmax[..., None])
+    return kv_len, (out[:, 0] if out.shape[1] == 1 else out)
 
 
 class MultiHeadAttention:
@@ -216,23 +272,22 @@ class MultiHeadAttention:
     def forward_masked(self, q, k, v, causal: bool = False, key_padding_mask=None,
                        attn_mask=None, dropout: float = 0.0):
         """ForwardMasked (nn/attention.go:305-341) on the fused core: causal,
-        an additive attn_mask in any of expandAttnMask's shapes (runs the
-        fp32-MFMA kernel), and a (B, Tk) key-padding mask (nonzero = ignore
-        the key) whose padded keys form a suffix of each row, which is how
-        padded batches look. Attention dropout (Go's math/rand stream) and a
-        padding mask with holes are not fused (the reference always runs
-        ForwardMasked on its CPU path; this library has none) and raise
-        ValueError."""
+        an additive attn_mask in any of expandAttnMask's shapes, and a (B, Tk)
+        key-padding mask (nonzero = ignore the key). A padding mask whose
+        padded keys form a suffix of each row (how padded batches look) runs
+        as per-sequence key counts; any other is added as -1e30 like
+        keyPaddingMaskAdd. Attention dropout (Go's math/rand stream) is not
+        fused, and a query row with no unblocked key is not defined (the
+        reference always runs ForwardMasked on its CPU path; this library has
+        none): both raise ValueError."""
         if dropout:
             raise ValueError("nn: the fused core takes no attention dropout")
         q, k, v = (np.asarray(x, dtype=np.float64) for x in (q, k, v))
         self._check(q, k, v)
         if not fused_attn_available():
             raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
-        kv_len = _kv_len_from_mask(key_padding_mask, q.shape[0], k.shape[1])
-        if attn_mask is not None:
-            hip.mask_strides(np.shape(attn_mask), q.shape[0], self.NumHeads, q.shape[1],
-                             k.shape[1])  # expandAttnMask's shape check
+        kv_len, attn_mask = _core_masks(key_padding_mask, attn_mask, q.shape[0], self.NumHeads,
+                                        q.shape[1], k.shape[1], causal)
         return self._fused(q, k, v, causal, kv_len, attn_mask)
 
     # ---- device-resident forward (new: weights and intermediates in HBM) ----

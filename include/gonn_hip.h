@@ -82,8 +82,10 @@ typedef struct {
  * prefix key-padding mask, nn/attention.go:261-272), combined with the
  * causal mask as ForwardMasked adds both (nn/attention.go:321-330). Values
  * are clamped to [0, Sk]; a sequence with kv_len 0 gets O = 0 and
- * LSE = -inf (the reference's fully masked row, a uniform average, is
- * outside this library's definition). */
+ * LSE = -inf. That is this ABI's own definition: GoNN gives such a row the
+ * uniform average of the -1e30-absorbed scores, which the kernels do not
+ * compute; the host mirrors (nn.py, nn_attention.cpp) and the Go gate
+ * refuse or decline such calls instead of passing kv_len 0. */
 typedef struct {
     gonn_buf q, k, v, o, lse;
     int B, H, Sq, Sk, D;
@@ -99,10 +101,14 @@ typedef struct {
      * broadcast: (Sq,Sk) -> 0, 0; (B,Sq,Sk) -> Sq*Sk, 0; (B*H,Sq,Sk) and
      * (B,H,Sq,Sk) -> H*Sq*Sk, Sq*Sk. A masked forward runs in the
      * requested mode (bf16 mode: Sq*Sk*4 bytes must stay below 4 GiB, else
-     * GONN_E_UNSUPPORTED); the fp32 mode needs GONN_F32 q, k, v. A row whose every
-     * key carries a -1e30-scale term (the mask's, or the mask's plus the
-     * causal one) has no finite LSE in fp32: such rows are outside this
-     * library's definition, as fully padded ones are.                      */
+     * GONN_E_UNSUPPORTED); the fp32 mode needs GONN_F32 q, k, v. Values
+     * are added in fp32: -1e30 blocks a key (weight exactly 0 when the row
+     * keeps another key), also when it blocks whole leading key tiles. A row
+     * whose every key is blocked (no unblocked key within its causal window
+     * and kv_len) is outside this ABI's definition, as kv_len 0 is; the host
+     * mirrors and the Go gate refuse or decline it. They also shift each
+     * mask row by its maximum, so a large common offset costs no fp32
+     * precision; callers of this entry with such masks should do the same. */
     gonn_buf attn_mask;
     int64_t mask_stride_b, mask_stride_h;
 } gonn_attn_fwd_args;

@@ -235,10 +235,13 @@ def mha_fwd(q, k, v, params, H, causal=False, key_pad=None, attn_mask=None):
     WithKeyPaddingMask (nn/attention.go:305-341) in fp64.
 
     params: dict with Wq,bq,Wk,bk,Wv,bv,Wo,bo (Linear weights are (out,in)).
-    key_pad: optional (B,Tk) array, nonzero = ignore the key; must be a prefix
-    mask (keys t >= len_b), which is the only form the GPU path exposes.
+    key_pad: optional (B,Tk) array, nonzero = ignore the key. A suffix mask
+    (keys t >= len_b padded) is applied as per-batch key counts; any other is
+    added to the scores as keyPaddingMaskAdd's -1e30 (nn/attention.go:
+    261-272), after attn_mask, as ForwardMasked orders them (:321-330).
     """
     B, Tq, E = q.shape
+    Tk = k.shape[1]
     qp = split_heads(linear(q, params["Wq"], params["bq"]), H)
     kp = split_heads(linear(k, params["Wk"], params["bk"]), H)
     vp = split_heads(linear(v, params["Wv"], params["bv"]), H)
@@ -248,9 +251,19 @@ def mha_fwd(q, k, v, params, H, causal=False, key_pad=None, attn_mask=None):
         kv_len = []
         for b in range(B):
             nz = np.nonzero(kp_arr[b])[0]
-            ln = int(nz[0]) if nz.size else kp_arr.shape[1]
-            assert np.all(kp_arr[b, ln:] != 0), "only prefix padding masks are supported"
+            ln = int(nz[0]) if nz.size else Tk
             kv_len.append(ln)
+        if not all(np.all(kp_arr[b, kv_len[b]:] != 0) for b in range(B)):
+            kv_len = None
+            add = np.where(kp_arr != 0, -1e30, 0.0)
+            if attn_mask is None:
+                attn_mask = np.broadcast_to(add[:, None, :], (B, Tq, Tk)).copy()
+            else:
+                _, sb, sh = mask_layout(attn_mask, B, H, Tq, Tk)
+                full = np.asarray(attn_mask, dtype=np.float64).reshape(
+                    B if sb else 1, H if sh else 1, Tq, Tk)
+                attn_mask = np.ascontiguousarray(
+                    np.broadcast_to(full, (B, H, Tq, Tk)) + add[:, None, None, :])
     O, _ = attn_fwd(qp, kp, vp, 1.0 / math.sqrt(E // H), causal, kv_len=kv_len, H=H,
                     attn_mask=attn_mask)
     ctx = merge_heads(O, B, H)

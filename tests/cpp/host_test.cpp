@@ -128,7 +128,8 @@ static Linear make_linear(Rng& r, int out, int in) {
 // Tq and Tk may differ, kvLen (empty = none) is a prefix key-padding mask.
 static std::vector<double> oracle_mha(const MultiHeadAttention& m, const Tensor& q,
                                       const Tensor& k, const Tensor& v, bool causal,
-                                      const std::vector<int>& kvLen = {}) {
+                                      const std::vector<int>& kvLen = {},
+                                      const std::vector<double>& maskBQK = {}) {
     const int B = q.Shape[0], Tq = q.Shape[1], Tk = k.Shape[1], E = m.EmbedDim, H = m.NumHeads,
               D = m.HeadDim;
     auto lin = [](const Linear& l, const Tensor& x) {
@@ -142,9 +143,11 @@ static std::vector<double> oracle_mha(const MultiHeadAttention& m, const Tensor&
     oracle_heads(qp.data(), qh.data(), B, Tq, H, D, 0);
     oracle_heads(kp.data(), kh.data(), B, Tk, H, D, 0);
     oracle_heads(vp.data(), vh.data(), B, Tk, H, D, 0);
-    oracle_attn_fwd(qh.data(), kh.data(), vh.data(), o.data(), nullptr, B * H, H, Tq, Tk, D,
-                    1.0 / std::sqrt((double)D), causal ? 1 : 0,
-                    kvLen.empty() ? nullptr : kvLen.data(), nullptr, 0);
+    // maskBQK: an optional (B, Tq, Tk) additive mask
+    oracle_attn_fwd_ex(qh.data(), kh.data(), vh.data(), o.data(), nullptr, B * H, H, Tq, Tk, D,
+                       1.0 / std::sqrt((double)D), causal ? 1 : 0,
+                       kvLen.empty() ? nullptr : kvLen.data(),
+                       maskBQK.empty() ? nullptr : maskBQK.data(), (long)Tq * Tk, 0, nullptr, 0);
     oracle_heads(o.data(), ctx.data(), B, Tq, H, D, 1);
     Tensor c = Tensor::New(ctx, {B, Tq, E});
     return lin(m.OutProj, c);
@@ -696,10 +699,30 @@ static void test_gpu() {
         const Tensor ym = m.ForwardMasked(q, mem, mem, causal, pad);
         CHECK(close(ym.Data, oracle_mha(m, q, mem, mem, causal, {Tk, 50, 7}), 1e-4, 0.0,
                     ("ForwardMasked" + tag).c_str()), "ForwardMasked%s", tag.c_str());
+        // a padding mask with holes: added as keyPaddingMaskAdd's -1e30
         Tensor holes = pad;
         holes.Data[3] = 1.0;
-        CHECK(throws_invalid([&] { m.ForwardMasked(q, mem, mem, causal, holes); }),
-              "padding mask with holes rejected");
+        // a blocked leading key (under causal, row 0 sees key 0 alone: keep it)
+        holes.Data[(size_t)2 * Tk + (causal ? 1 : 0)] = 1.0;
+        std::vector<double> kpAdd((size_t)B * Tq * Tk, 0.0);
+        for (int b = 0; b < B; b++)
+            for (int i = 0; i < Tq; i++)
+                for (int t = 0; t < Tk; t++)
+                    if (holes.Data[(size_t)b * Tk + t] != 0) kpAdd[((size_t)b * Tq + i) * Tk + t] = -1e30;
+        CHECK(close(m.ForwardMasked(q, mem, mem, causal, holes).Data,
+                    oracle_mha(m, q, mem, mem, causal, {}, kpAdd), 1e-4, 0.0,
+                    ("ForwardMasked holes" + tag).c_str()), "ForwardMasked holes%s", tag.c_str());
+        // a row with no unblocked key is refused
+        Tensor full = pad;
+        for (int t = 0; t < Tk; t++) full.Data[(size_t)1 * Tk + t] = 1.0;
+        CHECK(throws_invalid([&] { m.ForwardMasked(q, mem, mem, causal, full); }),
+              "fully padded row rejected");
+        if (causal) {  // row 0 attends key 0 only: blocking it leaves no key
+            Tensor am = Tensor::Zeros({Tq, Tk});
+            am.Data[0] = -1e30;
+            CHECK(throws_invalid([&] { m.ForwardMasked(q, mem, mem, true, Tensor{}, am); }),
+                  "causal row with its window blocked rejected");
+        }
     }
     // Incremental decoding: ForwardIncremental over a KV cache in two chunks
     // equals the causal rows of the oracle's MHA over the whole sequence (the

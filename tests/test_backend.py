@@ -196,21 +196,82 @@ def test_mask_strides_follow_expand_attn_mask():
 
 
 def test_key_padding_mask_to_kv_len():
-    # keyPaddingMaskAdd (nn/attention.go:261-272): nonzero = ignore; the fused
-    # path takes masks whose padded keys are a suffix of each row.
+    # keyPaddingMaskAdd (nn/attention.go:261-272): nonzero = ignore; suffix
+    # masks that leave a key become per-sequence key counts.
     from gonn_amd import nn
     m = np.zeros((4, 6))
     m[1, 4:] = 1
-    m[2, :] = 1          # every key padded: kv_len 0
     m[3, 5] = 2.5        # any nonzero value pads
-    assert list(nn._kv_len_from_mask(m, 4, 6)) == [6, 4, 0, 5]
+    assert list(nn._kv_len_from_mask(m, 4, 6)) == [6, 4, 6, 5]
     assert nn._kv_len_from_mask(None, 4, 6) is None
     holes = m.copy()
     holes[0, 2] = 1      # a padded key before valid ones
     with pytest.raises(ValueError, match="suffix"):
         nn._kv_len_from_mask(holes, 4, 6)
+    full = m.copy()
+    full[2, :] = 1       # every key padded: GoNN's uniform average, not defined here
+    with pytest.raises(ValueError, match="no unblocked key"):
+        nn._kv_len_from_mask(full, 4, 6)
     with pytest.raises(ValueError, match="key padding mask shape"):
         nn._kv_len_from_mask(np.zeros((4, 5)), 4, 6)
+
+
+def test_core_masks_forms():
+    """ForwardMasked's masks as the fused core takes them (nn._core_masks):
+    suffix padding -> kv_len; holes -> keyPaddingMaskAdd's -1e30 added to the
+    additive mask; rows shifted by their in-window maximum; rows with no
+    unblocked key refused. Checked against a direct restatement on small
+    cases, and by softmax invariance: the shifted mask gives the same
+    probabilities as GoNN's scores + mask in fp64."""
+    from gonn_amd import nn
+    B, H, Tq, Tk = 2, 3, 5, 7
+    r = np.random.default_rng(3)
+    pad = np.zeros((B, Tk))
+    pad[1, 5:] = 1
+    kv, am = nn._core_masks(pad, None, B, H, Tq, Tk, False)
+    assert list(kv) == [7, 5] and am is None
+    # a zero-max mask passes through unchanged (no copy)
+    z = np.zeros((Tq, Tk))
+    z[:, 3] = -1e30
+    kv, am = nn._core_masks(None, z, B, H, Tq, Tk, False)
+    assert kv is None and am is z
+    # holes + a (B*H, Tq, Tk) mask with a large common offset, causal
+    holes = pad.copy()
+    holes[0, 2] = 1
+    um = r.standard_normal((B * H, Tq, Tk)) - 1e4
+    scores = r.standard_normal((B, H, Tq, Tk))
+    kv, am = nn._core_masks(holes, um, B, H, Tq, Tk, True)
+    assert kv is None and am.shape == (B, H, Tq, Tk)
+    win = np.arange(Tk)[None, :] <= np.arange(Tq)[:, None]
+
+    def softmax(x):
+        x = np.where(win, x, -np.inf)
+        e = np.exp(x - x.max(-1, keepdims=True))
+        return e / e.sum(-1, keepdims=True)
+    ref = softmax(scores + um.reshape(B, H, Tq, Tk) + np.where(holes != 0, -1e30, 0.0)[:, None, None])
+    # (GoNN forms scores - 1e4 in fp64: its own rounding is ~1e-12 of the exponent)
+    np.testing.assert_allclose(softmax(scores + am), ref, rtol=1e-9, atol=1e-300)
+    inwin = np.where(win, am, -np.inf).max(-1)
+    assert np.all(inwin == 0.0)
+    # suffix padding + a (Tq, Tk) mask: the window max depends on kv_len
+    tm = r.standard_normal((Tq, Tk)) * 3
+    kv, am = nn._core_masks(pad, tm, B, H, Tq, Tk, False)
+    assert list(kv) == [7, 5] and am.shape == (B, Tq, Tk)
+    np.testing.assert_array_equal(am[0], tm - tm.max(-1, keepdims=True))
+    np.testing.assert_array_equal(am[1], tm - tm[:, :5].max(-1, keepdims=True))
+    # rows with no unblocked key: a fully padded sequence, and a causal row 0
+    # whose only key (key 0) the mask blocks
+    full = pad.copy()
+    full[0] = 1
+    with pytest.raises(ValueError, match="no unblocked key"):
+        nn._core_masks(full, None, B, H, Tq, Tk, False)
+    b0 = np.zeros((Tq, Tk))
+    b0[0, 0] = -1e30
+    nn._core_masks(None, b0, B, H, Tq, Tk, False)  # non-causal: keys 1.. remain
+    with pytest.raises(ValueError, match="no unblocked key"):
+        nn._core_masks(None, b0, B, H, Tq, Tk, True)
+    with pytest.raises(ValueError, match="attn mask shape"):
+        nn._core_masks(None, np.zeros((Tq, Tk + 1)), B, H, Tq, Tk, False)
 
 
 def test_resident_layer_and_cache_need_a_device():

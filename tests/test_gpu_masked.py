@@ -108,10 +108,19 @@ def test_mha_forward_masked_and_cross_attention(causal):
     got = mha.forward_masked(q, mem, mem, causal=causal, key_padding_mask=pad)
     ref = oracle.mha_fwd(q, mem, mem, p, H, causal=causal, key_pad=pad)
     assert_close(got, ref, "fp32", f"cross-attention + padding causal={causal}")
+    # a padding mask with holes (added as -1e30), with a padded leading key
+    # on a row that keeps later keys
     holes = pad.copy()
     holes[0, 3] = 1
-    with pytest.raises(ValueError):
-        mha.forward_masked(x, x, x, key_padding_mask=holes)
+    holes[2, 1 if causal else 0] = 1
+    got = mha.forward_masked(x, x, x, causal=causal, key_padding_mask=holes)
+    ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, key_pad=holes)
+    assert_close(got, ref, "fp32", f"forward_masked holes causal={causal}")
+    # a sequence with every key padded: GoNN's uniform average is not defined here
+    full = pad.copy()
+    full[1] = 1
+    with pytest.raises(ValueError, match="no unblocked key"):
+        mha.forward_masked(x, x, x, causal=causal, key_padding_mask=full)
     with pytest.raises(ValueError):
         mha.forward_masked(x, x, x, dropout=0.1)
     with pytest.raises(ValueError):
@@ -246,6 +255,68 @@ def test_attn_mask_fwd_bwd_matches_oracle(mode, kind, causal, D):
     assert_close(l.cpu().numpy(), rl, mode, f"LSE mask {kind}")
     for got, ref, n in ((dq, rq, "dQ"), (dk, rk, "dK"), (dv, rv, "dV")):
         assert_close(got.reshape(B * H, S, D).cpu().numpy(), ref, mode, f"{n} mask {kind}")
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("nblk", [64, 200])
+def test_attn_mask_blocked_key_prefix(mode, causal, D, nblk):
+    """An additive mask that blocks (-1e30) whole leading key tiles, as left
+    padding does: the kernels' softmax offset must not come from those
+    tiles (a -1e30 level folded into the scores would absorb every later
+    score). Under causal, rows that see only blocked keys are left unblocked
+    (such a row has no unblocked key; the mirrors refuse it). Forward and
+    backward against the oracle at the mode's bar."""
+    from gonn_amd import hip
+    B, H, Sq, Sk = 2, 2, 96 if not causal else 300, 300
+    say(f"[masked] blocked prefix nblk={nblk} mode={mode} D={D} causal={causal}")
+    rng = np.random.default_rng(1300 + nblk + D)
+    m = rng.standard_normal((B, Sq, Sk)) * 0.5
+    rows = np.arange(Sq) >= (nblk if causal else 0)
+    m[:, rows, :nblk] = -1e30
+    q, g = (randn((B * H, Sq, D), 1310 + i) for i in range(2))
+    k, v = (randn((B * H, Sk, D), 1320 + i) for i in range(2))
+    dev = [torch.from_numpy(x).cuda().reshape(B, H, -1, D) for x in (q, k, v, g)]
+    md = torch.from_numpy(m.astype(np.float32)).cuda()
+    o, l = hip.attn_fwd(*dev[:3], causal=causal, mode=mode, attn_mask=md)
+    dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=causal, mode=mode, attn_mask=md)
+    torch.cuda.synchronize()
+    ro, rl = oracle.attn_fwd(q, k, v, 1 / math.sqrt(D), causal, H=H, attn_mask=m)
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, H=H, attn_mask=m)
+    assert_close(o.reshape(B * H, Sq, D).cpu().numpy(), ro, mode, "O blocked prefix")
+    assert_close(l.cpu().numpy(), rl, mode, "LSE blocked prefix")
+    assert_close(dq.reshape(B * H, Sq, D).cpu().numpy(), rq, mode, "dQ blocked prefix")
+    assert_close(dk.reshape(B * H, Sk, D).cpu().numpy(), rk, mode, "dK blocked prefix")
+    assert_close(dv.reshape(B * H, Sk, D).cpu().numpy(), rv, mode, "dV blocked prefix")
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_forward_masked_large_offset_mask(mode):
+    """forward_masked with an additive mask carrying a large common offset
+    per row (-1e4 + N(0,1)) and a blocked leading key band: the mirror shifts
+    each row by its in-window maximum, so the fp32 scores keep their
+    precision; against the oracle (fp64, GoNN's order of additions) at the
+    mode's bar."""
+    from gonn_amd import hip, nn
+    E, H, B, T = 256, 4, 2, 150
+    p = _params(E, 1400)
+    mha = nn.MultiHeadAttention(E, H, p["Wq"], p["bq"], p["Wk"], p["bk"], p["Wv"], p["bv"],
+                                p["Wo"], p["bo"])
+    x = randn((B, T, E), 1401).astype(np.float64)
+    rng = np.random.default_rng(1402)
+    m = rng.standard_normal((B, T, T)) - 1e4
+    m[:, 70:, :66] = -1e30
+    prev = hip.AttnMode()
+    hip.SetAttnMode(mode)
+    try:
+        for causal in (False, True):
+            say(f"[masked] large-offset mask mode={mode} causal={causal}")
+            got = mha.forward_masked(x, x, x, causal=causal, attn_mask=m)
+            ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, attn_mask=m)
+            assert_close(got, ref, mode, f"large-offset mask causal={causal}")
+    finally:
+        hip.SetAttnMode(prev)
 
 
 def test_attn_mask_cross_attention_and_nn(mode="fp32"):
