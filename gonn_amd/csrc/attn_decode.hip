@@ -8,9 +8,12 @@
 //
 // One query row per (b,h) makes this a pair of GEMVs; the bound is HBM
 // bandwidth over the valid K/V rows, so the kernel is built for streaming:
-//  * split kernel: grid (nsplit, B*H); workgroup s of (b,h) owns keys
-//    [s*split_keys, min((s+1)*split_keys, len)) and exits at once when that
-//    range is empty, so only valid rows are ever fetched;
+//  * split kernel: a (b,h) of len keys takes ns = ceil(len / split_keys)
+//    workgroups, which split [0, len) evenly (each gets floor or ceil of
+//    len / ns keys, never a sliver), so only valid rows are ever fetched;
+//    the 1-D grid is split-major (every sequence's split 0, then split 1,
+//    ...), so the workgroups that exit at once (s >= ns) gather at the end
+//    of the grid instead of sitting between the working ones;
 //  * a row of 16 lanes covers one key (D=128: 8 bf16 = 16 bytes per lane), so
 //    one wave instruction reads 4 whole consecutive rows (1 KB contiguous);
 //    each lane keeps 8 keys' K and V loads in flight per iteration; the cache
@@ -38,12 +41,15 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int rr = lane >> 4, dc = lane & 15, d0 = dc * EPL;
-    const int s = blockIdx.x, bh = blockIdx.y, b = bh / p.H;
+    const int BH = p.B * p.H;
+    const int s = blockIdx.x / BH, bh = blockIdx.x - s * BH, b = bh / p.H;
     int len = p.kv_len[b];
     len = len < 0 ? 0 : (len > p.Lmax ? p.Lmax : len);
-    const int k0 = s * p.split_keys;
-    if (k0 >= len) return;  // uniform for the workgroup
-    const int k1 = (k0 + p.split_keys < len) ? k0 + p.split_keys : len;
+    const int ns = (len + p.split_keys - 1) / p.split_keys;
+    if (s >= ns) return;  // uniform for the workgroup
+    // [k0, k1): split s of ns even parts of [0, len), non-empty as ns <= len
+    const int k0 = (int)((long long)s * len / ns);
+    const int k1 = (int)((long long)(s + 1) * len / ns);
 
     float q[EPL];
     {
@@ -130,21 +136,50 @@ __global__ __launch_bounds__(256) void decode_split_kernel(DecodeParams p) {
     }
 }
 
+// One workgroup of D threads per (b,h). The partial (m, l) pairs are read by
+// all threads at once into LDS (one memory round trip), their max and
+// weights formed there, and each thread then sums its column of the partial
+// outputs with independent loads, CH splits at a time.
 template <int D>
 __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeParams p) {
+    constexpr int CH = D;  // splits per LDS chunk
+    __shared__ float sm[CH], sw[CH], sl[CH];
     const int bh = blockIdx.x, b = bh / p.H, tid = threadIdx.x;
     int len = p.kv_len[b];
     len = len < 0 ? 0 : (len > p.Lmax ? p.Lmax : len);
     const int ns = (len + p.split_keys - 1) / p.split_keys;
     const float* ml = p.part_ml + (size_t)bh * p.nsplit * 2;
     const float* po = p.part_o + (size_t)bh * p.nsplit * D;
-    float M = -INFINITY;
-    for (int s = 0; s < ns; s++) M = fmaxf(M, ml[2 * s]);
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < ns; s++) {
-        const float w = fast_exp2(ml[2 * s] - M);
-        L = __builtin_fmaf(w, ml[2 * s + 1], L);
-        O = __builtin_fmaf(w, po[(size_t)s * D + tid], O);
+    float M = -INFINITY, L = 0.f, O = 0.f;
+    for (int c0 = 0; c0 < ns; c0 += CH) {
+        const int nc = ns - c0 < CH ? ns - c0 : CH;
+        __syncthreads();
+        if (tid < nc) {
+            sm[tid] = ml[2 * (c0 + tid)];
+            sl[tid] = ml[2 * (c0 + tid) + 1];
+        }
+        __syncthreads();
+        float mc = M;
+        for (int i = 0; i < nc; i++) mc = fmaxf(mc, sm[i]);
+        if (tid < nc) sw[tid] = fast_exp2(sm[tid] - mc);
+        const float a = (M == -INFINITY) ? 0.f : fast_exp2(M - mc);
+        L *= a;
+        O *= a;
+        M = mc;
+        __syncthreads();
+        int i = 0;
+        for (; i + 4 <= nc; i += 4) {
+            float v[4];
+            for (int u = 0; u < 4; u++) v[u] = po[(size_t)(c0 + i + u) * D + tid];
+            for (int u = 0; u < 4; u++) {
+                L = __builtin_fmaf(sw[i + u], sl[i + u], L);
+                O = __builtin_fmaf(sw[i + u], v[u], O);
+            }
+        }
+        for (; i < nc; i++) {
+            L = __builtin_fmaf(sw[i], sl[i], L);
+            O = __builtin_fmaf(sw[i], po[(size_t)(c0 + i) * D + tid], O);
+        }
     }
     p.o[(size_t)bh * D + tid] = ns > 0 ? O / L : 0.f;
 }
@@ -201,7 +236,7 @@ hipError_t launch_kv_append(const void* ks, const void* vs, int src_bf16, void* 
 }
 
 hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStream_t s) {
-    dim3 grid(p.nsplit, p.B * p.H);
+    const unsigned grid = (unsigned)p.nsplit * (unsigned)(p.B * p.H);
     if (D == 128) {
         if (q_bf16) decode_split_kernel<128, bf16><<<grid, 256, 0, s>>>(p);
         else decode_split_kernel<128, float><<<grid, 256, 0, s>>>(p);
