@@ -221,6 +221,12 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
     };
     float mxc;  // row max of the tile the next step consumes
     bool grow;  // that tile moves the reference max
+    // Without the additive mask, S^T tiles are accumulated relative to m (the
+    // accumulator starts at -m), so P = exp2(s) needs no per-score subtract;
+    // a tile that moves m is shifted once, in the rare rescale branch. The
+    // masked variant keeps absolute tiles (a -1e30 level in m would absorb
+    // the scores accumulated onto it) and forms exp2(s - m).
+    constexpr bool REL = !MASK;
 
     // One tile step: softmax + PV of `cur` (tile kt, already masked, its row
     // max in mxc); with NEXT, also S^T(kt+1) into `nxt`, its mask and row max,
@@ -237,7 +243,16 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
             if constexpr (MASK) mrow.load(kt + 1, g, mreg);  // lands with the tiles
         }
         // Lazy rescale (wave-uniform branch, rare after the first tile).
-        if (__builtin_amdgcn_ballot_w64(grow)) {
+        if constexpr (REL) {
+            if (__builtin_amdgcn_ballot_w64(grow)) {
+                const float d = grow ? mxc : 0.f;  // the tile max, relative to m
+                const float alpha = fast_exp2(-d);
+                l *= alpha;
+                for (int t = 0; t < NDT; t++) oacc[t] *= alpha;
+                m += d;
+                for (int mt = 0; mt < 2; mt++) cur[mt] -= d;
+            }
+        } else if (__builtin_amdgcn_ballot_w64(grow)) {
             const float mnew = grow ? mxc : m;
             const float alpha = (m == -INFINITY) ? 0.f : fast_exp2((m - mnew) * c2);
             l *= alpha;
@@ -254,20 +269,27 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
         __builtin_amdgcn_s_setprio(1);
         float part[4] = {0.f, 0.f, 0.f, 0.f};
         bf16x8 pb[4];
+        // P of PV k-step ks as 8 bf16, and its row sum over the rounded
+        // values (v_dot2 of bf16 pairs with 1: the sum the PV product sees).
         auto make_p = [&](int ks) {
             const int mt = ks >> 1, b0 = (ks & 1) * 8;
             float e[8];
-            for (int i = 0; i < 8; i++) {
-                e[i] = fast_exp2(__builtin_fmaf(cur[mt][b0 + i], c2, -mc));
-                part[i & 3] += e[i];
-            }
+            for (int i = 0; i < 8; i++)
+                e[i] = REL ? fast_exp2(cur[mt][b0 + i])
+                           : fast_exp2(__builtin_fmaf(cur[mt][b0 + i], c2, -mc));
             pb[ks] = pack8(e[0], e[1], e[2], e[3], e[4], e[5], e[6], e[7]);
+            typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+            const bf16x2 one2 = {(__bf16)1.0f, (__bf16)1.0f};
+            for (int i = 0; i < 4; i++) {
+                const bf16x2 pr = {pb[ks][2 * i], pb[ks][2 * i + 1]};
+                part[i] = __builtin_amdgcn_fdot2_f32_bf16(pr, one2, part[i], false);
+            }
         };
         const bf16* sV = sVb + buf * VTILE + ln * VST + g * 8;
         const bf16* sK = sKb + (buf ^ 1) * KTILE + ln * KST + g * 8;
         if constexpr (NEXT) {
-            nxt[0] = f32x16{};
-            nxt[1] = f32x16{};
+            nxt[0] = f32x16{} - (REL ? m : 0.f);
+            nxt[1] = nxt[0];
         }
         constexpr int SKS = NKS / 4;  // S^T k-steps per PV k-step
         make_p(0);
@@ -307,7 +329,7 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
             }
             if (needs_mask(kt + 1)) mask(kt + 1, nxt);
             mxc = tile_max(nxt);
-            grow = (mxc - m) * c2 > kLazyLog2;
+            grow = REL ? mxc > kLazyLog2 : (mxc - m) * c2 > kLazyLog2;
         }
         dma_wait();
         __syncthreads();
@@ -329,7 +351,14 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
     }
     if (needs_mask(0)) mask(0, s0);
     mxc = tile_max(s0);
-    grow = (mxc - m) * c2 > kLazyLog2;
+    if constexpr (REL) {
+        // The first tile's max is the offset (key 0 is never masked here).
+        m = mxc;
+        for (int mt = 0; mt < 2; mt++) s0[mt] -= m;
+        grow = false;
+    } else {
+        grow = (mxc - m) * c2 > kLazyLog2;
+    }
     // Step 0 streams K(2) into the buffer qk(0) just read: every wave must be
     // done reading it first.
     __syncthreads();
@@ -404,12 +433,19 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
 constexpr float kSumBound = 16384.f;  // 2^14: row-sum bound of one 64-key tile
 // Wave issue priority (s_setprio) during a step's MFMA stream.
 constexpr int kFwdStreamPrio = 1;
-// Waves per workgroup of the D = 128 bf16 forward.
+// Waves per workgroup of the pipelined bf16 forward.
 constexpr int kFwdWaves = 4;
+// Resident workgroups per CU the pipelined forward is compiled for (its
+// register budget): two, or one with the additive mask's registers. The
+// kernel is written for any D that is a multiple of 32 and is instantiated
+// for D = 128. At D = 64 it measured slower on C2 than the two-stage kernel
+// (43 against 41 us): its two workgroups per CU run C2's 768 q-blocks in
+// 1.5 rounds, where the two-stage kernel fits three per CU, one round.
+constexpr int fwd_pipe_wgs(int D, bool mask) { return mask ? 1 : 2; }
 
-template <bool CAUSAL, typename QT, bool MASK>
-__global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdParams p) {
-    constexpr int NW = kFwdWaves, D = 128, BM = NW * 32, BN = 64, NT = NW * 64;
+template <int D, bool CAUSAL, typename QT, bool MASK>
+__global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kernel(FwdParams p) {
+    constexpr int NW = kFwdWaves, BM = NW * 32, BN = 64, NT = NW * 64;
     constexpr int NKS = D / 16, NDT = D / 32;
     constexpr int KST = D + 8, VST = BN + 8;          // padded row strides (bf16)
     constexpr uint32_t KTB = BN * KST * 2, VTB = D * VST * 2;  // slot bytes
@@ -588,7 +624,8 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
         const uint32_t vb = (uint32_t)(t & (NSLOT - 1)) * VTB;
         const uint32_t kb = (uint32_t)((t + 2) & (NSLOT - 1)) * KTB;
 
-        constexpr int GW = 8;              // MFMAs per PV k-step group
+        constexpr int SKS = NKS / 4;       // S^T k-steps per PV k-step
+        constexpr int GW = NDT + 2 * SKS;  // MFMAs per PV k-step group
         constexpr int NM = 4 * GW;         // MFMAs in the step
         constexpr int NU = 16;             // softmax micro-ops (one score pair each)
         constexpr int LA = 3;              // LDS read lead (MFMAs)
@@ -598,15 +635,15 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
         bf16x8 opr[4];
         auto fetch = [&](auto E) {
             constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
-            if constexpr (w < 4) opr[e & 3] = vfrag(vb, j, w);
-            else opr[e & 3] = kfrag(kb, 2 * j + ((w - 4) >> 1), (w - 4) & 1);
+            if constexpr (w < NDT) opr[e & 3] = vfrag(vb, j, w);
+            else opr[e & 3] = kfrag(kb, SKS * j + ((w - NDT) >> 1), (w - NDT) & 1);
         };
         auto issue = [&](auto E) {
             constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
-            if constexpr (w < 4) {
+            if constexpr (w < NDT) {
                 oacc[w] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pp[j]), oacc[w]);
             } else {
-                constexpr int kk = 2 * j + ((w - 4) >> 1), mt = (w - 4) & 1;
+                constexpr int kk = SKS * j + ((w - NDT) >> 1), mt = (w - NDT) & 1;
                 sA[mt] = mfma_bf16(opr[e & 3], qf[kk], kk == 0 ? nmc : sA[mt]);
             }
         };
@@ -637,7 +674,7 @@ __global__ __launch_bounds__(256, MASK ? 1 : 2) void fwd_bf16_d128_kernel(FwdPar
         // (1) bf16 pack into pp and row sum. Stage 1 lands in slot uslot(k),
         // after the PV MFMAs of k-step j read pp[j]; micro-ops past the
         // stream's end run after it.
-        auto uslot = [](int k) { return (k >> 2) * GW + 4 + (k & 3); };
+        auto uslot = [](int k) { return (k >> 2) * GW + NDT + (k & 3); };
         float ub[16][2];
         auto uop = [&](auto U, auto S) {
             constexpr int k = decltype(U)::value, stage = decltype(S)::value;
@@ -953,14 +990,14 @@ static void launch_bf16_d(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t
     }
 }
 
-template <bool C>
-static void launch_bf16_d128(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t s) {
+template <int D, bool C>
+static void launch_bf16_pipe(const FwdParams& p, int q_bf16, dim3 grid, hipStream_t s) {
     if (p.mask) {
-        if (q_bf16) fwd_bf16_d128_kernel<C, bf16, true><<<grid, kFwdWaves * 64, 0, s>>>(p);
-        else fwd_bf16_d128_kernel<C, float, true><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        if (q_bf16) fwd_bf16_pipe_kernel<D, C, bf16, true><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        else fwd_bf16_pipe_kernel<D, C, float, true><<<grid, kFwdWaves * 64, 0, s>>>(p);
     } else {
-        if (q_bf16) fwd_bf16_d128_kernel<C, bf16, false><<<grid, kFwdWaves * 64, 0, s>>>(p);
-        else fwd_bf16_d128_kernel<C, float, false><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        if (q_bf16) fwd_bf16_pipe_kernel<D, C, bf16, false><<<grid, kFwdWaves * 64, 0, s>>>(p);
+        else fwd_bf16_pipe_kernel<D, C, float, false><<<grid, kFwdWaves * 64, 0, s>>>(p);
     }
 }
 
@@ -992,8 +1029,8 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
             if (causal) launch_bf16_d<64, true>(p, q_bf16, grid, s);
             else launch_bf16_d<64, false>(p, q_bf16, grid, s);
         } else if (D == 128) {
-            if (causal) launch_bf16_d128<true>(p, q_bf16, grid, s);
-            else launch_bf16_d128<false>(p, q_bf16, grid, s);
+            if (causal) launch_bf16_pipe<128, true>(p, q_bf16, grid, s);
+            else launch_bf16_pipe<128, false>(p, q_bf16, grid, s);
         } else {
             return hipErrorInvalidValue;
         }
