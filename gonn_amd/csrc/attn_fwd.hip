@@ -417,8 +417,11 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
 //
 // LDS: two-slot rings of K tiles (64 keys x D) and Vt tiles (D x 64 keys)
 // filled straight from HBM/L2 by buffer_load ... lds, one barrier per step;
-// step t loads K(t+3) and V(t+1), one step ahead, spread over the first half
-// of the MFMA stream. Rows keep one spare 16-byte chunk (conflict-free MFMA
+// step t loads K(t+3) and V(t+1), one step ahead, in every other slot of the
+// first 20 of its 32 MFMA slots (the last load then still has a third of the
+// step to arrive before the step's closing wait). The prologue stages K(0) in
+// Vt slot 1 (free until step 0 loads V(1)), so K(0), K(1), K(2), V(0) and the
+// Q fragment arrive in one memory round trip. Rows keep one spare 16-byte chunk (conflict-free MFMA
 // operand reads with one address register per ring); lanes that land on a
 // spare chunk load a dummy. Each load's M0 (its LDS base) is written one slot
 // ahead, so the M0 -> LDS-DMA wait state is filled by an MFMA, not a nop.
@@ -480,8 +483,10 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     if constexpr (MASK) mrow.init(p.mask, p.mask_sb, p.mask_sh, p.H, p.Sq, p.Sk, bh, qi);
 
     // Q fragment: qf[ks] = Q[qi][16ks + 8g .. +7] * sign(scale) * c2, in bf16.
+    // Loaded in the prologue after the first tile loads are issued, so the
+    // Q load and the K/V tile loads share one memory round trip.
     bf16x8 qf[NKS];
-    {
+    auto load_q = [&]() {
         const QT* qrow = (const QT*)p.q + ((size_t)bh * Sq + (qi < Sq ? qi : 0)) * D;
         const float sg = qi < Sq ? p.qsign * c2 : 0.f;
         for (int ks = 0; ks < NKS; ks++) {
@@ -497,7 +502,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
             qf[ks] = pack8(v[0] * sg, v[1] * sg, v[2] * sg, v[3] * sg, v[4] * sg, v[5] * sg,
                            v[6] * sg, v[7] * sg);
         }
-    }
+    };
 
     // ---- tile loads: instruction i of thread tid fills 16-byte chunk
     // position i*NT + tid of a padded tile (K: 64 x 17 positions, Vt:
@@ -523,16 +528,25 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     const brsrc vrs = make_rsrc(Vg, (uint32_t)Skp * D * 2);
     const uint32_t kl = lds_addr(sKb) + wave * 1024, vl = lds_addr(sVb) + wave * 1024;
     // Load i of K / Vt tile kt into ring slot `slot` (M0 written by the call).
-    auto dma_ki = [&](int kt, int slot, int i) {
-        if (i < NKI - 1) dma16(krs, kl + slot * KTB + i * NT * 16, koff[i], kt * BN * D * 2);
-        else dma16_if(krs, kl + slot * KTB + i * NT * 16, koff[i], kt * BN * D * 2, klast);
+    // Load i of K tile kt into the K-layout tile at LDS address base (this
+    // wave's part of it).
+    auto dma_ki_at = [&](int kt, uint32_t base, int i) {
+        if (i < NKI - 1) dma16(krs, base + i * NT * 16, koff[i], kt * BN * D * 2);
+        else dma16_if(krs, base + i * NT * 16, koff[i], kt * BN * D * 2, klast);
     };
+    auto dma_ki = [&](int kt, int slot, int i) { dma_ki_at(kt, kl + slot * KTB, i); };
     auto dma_vi = [&](int kt, int slot, int i) {
         if (i < NVI - 1) dma16(vrs, vl + slot * VTB + i * NT * 16, voff[i], kt * BN * 2);
         else dma16_if(vrs, vl + slot * VTB + i * NT * 16, voff[i], kt * BN * 2, vlast);
     };
     auto dma_k = [&](int kt, int slot) {
         for (int i = 0; i < NKI; i++) dma_ki(kt, slot, i);
+    };
+    // K(0) is staged in Vt slot 1, which no tile occupies before step 0
+    // loads V(1), so the prologue issues K(0), K(1), K(2) and V(0) at once.
+    static_assert(BN * KST <= D * VST, "a K tile fits in a Vt slot");
+    auto dma_k0_staged = [&]() {
+        for (int i = 0; i < NKI; i++) dma_ki_at(0, vl + VTB, i);
     };
     auto dma_v = [&](int kt, int slot) {
         for (int i = 0; i < NVI; i++) dma_vi(kt, slot, i);
@@ -630,8 +644,11 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         constexpr int NU = 16;             // softmax micro-ops (one score pair each)
         constexpr int LA = 3;              // LDS read lead (MFMAs)
         constexpr int NDMA = 2 * NKI;      // tile loads of a step
-        constexpr int DS = NM / NDMA;      // slots between tile loads
-        static_assert(DS >= 2, "an M0 write needs the slot before its load");
+        // Slots between tile loads: two (an M0 write needs the slot before
+        // its load), so every load of the step is issued in its first
+        // 2 NDMA slots and has the rest of the step to arrive.
+        constexpr int DS = 2;
+        static_assert(DS * NDMA <= NM, "the step's tile loads fit in its slots");
         bf16x8 opr[4];
         auto fetch = [&](auto E) {
             constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
@@ -764,19 +781,26 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
 
     // ---- prologue: S^T(0) -> P(0), S^T(1); the rings hold what step 0 needs ----
     f32x16 s0[2], s1[2];
-    auto qk_slot = [&](int slot, f32x16* s, f32x16 c) {
+    // S^T of the K-layout tile starting at LDS byte `tile`.
+    auto qk_tile = [&](const char* tile, f32x16* s, f32x16 c) {
         s[0] = c;
         s[1] = c;
         for (int ks = 0; ks < NKS; ks++)
-            for (int mt = 0; mt < 2; mt++) s[mt] = mfma_bf16(kfrag(slot * KTB, ks, mt), qf[ks], s[mt]);
+            for (int mt = 0; mt < 2; mt++)
+                s[mt] = mfma_bf16(*(const bf16x8*)(tile + kq + (mt * 32 * KST + ks * 16) * 2),
+                                  qf[ks], s[mt]);
     };
     auto last = [&](int kt) { return kt < ntiles ? kt : ntiles - 1; };
-    dma_k(0, 0);
+    // One memory round trip: K(0) (staged in Vt slot 1), K(1), K(2), V(0)
+    // and the Q fragment are all in flight together.
+    dma_k0_staged();
     dma_k(last(1), 1);
+    dma_k(last(2), 0);
     dma_v(0, 0);
+    load_q();
     GONN_VMCNT(0);
     __syncthreads();
-    qk_slot(0, s0, f32x16{});
+    qk_tile(sVc + VTB, s0, f32x16{});
     if constexpr (MASK) {
         mrow.load(0, g, mreg);
         MaskRow::add(mreg, s0);
@@ -792,14 +816,12 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         nmc = f32x16{} - mc;
     }
     l = p_tile(s0, pp, -mc);
-    qk_slot(1, s1, nmc);  // K(1), or for a one-tile block a masked copy of K(0)
+    qk_tile(sKc + KTB, s1, nmc);  // K(1), or for a one-tile block a masked copy of K(0)
     if constexpr (MASK) {
         mrow.load(last(1), g, mreg);
         MaskRow::add(mreg, s1);
     }
-    __syncthreads();      // K(0) read by every wave: its slot takes K(2)
-    dma_k(last(2), 0);
-    GONN_VMCNT(0);
+    // K(0) and K(1) read by every wave: step 0 loads V(1) and K(3) over them.
     __syncthreads();
 
     {
