@@ -418,13 +418,14 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
 // LDS: two-slot rings of K tiles (64 keys x D) and Vt tiles (D x 64 keys)
 // filled straight from HBM/L2 by buffer_load ... lds, one barrier per step;
 // step t loads K(t+3) and V(t+1), one step ahead, in every other slot of the
-// first 20 of its 32 MFMA slots (the last load then still has a third of the
-// step to arrive before the step's closing wait). The prologue stages K(0) in
-// Vt slot 1 (free until step 0 loads V(1)), so K(0), K(1), K(2), V(0) and the
-// Q fragment arrive in one memory round trip. Rows keep one spare 16-byte chunk (conflict-free MFMA
-// operand reads with one address register per ring); lanes that land on a
-// spare chunk load a dummy. Each load's M0 (its LDS base) is written one slot
-// ahead, so the M0 -> LDS-DMA wait state is filled by an MFMA, not a nop.
+// first 16 of its 32 MFMA slots (the last load then still has half the step
+// to arrive before the step's closing wait). The prologue stages K(0) in Vt
+// slot 1 (free until step 0 loads V(1)), so K(0), K(1), K(2), V(0) and the Q
+// fragment arrive in one memory round trip. Tiles are stored without padding
+// in the swizzled layout of fwd_tile_swz (conflict-free MFMA operand reads,
+// 64 contiguous bytes per row per load, no dummy or partial loads: four load
+// instructions per 16 KB tile). Each load's M0 (its LDS base) is written one
+// slot ahead, so the M0 -> LDS-DMA wait state is filled by an MFMA, not a nop.
 //
 // Every step has the same form: the last two steps compute S^T of tiles past
 // the end and the last one their softmax; those keys lie past the key end
@@ -433,6 +434,23 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
 // the same in every step (tail variants spilled), for two masked S^T tiles
 // per q-block.
 // ---------------------------------------------------------------------------
+// Swizzled tile layout of the pipelined forward. A tile of `rows` rows of
+// 16-byte chunks (K: 64 keys x D/8; Vt: D x 8) is stored in 64-byte
+// segments of four chunks: position (16 bytes each)
+//   pos(row, chunk) = ((chunk / 4) * rows + row) * 4 + ((chunk % 4) ^ h(row)),
+//   h(row) = ((row >> 1) ^ (row >> 3)) & 3.
+// A load instruction then fills 16 rows x 64 contiguous bytes (coalesced), and
+// the 16 (or 8) lanes an LDS read serves together, rows 32m + ln and one
+// chunk, hit distinct bank groups under either 64 or 32 banks. No padding:
+// a tile is 16 KB at D = 128 (the padded tiles were 17 and 18 KB).
+GONN_DEV int fwd_tile_swz(int row) { return ((row >> 1) ^ (row >> 3)) & 3; }
+// Row and chunk held by position `pos` of a tile of `rows` rows.
+GONN_DEV void fwd_tile_chunk(int pos, int rows, int& row, int& chunk) {
+    const int q = pos >> 2;
+    row = q % rows;
+    chunk = (q / rows) * 4 + ((pos & 3) ^ fwd_tile_swz(row));
+}
+
 constexpr float kSumBound = 16384.f;  // 2^14: row-sum bound of one 64-key tile
 // Wave issue priority (s_setprio) during a step's MFMA stream.
 constexpr int kFwdStreamPrio = 1;
@@ -450,12 +468,14 @@ template <int D, bool CAUSAL, typename QT, bool MASK>
 __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kernel(FwdParams p) {
     constexpr int NW = kFwdWaves, BM = NW * 32, BN = 64, NT = NW * 64;
     constexpr int NKS = D / 16, NDT = D / 32;
-    constexpr int KST = D + 8, VST = BN + 8;          // padded row strides (bf16)
-    constexpr uint32_t KTB = BN * KST * 2, VTB = D * VST * 2;  // slot bytes
-    constexpr int NSLOT = 2;
-    constexpr int KLEAD = 3, VLEAD = 1;  // load distance (tiles)
-    __shared__ __attribute__((aligned(16))) bf16 sKb[NSLOT * BN * KST];
-    __shared__ __attribute__((aligned(16))) bf16 sVb[NSLOT * D * VST];
+    // Swizzled tiles without padding (layout at fwd_tile_swz): 16 KB per tile
+    // at D = 128, two-slot K and Vt rings, 64 KB per workgroup. Step t loads
+    // K(t+3) and V(t+1), each one step ahead of its use.
+    constexpr uint32_t KTB = BN * D * 2, VTB = D * BN * 2;  // slot bytes
+    constexpr int KSLOTS = 2, VSLOTS = 2;
+    constexpr int KLEAD = 3, VLEAD = 1;
+    __shared__ __attribute__((aligned(16))) bf16 sKb[KSLOTS * BN * D];
+    __shared__ __attribute__((aligned(16))) bf16 sVb[VSLOTS * D * BN];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -504,64 +524,60 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         }
     };
 
-    // ---- tile loads: instruction i of thread tid fills 16-byte chunk
-    // position i*NT + tid of a padded tile (K: 64 x 17 positions, Vt:
-    // 128 x 9); the last instruction of a tile covers its first waves only ----
-    constexpr int KCP = KST / 8, NKP = BN * KCP, VCP = VST / 8, NVP = D * VCP;
-    constexpr int NKI = (NKP + NT - 1) / NT, NVI = (NVP + NT - 1) / NT;  // loads per tile
-    constexpr int KLAST = NKP - (NKI - 1) * NT, VLAST = NVP - (NVI - 1) * NT;
-    static_assert(KLAST % 64 == 0 && VLAST % 64 == 0, "partial loads must be whole waves");
-    static_assert(NKI == NVI, "K and Vt tiles take the same number of loads");
+    // ---- tile loads: instruction i of thread tid fills 16-byte position
+    // i*NT + tid of a tile (fwd_tile_chunk gives the row and chunk it holds) ----
+    constexpr int NKP = BN * D / 8, NVP = D * BN / 8;  // 16-byte chunks per tile
+    static_assert(NKP % NT == 0 && NVP % NT == 0, "tiles are whole load instructions");
+    constexpr int NKI = NKP / NT, NVI = NVP / NT;      // loads per tile
     uint32_t koff[NKI], voff[NVI];
     for (int i = 0; i < NKI; i++) {
-        const int pos = i * NT + tid;
-        const int kr = pos / KCP, kc = pos % KCP;
-        koff[i] = (uint32_t)((((pos < NKP) ? kr : 0) * D + (kc < D / 8 ? kc : 0) * 8) * 2);
-        const int vr = pos / VCP, vc = pos % VCP;
-        voff[i] = (uint32_t)((((pos < NVP) ? vr : 0) * Skp + (vc < BN / 8 ? vc : 0) * 8) * 2);
+        int r, c;
+        fwd_tile_chunk(i * NT + tid, BN, r, c);
+        koff[i] = (uint32_t)((r * D + c * 8) * 2);
+        fwd_tile_chunk(i * NT + tid, D, r, c);
+        voff[i] = (uint32_t)((r * Skp + c * 8) * 2);
     }
-    // Waves that issue the last (partial) load of a K / Vt tile.
-    const uint32_t klast = wave * 64 < KLAST, vlast = wave * 64 < VLAST;
     const bf16* Kg = (const bf16*)p.k + (size_t)bh * Skp * D;
     const bf16* Vg = (const bf16*)p.v + (size_t)bh * D * Skp;
     const brsrc krs = make_rsrc(Kg, (uint32_t)Skp * D * 2);
     const brsrc vrs = make_rsrc(Vg, (uint32_t)Skp * D * 2);
     const uint32_t kl = lds_addr(sKb) + wave * 1024, vl = lds_addr(sVb) + wave * 1024;
-    // Load i of K / Vt tile kt into ring slot `slot` (M0 written by the call).
     // Load i of K tile kt into the K-layout tile at LDS address base (this
-    // wave's part of it).
+    // wave's part of it; M0 written by the call).
     auto dma_ki_at = [&](int kt, uint32_t base, int i) {
-        if (i < NKI - 1) dma16(krs, base + i * NT * 16, koff[i], kt * BN * D * 2);
-        else dma16_if(krs, base + i * NT * 16, koff[i], kt * BN * D * 2, klast);
-    };
-    auto dma_ki = [&](int kt, int slot, int i) { dma_ki_at(kt, kl + slot * KTB, i); };
-    auto dma_vi = [&](int kt, int slot, int i) {
-        if (i < NVI - 1) dma16(vrs, vl + slot * VTB + i * NT * 16, voff[i], kt * BN * 2);
-        else dma16_if(vrs, vl + slot * VTB + i * NT * 16, voff[i], kt * BN * 2, vlast);
+        dma16(krs, base + i * NT * 16, koff[i], kt * BN * D * 2);
     };
     auto dma_k = [&](int kt, int slot) {
-        for (int i = 0; i < NKI; i++) dma_ki(kt, slot, i);
+        for (int i = 0; i < NKI; i++) dma_ki_at(kt, kl + slot * KTB, i);
     };
     // K(0) is staged in Vt slot 1, which no tile occupies before step 0
     // loads V(1), so the prologue issues K(0), K(1), K(2) and V(0) at once.
-    static_assert(BN * KST <= D * VST, "a K tile fits in a Vt slot");
+    static_assert(KTB <= VTB, "a K tile fits in a Vt slot");
     auto dma_k0_staged = [&]() {
         for (int i = 0; i < NKI; i++) dma_ki_at(0, vl + VTB, i);
     };
     auto dma_v = [&](int kt, int slot) {
-        for (int i = 0; i < NVI; i++) dma_vi(kt, slot, i);
+        for (int i = 0; i < NVI; i++)
+            dma16(vrs, vl + slot * VTB + i * NT * 16, voff[i], kt * BN * 2);
     };
 
     // ---- MFMA operand reads: K row mt*32 + ln, Vt row dt*32 + ln; chunk
-    // 2ks + g (bytes from a slot's start) ----
-    const uint32_t kq = (uint32_t)(ln * KST + g * 8) * 2, vq = (uint32_t)(ln * VST + g * 8) * 2;
+    // 2ks + g. In the layout of fwd_tile_swz the byte offset of (row, chunk) in a tile is
+    // (chunk / 4) * rows * 64 + row * 64 + ((chunk % 4) ^ h(row)) * 16; for
+    // row = 32 m + ln and chunk = 2 ks + g the lane part depends on ks only
+    // through ks & 1, so two lane offsets serve every K and Vt read. ----
+    const int hs = fwd_tile_swz(ln);
+    const uint32_t qa0 = (uint32_t)(ln * 64 + ((0 + g) ^ hs) * 16);  // k-step even
+    const uint32_t qa1 = (uint32_t)(ln * 64 + ((2 + g) ^ hs) * 16);  // k-step odd
     const char* sKc = (const char*)sKb;
     const char* sVc = (const char*)sVb;
     auto kfrag = [&](uint32_t base, int ks, int mt) {
-        return *(const bf16x8*)(sKc + (base + kq) + (mt * 32 * KST + ks * 16) * 2);
+        return *(const bf16x8*)(sKc + (base + ((ks & 1) ? qa1 : qa0)) +
+                                ((ks >> 1) * BN + mt * 32) * 64);
     };
     auto vfrag = [&](uint32_t base, int ks, int dt) {
-        return *(const bf16x8*)(sVc + (base + vq) + (dt * 32 * VST + ks * 16) * 2);
+        return *(const bf16x8*)(sVc + (base + ((ks & 1) ? qa1 : qa0)) +
+                                ((ks >> 1) * D + dt * 32) * 64);
     };
 
     f32x16 oacc[NDT];
@@ -626,7 +642,8 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     // PV(j, dt = 0..3), then S^T k-steps 2j and 2j+1 (mt = 0, 1), so six
     // accumulator chains interleave.
     auto step = [&](int t, f32x16* sA, f32x16* sB) __attribute__((always_inline)) {
-        const int kslot = (t + KLEAD) & (NSLOT - 1), vslot = (t + VLEAD) & (NSLOT - 1);
+        const int kslot = (t + KLEAD) & (KSLOTS - 1);
+        const int vslot = (t + 1) & 1;
         // Tiles past the last one are clamped to it: such a load refills a
         // slot no later step reads as real data (its S^T tile is masked).
         const int kload = t + KLEAD < ntiles ? t + KLEAD : ntiles - 1;
@@ -635,15 +652,15 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         // step's MFMA stream).
         if (needs_mask(t + 1)) mask(t + 1, sB);
         if constexpr (MASK) mrow.load(t + 2 < ntiles ? t + 2 : ntiles - 1, g, mreg);
-        const uint32_t vb = (uint32_t)(t & (NSLOT - 1)) * VTB;
-        const uint32_t kb = (uint32_t)((t + 2) & (NSLOT - 1)) * KTB;
+        const uint32_t vb = (uint32_t)(t & 1) * VTB;
+        const uint32_t kb = (uint32_t)((t + 2) & (KSLOTS - 1)) * KTB;
 
         constexpr int SKS = NKS / 4;       // S^T k-steps per PV k-step
         constexpr int GW = NDT + 2 * SKS;  // MFMAs per PV k-step group
         constexpr int NM = 4 * GW;         // MFMAs in the step
         constexpr int NU = 16;             // softmax micro-ops (one score pair each)
         constexpr int LA = 3;              // LDS read lead (MFMAs)
-        constexpr int NDMA = 2 * NKI;      // tile loads of a step
+        constexpr int NDMA = NKI + NVI;    // tile loads of a step (K first)
         // Slots between tile loads: two (an M0 write needs the slot before
         // its load), so every load of the step is issued in its first
         // 2 NDMA slots and has the rest of the step to arrive.
@@ -664,25 +681,20 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
                 sA[mt] = mfma_bf16(opr[e & 3], qf[kk], kk == 0 ? nmc : sA[mt]);
             }
         };
-        // Tile load d (0 .. NDMA-1) at slot 1 + d*DS, alternating K and V;
-        // its M0 is written at the slot before.
+        // Tile load d (0 .. NDMA-1) at slot 1 + d*DS: the K(t+3) loads, then
+        // the V(t+1) loads. Its M0 is written at the slot before.
         auto dma_slot = [&](auto E) {
             constexpr int e = decltype(E)::value;
-            if constexpr (e + 1 >= 1 && e % DS == 0 && e / DS < NDMA) {
-                constexpr int d = e / DS, i = d / 2;
-                const uint32_t lds = d % 2 == 0 ? kl + kslot * KTB + i * NT * 16
-                                                : vl + vslot * VTB + i * NT * 16;
+            if constexpr (e % DS == 0 && e / DS < NDMA) {
+                constexpr int d = e / DS;
+                const uint32_t lds = d < NKI ? kl + kslot * KTB + d * NT * 16
+                                             : vl + vslot * VTB + (d - NKI) * NT * 16;
                 dma_set_m0(lds);
             }
             if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
-                constexpr int d = (e - 1) / DS, i = d / 2;
-                if constexpr (d % 2 == 0) {
-                    if constexpr (i < NKI - 1) dma16_m0(krs, koff[i], kload * BN * D * 2);
-                    else dma16_m0_if(krs, koff[i], kload * BN * D * 2, klast);
-                } else {
-                    if constexpr (i < NVI - 1) dma16_m0(vrs, voff[i], vload * BN * 2);
-                    else dma16_m0_if(vrs, voff[i], vload * BN * 2, vlast);
-                }
+                constexpr int d = (e - 1) / DS;
+                if constexpr (d < NKI) dma16_m0(krs, koff[d], kload * BN * D * 2);
+                else dma16_m0(vrs, voff[d - NKI], vload * BN * 2);
             }
         };
         float part[4] = {0.f, 0.f, 0.f, 0.f};
@@ -772,6 +784,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         }
         l = l * alpha + ts;
 
+        // K(t+3) and V(t+1), which step t+1 reads, have landed.
         GONN_VMCNT(0);
         __syncthreads();
         if constexpr (MASK) MaskRow::add(mreg, sA);
@@ -787,7 +800,8 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         s[1] = c;
         for (int ks = 0; ks < NKS; ks++)
             for (int mt = 0; mt < 2; mt++)
-                s[mt] = mfma_bf16(*(const bf16x8*)(tile + kq + (mt * 32 * KST + ks * 16) * 2),
+                s[mt] = mfma_bf16(*(const bf16x8*)(tile + ((ks & 1) ? qa1 : qa0) +
+                                                   ((ks >> 1) * BN + mt * 32) * 64),
                                   qf[ks], s[mt]);
     };
     auto last = [&](int kt) { return kt < ntiles ? kt : ntiles - 1; };
@@ -821,7 +835,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         mrow.load(last(1), g, mreg);
         MaskRow::add(mreg, s1);
     }
-    // K(0) and K(1) read by every wave: step 0 loads V(1) and K(3) over them.
+    // K(0) and K(1) read by every wave: step 0 loads V(2) and K(3) over them.
     __syncthreads();
 
     {
@@ -832,6 +846,9 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         }
         if (t < ntiles) step(t, s0, s1);
     }
+    // The last steps leave V loads in flight; they write this workgroup's
+    // LDS, so they land before the waves exit.
+    GONN_VMCNT(0);
 
     const float lt = pair_sum32(l);
     if (qi < Sq) {
