@@ -151,6 +151,75 @@ def bench_decode(torch, hip, steps, warmup):
                 median_ms=med, split_ms=st / max(sn, 1), combine_ms=ct / max(cn, 1))
 
 
+def bench_incremental(torch, hip, steps, warmup, Ts=(1, 4)):
+    """Device-resident incremental decoding through one MHA layer at the C4
+    cache shape: B=64 sequences, H=32 heads of D=128 (E=4096), a bf16 cache
+    of 8192 positions holding ~U[512, 7900] per sequence. One step appends T
+    new positions of every sequence (gonn_hip_mha_forward_incremental_dev:
+    fp64 q/k/v projection, append, causal multi-token attend, merge, output
+    projection, one host synchronisation). Weights and inputs are seeded
+    N(0,1) (weights scaled by 1/sqrt(E))."""
+    import numpy as np
+    B, H, D, Lmax = 64, 32, 128, 8192
+    E = H * D
+    lens = np.random.default_rng(5).integers(512, 7900, B).astype(np.int32)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(55)
+    W = [(torch.randn((E, E), generator=g, device="cuda", dtype=torch.float64) / math.sqrt(E))
+         .cpu().numpy() for _ in range(4)]
+    bs = [np.zeros(E) for _ in range(4)]
+    dev = hip.DeviceMHA(E, H, W[0], bs[0], W[1], bs[1], W[2], bs[2], W[3], bs[3])
+    del W
+    cache = hip.KVCache(B, H, Lmax, D)
+    chunk = 1024
+    for c0 in range(0, int(lens.max()), chunk):
+        cnt = np.clip(lens - c0, 0, chunk).astype(np.int32)
+        k = torch.randn((B, H, chunk, D), generator=g, device="cuda", dtype=torch.bfloat16)
+        v = torch.randn((B, H, chunk, D), generator=g, device="cuda", dtype=torch.bfloat16)
+        cache.append(k, v, counts=cnt)
+        del k, v
+    torch.cuda.synchronize()
+    res = {"config": {"workload": "resident MHA incremental decoding over a bf16 KV cache",
+                      "B": B, "H": H, "E": E, "D": D, "Lmax": Lmax,
+                      "mean_len_at_start": float(lens.mean())}}
+    for T in Ts:
+        x = torch.randn((B, T, E), generator=g, device="cuda", dtype=torch.float64)
+        out = torch.empty_like(x)
+        ws = torch.empty(dev.incremental_workspace_bytes(cache, T), dtype=torch.uint8,
+                         device="cuda")
+        run = lambda: dev.forward_incremental_dev(x, cache, out=out, ws=ws)  # noqa: E731
+        for _ in range(warmup):
+            run()
+        torch.cuda.synchronize()
+        len0 = cache.lengths().astype(np.int64)
+        ms, med, _ = _run_steps(torch, run, steps)
+        hip.profile_reset()
+        hip.profile_enable(True)
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+        hip.profile_enable(False)
+        st, sn = hip.profile_read("decode_causal_split")
+        ct, cn = hip.profile_read("decode_causal_combine")
+        hip.profile_reset()
+        # attend bytes: every valid K and V row once per group of queries, at
+        # the mean cache length of the profiled pass
+        groups = -(-T // 4)
+        mean_len = float((len0 + steps * T + steps * T / 2).mean())
+        abytes = groups * 2 * H * D * 2 * mean_len * B
+        split_ms = st / max(sn, 1)
+        res[f"T{T}"] = {"ms_per_step": round(ms, 5), "median_ms_per_step": round(med, 5),
+                        "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+                        "attend_split_ms": round(split_ms, 5),
+                        "attend_combine_ms": round(ct / max(cn, 1), 5),
+                        "attend_GBps": round(abytes / (split_ms * 1e-3) / 1e9, 2),
+                        "attend_frac": round(abytes / (split_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        del x, out, ws
+    cache.close()
+    dev.close()
+    return res
+
+
 def _timed(torch, hip, run, steps, warmup, stages):
     """Mean ms per step over `steps` launches bracketed by events on the current
     stream, then a second pass with the library's per-stage event profiler;
@@ -362,6 +431,8 @@ def main():
     ap.add_argument("--no-bwd", action="store_true")
     ap.add_argument("--no-encoder", action="store_true")
     ap.add_argument("--no-mha", action="store_true")
+    ap.add_argument("--no-incremental", action="store_true",
+                    help="skip the resident incremental-decoding leg")
     ap.add_argument("--no-wide", action="store_true", help="skip the masked / cross legs")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the headline leg (profiling runs of the other legs only)")
@@ -407,6 +478,9 @@ def main():
                 log(f"[bench] wide gate {kind}")
                 bench_wide_gate(torch, hip, max(args.steps // 5, 3), max(args.warmup // 2, 1),
                                 kind)
+        if not args.no_incremental:
+            log("[bench] resident incremental decoding")
+            bench_incremental(torch, hip, max(args.steps // 5, 5), max(args.warmup // 2, 2))
         return
     log("[bench] prefill C3")
     pre = bench_prefill(torch, hip, args.steps, args.warmup)
@@ -504,6 +578,10 @@ def main():
     if not args.no_mha:
         log("[bench] MHA C1")
         line["mha"] = bench_mha(torch, hip, args.steps, args.warmup)
+    if not args.no_incremental:
+        log("[bench] resident incremental decoding")
+        line["kv_incremental"] = bench_incremental(torch, hip, max(args.steps // 5, 5),
+                                                   max(args.warmup // 2, 2))
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline")
         line["cpu_baseline"] = cpu_baseline(pre, args.cpu_seconds)

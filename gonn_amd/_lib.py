@@ -50,6 +50,8 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_mha_workspace_bytes", "gonn_hip_mha_forward_dev", "gonn_hip_flash_attn_f64_bwd_ex",
     "gonn_hip_flash_attn_f64_masked", "gonn_hip_flash_attn_f64_bwd_masked",
     "gonn_hip_attn_decode_noalloc",
+    "gonn_hip_kvcache_attend_causal_workspace_bytes", "gonn_hip_kvcache_attend_causal",
+    "gonn_hip_mha_incremental_workspace_bytes", "gonn_hip_mha_forward_incremental_dev",
 )
 
 # Size of the library-owned scratch array of gonn_hip_attn_decode_noalloc
@@ -172,6 +174,14 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_mha_workspace_bytes.argtypes = [vp, i, i, i]
     lib.gonn_hip_mha_workspace_bytes.restype = ctypes.c_size_t
     lib.gonn_hip_mha_forward_dev.argtypes = [vp] + [ctypes.POINTER(Buf)] * 4 + [i, i, i, i, ctypes.POINTER(Buf), vp, ctypes.c_size_t, vp]
+    lib.gonn_hip_kvcache_attend_causal_workspace_bytes.restype = sz
+    lib.gonn_hip_kvcache_attend_causal_workspace_bytes.argtypes = [vp, i]
+    lib.gonn_hip_kvcache_attend_causal.argtypes = [vp, ctypes.POINTER(Buf), ctypes.POINTER(Buf), i,
+                                                   ctypes.c_double, vp, sz, vp]
+    lib.gonn_hip_mha_incremental_workspace_bytes.restype = sz
+    lib.gonn_hip_mha_incremental_workspace_bytes.argtypes = [vp, vp, i]
+    lib.gonn_hip_mha_forward_incremental_dev.argtypes = [vp, vp, ctypes.POINTER(Buf),
+                                                         ctypes.POINTER(Buf), i, vp, sz, vp]
     _lib = lib
     return lib
 

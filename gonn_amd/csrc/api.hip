@@ -19,6 +19,7 @@
 #include "../../include/gonn_hip.h"
 #include "common.h"
 #include "kernels.h"
+#include "kvcache_internal.h"
 
 #define GONN_HIP_VERSION "gonn-hip 0.1.0 (gfx950)"
 
@@ -543,7 +544,81 @@ int kv_append_dev(gonn_kvcache* c, const void* k, const void* v, int src_bf16, i
     return GONN_OK;
 }
 
+// Split size of the causal multi-token attend: the decode rule of
+// decode_split with one (b,h) counted once per query group.
+int causal_split(const gonn_kvcache* c, int T) {
+    const long long units = (long long)c->B * c->H * ((T + gonn::kDecodeGroup - 1) / gonn::kDecodeGroup);
+    int sk = 2048;
+    while (sk > 64 && units * ((c->Lmax + sk - 1) / sk) < 2048) sk /= 2;
+    return sk;
+}
+
 }  // namespace
+
+namespace gonn {
+
+void kvcache_dims(const gonn_kvcache* c, int* B, int* H, int* Lmax, int* D) {
+    *B = c->B;
+    *H = c->H;
+    *Lmax = c->Lmax;
+    *D = c->D;
+}
+
+int kvcache_append_pending(gonn_kvcache* c, const float* k, const float* v, int T, hipStream_t s,
+                           std::vector<int>* new_len) {
+    TRY(kv_check_append(c, T, nullptr));
+    TRYH(hipMemcpyAsync(c->d_pc, c->h_pc.data(), 2 * (size_t)c->B * sizeof(int),
+                        hipMemcpyHostToDevice, s));
+    TRYH(launch_kv_append(k, v, 0, c->k, c->v, c->d_pc, c->d_pc + c->B, c->B, c->H, T, c->Lmax,
+                          c->D, s));
+    *new_len = c->h_len;
+    for (int b = 0; b < c->B; b++) (*new_len)[b] += T;
+    return herr(hipMemcpyAsync(c->d_len, new_len->data(), (size_t)c->B * sizeof(int),
+                               hipMemcpyHostToDevice, s));
+}
+
+void kvcache_commit(gonn_kvcache* c, std::vector<int>* new_len) { c->h_len.swap(*new_len); }
+
+void kvcache_restore(gonn_kvcache* c) {
+    (void)hipMemcpy(c->d_len, c->h_len.data(), (size_t)c->B * sizeof(int), hipMemcpyHostToDevice);
+}
+
+size_t kvcache_attend_causal_ws(const gonn_kvcache* c, int T) {
+    if (!c || T <= 0) return 0;
+    const int sk = causal_split(c, T);
+    const size_t ns = ((size_t)c->Lmax + sk - 1) / sk;
+    const size_t parts = (size_t)c->B * c->H * T * ns;
+    return round_up(parts * 2, 64) * sizeof(float) + parts * c->D * sizeof(float) + 1024;
+}
+
+int kvcache_attend_causal_run(gonn_kvcache* c, const float* q, float* o, int T, double scale,
+                              void* ws, hipStream_t s, bool profile) {
+    DecodeParams p{};
+    const int sk = causal_split(c, T);
+    p.q = q;
+    p.kc = c->k;
+    p.vc = c->v;
+    p.kv_len = c->d_len;
+    p.o = o;
+    p.B = c->B;
+    p.H = c->H;
+    p.Lmax = c->Lmax;
+    p.T = T;
+    p.split_keys = sk;
+    p.nsplit = (c->Lmax + sk - 1) / sk;
+    float* w = (float*)round_up((size_t)ws, 256);
+    p.part_ml = w;
+    p.part_o = w + round_up((size_t)c->B * c->H * T * p.nsplit * 2, 64);
+    p.scale_log2 = (float)scale * kLog2e;
+    {
+        ProfScope ps(profile ? "decode_causal_split" : nullptr, s);
+        TRYH(launch_decode_causal_split(p, c->D, s));
+    }
+    ProfScope ps(profile ? "decode_causal_combine" : nullptr, s);
+    return herr(launch_decode_causal_combine(p, c->D, s));
+}
+
+}  // namespace gonn
 
 extern "C" {
 
@@ -1242,6 +1317,23 @@ int gonn_hip_kvcache_attend_f64(gonn_kvcache* c, const double* q, double* o, dou
     TRY(gonn_hip_kvcache_attend(c, &qb, &ob, scale, hs));
     TRY(download_padded(mem, (const float*)od, rows, c->D, c->D, o));
     return herr(hipStreamSynchronize(hs));
+}
+
+size_t gonn_hip_kvcache_attend_causal_workspace_bytes(const gonn_kvcache* c, int T) {
+    return gonn::kvcache_attend_causal_ws(c, T);
+}
+
+int gonn_hip_kvcache_attend_causal(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, int T,
+                                   double scale, void* ws, size_t ws_bytes, void* stream) {
+    if (!c || !q || !o || T <= 0 || !std::isfinite(scale)) return GONN_E_INVALID;
+    const size_t n = (size_t)c->B * c->H * T * c->D;
+    if (!buf_ok(*q, n, GONN_F32) || !buf_ok(*o, n, GONN_F32)) return GONN_E_INVALID;
+    // The T queries' own positions are the last T cached ones.
+    for (int b = 0; b < c->B; b++)
+        if (c->h_len[b] < T) return GONN_E_INVALID;
+    if (!ws || ws_bytes < gonn::kvcache_attend_causal_ws(c, T)) return GONN_E_WORKSPACE;
+    return gonn::kvcache_attend_causal_run(c, (const float*)q->ptr, (float*)o->ptr, T, scale, ws,
+                                           (hipStream_t)stream, true);
 }
 
 }  // extern "C"

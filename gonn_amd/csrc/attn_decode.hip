@@ -184,6 +184,177 @@ __global__ __launch_bounds__(D) void decode_combine_kernel(DecodeParams p) {
     p.o[(size_t)bh * D + tid] = ns > 0 ? O / L : 0.f;
 }
 
+// ---------------------------------------------------------------------------
+// Causal multi-token attend over the cache: T new queries per (b,h) whose own
+// K/V rows are the last T cached positions of their sequence (chunked
+// prefill into a cache, several tokens of one decoding step). Query t sees
+// keys [0, lim_t), lim_t = kv_len[b] - (T - 1 - t): the top-left causal mask
+// of nn/attention.go:185-196 aligned at the sequence's end, which is what
+// decoding one position at a time over the cache computes.
+//
+// Queries go in groups of G = kDecodeGroup: a workgroup takes one split of
+// the group's key range [0, lim of its last query) and scores each key it
+// loads against all G queries, so the cache is read once per group. The key
+// range, its even splits and the lane-row layout are the decode kernel's;
+// each lane keeps G online-softmax states. Key j of the split counts for
+// query t only when j < lim_t; a query with no key in a split leaves the
+// partial (m, l) = (-inf, 0), which the combine weights by zero.
+// ---------------------------------------------------------------------------
+GONN_DEV int causal_group_keys(int len, int T, int t_last) { return len - (T - 1 - t_last); }
+
+template <int D>
+__global__ __launch_bounds__(256) void decode_causal_split_kernel(DecodeParams p) {
+    constexpr int G = kDecodeGroup;
+    constexpr int EPL = D / 16;  // elements per lane
+    constexpr int U = 4;         // keys per lane row per iteration
+    constexpr int NROWS = 16;    // lane rows per workgroup
+    __shared__ float pm[G][NROWS], pl[G][NROWS];
+    __shared__ float po[G][NROWS][D];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int rr = lane >> 4, dc = lane & 15, d0 = dc * EPL;
+    const int BH = p.B * p.H, T = p.T, NG = (T + G - 1) / G;
+    const int per = BH * NG;
+    const int s = blockIdx.x / per, rem = blockIdx.x - s * per;
+    const int gr = rem / BH, bh = rem - gr * BH, b = bh / p.H;
+    int len = p.kv_len[b];
+    len = len < 0 ? 0 : (len > p.Lmax ? p.Lmax : len);
+    const int t0 = gr * G, ng = T - t0 < G ? T - t0 : G;
+    const int kmax = causal_group_keys(len, T, t0 + ng - 1);
+    const int ns = kmax > 0 ? (kmax + p.split_keys - 1) / p.split_keys : 0;
+    if (s >= ns) return;  // uniform for the workgroup
+    const int k0 = (int)((long long)s * kmax / ns);
+    const int k1 = (int)((long long)(s + 1) * kmax / ns);
+
+    float q[G][EPL];
+    int lim[G];
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+        const bool on = i < ng;
+        const float* qp = (const float*)p.q + ((size_t)bh * T + t0 + (on ? i : 0)) * D + d0;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) q[i][e] = on ? qp[e] * p.scale_log2 : 0.f;
+        lim[i] = on ? causal_group_keys(len, T, t0 + i) : 0;
+    }
+    const bf16* Kb = (const bf16*)p.kc + (size_t)bh * p.Lmax * D + d0;
+    const bf16* Vb = (const bf16*)p.vc + (size_t)bh * p.Lmax * D + d0;
+
+    float m[G], l[G], o[G][EPL];
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+        m[i] = -INFINITY;
+        l[i] = 0.f;
+#pragma unroll
+        for (int e = 0; e < EPL; e++) o[i][e] = 0.f;
+    }
+
+    typedef uint16_t ld_t __attribute__((ext_vector_type(EPL)));
+    for (int base = k0 + wave * (4 * U); base < k1; base += 4 * 4 * U) {
+        // Keys past k1 are clamped to k1-1 (a valid row) and masked below.
+        ld_t kr[U], vr[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            int key = base + u * 4 + rr;
+            key = key < k1 ? key : k1 - 1;
+            kr[u] = __builtin_nontemporal_load((const ld_t*)(Kb + (size_t)key * D));
+            vr[u] = __builtin_nontemporal_load((const ld_t*)(Vb + (size_t)key * D));
+        }
+        float kf[U][EPL];
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int e = 0; e < EPL; e++) kf[u][e] = bf16_to_f32(kr[u][e]);
+#pragma unroll
+        for (int i = 0; i < G; i++) {
+            float sc[U];
+            float mb = -INFINITY;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                float a = 0.f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) a = __builtin_fmaf(q[i][e], kf[u][e], a);
+                a = row_sum16(a);
+                const int key = base + u * 4 + rr;
+                sc[u] = (key < k1 && key < lim[i]) ? a : -INFINITY;
+                mb = fmaxf(mb, sc[u]);
+            }
+            const float mnew = fmaxf(m[i], mb);
+            // A state that has seen no valid key keeps m = -inf, l = o = 0.
+            const float mref = (mnew == -INFINITY) ? 0.f : mnew;
+            const float alpha = fast_exp2(m[i] - mref);
+            float rs = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) o[i][e] *= alpha;
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const float pu = fast_exp2(sc[u] - mref);
+                rs += pu;
+#pragma unroll
+                for (int e = 0; e < EPL; e++)
+                    o[i][e] = __builtin_fmaf(pu, bf16_to_f32(vr[u][e]), o[i][e]);
+            }
+            l[i] = l[i] * alpha + rs;
+            m[i] = mnew;
+        }
+    }
+
+    const int row = wave * 4 + rr;
+#pragma unroll
+    for (int i = 0; i < G; i++) {
+        if (dc == 0) {
+            pm[i][row] = m[i];
+            pl[i][row] = l[i];
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; e++) po[i][row][d0 + e] = o[i][e];
+    }
+    __syncthreads();
+    if (tid < D) {
+        for (int i = 0; i < ng; i++) {
+            float M = -INFINITY;
+            for (int r = 0; r < NROWS; r++) M = fmaxf(M, pm[i][r]);
+            float L = 0.f, O = 0.f;
+            for (int r = 0; r < NROWS; r++) {
+                const float w = (pm[i][r] == -INFINITY) ? 0.f : fast_exp2(pm[i][r] - M);
+                L = __builtin_fmaf(w, pl[i][r], L);
+                O = __builtin_fmaf(w, po[i][r][tid], O);
+            }
+            const size_t part = ((size_t)bh * T + t0 + i) * p.nsplit + s;
+            p.part_o[part * D + tid] = O;
+            if (tid == 0) {
+                p.part_ml[part * 2 + 0] = M;
+                p.part_ml[part * 2 + 1] = L;
+            }
+        }
+    }
+}
+
+// One workgroup of D threads per (b,h,t): the combine of decode_combine_kernel
+// over the splits of query t's group. A split in which query t saw no key
+// has M = -inf and weight 0; every query sees at least its own key.
+template <int D>
+__global__ __launch_bounds__(D) void decode_causal_combine_kernel(DecodeParams p) {
+    constexpr int G = kDecodeGroup;
+    const int T = p.T;
+    const int bht = blockIdx.x, bh = bht / T, t = bht - bh * T, b = bh / p.H, tid = threadIdx.x;
+    int len = p.kv_len[b];
+    len = len < 0 ? 0 : (len > p.Lmax ? p.Lmax : len);
+    const int t0 = t / G * G, ng = T - t0 < G ? T - t0 : G;
+    const int kmax = causal_group_keys(len, T, t0 + ng - 1);
+    const int ns = kmax > 0 ? (kmax + p.split_keys - 1) / p.split_keys : 0;
+    const float* ml = p.part_ml + (size_t)bht * p.nsplit * 2;
+    const float* po = p.part_o + (size_t)bht * p.nsplit * D;
+    float M = -INFINITY;
+    for (int i = 0; i < ns; i++) M = fmaxf(M, ml[2 * i]);
+    float L = 0.f, O = 0.f;
+    for (int i = 0; i < ns; i++) {
+        const float w = (ml[2 * i] == -INFINITY) ? 0.f : fast_exp2(ml[2 * i] - M);
+        L = __builtin_fmaf(w, ml[2 * i + 1], L);
+        O = __builtin_fmaf(w, po[(size_t)i * D + tid], O);
+    }
+    p.o[(size_t)bht * D + tid] = L > 0.f ? O / L : 0.f;
+}
+
 // KV-cache append: row t < cnt[b] of (b, h) in the sources (B,H,T,D), f32 or
 // bf16, goes to position pos[b] + t of the bf16 cache (B,H,Lmax,D); rows at
 // or past Lmax are dropped (the host rejects such appends beforehand). One
@@ -246,6 +417,25 @@ hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStre
     } else {
         return hipErrorInvalidValue;
     }
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_causal_split(const DecodeParams& p, int D, hipStream_t s) {
+    if (p.T <= 0) return hipErrorInvalidValue;
+    const unsigned groups = (unsigned)((p.T + kDecodeGroup - 1) / kDecodeGroup);
+    const unsigned grid = (unsigned)p.nsplit * groups * (unsigned)(p.B * p.H);
+    if (D == 128) decode_causal_split_kernel<128><<<grid, 256, 0, s>>>(p);
+    else if (D == 64) decode_causal_split_kernel<64><<<grid, 256, 0, s>>>(p);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_decode_causal_combine(const DecodeParams& p, int D, hipStream_t s) {
+    if (p.T <= 0) return hipErrorInvalidValue;
+    const unsigned grid = (unsigned)(p.B * p.H) * (unsigned)p.T;
+    if (D == 128) decode_causal_combine_kernel<128><<<grid, 128, 0, s>>>(p);
+    else if (D == 64) decode_causal_combine_kernel<64><<<grid, 64, 0, s>>>(p);
+    else return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

@@ -39,6 +39,10 @@ struct DecodeParams {
     float* part_ml;    // (B*H, nsplit, 2) partial (max, sum) in log2 units
     int B, H, Lmax, nsplit, split_keys;
     float scale_log2;  // scale * log2(e) (any sign)
+    // Causal multi-token attend only: T new queries per (b,h) (q and o are
+    // (B,H,T,D) f32), the last T cached positions of each sequence; query t
+    // sees keys [0, kv_len[b] - (T - 1 - t)). Partials are (B*H*T, nsplit).
+    int T;
 };
 
 // Up to two sources packed by one launch (attn_pack.hip): src[i] (BH,S,D)
@@ -173,6 +177,12 @@ hipError_t launch_fwd(const FwdParams& p, int mode, int D, int causal, int q_bf1
                       hipStream_t s);
 hipError_t launch_decode_split(const DecodeParams& p, int D, int q_bf16, hipStream_t s);
 hipError_t launch_decode_combine(const DecodeParams& p, int D, hipStream_t s);
+// Causal multi-token attend over the cache (attn_decode.hip): the split and
+// combine kernels for p.T new queries per (b,h), kDecodeGroup queries per
+// workgroup sharing each K/V row read.
+constexpr int kDecodeGroup = 4;
+hipError_t launch_decode_causal_split(const DecodeParams& p, int D, hipStream_t s);
+hipError_t launch_decode_causal_combine(const DecodeParams& p, int D, hipStream_t s);
 // KV-cache append (attn_decode.hip): row t < cnt[b] of the (B,H,T,D) sources
 // (f32, or bf16 when src_bf16) to position pos[b] + t of the bf16 cache
 // (B,H,Lmax,D). pos and cnt are device int32[B].

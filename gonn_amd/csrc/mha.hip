@@ -23,8 +23,10 @@
 #include <cstring>
 #include <mutex>
 #include <new>
+#include <vector>
 
 #include "../../include/gonn_hip.h"
+#include "kvcache_internal.h"
 
 namespace {
 
@@ -259,9 +261,116 @@ int run_forward(gonn_mha* m, const double* xq, const double* xk, const double* x
     return herr(hipGetLastError());
 }
 
+// Workspace of the incremental forward (256-byte aligned pieces): Y (B T 3E)
+// f64 | hq, hk, hv, ho (B H T dp) f32 | causal-attend workspace.
+struct IncLayout {
+    size_t y, hq, hk, hv, ho, aw, total;
+};
+
+IncLayout inc_layout(const gonn_mha* m, const gonn_kvcache* c, int B, int T) {
+    IncLayout L{};
+    const size_t n = (size_t)B * T;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = off;
+        off += al(bytes);
+        return at;
+    };
+    L.y = take(n * 3 * m->E * 8);
+    L.hq = take(n * m->H * m->dp * 4);
+    L.hk = take(n * m->H * m->dp * 4);
+    L.hv = take(n * m->H * m->dp * 4);
+    L.ho = take(n * m->H * m->dp * 4);
+    L.aw = take(gonn::kvcache_attend_causal_ws(c, T));
+    L.total = off + 256;
+    return L;
+}
+
+// The cache must hold this layer's heads at the padded head dim, and the
+// layer must be a square self-attention (one stacked q/k/v projection).
+bool inc_ok(const gonn_mha* m, const gonn_kvcache* c, int T, int* B) {
+    if (!m || !c || T <= 0) return false;
+    int H = 0, Lmax = 0, D = 0;
+    gonn::kvcache_dims(c, B, &H, &Lmax, &D);
+    return H == m->H && D == m->dp && m->kdim == m->E && m->vdim == m->E && T <= Lmax &&
+           (double)*B * T * 3 * m->E < 9.0e15;
+}
+
+// Incremental self-attention on device data: x, out fp64 (B, T, E).
+int run_incremental(gonn_mha* m, gonn_kvcache* c, const double* x, double* out, int B, int T,
+                    uint8_t* w, const IncLayout& L, hipStream_t s) {
+    const int E = m->E, H = m->H, D = m->D, dp = m->dp;
+    const size_t n = (size_t)B * T;
+    double* Y = (double*)(w + L.y);
+    float* hq = (float*)(w + L.hq);
+    float* hk = (float*)(w + L.hk);
+    float* hv = (float*)(w + L.hv);
+    float* ho = (float*)(w + L.ho);
+    {
+        const gonn_buf A = f64buf(x, n * E), Wb = f64buf(m->W[0], (size_t)3 * E * E);
+        gonn_buf C = f64buf(Y, n * 3 * E);
+        TRY(gonn_hip_gemm_f64_dev(&A, &Wb, &C, 1, (int)n, E, 3 * E, 0, 1, s));
+        const size_t per = n * H * dp;
+        hipLaunchKernelGGL(split_heads3_kernel, dim3(grid_for(3 * per)), dim3(256), 0, s, Y,
+                           m->b[0], hq, hk, hv, T, H, D, dp, per);
+        TRY(herr(hipGetLastError()));
+    }
+    std::vector<int> new_len;
+    TRY(gonn::kvcache_append_pending(c, hk, hv, T, s, &new_len));
+    int rc = gonn::kvcache_attend_causal_run(c, hq, ho, T, 1.0 / std::sqrt((double)D), w + L.aw, s,
+                                             true);  // nn/attention.go:136
+    if (rc == GONN_OK) {
+        const size_t tot = n * E;
+        hipLaunchKernelGGL(merge_heads_kernel, dim3(grid_for(tot)), dim3(256), 0, s, ho, Y, T, H,
+                           D, dp, tot);
+        rc = herr(hipGetLastError());
+        if (rc == GONN_OK) {
+            const gonn_buf A = f64buf(Y, tot), Wb = f64buf(m->W[3], (size_t)E * E);
+            gonn_buf C = f64buf(out, tot);
+            rc = gonn_hip_gemm_f64_dev(&A, &Wb, &C, 1, (int)n, E, E, 0, 1, s);
+        }
+        if (rc == GONN_OK) {
+            hipLaunchKernelGGL(add_bias_kernel, dim3(grid_for(tot)), dim3(256), 0, s, out,
+                               m->b[3], E, tot);
+            rc = herr(hipGetLastError());
+        }
+    }
+    // The new lengths become the cache's once everything has run.
+    if (rc == GONN_OK) rc = herr(hipStreamSynchronize(s));
+    if (rc == GONN_OK) {
+        gonn::kvcache_commit(c, &new_len);
+    } else {
+        (void)hipStreamSynchronize(s);
+        gonn::kvcache_restore(c);
+    }
+    return rc;
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t gonn_hip_mha_incremental_workspace_bytes(const gonn_mha* m, const gonn_kvcache* c, int T) {
+    int B = 0;
+    if (!inc_ok(m, c, T, &B)) return 0;
+    return inc_layout(m, c, B, T).total;
+}
+
+int gonn_hip_mha_forward_incremental_dev(gonn_mha* m, gonn_kvcache* c, const gonn_buf* x,
+                                         gonn_buf* out, int T, void* ws, size_t ws_bytes,
+                                         void* stream) {
+    int B = 0;
+    if (!inc_ok(m, c, T, &B) || !x || !out) return GONN_E_INVALID;
+    const size_t n = (size_t)B * T * m->E;
+    if (x->dtype != GONN_F64 || !x->ptr || x->bytes < n * 8 || out->dtype != GONN_F64 ||
+        !out->ptr || out->bytes < n * 8)
+        return GONN_E_INVALID;
+    const IncLayout L = inc_layout(m, c, B, T);
+    if (!ws || ws_bytes < L.total) return GONN_E_WORKSPACE;
+    uint8_t* base = (uint8_t*)al((size_t)ws);
+    return run_incremental(m, c, (const double*)x->ptr, (double*)out->ptr, B, T, base, L,
+                           (hipStream_t)stream);
+}
 
 int gonn_hip_mha_create(gonn_mha** out, int E, int H, int kdim, int vdim, const double* Wq,
                         const double* bq, const double* Wk, const double* bk, const double* Wv,

@@ -540,6 +540,32 @@ class KVCache:
                                                    _stream(stream)), "KVCache.attend")
         return out
 
+    def attend_causal_workspace_bytes(self, T: int) -> int:
+        return int(_lib.load().gonn_hip_kvcache_attend_causal_workspace_bytes(self._live(), int(T)))
+
+    def attend_causal(self, q, scale=None, out=None, ws=None, stream=None):
+        """Causal multi-token attend: q device (B,H,T,D) float32, the queries of
+        the last T cached positions of every sequence -> o (B,H,T,D) float32;
+        query t sees cached positions [0, len_b - T + t]. New relative to the
+        reference (no KV cache); equal to the rows of a top-left causal
+        attention over each whole sequence (nn/attention.go:185-196)."""
+        torch = _torch()
+        if q.dim() != 4 or tuple(q.shape[:2]) != (self.B, self.H) or q.shape[3] != self.D:
+            raise ValueError(f"KVCache.attend_causal: q must be ({self.B},{self.H},T,{self.D})")
+        T = int(q.shape[2])
+        if scale is None:
+            scale = 1.0 / math.sqrt(self.D)
+        if out is None:
+            out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+        need = self.attend_causal_workspace_bytes(T)
+        if ws is None:
+            ws = torch.empty(need, dtype=torch.uint8, device=q.device)
+        qb, ob = buf(q), buf(out)
+        check(_lib.load().gonn_hip_kvcache_attend_causal(
+            self._live(), ctypes.byref(qb), ctypes.byref(ob), T, float(scale),
+            ctypes.c_void_p(ws.data_ptr()), ws.numel(), _stream(stream)), "KVCache.attend_causal")
+        return out
+
 
 class DeviceMHA:
     """Device-resident multi-head attention (gonn_hip_mha_*): the forward of
@@ -639,6 +665,39 @@ class DeviceMHA:
             ctypes.byref(buf(out)), B, Tq, Tk, int(bool(causal)),
             ctypes.byref(kb) if kb is not None else None, ctypes.c_void_p(ws.data_ptr()),
             ws.numel(), st), "DeviceMHA.forward_dev")
+        return out
+
+    def incremental_workspace_bytes(self, cache: "KVCache", T: int) -> int:
+        return int(_lib.load().gonn_hip_mha_incremental_workspace_bytes(
+            self._live(), cache._live(), int(T)))
+
+    def forward_incremental_dev(self, x, cache: "KVCache", out=None, ws=None):
+        """Incremental self-attention on the device: x a contiguous torch
+        float64 CUDA tensor (B, T, E) of T new positions per sequence; their
+        K/V rows are appended to `cache` and out (B, T, E) float64 holds the
+        last T rows of the causal forward over everything the cache holds.
+        One host synchronisation per call; runs on torch's current stream.
+        New relative to the reference (no KV cache)."""
+        import torch
+        if x.dim() != 3 or x.shape[2] != self.E or x.dtype != torch.float64 or not x.is_cuda \
+                or not x.is_contiguous():
+            raise ValueError(f"DeviceMHA.forward_incremental_dev: x must be a contiguous "
+                             f"float64 CUDA tensor (B, T, {self.E})")
+        B, T = int(x.shape[0]), int(x.shape[1])
+        if B != cache.B:
+            raise ValueError(f"DeviceMHA.forward_incremental_dev: cache holds {cache.B} sequences")
+        need = self.incremental_workspace_bytes(cache, T)
+        if need == 0:
+            raise ValueError("DeviceMHA.forward_incremental_dev: cache and layer do not match "
+                             "(cache must be (B, H, *, 64|128) of a self-attention layer)")
+        if out is None:
+            out = torch.empty((B, T, self.E), dtype=torch.float64, device=x.device)
+        if ws is None:
+            ws = torch.empty(need, dtype=torch.uint8, device=x.device)
+        st = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        check(_lib.load().gonn_hip_mha_forward_incremental_dev(
+            self._live(), cache._live(), ctypes.byref(buf(x)), ctypes.byref(buf(out)), T,
+            ctypes.c_void_p(ws.data_ptr()), ws.numel(), st), "DeviceMHA.forward_incremental_dev")
         return out
 
 

@@ -379,3 +379,24 @@ class ResidentMultiHeadAttention:
         self._mha._check(q, k, v)
         kv_len = _kv_len_from_mask(key_padding_mask, q.shape[0], k.shape[1])
         return self.dev.forward(q, k, v, causal, kv_len)
+
+    def new_cache(self, batch: int, max_len: int) -> "hip.KVCache":
+        """A device KV cache for forward_incremental: batch sequences of up to
+        max_len positions, heads at the padded head dim (64 or 128)."""
+        dp = 64 if self._mha.HeadDim <= 64 else 128
+        return hip.KVCache(batch, self._mha.NumHeads, max_len, dp)
+
+    def forward_incremental(self, x, cache: "hip.KVCache"):
+        """MultiHeadAttention.forward_incremental on the device: the T new
+        positions of every sequence (x (B, T, E) host fp64) are projected,
+        appended and attended in one device pass (the causal multi-token
+        attend), with one upload, one download and one host synchronisation
+        per call instead of a round trip per position. Output row t equals row
+        (cached + t) of the causal forward over the whole sequence."""
+        torch = hip._torch()
+        x = np.ascontiguousarray(x, dtype=np.float64)
+        E = self._mha.EmbedDim
+        if x.ndim != 3 or x.shape[2] != E:
+            raise ValueError(f"MultiHeadAttention: x shape {x.shape}, want (B, T, {E})")
+        out = self.dev.forward_incremental_dev(torch.from_numpy(x).cuda(), cache)
+        return out.cpu().numpy()

@@ -253,6 +253,17 @@ int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, dou
                             void* stream);
 /* As gonn_hip_kvcache_attend with host fp64 q and o (B,H,D); synchronous. */
 int gonn_hip_kvcache_attend_f64(gonn_kvcache* c, const double* q, double* o, double scale);
+/* Causal multi-token attend (no counterpart in the reference, which has no
+ * KV cache; the result is nn/attention.go:185-196's top-left causal mask
+ * over the whole sequence): T new queries per (b,h), q and o GONN_F32
+ * (B,H,T,D) device buffers, whose own K/V rows are the last T cached
+ * positions of their sequence; query t attends cached positions
+ * [0, len_b - T + t]. Every length must be >= T (GONN_E_INVALID otherwise).
+ * Workspace: gonn_hip_kvcache_attend_causal_workspace_bytes(c, T) bytes; on
+ * `stream`, allocates nothing. T = 1 is gonn_hip_kvcache_attend.          */
+size_t gonn_hip_kvcache_attend_causal_workspace_bytes(const gonn_kvcache* c, int T);
+int gonn_hip_kvcache_attend_causal(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, int T,
+                                   double scale, void* ws, size_t ws_bytes, void* stream);
 
 /* ---- fp64 GEMM of the backend -------------------------------------------
  * backend.Backend.Gemm (backend/backend.go:61-78) on the device: row-major
@@ -321,6 +332,21 @@ size_t gonn_hip_mha_workspace_bytes(const gonn_mha* m, int B, int Tq, int Tk);
 int gonn_hip_mha_forward_dev(gonn_mha* m, const gonn_buf* q, const gonn_buf* k, const gonn_buf* v,
                              gonn_buf* out, int B, int Tq, int Tk, int causal,
                              const gonn_buf* kv_len, void* ws, size_t ws_bytes, void* stream);
+/* Incremental self-attention on the device (no counterpart in the reference,
+ * which has no KV cache): x (B, T, E) GONN_F64 device -> out (B, T, E), the
+ * last T rows of a causal Forward(seq, seq, seq) over every position the
+ * cache holds plus these. One stream: the stacked q/k/v projection, head
+ * split, append of the T new K/V rows to the cache, the causal multi-token
+ * attend, head merge and output projection; one host synchronisation per
+ * call, after which the cache lengths advance by T (they stay as they were
+ * on failure). The cache must be (B, H, *, dp) with dp = 64 or 128 (E/H
+ * zero-padded) and the layer a self-attention with kdim = vdim = E. The
+ * workspace is gonn_hip_mha_incremental_workspace_bytes(m, c, T) bytes (0:
+ * the handles do not fit together).                                       */
+size_t gonn_hip_mha_incremental_workspace_bytes(const gonn_mha* m, const gonn_kvcache* c, int T);
+int gonn_hip_mha_forward_incremental_dev(gonn_mha* m, gonn_kvcache* c, const gonn_buf* x,
+                                         gonn_buf* out, int T, void* ws, size_t ws_bytes,
+                                         void* stream);
 
 /* ---- device buffers ------------------------------------------------------
  * Replace gonn_dev_alloc / gonn_dev_free / gonn_dev_upload / gonn_dev_download
