@@ -505,7 +505,7 @@ def main():
                    "flop_per_step": pre["flop"], "wall_s": round(pre["wall_s"], 4)},
         "roofline": {"bound": "mfma", "achieved": round(ach, 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(ach / PEAK_BF16_TFLOPS, 4),
-                     "traffic": load_traffic("fwd_bf16:C3"), "kernel": "fwd_bf16_d128_kernel",
+                     "traffic": load_traffic("fwd_bf16:C3"), "kernel": "fwd_bf16_pipe_kernel",
                      "kernel_ms": round(pre["kernel_ms"], 5),
                      "launches_per_step": pre["launches"],
                      "pack_kv_ms": round(pre["pack_ms"], 5)},

@@ -133,6 +133,8 @@ class KVCache {
     std::vector<double> Attend(const std::vector<double>& q, double scale) const;
     std::vector<int> Lengths() const;
     void Reset();
+    // The C handle (gonn_kvcache*), for entries that take the cache.
+    void* Handle() const { return h_; }
     int B() const { return B_; }
     int H() const { return H_; }
     int Lmax() const { return Lmax_; }
@@ -167,6 +169,12 @@ class DeviceMHA {
     std::vector<double> Forward(const std::vector<double>& q, const std::vector<double>& k,
                                 const std::vector<double>& v, int B, int Tq, int Tk, bool causal,
                                 const std::vector<int>& kvLen = {}) const;
+    // Incremental self-attention over `cache` (gonn_hip_mha_forward_incremental_dev;
+    // new, the reference has no KV cache): x flat (B,T,E) fp64, the T new
+    // positions of every sequence -> (B,T,E), the last T rows of the causal
+    // forward over everything the cache then holds. One upload, one download.
+    std::vector<double> ForwardIncremental(const std::vector<double>& x, int B, int T,
+                                           KVCache& cache) const;
 
   private:
     void* h_ = nullptr;
@@ -352,6 +360,12 @@ class ResidentMultiHeadAttention {
     Tensor Forward(const Tensor& q, const Tensor& k, const Tensor& v, bool causal) const;
     Tensor ForwardMasked(const Tensor& q, const Tensor& k, const Tensor& v, bool causal,
                          const Tensor& keyPad) const;
+    // A KV cache for ForwardIncremental: heads at the padded head dim (64 or 128).
+    hip::KVCache NewCache(int batch, int maxLen) const;
+    // MultiHeadAttention::ForwardIncremental on the device: the T new
+    // positions are projected, appended and attended in one device pass
+    // (one host synchronisation per call, none per position).
+    Tensor ForwardIncremental(const Tensor& x, hip::KVCache& cache) const;
 
   private:
     MultiHeadAttention layer_;

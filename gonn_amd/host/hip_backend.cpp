@@ -354,5 +354,42 @@ std::vector<double> DeviceMHA::Forward(const std::vector<double>& q, const std::
     return out;
 }
 
+std::vector<double> DeviceMHA::ForwardIncremental(const std::vector<double>& x, int B, int T,
+                                                  KVCache& cache) const {
+    if (!h_) throw std::invalid_argument("hip: DeviceMHA: moved-from handle");
+    if (!cache.Handle()) throw std::invalid_argument("hip: KVCache: moved-from cache");
+    if (B != cache.B() || T <= 0)
+        throw std::invalid_argument("hip: DeviceMHA.ForwardIncremental: B must match the cache, T >= 1");
+    const size_t n = (size_t)B * T * E_;
+    need(x, n, "DeviceMHA.ForwardIncremental x");
+    const size_t wsb = gonn_hip_mha_incremental_workspace_bytes(
+        (const gonn_mha*)h_, (const gonn_kvcache*)cache.Handle(), T);
+    if (wsb == 0)
+        throw std::invalid_argument("hip: DeviceMHA.ForwardIncremental: the cache does not fit "
+                                    "the layer (B, H, *, 64|128) of a self-attention");
+    // Device buffers for x, out and the workspace, freed on every path.
+    struct Bufs {
+        gonn_buf x{}, out{}, ws{};
+        ~Bufs() {
+            (void)gonn_hip_free(&x);
+            (void)gonn_hip_free(&out);
+            (void)gonn_hip_free(&ws);
+        }
+    } b;
+    check(gonn_hip_alloc(&b.x, n, GONN_F64), "DeviceMHA.ForwardIncremental alloc");
+    check(gonn_hip_alloc(&b.out, n, GONN_F64), "DeviceMHA.ForwardIncremental alloc");
+    check(gonn_hip_alloc(&b.ws, (wsb + 3) / 4, GONN_I32), "DeviceMHA.ForwardIncremental alloc");
+    check(gonn_hip_memcpy_h2d(b.x.ptr, x.data(), n * sizeof(double), nullptr),
+          "DeviceMHA.ForwardIncremental upload");
+    check(gonn_hip_mha_forward_incremental_dev((gonn_mha*)h_, (gonn_kvcache*)cache.Handle(),
+                                               &b.x, &b.out, T, b.ws.ptr, b.ws.bytes, nullptr),
+          "DeviceMHA.ForwardIncremental");
+    std::vector<double> out(n);
+    check(gonn_hip_memcpy_d2h(out.data(), b.out.ptr, n * sizeof(double), nullptr),
+          "DeviceMHA.ForwardIncremental download");
+    check(gonn_hip_stream_sync(nullptr), "DeviceMHA.ForwardIncremental");
+    return out;
+}
+
 }  // namespace hip
 }  // namespace gonn

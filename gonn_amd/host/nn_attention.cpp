@@ -435,5 +435,17 @@ Tensor ResidentMultiHeadAttention::ForwardMasked(const Tensor& q, const Tensor& 
                        {B, Tq, layer_.EmbedDim});
 }
 
+hip::KVCache ResidentMultiHeadAttention::NewCache(int batch, int maxLen) const {
+    return hip::KVCache(batch, layer_.NumHeads, maxLen, layer_.HeadDim <= 64 ? 64 : 128);
+}
+
+Tensor ResidentMultiHeadAttention::ForwardIncremental(const Tensor& x, hip::KVCache& cache) const {
+    if (x.Shape.size() != 3 || x.Shape[2] != layer_.EmbedDim)
+        throw std::invalid_argument("MultiHeadAttention: x shape " + shape_str(x.Shape) +
+                                    ", want (B, T, " + std::to_string(layer_.EmbedDim) + ")");
+    const int B = x.Shape[0], T = x.Shape[1];
+    return Tensor::New(dev_.ForwardIncremental(x.Data, B, T, cache), {B, T, layer_.EmbedDim});
+}
+
 }  // namespace nn
 }  // namespace gonn

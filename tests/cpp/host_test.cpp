@@ -761,6 +761,23 @@ static void test_gpu() {
                                : y2.Data[((size_t)b * (T - 10) + (t - 10)) * E + e];
         const std::string tag = "ForwardIncremental H=" + std::to_string(H);
         CHECK(close(got, ref, 2e-2, 1e-2, tag.c_str()), "%s", tag.c_str());
+        // The resident layer decodes the same chunks on the device.
+        {
+            auto res = m.ToDevice();
+            gonn::hip::KVCache dc = res.NewCache(B, 32);
+            const Tensor r1 = res.ForwardIncremental(part(0, 10), dc);
+            const Tensor r2 = res.ForwardIncremental(part(10, T), dc);
+            CHECK(dc.Lengths() == std::vector<int>({T, T}), "resident cache lengths");
+            std::vector<double> rg(got.size());
+            for (int b = 0; b < B; b++)
+                for (int t = 0; t < T; t++)
+                    for (int e = 0; e < E; e++)
+                        rg[((size_t)b * T + t) * E + e] =
+                            t < 10 ? r1.Data[((size_t)b * 10 + t) * E + e]
+                                   : r2.Data[((size_t)b * (T - 10) + (t - 10)) * E + e];
+            const std::string rtag = "resident ForwardIncremental H=" + std::to_string(H);
+            CHECK(close(rg, ref, 2e-2, 1e-2, rtag.c_str()), "%s", rtag.c_str());
+        }
         // past Lmax: rejected, nothing written
         bool threw = false;
         try {
