@@ -240,8 +240,25 @@ int check_bwd(const gonn_attn_bwd_args* a) {
 // and Kt (BH,D,Skp) bf16, each region 256-byte aligned (Sp, Skp: the query
 // and key counts rounded up to kBwdPad).
 struct BwdLayout {
-    size_t lse2, delta, packed[7], total;
+    size_t lse2, delta, packed[5], ds, total;
 };
+
+// The bf16 backward stores dS (BH x Skp x Sp bf16, in the blocks of
+// BwdParams::ds) and computes dQ from it in one GEMM when that buffer is at
+// most kDsMaxBytes and one slice of it fits the kernels' 32-bit buffer
+// offsets; otherwise (and with
+// GONN_HIP_BWD_DQ=recompute) the dQ kernel forms S and dP again. The choice
+// depends on the shape only (and the environment), so a workspace sized by
+// gonn_hip_attn_workspace_bytes fits the call that follows.
+constexpr double kDsMaxBytes = 16.0 * 1024 * 1024 * 1024;
+bool bwd_use_ds(int mode, size_t BH, int S, int Sk) {
+    if (mode != GONN_ATTN_BF16_MFMA) return false;
+    const char* e = std::getenv("GONN_HIP_BWD_DQ");
+    if (e && std::strcmp(e, "recompute") == 0) return false;
+    const double Sp = (double)round_up((size_t)S, gonn::kBwdPad);
+    const double Skp = (double)round_up((size_t)Sk, gonn::kBwdPad);
+    return Skp * Sp * 2 < 2147483648.0 && (double)BH * Skp * Sp * 2 <= kDsMaxBytes;
+}
 
 BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D) {
     BwdLayout L{};
@@ -252,10 +269,15 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D) {
     L.delta = off;
     off = round_up(off + BH * Sp * 4, 256);
     if (mode == GONN_ATTN_BF16_MFMA) {
-        const bool keyside[7] = {false, false, true, true, false, false, true};
-        for (int i = 0; i < 7; i++) {
+        // Qb, dOb, Kb, Vb, Kt
+        const bool keyside[5] = {false, false, true, true, true};
+        for (int i = 0; i < 5; i++) {
             L.packed[i] = off;
             off = round_up(off + BH * (keyside[i] ? Skp : Sp) * D * 2, 256);
+        }
+        if (bwd_use_ds(mode, BH, S, Sk)) {
+            L.ds = off;
+            off = round_up(off + BH * Skp * Sp * 2, 256);
         }
     }
     L.total = off;
@@ -800,17 +822,13 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         void* dOb = w + L.packed[1];
         void* Kb = w + L.packed[2];
         void* Vb = w + L.packed[3];
-        void* Qt = w + L.packed[4];
-        void* dOt = w + L.packed[5];
-        void* Kt = w + L.packed[6];
+        void* Kt = w + L.packed[4];
         ProfScope ps("bwd_pack", s);
         gonn::PackParams p1{};
         p1.src[0] = a->q.ptr;
         p1.row[0] = Qb;
-        p1.tr[0] = Qt;
         p1.src[1] = a->dO.ptr;
         p1.row[1] = dOb;
-        p1.tr[1] = dOt;
         p1.mul[0] = qf.sign * qf.c2;
         p1.mul[1] = 1.f;
         p1.S = S;
@@ -830,8 +848,6 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p.dO = dOb;
         p.k = Kb;
         p.v = Vb;
-        p.qt = Qt;
-        p.dot = dOt;
         p.kt = Kt;
     } else {
         p.q = a->q.ptr;
@@ -839,11 +855,14 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p.k = a->k.ptr;
         p.v = a->v.ptr;
     }
+    const bool use_ds = bwd_use_ds(mode, (size_t)BH, S, p.Sk);
+    p.ds = use_ds ? (bf16*)(w + L.ds) : nullptr;
     {
         ProfScope ps("bwd_dkdv", s);
         TRYH(gonn::launch_bwd_dkdv(p, mode, D, a->causal, s));
     }
     ProfScope ps("bwd_dq", s);
+    if (use_ds) return herr(gonn::launch_bwd_dq_ds(p, D, a->causal, s));
     return herr(gonn::launch_bwd_dq(p, mode, D, a->causal, s));
 }
 

@@ -82,7 +82,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 // issues, with no dependency between them inside the step,
 //   MFMA  S(i+1) = Q K^T, dP(i+1) = dO V^T        (row tiles of query tile i+1)
 //   VALU  P(i) = exp2(S c - L log2e), dS(i) = P (dP - D), packed to bf16
-//   MFMA  dV^T += dO^T P(i-1), dK^T += Q^T dS(i-1) (transposed tiles of i-1)
+//   MFMA  dV^T += dO^T P(i-1), dK^T += Q^T dS(i-1) (row tiles of i-1, read
+//         transposed)
 // so no MFMA waits on the VALU of its own step. P(i) / dS(i) overwrite
 // P(i-1) / dS(i-1) 16 queries at a time, after the dV / dK MFMAs that read
 // those 16 queries were issued. The step is scheduled by hand: slot e issues
@@ -92,11 +93,15 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 // dV(ks, d-tiles), dK(ks, d-tiles), then a quarter of S/dP(i+1): 4 NDT + 4
 // accumulator chains interleave.
 //
-// LDS: 2-slot rings. Step i loads row tile i+2 into the slot row tile i left
-// (read by step i-1), transposed tile i into the slot of tile i-2, and L/D of
-// tile i+1; all land by the end of step i (one barrier per step). Causal
-// masks exist only on the first two query tiles of a key block (its query
-// tiles start at the block's first key).
+// LDS: the Q and dO tiles of 64 queries sit in 4-slot rings in the swizzled
+// slab layout of slab_swz, without padding. Step i reads tile i+1 (S, dP)
+// and tile i-1 (dV, dK) and keeps tile i for step i+1; it loads tile i+2
+// into the slot of tile i-2 and L/D of tile i+1, all landing by the end of
+// step i (one barrier per step). The dV / dK MFMAs take dO^T and Q^T as
+// their A operand (d rows, query k-slots): ds_read_b64_tr_b16 reads them
+// from the row tiles, so no transposed copy of Q or dO is packed, streamed
+// or staged. Causal masks exist only on the first two query tiles of a key
+// block (its query tiles start at the block's first key).
 // ---------------------------------------------------------------------------
 constexpr int kDkdvLookahead = 3;
 constexpr int kDkdvDmaSpan = 40;  // slots over which a step's tile loads are spread (0: all)
@@ -105,22 +110,17 @@ template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     constexpr int BN = 128;      // keys per workgroup
     constexpr int BM = 64;       // queries per tile
-    constexpr int RST = D + 8;   // Q / dO tile row stride (bf16)
-    constexpr int TST = BM + 8;  // Q^T / dO^T tile row stride (bf16)
     constexpr int NKS = D / 16;
     constexpr int NDT = D / 32;
-    // LDS slots (16 B) of one tile and the load instructions that fill them.
-    constexpr int RCP = RST / 8, RCD = D / 8, NRP = BM * RCP;
-    constexpr int TCP = TST / 8, TCD = BM / 8, NTP = D * TCP;
-    constexpr int NRI = (NRP + 255) / 256, NTI = (NTP + 255) / 256;
-    constexpr int RLAST = NRP - (NRI - 1) * 256, TLAST = NTP - (NTI - 1) * 256;
-    static_assert(RLAST % 64 == 0 && TLAST % 64 == 0, "partial loads must be whole waves");
-    constexpr int RTILE = BM * RST, TTILE = D * TST;  // bf16 elements
-    constexpr uint32_t RTB = RTILE * 2, TTB = TTILE * 2;
-    __shared__ __attribute__((aligned(16))) bf16 sQ[2 * RTILE];
-    __shared__ __attribute__((aligned(16))) bf16 sdO[2 * RTILE];
-    __shared__ __attribute__((aligned(16))) bf16 sQt[2 * TTILE];
-    __shared__ __attribute__((aligned(16))) bf16 sdOt[2 * TTILE];
+    // A Q / dO tile: BM rows x D/8 chunks of 16 bytes (slab layout), filled
+    // by NRI load instructions of 256 x 16 bytes.
+    constexpr int RTILE = BM * D;  // bf16 elements
+    constexpr uint32_t RTB = RTILE * 2;
+    constexpr int NRI = RTILE / 8 / 256;
+    static_assert(NRI * 256 * 8 == RTILE, "whole load instructions per tile");
+    constexpr int NSLOT = 4;
+    __shared__ __attribute__((aligned(16))) bf16 sQ[NSLOT * RTILE];
+    __shared__ __attribute__((aligned(16))) bf16 sdO[NSLOT * RTILE];
     __shared__ __attribute__((aligned(16))) float sLD[2][2 * BM];  // L*log2e, then D
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -156,29 +156,21 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     }
     const bf16* Qg = (const bf16*)p.q + (size_t)bh * Sp * D;
     const bf16* dOg = (const bf16*)p.dO + (size_t)bh * Sp * D;
-    const bf16* Qtg = (const bf16*)p.qt + (size_t)bh * D * Sp;
-    const bf16* dOtg = (const bf16*)p.dot + (size_t)bh * D * Sp;
     const float* lg = p.lse2 + (size_t)bh * Sp;
     const float* dg = p.delta + (size_t)bh * Sp;
 
-    // Byte offsets of this thread's slots inside one tile (pad slots and
-    // lanes past the tile load a dummy chunk of the tile).
-    uint32_t roff[NRI], toff[NTI];
+    // Byte offset in the (b,h) slice of the chunk this thread loads into
+    // tile position i*256 + tid (slab_chunk gives its row and chunk).
+    uint32_t roff[NRI];
     for (int i = 0; i < NRI; i++) {
-        const int pos = i * 256 + tid, r = pos / RCP, ch = pos % RCP;
-        roff[i] = (uint32_t)(((pos < NRP ? r : 0) * D + (ch < RCD ? ch : 0) * 8) * 2);
+        int r, c;
+        slab_chunk(i * 256 + tid, BM, r, c);
+        roff[i] = (uint32_t)((r * D + c * 8) * 2);
     }
-    for (int i = 0; i < NTI; i++) {
-        const int pos = i * 256 + tid, r = pos / TCP, ch = pos % TCP;
-        toff[i] = (uint32_t)(((pos < NTP ? r : 0) * Sp + (ch < TCD ? ch : 0) * 8) * 2);
-    }
-    const uint32_t rlast = wave * 64 < RLAST, tlast = wave * 64 < TLAST;  // wave-uniform
     const uint32_t slice = (uint32_t)Sp * D * 2;  // bytes of one (b,h) slice
     const brsrc rq = make_rsrc(Qg, slice), rdo = make_rsrc(dOg, slice);
-    const brsrc rqt = make_rsrc(Qtg, slice), rdot = make_rsrc(dOtg, slice);
     const brsrc rl = make_rsrc(lg, (uint32_t)Sp * 4), rd = make_rsrc(dg, (uint32_t)Sp * 4);
     const uint32_t lq = lds_addr(sQ) + wave * 1024, ldo = lds_addr(sdO) + wave * 1024;
-    const uint32_t lqt = lds_addr(sQt) + wave * 1024, ldot = lds_addr(sdOt) + wave * 1024;
     // Load j of the row tiles (Q: j < NRI, dO: j >= NRI) of query tile qb,
     // issued when the wave-uniform `on` is set (a scalar branch inside the
     // load statement keeps the step one basic block).
@@ -187,15 +179,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         const int i = j % NRI;
         const brsrc r = j < NRI ? rq : rdo;
         const uint32_t dst = (j < NRI ? lq : ldo) + slot * RTB + i * 4096;
-        dma16_if(r, dst, roff[i], so, i < NRI - 1 ? on : on & rlast);
-    };
-    // Load j of the transposed tiles (Q^T: j < NTI, dO^T: j >= NTI).
-    auto dma_tr = [&](int qb, int slot, int j, uint32_t on) {
-        const uint32_t so = (uint32_t)qb * BM * 2;
-        const int i = j % NTI;
-        const brsrc r = j < NTI ? rqt : rdot;
-        const uint32_t dst = (j < NTI ? lqt : ldot) + slot * TTB + i * 4096;
-        dma16_if(r, dst, toff[i], so, i < NTI - 1 ? on : on & tlast);
+        dma16_if(r, dst, roff[i], so, on);
     };
     // L and D of query tile qb: wave 0, lanes 0-15 load the 64 L values
     // (bytes 0-255 of sLD[slot]), lanes 16-31 the 64 D values (256-511).
@@ -208,11 +192,38 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     };
 
     // ---- MFMA operand reads (bytes from a slot's start) ----
-    const uint32_t rq0 = (uint32_t)(ln * RST + g * 8) * 2, tq0 = (uint32_t)(ln * TST + g * 8) * 2;
+    // S / dP A operand (Q / dO rows, d k-slots; ds_read_b128): row 32 mt + ln,
+    // chunk 2 kk + g at ((kk / 2) * BM + 32 mt) * 64 + (kk odd ? ra1 : ra0)
+    // (slab layout; h(32 mt + ln) = h(ln)).
+    const int hs = slab_swz(ln);
+    const uint32_t ra0 = (uint32_t)(ln * 64 + ((0 + g) ^ hs) * 16);
+    const uint32_t ra1 = (uint32_t)(ln * 64 + ((2 + g) ^ hs) * 16);
+    // dV / dK A operand (dO^T / Q^T: row d = 32 t + ln, k-slots 0-3 = queries
+    // 16 ks + 4g + 0..3, k-slots 4-7 = 16 ks + 8 + 4g + 0..3, the order of
+    // the P / dS words in pp / pd) by two ds_read_b64_tr_b16. That
+    // instruction gives lane L of a 16-lane group element L % 4 of the 8-byte
+    // reads of group lanes 4i + L / 4 (i = 0..3). Group lane s reads query
+    // row base + s / 4 at d = 32 t + 16 ((ln >> 4) & 1) + 4 (s % 4), so lane
+    // L receives d = 32 t + 16 ((ln >> 4) & 1) + L for queries base + 0..3.
+    // In the slab layout: slab t, row base + s / 4, chunk 2 ((ln >> 4) & 1) +
+    // (s / 2) % 2, byte 8 (s % 2); h(row) = g (+2 for the upper quads). A
+    // half-wave reads 4 rows x 64 bytes of one slab: 4 distinct 16-bank
+    // quarters, no conflict.
+    const int s16 = lane & 15;
+    const int tcx = 2 * ((ln >> 4) & 1) + ((s16 >> 1) & 1);
+    const uint32_t ta0 = (uint32_t)((4 * g + (s16 >> 2)) * 64 + (tcx ^ g) * 16 + 8 * (s16 & 1));
+    const uint32_t ta1 =
+        (uint32_t)((8 + 4 * g + (s16 >> 2)) * 64 + (tcx ^ (2 + g)) * 16 + 8 * (s16 & 1));
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4 lds_s4;
+    typedef __attribute__((address_space(3))) char lds_char;
+    lds_char* const tQ = (lds_char*)sQ;
+    lds_char* const tdO = (lds_char*)sdO;
     const char* cQ = (const char*)sQ;
     const char* cdO = (const char*)sdO;
-    const char* cQt = (const char*)sQt;
-    const char* cdOt = (const char*)sdOt;
+    auto rowa = [&](int kk, int mt) {  // S / dP operand offset inside a slot
+        return (uint32_t)(((kk >> 1) * BM + mt * 32) * 64) + ((kk & 1) ? ra1 : ra0);
+    };
 
     f32x16 dvacc[NDT], dkacc[NDT];
     for (int t = 0; t < NDT; t++) dvacc[t] = dkacc[t] = f32x16{};
@@ -224,6 +235,19 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     f32x4 mreg[8];
     if constexpr (MASK) mcol.init(p.mask, p.mask_sb, p.mask_sh, p.H, S, Sk, bh, kj);
     u32x4 pp[4], pd[4];  // P and dS of the tile dV/dK consume next, bf16 pairs per word
+    // dS-store path (layout at BwdParams::ds): this key block's dS for every
+    // query tile. Lane (ln, g) holds, in pd[ks], the dS of its key for the
+    // 8 queries of chunk 2 ks + g of a 64-query tile (queries 16 ks +
+    // {4g..4g+3, 8+4g..8+4g+3}, the vt_pos order); chunk c of the tile keeps
+    // the 128 keys' 16-byte pieces in key order, so one store writes two
+    // contiguous 512-byte runs. A padded key (kj >= Skv) stores zeros. Without
+    // p.ds the resource has no range and every store is dropped.
+    const bool store_ds = p.ds != nullptr;
+    const brsrc dsrs = make_rsrc(
+        store_ds ? p.ds + ((size_t)bh * (Skp / BN) + kb) * (size_t)(Sp / BM) * kDsTileElems : p.ds,
+        store_ds ? (uint32_t)(Sp / BM) * kDsTileElems * 2 : 0u);
+    const uint32_t dsvo = (uint32_t)((wave * 32 + ln) * 16 + g * BN * 16);
+    const bool ds_live = kj < Skv;
 
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
     // One pipeline step. sA <- S(i+1), dA <- dP(i+1); sB, dB = S(i), dP(i).
@@ -235,8 +259,8 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         constexpr bool MK = decltype(mk_tag)::value;  // tile i may need the causal mask
         const int qb = qb0 + i;
         if constexpr (MASK && HA) mcol.load(qb + 1, g, mreg);
-        // Loads for the next step: row tile i+2, transposed tile i, L/D i+1.
-        const uint32_t dr = HA && i + 2 < nq, dt = HB;
+        // Loads for the next steps: row tiles i+2, L/D i+1.
+        const uint32_t dr = HA && i + 2 < nq;
         const bool dl = HA;
         if (dl) dma_ld(qb + 1, (i + 1) & 1);
         // Causal mask (key > query), only on the first two tiles (steps with
@@ -252,8 +276,9 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
                         sB[mt][r] = kq > mt * 32 + 8 * (r >> 2) + (r & 3) ? -INFINITY : sB[mt][r];
             }
         }
-        const uint32_t rsl = (uint32_t)((i + 1) & 1) * RTB;   // row tile i+1
-        const uint32_t tsl = (uint32_t)((i + 1) & 1) * TTB;   // transposed tile i-1
+        const uint32_t rsl = (uint32_t)((i + 1) & 3) * RTB;   // row tile i+1 (S, dP)
+        const uint32_t tsl = (uint32_t)((i + 3) & 3) * RTB;   // row tile i-1 (dV, dK)
+        const uint32_t nsl = (uint32_t)((i + 2) & 3);     // slot of row tile i+2
         const int lsl = i & 1;                                 // L/D of tile i
 
         constexpr int HCn = HC ? 2 * NDT : 0, HAn = HA ? NKS : 0;
@@ -261,7 +286,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
         constexpr int NM = 4 * GW;
         constexpr int LA = kDkdvLookahead;  // LDS operand lead (MFMA slots)
         constexpr int NO = LA < 4 ? 4 : 8;
-        constexpr int NDMA = 2 * NRI + 2 * NTI;
+        constexpr int NDMA = 2 * NRI;
         constexpr int SPAN = kDkdvDmaSpan > 0 && kDkdvDmaSpan < NM ? kDkdvDmaSpan : NM;
         constexpr int DS = SPAN / NDMA > 0 ? SPAN / NDMA : 1;
         bf16x8 opr[NO];
@@ -269,12 +294,15 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             constexpr int e = decltype(E)::value, ks = e / GW, w = e % GW;
             if constexpr (w < HCn) {
                 constexpr int t = w % NDT;
-                const char* base = (w < NDT ? cdOt : cQt) + tsl + tq0;
-                opr[e % NO] = *(const bf16x8*)(base + (t * 32 * TST + ks * 16) * 2);
+                lds_char* const base = (w < NDT ? tdO : tQ) + tsl + (t * BM + 16 * ks) * 64;
+                const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + ta0));
+                const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(base + ta1));
+                const s4 b8[2] = {lo, hi};
+                opr[e % NO] = __builtin_bit_cast(bf16x8, b8);
             } else {
                 constexpr int u = w - HCn, kk = ks * (NKS / 4) + u / 4, mt = u & 1;
-                const char* base = ((u & 2) ? cdO : cQ) + rsl + rq0;
-                opr[e % NO] = *(const bf16x8*)(base + (mt * 32 * RST + kk * 16) * 2);
+                const char* base = ((u & 2) ? cdO : cQ) + rsl;
+                opr[e % NO] = *(const bf16x8*)(base + rowa(kk, mt));
             }
         };
         auto issue = [&](auto E) {
@@ -348,22 +376,29 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             constexpr int e = decltype(E)::value;
             if constexpr (e + LA < NM) fetch(std::integral_constant<int, e + LA>{});
             issue(E);
-            // Tile loads spread over the first SPAN slots: 1, 1 + DS, ...
-            if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
-                constexpr int d = (e - 1) / DS;
-                if constexpr (d < 2 * NRI) dma_row(qb + 2, i & 1, d, dr);
-                else dma_tr(qb, i & 1, d - 2 * NRI, dt);
+            // dS-store path: the dS of tile i-1 (pd, read by this step's dK
+            // MFMAs) goes out in the first four slots, before this step's
+            // VALU overwrites pd.
+            if constexpr (HC && e < 4) {
+                typedef int i32x4 __attribute__((ext_vector_type(4)));
+                const u32x4 v = ds_live ? pd[e] : u32x4{};
+                // Non-temporal (nt): the stream of dS is read once, by the dQ
+                // kernel, and would otherwise evict the Q / dO tiles this
+                // kernel re-reads from L2.
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    __builtin_bit_cast(i32x4, v), dsrs, dsvo,
+                    (uint32_t)((qb - 1) * kDsTileElems * 2 + 2 * e * BN * 16), 2);
             }
+            // Tile loads spread over the first SPAN slots: 1, 1 + DS, ...
+            if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA)
+                dma_row(qb + 2, nsl, (e - 1) / DS, dr);
             uops_at(E);
             __builtin_amdgcn_sched_barrier(0);
         });
         // Loads not placed in the stream (a step with too few MFMAs).
         static_for<NDMA>([&](auto Dd) {
             constexpr int d = decltype(Dd)::value;
-            if constexpr (NM == 0 || 1 + d * DS >= NM) {
-                if constexpr (d < 2 * NRI) dma_row(qb + 2, i & 1, d, dr);
-                else dma_tr(qb, i & 1, d - 2 * NRI, dt);
-            }
+            if constexpr (NM == 0 || 1 + d * DS >= NM) dma_row(qb + 2, nsl, d, dr);
         });
         uops_at(std::integral_constant<int, NM>{});
         GONN_VMCNT(0);
@@ -383,14 +418,13 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     for (int mt = 0; mt < 2; mt++) sX[mt] = dX[mt] = f32x16{};
     for (int kk = 0; kk < NKS; kk++)
         for (int mt = 0; mt < 2; mt++) {
-            sX[mt] = mfma_bf16(*(const bf16x8*)(cQ + rq0 + (mt * 32 * RST + kk * 16) * 2), kf[kk], sX[mt]);
-            dX[mt] = mfma_bf16(*(const bf16x8*)(cdO + rq0 + (mt * 32 * RST + kk * 16) * 2), vf[kk], dX[mt]);
+            sX[mt] = mfma_bf16(*(const bf16x8*)(cQ + rowa(kk, mt)), kf[kk], sX[mt]);
+            dX[mt] = mfma_bf16(*(const bf16x8*)(cdO + rowa(kk, mt)), vf[kk], dX[mt]);
         }
     if constexpr (MASK) {
         mcol.load(qb0, g, mreg);
         MaskRow::add(mreg, sX);
     }
-    __syncthreads();  // row slot 0 is reloaded by step 0
 
     // Steps 0 .. nq: step i has S/dP(i+1) while i+1 < nq, P/dS(i) while
     // i < nq, dV/dK(i-1) from i = 1.

@@ -1,0 +1,184 @@
+// attn_bwd_dqds.hip -- dQ of the bf16 backward from the dS the dK/dV kernel
+// stored (the dS-store path).
+//
+// Same result as bwd_dq_bf16_kernel (attn_bwd_dq.hip): dQ_i = scale *
+// sum_j dS_ij k_j over the keys query i attends (the reference's identity,
+// backend/cuda/gonn_cuda.cu:333-340). There the dQ kernel forms S and dP a
+// second time to get dS (three GEMM-equivalents per (query, key) pair); here
+// bwd_dkdv_bf16_kernel writes the dS it already formed, so dQ is one GEMM:
+//
+//   dQ^T (D x 128 queries of a block) = K^T (D x keys) . dS^T (keys x queries)
+//
+// The stored dS (layout at BwdParams::ds) keeps each 16-query group in the
+// vt_pos order in which a dK/dV lane holds it. K^T is the packed Kt
+// (BH, D, Skp) of attn_pack.hip, whose 16-key groups carry the same
+// permutation, so the A and B operands of v_mfma_f32_32x32x16_bf16 agree on
+// the key of every k-slot.
+//
+// One workgroup per 128 queries (4 waves x 32 queries), key tiles of 64
+// streamed through two-slot LDS rings (tile t+1 loads during step t):
+//  * Kt tile: D rows x 64 keys, rows padded to 72 bf16 (144 bytes), read as
+//    the A operand with one ds_read_b128 per MFMA;
+//  * dS^T tile: 64 keys x 128 queries, stored chunk-major: 16 columns of
+//    8 queries, each 64 keys x 16 bytes, 1088 bytes apart (64 bytes of pad).
+//    One load instruction fills one column from 1 KB contiguous in HBM. It
+//    is read as the B operand with ds_read_b64_tr_b16: per 16-lane group
+//    that instruction returns to lane L the element L % 4 of the 8-byte
+//    reads of lanes 4i + L / 4 (i = 0..3); with lane s of the group reading
+//    key k0 + s / 4 at query column c0 + 4 (s % 4), lane L receives keys
+//    k0 .. k0+3 of column c0 + L, i.e. 4 k-slots of the MFMA B operand.
+//    Two such reads (keys 16ks + 4g.. and 16ks + 8 + 4g..) fill the 8
+//    k-slots of lane group g in Kt's key order. A half-wave reads 4 keys x
+//    32 queries, 4 columns x 64 bytes, which the 1088-byte column stride
+//    puts on 64 distinct banks.
+// Causal: a query block attends keys below its end (top-left mask); the
+// masked (key > query) entries of the diagonal tiles were stored as zeros.
+// Key padding: keys at or past kv_len were stored as zeros, and key tiles
+// past the last valid key are not read. Query columns past S hold values
+// the dK/dV kernel never wrote; a dQ^T column depends on its own dS^T column
+// only, and those rows are not written.
+#include "common.h"
+#include "kernels.h"
+
+namespace gonn {
+
+template <int D, bool CAUSAL>
+__global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
+    constexpr int BM = 128, BN = 64, NT = 256;
+    constexpr int NDT = D / 32;
+    constexpr int KST = BN + 8;   // Kt tile row stride (bf16)
+    constexpr int SCB = BN * 16 + 64;  // dS^T tile column stride (bytes)
+    constexpr int NSC = BM / 8;        // dS^T tile columns
+    constexpr uint32_t KTB = D * KST * 2, STB = NSC * SCB;
+    __shared__ __attribute__((aligned(16))) bf16 sK[2 * D * KST];
+    __shared__ __attribute__((aligned(16))) char sS[2 * STB];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 5, ln = lane & 31;
+    int bh, qb;
+    map_block(blockIdx.x, p.Sp / BM, p.BH, CAUSAL, bh, qb);
+    const int S = p.S, Sp = p.Sp, Skp = p.Skp;
+    const int q0 = qb * BM;
+    if (q0 >= S) return;  // padding rows only
+    int kend = bwd_keys(p, bh);
+    if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
+    const int ntiles = (kend + BN - 1) / BN;
+
+    // ---- tile loads (direct to LDS): instruction i of thread tid fills the
+    // 16-byte position i*NT + tid of a padded tile; pad positions load a
+    // dummy chunk of their row ----
+    constexpr int KCP = KST / 8, NKP = D * KCP;          // Kt: D rows x 9
+    constexpr int NKI = (NKP + NT - 1) / NT;
+    constexpr int KLAST = NKP - (NKI - 1) * NT;
+    static_assert(KLAST % 64 == 0, "partial loads must be whole waves");
+    static_assert(NSC % 4 == 0, "dS^T columns spread over the four waves");
+    uint32_t koff[NKI];
+    for (int i = 0; i < NKI; i++) {
+        const int pos = i * NT + tid, r = pos / KCP, c = pos % KCP;
+        koff[i] = (uint32_t)((((pos < NKP) ? r : 0) * Skp + (c < BN / 8 ? c : 0) * 8) * 2);
+    }
+    const uint32_t klast = wave * 64 < KLAST;
+    const bf16* Ktg = (const bf16*)p.kt + (size_t)bh * D * Skp;
+    const brsrc krs = make_rsrc(Ktg, (uint32_t)D * Skp * 2);
+    // This slice's stored dS: (Skp/128 key blocks) x (Sp/64 query tiles)
+    // blocks of kDsTileElems.
+    const int nqt = Sp / 64, qt0 = q0 / 64;
+    const brsrc srs = make_rsrc((const bf16*)p.ds + (size_t)bh * (Skp / 128) * nqt * kDsTileElems,
+                                (uint32_t)(Skp / 128) * nqt * kDsTileElems * 2);
+    const uint32_t kl = lds_addr(sK) + wave * 1024, sl = lds_addr(sS);
+    auto load_tile = [&](int t, int slot) {
+        for (int i = 0; i < NKI; i++) {
+            const uint32_t dst = kl + slot * KTB + i * NT * 16;
+            if (i < NKI - 1) dma16(krs, dst, koff[i], (uint32_t)t * BN * 2);
+            else dma16_if(krs, dst, koff[i], (uint32_t)t * BN * 2, klast);
+        }
+        // Column c = 4 i + wave: query tile qt0 + c / 8, chunk c % 8, the 64
+        // keys of half t % 2 of key block t / 2: lane L loads key L.
+        for (int i = 0; i < NSC / 4; i++) {
+            const int c = 4 * i + wave;
+            const uint32_t so = (uint32_t)(((t / 2) * nqt + qt0 + c / 8) * kDsTileElems * 2 +
+                                           ((c % 8) * 128 + (t % 2) * 64) * 16);
+            dma16_nt(srs, sl + slot * STB + c * SCB, (uint32_t)lane * 16, so);
+        }
+    };
+
+    // ---- operand reads ----
+    // A (Kt): row dt*32 + ln, chunk 2ks + g.
+    const uint32_t ka = (uint32_t)(ln * KST + g * 8) * 2;
+    // B (dS^T): this lane reads key 4g + (lane & 15) / 4 (+16ks, +8 for the
+    // second half of the k-slots) at query column qc = 32 wave + 16
+    // ((lane >> 4) & 1) + 4 (lane & 3): column qc / 8, byte 2 (qc % 8).
+    const int s16 = lane & 15;
+    const int qc = 32 * wave + 16 * ((lane >> 4) & 1) + 4 * (s16 & 3);
+    const uint32_t sb = (uint32_t)((qc / 8) * SCB + (4 * g + (s16 >> 2)) * 16 + (qc % 8) * 2);
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s4 lds_s4;
+    typedef __attribute__((address_space(3))) char lds_char;
+    lds_char* const sS3 = (lds_char*)sS;
+    // byte: offset from the start of sS
+    auto tr_read = [&](uint32_t byte) {
+        return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sS3 + byte));
+    };
+
+    f32x16 acc[NDT];
+    for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x16{};
+    if (ntiles > 0) {
+        load_tile(0, 0);
+        GONN_VMCNT(0);
+        __syncthreads();
+        for (int t = 0; t < ntiles; t++) {
+            const int cur = t & 1;
+            if (t + 1 < ntiles) load_tile(t + 1, cur ^ 1);
+            const char* kbase = (const char*)sK + cur * KTB + ka;
+            const uint32_t sbase = cur * STB + sb;
+            for (int ks = 0; ks < BN / 16; ks++) {
+                const s4 lo = tr_read(sbase + (uint32_t)(16 * ks) * 16);
+                const s4 hi = tr_read(sbase + (uint32_t)(16 * ks + 8) * 16);
+                const s4 b8[2] = {lo, hi};
+                const bf16x8 bop = __builtin_bit_cast(bf16x8, b8);
+                for (int dt = 0; dt < NDT; dt++) {
+                    const bf16x8 aop =
+                        *(const bf16x8*)(kbase + (dt * 32 * KST + ks * 16) * 2);
+                    acc[dt] = mfma_bf16(aop, bop, acc[dt]);
+                }
+            }
+            GONN_VMCNT(0);
+            __syncthreads();
+        }
+    }
+
+    // Lane (ln, g) holds query column 32 wave + ln of the block (stored
+    // order), i.e. query q0 + 16 (c / 16) + vt_pos(c % 16); dQ^T register r
+    // of d-tile dt is d = 32 dt + 8 (r / 4) + 4 g + r % 4.
+    const int c = 32 * wave + ln;
+    const int qi = q0 + (c & ~15) + vt_pos(c & 15);
+    if (qi < S) {
+        const float sc = p.dqs;
+        float* dqr = p.dq + ((size_t)bh * S + qi) * D;
+        for (int dt = 0; dt < NDT; dt++)
+            for (int rq4 = 0; rq4 < 4; rq4++) {
+                f32x4 a;
+                for (int k = 0; k < 4; k++) a[k] = acc[dt][rq4 * 4 + k] * sc;
+                *(f32x4*)(dqr + dt * 32 + rq4 * 8 + g * 4) = a;
+            }
+    }
+}
+
+hipError_t launch_bwd_dq_ds(const BwdParams& p, int D, int causal, hipStream_t s) {
+    if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0 || !p.ds || !p.kt)
+        return hipErrorInvalidValue;
+    const dim3 grid((p.Sp / 128) * p.BH);
+    if (D == 64) {
+        if (causal) bwd_dq_ds_kernel<64, true><<<grid, 256, 0, s>>>(p);
+        else bwd_dq_ds_kernel<64, false><<<grid, 256, 0, s>>>(p);
+    } else if (D == 128) {
+        if (causal) bwd_dq_ds_kernel<128, true><<<grid, 256, 0, s>>>(p);
+        else bwd_dq_ds_kernel<128, false><<<grid, 256, 0, s>>>(p);
+    } else {
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace gonn

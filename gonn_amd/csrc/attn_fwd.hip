@@ -422,7 +422,7 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
 // to arrive before the step's closing wait). The prologue stages K(0) in Vt
 // slot 1 (free until step 0 loads V(1)), so K(0), K(1), K(2), V(0) and the Q
 // fragment arrive in one memory round trip. Tiles are stored without padding
-// in the swizzled layout of fwd_tile_swz (conflict-free MFMA operand reads,
+// in the swizzled layout of slab_swz (conflict-free MFMA operand reads,
 // 64 contiguous bytes per row per load, no dummy or partial loads: four load
 // instructions per 16 KB tile). Each load's M0 (its LDS base) is written one
 // slot ahead, so the M0 -> LDS-DMA wait state is filled by an MFMA, not a nop.
@@ -434,29 +434,6 @@ __global__ __launch_bounds__(256, MASK ? 2 : 3) void fwd_bf16_kernel(FwdParams p
 // the same in every step (tail variants spilled), for two masked S^T tiles
 // per q-block.
 // ---------------------------------------------------------------------------
-// Swizzled tile layout of the pipelined forward. A tile of `rows` rows of
-// 16-byte chunks (K: 64 keys x D/8; Vt: D x 8) is stored in 64-byte
-// segments of four chunks: position (16 bytes each)
-//   pos(row, chunk) = ((chunk / 4) * rows + row) * 4 + ((chunk % 4) ^ h(row)),
-//   h(row) = (row >> 2) & 3.
-// A load instruction then fills 16 rows x 64 contiguous bytes (coalesced).
-// LDS on gfx950 has 64 banks (256 bytes); a ds_read_b128 serves 16 lanes per
-// cycle, but not 16 consecutive ones: a probe of SQ_LDS_BANK_CONFLICT over
-// 50 lane patterns fits only groups within one half-wave made of 4-lane
-// quads {0, 2, 5, 7} and {1, 3, 4, 6} of that half (or {0, 3, 5, 6} and
-// {1, 2, 4, 7}). A read of rows 32m + ln, one chunk, puts quad q of a half
-// on banks 4 (ln & 3) + (chunk % 4 ^ (q & 3)): distinct within every such
-// group, so the operand reads are conflict-free. (h = ((row >> 1) ^
-// (row >> 3)) & 3, distinct over 16 consecutive lanes, measured 2-way.)
-// No padding: a tile is 16 KB at D = 128 (the padded tiles were 17 and 18 KB).
-GONN_DEV int fwd_tile_swz(int row) { return (row >> 2) & 3; }
-// Row and chunk held by position `pos` of a tile of `rows` rows.
-GONN_DEV void fwd_tile_chunk(int pos, int rows, int& row, int& chunk) {
-    const int q = pos >> 2;
-    row = q % rows;
-    chunk = (q / rows) * 4 + ((pos & 3) ^ fwd_tile_swz(row));
-}
-
 constexpr float kSumBound = 16384.f;  // 2^14: row-sum bound of one 64-key tile
 // Wave issue priority (s_setprio) during a step's MFMA stream.
 constexpr int kFwdStreamPrio = 1;
@@ -474,7 +451,7 @@ template <int D, bool CAUSAL, typename QT, bool MASK>
 __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kernel(FwdParams p) {
     constexpr int NW = kFwdWaves, BM = NW * 32, BN = 64, NT = NW * 64;
     constexpr int NKS = D / 16, NDT = D / 32;
-    // Swizzled tiles without padding (layout at fwd_tile_swz): 16 KB per tile
+    // Swizzled tiles without padding (layout at slab_swz): 16 KB per tile
     // at D = 128, two-slot K and Vt rings, 64 KB per workgroup. Step t loads
     // K(t+3) and V(t+1), each one step ahead of its use.
     constexpr uint32_t KTB = BN * D * 2, VTB = D * BN * 2;  // slot bytes
@@ -531,16 +508,16 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     };
 
     // ---- tile loads: instruction i of thread tid fills 16-byte position
-    // i*NT + tid of a tile (fwd_tile_chunk gives the row and chunk it holds) ----
+    // i*NT + tid of a tile (slab_chunk gives the row and chunk it holds) ----
     constexpr int NKP = BN * D / 8, NVP = D * BN / 8;  // 16-byte chunks per tile
     static_assert(NKP % NT == 0 && NVP % NT == 0, "tiles are whole load instructions");
     constexpr int NKI = NKP / NT, NVI = NVP / NT;      // loads per tile
     uint32_t koff[NKI], voff[NVI];
     for (int i = 0; i < NKI; i++) {
         int r, c;
-        fwd_tile_chunk(i * NT + tid, BN, r, c);
+        slab_chunk(i * NT + tid, BN, r, c);
         koff[i] = (uint32_t)((r * D + c * 8) * 2);
-        fwd_tile_chunk(i * NT + tid, D, r, c);
+        slab_chunk(i * NT + tid, D, r, c);
         voff[i] = (uint32_t)((r * Skp + c * 8) * 2);
     }
     const bf16* Kg = (const bf16*)p.k + (size_t)bh * Skp * D;
@@ -568,11 +545,11 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     };
 
     // ---- MFMA operand reads: K row mt*32 + ln, Vt row dt*32 + ln; chunk
-    // 2ks + g. In the layout of fwd_tile_swz the byte offset of (row, chunk) in a tile is
+    // 2ks + g. In the layout of slab_swz the byte offset of (row, chunk) in a tile is
     // (chunk / 4) * rows * 64 + row * 64 + ((chunk % 4) ^ h(row)) * 16; for
     // row = 32 m + ln and chunk = 2 ks + g the lane part depends on ks only
     // through ks & 1, so two lane offsets serve every K and Vt read. ----
-    const int hs = fwd_tile_swz(ln);
+    const int hs = slab_swz(ln);
     const uint32_t qa0 = (uint32_t)(ln * 64 + ((0 + g) ^ hs) * 16);  // k-step even
     const uint32_t qa1 = (uint32_t)(ln * 64 + ((2 + g) ^ hs) * 16);  // k-step odd
     const char* sKc = (const char*)sKb;

@@ -161,6 +161,12 @@ GONN_DEV void dma16(brsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
                  :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff)
                  : "memory");
 }
+// dma16 with the non-temporal hint, for data read exactly once.
+GONN_DEV void dma16_nt(brsrc r, uint32_t lds, uint32_t voff, uint32_t soff) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen nt lds"
+                 :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(r), "s"(soff)
+                 : "memory");
+}
 // dma16 when the wave-uniform `on` is non-zero. The skip is a scalar branch
 // inside the asm statement, so the caller's code stays one basic block (an
 // exec-masked branch around the load would split the hand-scheduled MFMA
@@ -197,6 +203,29 @@ GONN_DEV uint32_t lds_addr(const void* p) {
 }
 // s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained), n < 16.
 #define GONN_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+
+// Swizzled slab layout of LDS tiles (forward K / Vt tiles, dK/dV Q / dO
+// tiles). A tile of `rows` rows of 16-byte chunks is stored in 64-byte
+// segments of four chunks: position (16 bytes each)
+//   pos(row, chunk) = ((chunk / 4) * rows + row) * 4 + ((chunk % 4) ^ h(row)),
+//   h(row) = (row >> 2) & 3.
+// A load instruction then fills 16 rows x 64 contiguous bytes (coalesced).
+// LDS on gfx950 has 64 banks (256 bytes); a ds_read_b128 serves 16 lanes per
+// cycle, but not 16 consecutive ones: a probe of SQ_LDS_BANK_CONFLICT over
+// 50 lane patterns fits only groups within one half-wave made of 4-lane
+// quads {0, 2, 5, 7} and {1, 3, 4, 6} of that half (or {0, 3, 5, 6} and
+// {1, 2, 4, 7}). A read of rows 32m + ln, one chunk, puts quad q of a half
+// on banks 4 (ln & 3) + (chunk % 4 ^ (q & 3)): distinct within every such
+// group, so the operand reads are conflict-free. (h = ((row >> 1) ^
+// (row >> 3)) & 3, distinct over 16 consecutive lanes, measured 2-way.)
+// No padding: a tile of 64 rows x 128 bf16 is 16 KB.
+GONN_DEV int slab_swz(int row) { return (row >> 2) & 3; }
+// Row and chunk held by position `pos` of a tile of `rows` rows.
+GONN_DEV void slab_chunk(int pos, int rows, int& row, int& chunk) {
+    const int q = pos >> 2;
+    row = q % rows;
+    chunk = (q / rows) * 4 + ((pos & 3) ^ slab_swz(row));
+}
 
 // ---- hand scheduling helpers ----
 // Forces x to be computed at this point of the program (an empty asm that

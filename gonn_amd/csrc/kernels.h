@@ -58,16 +58,21 @@ struct PackParams {
 };
 
 struct BwdParams {
-    // bf16 mode: packed operands in the workspace (row-major (BH,Sp,D) and
-    // transposed (BH,D,Sp)); fp32 mode: the caller's (BH,S,D) f32 buffers in
-    // q, k, v, dO and null transposes.
+    // bf16 mode: packed operands in the workspace (row-major (BH,Sp,D), K^T
+    // (BH,D,Skp)); fp32 mode: the caller's (BH,S,D) f32 buffers in q, k, v,
+    // dO and a null kt.
     const void* q;
     const void* k;
     const void* v;
     const void* dO;
-    const void* qt;   // Q^T  bf16 mode only
     const void* kt;   // K^T  bf16 mode only
-    const void* dot;  // dO^T bf16 mode only
+    // dS-store path (bf16 mode): dS in blocks of kDsTileElems bf16, block
+    // ((bh * Skp/128 + key block) * Sp/64 + query tile); inside a block,
+    // 16-byte piece (c * 128 + key) holds the key's dS for the 8 queries of
+    // chunk c (queries 16 (c/2) + {4(c%2)..+3, 8+4(c%2)..+3}, the vt_pos
+    // order of a 16-query group). Written by the dK/dV kernel when set, read
+    // by bwd_dq_ds_kernel; null: the dQ kernel forms dS itself.
+    bf16* ds;
     const float* lse2;   // (BH,Sp) LSE * log2(e); +inf on pad rows
     const float* delta;  // (BH,Sp) rowsum(dO * O); 0 on pad rows
     float* dq;           // (BH,S,D)
@@ -88,7 +93,7 @@ struct BwdParams {
     // their dK, dV rows are zero and they add nothing to dQ.
     const int* kv_len;
     int H;
-    // Optional additive mask, as in FwdParams (fp32 kernels only).
+    // Optional additive mask, as in FwdParams.
     const float* mask;
     long long mask_sb, mask_sh;
 };
@@ -198,8 +203,12 @@ hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipS
 hipError_t launch_bwd_dq(const BwdParams& p, int mode, int D, int causal, hipStream_t s);
 // bf16 dQ (attn_bwd_dq.hip); launch_bwd_dq dispatches mode 1 here.
 hipError_t launch_bwd_dq_bf16(const BwdParams& p, int D, int causal, hipStream_t s);
+// bf16 dQ from the stored dS (attn_bwd_dqds.hip): p.ds and p.kt set.
+hipError_t launch_bwd_dq_ds(const BwdParams& p, int D, int causal, hipStream_t s);
 // Sequence padding of the backward's workspace layouts.
 constexpr int kBwdPad = 128;
+// bf16 elements of one (128-key block, 64-query tile) block of stored dS.
+constexpr int kDsTileElems = 128 * 64;
 
 // f64 <-> f32/bf16 conversion with optional head-dim padding:
 // dst (rows, dpad) <- src (rows, d); pad columns are zero.

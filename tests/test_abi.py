@@ -223,7 +223,8 @@ def test_bwd_argument_errors():
 
 def test_bwd_workspace_contract():
     """fp32 mode needs LSE*log2(e) and D_i rows (BH, Sp) in f32; bf16 mode adds
-    seven packed bf16 operands (BH, Sp, D), with Sp = S rounded up to 128."""
+    five packed bf16 operands (Q, dO, K, V rows and K^T; BH x Sp x D each),
+    with Sp = S rounded up to 128."""
     lib = _lib.load()
     B, H, S, D = 1, 2, 200, 128
     n = B * H * S * D * 4
@@ -236,7 +237,7 @@ def test_bwd_workspace_contract():
     assert lib.gonn_hip_attn_bwd(ctypes.byref(a), P, nb32 - 1, None) == GONN_E_WORKSPACE
     a.mode = 1
     nb16 = lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
-    assert nb16 >= nb32 + 7 * B * H * Sp * D * 2
+    assert nb16 >= nb32 + 5 * B * H * Sp * D * 2
     assert lib.gonn_hip_attn_bwd(ctypes.byref(a), P, nb32, None) == GONN_E_WORKSPACE
 
 

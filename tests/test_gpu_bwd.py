@@ -77,6 +77,45 @@ def test_bwd_scale_variants(mode):
         assert_close(dv, rv, mode, f"dV scale={scale}")
 
 
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("case", ["self", "kv_len", "mask"])
+def test_bwd_bf16_dq_paths(D, causal, case, monkeypatch):
+    """The bf16 backward's two dQ paths: dQ from the dS the dK/dV kernel
+    stores (the default) and dQ with S and dP formed a second time
+    (GONN_HIP_BWD_DQ=recompute; also taken when the dS buffer would exceed
+    its cap). Both are held to the bf16 bar against the oracle, with key
+    padding and an additive mask; dK and dV come from the same kernel on
+    either path and agree bitwise."""
+    from gonn_amd import hip
+    from tests.test_gpu_masked import _mask_of
+    B, H, S = 2, 2, 300
+    lens = np.array([300, 171], dtype=np.int32) if case != "self" else None
+    m = _mask_of("BHTqTk4", B, H, S, S, 77)[0] if case == "mask" else None
+    q, k, v, g = (randn((B * H, S, D), 4100 + D + i) for i in range(4))
+    dev = [torch.from_numpy(x).cuda().reshape(B, H, S, D) for x in (q, k, v, g)]
+    kl = torch.from_numpy(lens).cuda() if lens is not None else None
+    md = torch.from_numpy(m.astype(np.float32)).cuda() if m is not None else None
+    o, l = hip.attn_fwd(*dev[:3], causal=causal, mode="bf16", kv_len=kl, attn_mask=md)
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H,
+                                          attn_mask=m)
+    got = {}
+    for path in ("ds", "recompute"):
+        if path == "recompute":
+            monkeypatch.setenv("GONN_HIP_BWD_DQ", "recompute")
+        else:
+            monkeypatch.delenv("GONN_HIP_BWD_DQ", raising=False)
+        say(f"bwd dq path={path} D={D} causal={causal} case={case}")
+        dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=causal, mode="bf16",
+                                  kv_len=kl, attn_mask=md)
+        torch.cuda.synchronize()
+        got[path] = [x.reshape(B * H, S, D).cpu().numpy() for x in (dq, dk, dv)]
+        for x, ref, n in zip(got[path], (rq, rk, rv), ("dQ", "dK", "dV")):
+            assert_close(x, ref, "bf16", f"{n} path={path}")
+    assert np.array_equal(got["ds"][1], got["recompute"][1])
+    assert np.array_equal(got["ds"][2], got["recompute"][2])
+
+
 def test_bwd_golden_fixtures_via_f64_entry():
     """The committed torch-fp64 fixtures (square cases) through the reference-
     named f64 entry points FlashAttnF64Fwd / FlashAttnF64Bwd (head dims below
