@@ -238,15 +238,18 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     // dS-store path (layout at BwdParams::ds): this key block's dS for every
     // query tile. Lane (ln, g) holds, in pd[ks], the dS of its key for the
     // 8 queries of chunk 2 ks + g of a 64-query tile (queries 16 ks +
-    // {4g..4g+3, 8+4g..8+4g+3}, the vt_pos order); chunk c of the tile keeps
-    // the 128 keys' 16-byte pieces in key order, so one store writes two
-    // contiguous 512-byte runs. A padded key (kj >= Skv) stores zeros. Without
+    // {4g..4g+3, 8+4g..8+4g+3}, the vt_pos order); a block keeps the 16-byte
+    // pieces of each half of the 128 keys chunk by chunk, so one store
+    // writes contiguous 512-byte runs and the dQ kernel reads the 64 keys of
+    // one of its steps as one contiguous 8 KB. A padded key (kj >= Skv) stores zeros. Without
     // p.ds the resource has no range and every store is dropped.
     const bool store_ds = p.ds != nullptr;
     const brsrc dsrs = make_rsrc(
         store_ds ? p.ds + ((size_t)bh * (Skp / BN) + kb) * (size_t)(Sp / BM) * kDsTileElems : p.ds,
         store_ds ? (uint32_t)(Sp / BM) * kDsTileElems * 2 : 0u);
-    const uint32_t dsvo = (uint32_t)((wave * 32 + ln) * 16 + g * BN * 16);
+    // Piece (key / 64) * 512 + chunk * 64 + key % 64 of a block, chunk 2e + g
+    // for store e.
+    const uint32_t dsvo = (uint32_t)(((wave >> 1) * 512 + (wave & 1) * 32 + ln + g * 64) * 16);
     const bool ds_live = kj < Skv;
 
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
@@ -387,7 +390,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
                 // kernel re-reads from L2.
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(i32x4, v), dsrs, dsvo,
-                    (uint32_t)((qb - 1) * kDsTileElems * 2 + 2 * e * BN * 16), 2);
+                    (uint32_t)((qb - 1) * kDsTileElems * 2 + e * 2048), 2);
             }
             // Tile loads spread over the first SPAN slots: 1, 1 + DS, ...
             if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA)

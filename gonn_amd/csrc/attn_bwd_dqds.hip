@@ -7,7 +7,7 @@
 // second time to get dS (three GEMM-equivalents per (query, key) pair); here
 // bwd_dkdv_bf16_kernel writes the dS it already formed, so dQ is one GEMM:
 //
-//   dQ^T (D x 128 queries of a block) = K^T (D x keys) . dS^T (keys x queries)
+//   dQ^T (D x 256 queries of a block) = K^T (D x keys) . dS^T (keys x queries)
 //
 // The stored dS (layout at BwdParams::ds) keeps each 16-query group in the
 // vt_pos order in which a dK/dV lane holds it. K^T is the packed Kt
@@ -15,11 +15,16 @@
 // permutation, so the A and B operands of v_mfma_f32_32x32x16_bf16 agree on
 // the key of every k-slot.
 //
-// One workgroup per 128 queries (4 waves x 32 queries), key tiles of 64
-// streamed through two-slot LDS rings (tile t+1 loads during step t):
-//  * Kt tile: D rows x 64 keys, rows padded to 72 bf16 (144 bytes), read as
-//    the A operand with one ds_read_b128 per MFMA;
-//  * dS^T tile: 64 keys x 128 queries, stored chunk-major: 16 columns of
+// One workgroup per 256 queries (8 waves x 32 queries), one per CU, key
+// tiles of 64 streamed through three-slot LDS rings (step t loads tile t+2).
+// The kernel is bound by its two load streams, dS from HBM and Kt from L2
+// (timing builds without the MFMAs run as long); 256 queries per workgroup
+// halve the Kt bytes per query against 128. Measured at C5: the dS stream
+// alone runs at about 5.4 TB/s, whether one or three tiles are in flight,
+// and with the block order or the piece order inside a block changed.
+//  * Kt tile: D rows x 64 keys in the swizzled slab layout (slab_swz), read
+//    as the A operand with one ds_read_b128 per MFMA;
+//  * dS^T tile: 64 keys x 256 queries, stored chunk-major: 32 columns of
 //    8 queries, each 64 keys x 16 bytes, 1088 bytes apart (64 bytes of pad).
 //    One load instruction fills one column from 1 KB contiguous in HBM. It
 //    is read as the B operand with ds_read_b64_tr_b16: per 16-lane group
@@ -32,7 +37,8 @@
 //    32 queries, 4 columns x 64 bytes, which the 1088-byte column stride
 //    puts on 64 distinct banks.
 // Causal: a query block attends keys below its end (top-left mask); the
-// masked (key > query) entries of the diagonal tiles were stored as zeros.
+// masked (key > query) entries of the diagonal tiles were stored as zeros,
+// and a wave skips the key tiles past its own 64-query tile.
 // Key padding: keys at or past kv_len were stored as zeros, and key tiles
 // past the last valid key are not read. Query columns past S hold values
 // the dK/dV kernel never wrote; a dQ^T column depends on its own dS^T column
@@ -42,22 +48,24 @@
 
 namespace gonn {
 
+constexpr int kDqDsWaves = 8;  // waves (32 queries each) per workgroup
+
 template <int D, bool CAUSAL>
-__global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
-    constexpr int BM = 128, BN = 64, NT = 256;
+__global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams p) {
+    constexpr int NW = kDqDsWaves, BM = NW * 32, BN = 64, NT = NW * 64;
     constexpr int NDT = D / 32;
-    constexpr int KST = BN + 8;   // Kt tile row stride (bf16)
+    constexpr int NSLOT = 3, PF = NSLOT - 1;  // ring slots, tiles loaded ahead
     constexpr int SCB = BN * 16 + 64;  // dS^T tile column stride (bytes)
     constexpr int NSC = BM / 8;        // dS^T tile columns
-    constexpr uint32_t KTB = D * KST * 2, STB = NSC * SCB;
-    __shared__ __attribute__((aligned(16))) bf16 sK[2 * D * KST];
-    __shared__ __attribute__((aligned(16))) char sS[2 * STB];
+    constexpr uint32_t KTB = D * BN * 2, STB = NSC * SCB;
+    __shared__ __attribute__((aligned(16))) bf16 sK[NSLOT * D * BN];
+    __shared__ __attribute__((aligned(16))) char sS[NSLOT * STB];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 5, ln = lane & 31;
     int bh, qb;
-    map_block(blockIdx.x, p.Sp / BM, p.BH, CAUSAL, bh, qb);
+    map_block(blockIdx.x, (p.Sp + BM - 1) / BM, p.BH, CAUSAL, bh, qb);
     const int S = p.S, Sp = p.Sp, Skp = p.Skp;
     const int q0 = qb * BM;
     if (q0 >= S) return;  // padding rows only
@@ -66,46 +74,49 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
     const int ntiles = (kend + BN - 1) / BN;
 
     // ---- tile loads (direct to LDS): instruction i of thread tid fills the
-    // 16-byte position i*NT + tid of a padded tile; pad positions load a
-    // dummy chunk of their row ----
-    constexpr int KCP = KST / 8, NKP = D * KCP;          // Kt: D rows x 9
-    constexpr int NKI = (NKP + NT - 1) / NT;
-    constexpr int KLAST = NKP - (NKI - 1) * NT;
-    static_assert(KLAST % 64 == 0, "partial loads must be whole waves");
-    static_assert(NSC % 4 == 0, "dS^T columns spread over the four waves");
+    // 16-byte position i*NT + tid of a Kt tile (slab_chunk gives its row and
+    // chunk); every thread issues NKI + NSC/4 loads per tile ----
+    constexpr int NKI = D * BN / 8 / NT;
+    static_assert(NKI * NT * 8 == D * BN, "whole Kt load instructions");
+    static_assert(NSC % NW == 0, "dS^T columns spread over the waves");
+    constexpr int NLD = NKI + NSC / NW;  // loads per tile per thread
     uint32_t koff[NKI];
     for (int i = 0; i < NKI; i++) {
-        const int pos = i * NT + tid, r = pos / KCP, c = pos % KCP;
-        koff[i] = (uint32_t)((((pos < NKP) ? r : 0) * Skp + (c < BN / 8 ? c : 0) * 8) * 2);
+        int r, c;
+        slab_chunk(i * NT + tid, D, r, c);
+        koff[i] = (uint32_t)((r * Skp + c * 8) * 2);
     }
-    const uint32_t klast = wave * 64 < KLAST;
     const bf16* Ktg = (const bf16*)p.kt + (size_t)bh * D * Skp;
     const brsrc krs = make_rsrc(Ktg, (uint32_t)D * Skp * 2);
     // This slice's stored dS: (Skp/128 key blocks) x (Sp/64 query tiles)
-    // blocks of kDsTileElems.
+    // blocks of kDsTileElems. Concurrent workgroups of a head read adjacent
+    // blocks (a query-major order, which makes each workgroup's reads one
+    // stream but puts concurrent workgroups 1 MB apart, measured 10% slower).
     const int nqt = Sp / 64, qt0 = q0 / 64;
     const brsrc srs = make_rsrc((const bf16*)p.ds + (size_t)bh * (Skp / 128) * nqt * kDsTileElems,
                                 (uint32_t)(Skp / 128) * nqt * kDsTileElems * 2);
     const uint32_t kl = lds_addr(sK) + wave * 1024, sl = lds_addr(sS);
     auto load_tile = [&](int t, int slot) {
-        for (int i = 0; i < NKI; i++) {
-            const uint32_t dst = kl + slot * KTB + i * NT * 16;
-            if (i < NKI - 1) dma16(krs, dst, koff[i], (uint32_t)t * BN * 2);
-            else dma16_if(krs, dst, koff[i], (uint32_t)t * BN * 2, klast);
-        }
-        // Column c = 4 i + wave: query tile qt0 + c / 8, chunk c % 8, the 64
-        // keys of half t % 2 of key block t / 2: lane L loads key L.
-        for (int i = 0; i < NSC / 4; i++) {
-            const int c = 4 * i + wave;
+        for (int i = 0; i < NKI; i++)
+            dma16(krs, kl + slot * KTB + i * NT * 16, koff[i], (uint32_t)t * BN * 2);
+        // Column c = NW i + wave: query tile qt0 + c / 8, chunk c % 8, the 64
+        // keys of half t % 2 of key block t / 2: lane L loads key L. (Query
+        // tiles past Sp read the next key block's blocks, or zeros past the
+        // slice: only dQ rows past S, which are not written, use them.)
+        for (int i = 0; i < NSC / NW; i++) {
+            const int c = NW * i + wave;
             const uint32_t so = (uint32_t)(((t / 2) * nqt + qt0 + c / 8) * kDsTileElems * 2 +
-                                           ((c % 8) * 128 + (t % 2) * 64) * 16);
+                                           ((t % 2) * 512 + (c % 8) * 64) * 16);
             dma16_nt(srs, sl + slot * STB + c * SCB, (uint32_t)lane * 16, so);
         }
     };
 
     // ---- operand reads ----
-    // A (Kt): row dt*32 + ln, chunk 2ks + g.
-    const uint32_t ka = (uint32_t)(ln * KST + g * 8) * 2;
+    // A (Kt): row dt*32 + ln, chunk 2ks + g, at (dt*32 + (ks/2)*D) * 64 +
+    // (ks odd ? ka1 : ka0) in the slab layout.
+    const int hs = slab_swz(ln);
+    const uint32_t ka0 = (uint32_t)(ln * 64 + ((0 + g) ^ hs) * 16);
+    const uint32_t ka1 = (uint32_t)(ln * 64 + ((2 + g) ^ hs) * 16);
     // B (dS^T): this lane reads key 4g + (lane & 15) / 4 (+16ks, +8 for the
     // second half of the k-slots) at query column qc = 32 wave + 16
     // ((lane >> 4) & 1) + 4 (lane & 3): column qc / 8, byte 2 (qc % 8).
@@ -123,29 +134,39 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
 
     f32x16 acc[NDT];
     for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x16{};
+    // Tiles past the last are clamped to it (a redundant load into a slot
+    // no step reads), so every step issues NLD loads and the wait for tile
+    // t+1 at the end of step t is always "all but the newest PF-1 tiles".
     if (ntiles > 0) {
-        load_tile(0, 0);
-        GONN_VMCNT(0);
+        for (int j = 0; j < PF; j++) load_tile(j < ntiles ? j : ntiles - 1, j);
+        GONN_VMCNT((PF - 1) * NLD);
         __syncthreads();
         for (int t = 0; t < ntiles; t++) {
-            const int cur = t & 1;
-            if (t + 1 < ntiles) load_tile(t + 1, cur ^ 1);
-            const char* kbase = (const char*)sK + cur * KTB + ka;
+            const int cur = t % NSLOT;
+            load_tile(t + PF < ntiles ? t + PF : ntiles - 1, (t + PF) % NSLOT);
+            const char* kbase = (const char*)sK + cur * KTB;
             const uint32_t sbase = cur * STB + sb;
-            for (int ks = 0; ks < BN / 16; ks++) {
+            // Causal: this wave's 32 queries lie in query tile qt0 + wave/2,
+            // which sees key tiles up to its own index; later key tiles are
+            // fully masked, and the dK/dV kernel (whose key block kb starts
+            // at query tile 2 kb) wrote no dS for some of them. Wave-uniform;
+            // the loads above stay uniform so every wave's vmcnt counts match.
+            const bool live = !CAUSAL || t <= qt0 + (wave >> 1);
+            for (int ks = 0; ks < (live ? BN / 16 : 0); ks++) {
                 const s4 lo = tr_read(sbase + (uint32_t)(16 * ks) * 16);
                 const s4 hi = tr_read(sbase + (uint32_t)(16 * ks + 8) * 16);
                 const s4 b8[2] = {lo, hi};
                 const bf16x8 bop = __builtin_bit_cast(bf16x8, b8);
                 for (int dt = 0; dt < NDT; dt++) {
-                    const bf16x8 aop =
-                        *(const bf16x8*)(kbase + (dt * 32 * KST + ks * 16) * 2);
+                    const bf16x8 aop = *(const bf16x8*)(kbase + (ks & 1 ? ka1 : ka0) +
+                                                        (dt * 32 + (ks >> 1) * D) * 64);
                     acc[dt] = mfma_bf16(aop, bop, acc[dt]);
                 }
             }
-            GONN_VMCNT(0);
+            GONN_VMCNT((PF - 1) * NLD);
             __syncthreads();
         }
+        GONN_VMCNT(0);
     }
 
     // Lane (ln, g) holds query column 32 wave + ln of the block (stored
@@ -168,13 +189,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_ds_kernel(BwdParams p) {
 hipError_t launch_bwd_dq_ds(const BwdParams& p, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0 || !p.ds || !p.kt)
         return hipErrorInvalidValue;
-    const dim3 grid((p.Sp / 128) * p.BH);
+    constexpr int BM = kDqDsWaves * 32, NT = kDqDsWaves * 64;
+    const dim3 grid(((p.Sp + BM - 1) / BM) * p.BH);
     if (D == 64) {
-        if (causal) bwd_dq_ds_kernel<64, true><<<grid, 256, 0, s>>>(p);
-        else bwd_dq_ds_kernel<64, false><<<grid, 256, 0, s>>>(p);
+        if (causal) bwd_dq_ds_kernel<64, true><<<grid, NT, 0, s>>>(p);
+        else bwd_dq_ds_kernel<64, false><<<grid, NT, 0, s>>>(p);
     } else if (D == 128) {
-        if (causal) bwd_dq_ds_kernel<128, true><<<grid, 256, 0, s>>>(p);
-        else bwd_dq_ds_kernel<128, false><<<grid, 256, 0, s>>>(p);
+        if (causal) bwd_dq_ds_kernel<128, true><<<grid, NT, 0, s>>>(p);
+        else bwd_dq_ds_kernel<128, false><<<grid, NT, 0, s>>>(p);
     } else {
         return hipErrorInvalidValue;
     }

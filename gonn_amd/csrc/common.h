@@ -201,8 +201,10 @@ GONN_DEV void dma16_m0_if(brsrc r, uint32_t voff, uint32_t soff, uint32_t on) {
 GONN_DEV uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void*)p;
 }
-// s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained), n < 16.
-#define GONN_VMCNT(n) __builtin_amdgcn_s_waitcnt(0x0F70 | (n))
+// s_waitcnt vmcnt(n) (expcnt, lgkmcnt unconstrained), n < 64: the gfx9
+// encoding splits vmcnt into bits 3:0 and 15:14.
+#define GONN_VMCNT(n) \
+    __builtin_amdgcn_s_waitcnt(0x0F70 | ((n) & 15) | ((((n) >> 4) & 3) << 14))
 
 // Swizzled slab layout of LDS tiles (forward K / Vt tiles, dK/dV Q / dO
 // tiles). A tile of `rows` rows of 16-byte chunks is stored in 64-byte

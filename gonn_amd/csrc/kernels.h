@@ -68,7 +68,8 @@ struct BwdParams {
     const void* kt;   // K^T  bf16 mode only
     // dS-store path (bf16 mode): dS in blocks of kDsTileElems bf16, block
     // ((bh * Skp/128 + key block) * Sp/64 + query tile); inside a block,
-    // 16-byte piece (c * 128 + key) holds the key's dS for the 8 queries of
+    // 16-byte piece ((key / 64) * 512 + c * 64 + key % 64) (key of the
+    // block's 128) holds the key's dS for the 8 queries of
     // chunk c (queries 16 (c/2) + {4(c%2)..+3, 8+4(c%2)..+3}, the vt_pos
     // order of a 16-query group). Written by the dK/dV kernel when set, read
     // by bwd_dq_ds_kernel; null: the dQ kernel forms dS itself.
