@@ -24,7 +24,7 @@ GONN_E_INJECTED = -6
 GONN_E_BLAS = -7
 
 GONN_F32, GONN_BF16, GONN_F64, GONN_I32 = 0, 1, 2, 3
-GONN_ATTN_FP32_MFMA, GONN_ATTN_BF16_MFMA = 0, 1
+GONN_ATTN_FP32_MFMA, GONN_ATTN_BF16_MFMA, GONN_ATTN_FP64 = 0, 1, 2
 # backend.UnaryKind / BinaryKind values (backend/backend.go:26-58): a shared ABI.
 (GONN_UN_RELU, GONN_UN_SIGMOID, GONN_UN_TANH, GONN_UN_EXP, GONN_UN_LOG, GONN_UN_GELU,
  GONN_UN_SILU, GONN_UN_GELU_EXACT) = range(8)

@@ -61,6 +61,7 @@ struct ProfScope {
 int env_mode() {
     const char* e = std::getenv("GONN_HIP_ATTN_MODE");
     if (e && (std::strcmp(e, "bf16") == 0 || std::strcmp(e, "1") == 0)) return GONN_ATTN_BF16_MFMA;
+    if (e && (std::strcmp(e, "f64") == 0 || std::strcmp(e, "2") == 0)) return GONN_ATTN_FP64;
     return GONN_ATTN_FP32_MFMA;
 }
 
@@ -688,7 +689,8 @@ int gonn_hip_attn_supports(int D, int Sq, int Sk) {
 }
 
 int gonn_hip_set_attn_mode(int mode) {
-    if (mode != GONN_ATTN_FP32_MFMA && mode != GONN_ATTN_BF16_MFMA) return GONN_E_INVALID;
+    if (mode != GONN_ATTN_FP32_MFMA && mode != GONN_ATTN_BF16_MFMA && mode != GONN_ATTN_FP64)
+        return GONN_E_INVALID;
     g_mode.store(mode);
     return GONN_OK;
 }
@@ -965,8 +967,131 @@ int gonn_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream) 
 
 int gonn_hip_stream_sync(void* stream) { return herr(hipStreamSynchronize((hipStream_t)stream)); }
 
+// ---- exact fp64 path of the f64 entry points (GONN_ATTN_FP64) ----
+namespace {
+
+int upload_f64(DevMem& mem, const double* host, size_t n, double** out) {
+    void* dst = nullptr;
+    TRY(mem.alloc(&dst, n * sizeof(double)));
+    TRYH(hipMemcpyAsync(dst, host, n * sizeof(double), hipMemcpyHostToDevice, mem.s));
+    *out = (double*)dst;
+    return GONN_OK;
+}
+
+int upload_kv_len(DevMem& mem, const int* kv_len, int B, const int** out) {
+    *out = nullptr;
+    if (!kv_len) return GONN_OK;
+    void* dst = nullptr;
+    TRY(mem.alloc(&dst, (size_t)B * sizeof(int)));
+    TRYH(hipMemcpyAsync(dst, kv_len, (size_t)B * sizeof(int), hipMemcpyHostToDevice, mem.s));
+    *out = (const int*)dst;
+    return GONN_OK;
+}
+
+// Forward on host fp64 data: O (and L when non-null) back in host memory.
+int f64_exact_fwd(const double* Q, const double* K, const double* V, double* O, double* L, int B,
+                  int H, int Sq, int Sk, int d, double scale, int causal, const int* kv_len,
+                  const double* mask, size_t mask_n, long mask_sb, long mask_sh) {
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
+    const size_t nq = (size_t)B * H * Sq * d, nk = (size_t)B * H * Sk * d;
+    gonn::F64Params p{};
+    double *q, *k, *v, *o, *l = nullptr, *m = nullptr;
+    TRY(upload_f64(mem, Q, nq, &q));
+    TRY(upload_f64(mem, K, nk, &k));
+    TRY(upload_f64(mem, V, nk, &v));
+    if (mask) TRY(upload_f64(mem, mask, mask_n, &m));
+    TRY(upload_kv_len(mem, kv_len, B, &p.kv_len));
+    TRY(mem.alloc((void**)&o, nq * sizeof(double)));
+    if (L) TRY(mem.alloc((void**)&l, (size_t)B * H * Sq * sizeof(double)));
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.out_o = o;
+    p.out_lse = l;
+    p.mask = m;
+    p.mask_sb = mask_sb;
+    p.mask_sh = mask_sh;
+    p.B = B;
+    p.H = H;
+    p.Sq = Sq;
+    p.Sk = Sk;
+    p.d = d;
+    p.scale = scale;
+    p.causal = causal;
+    {
+        ProfScope ps("fwd_f64", hs);
+        TRYH(gonn::launch_f64_fwd(p, hs));
+    }
+    TRYH(hipMemcpyAsync(O, o, nq * sizeof(double), hipMemcpyDeviceToHost, hs));
+    if (L)
+        TRYH(hipMemcpyAsync(L, l, (size_t)B * H * Sq * sizeof(double), hipMemcpyDeviceToHost,
+                            hs));
+    return herr(hipStreamSynchronize(hs));
+}
+
+// Backward on host fp64 data from the saved O and L (natural-log LSE).
+int f64_exact_bwd(const double* Q, const double* K, const double* V, const double* O,
+                  const double* L, const double* dO, double* dQ, double* dK, double* dV, int B,
+                  int H, int Sq, int Sk, int d, double scale, int causal, const int* kv_len,
+                  const double* mask, size_t mask_n, long mask_sb, long mask_sh) {
+    hipStream_t hs = nullptr;
+    TRY(host_stream(&hs));
+    DevMem mem(hs);
+    StreamSync wait_on_exit{hs};
+    const size_t rq = (size_t)B * H * Sq, nq = rq * d, nk = (size_t)B * H * Sk * d;
+    gonn::F64Params p{};
+    double *q, *k, *v, *o, *l, *g, *m = nullptr;
+    TRY(upload_f64(mem, Q, nq, &q));
+    TRY(upload_f64(mem, K, nk, &k));
+    TRY(upload_f64(mem, V, nk, &v));
+    TRY(upload_f64(mem, O, nq, &o));
+    TRY(upload_f64(mem, L, rq, &l));
+    TRY(upload_f64(mem, dO, nq, &g));
+    if (mask) TRY(upload_f64(mem, mask, mask_n, &m));
+    TRY(upload_kv_len(mem, kv_len, B, &p.kv_len));
+    TRY(mem.alloc((void**)&p.delta, rq * sizeof(double)));
+    TRY(mem.alloc((void**)&p.dq, nq * sizeof(double)));
+    TRY(mem.alloc((void**)&p.dk, nk * sizeof(double)));
+    TRY(mem.alloc((void**)&p.dv, nk * sizeof(double)));
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.lse = l;
+    p.dO = g;
+    p.mask = m;
+    p.mask_sb = mask_sb;
+    p.mask_sh = mask_sh;
+    p.B = B;
+    p.H = H;
+    p.Sq = Sq;
+    p.Sk = Sk;
+    p.d = d;
+    p.scale = scale;
+    p.causal = causal;
+    {
+        ProfScope ps("bwd_f64", hs);
+        TRYH(gonn::launch_f64_bwd(p, hs));
+    }
+    TRYH(hipMemcpyAsync(dQ, p.dq, nq * sizeof(double), hipMemcpyDeviceToHost, hs));
+    TRYH(hipMemcpyAsync(dK, p.dk, nk * sizeof(double), hipMemcpyDeviceToHost, hs));
+    TRYH(hipMemcpyAsync(dV, p.dv, nk * sizeof(double), hipMemcpyDeviceToHost, hs));
+    return herr(hipStreamSynchronize(hs));
+}
+
+}  // namespace
+
 int gonn_hip_flash_attn_f64(const double* Q, const double* K, const double* V, double* O, int BH,
                             int S, int d, double scale, int causal) {
+    if (current_mode() == GONN_ATTN_FP64) {
+        if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O) return GONN_E_INVALID;
+        if (!gonn_hip_available()) return GONN_E_NODEVICE;
+        return f64_exact_fwd(Q, K, V, O, nullptr, BH, 1, S, S, d, scale, causal, nullptr,
+                             nullptr, 0, 0, 0);
+    }
     if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
     hipStream_t hs = nullptr;
@@ -989,6 +1114,9 @@ int gonn_hip_flash_attn_f64_fwd(const double* Q, const double* K, const double* 
                                 double* L, int BH, int S, int d, double scale, int causal) {
     if (!shim_args_ok(BH, S, d) || !Q || !K || !V || !O || !L) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    if (current_mode() == GONN_ATTN_FP64)
+        return f64_exact_fwd(Q, K, V, O, L, BH, 1, S, S, d, scale, causal, nullptr, nullptr, 0, 0,
+                             0);
     hipStream_t hs = nullptr;
     TRY(host_stream(&hs));
     DevMem mem(hs);
@@ -1030,6 +1158,9 @@ int gonn_hip_flash_attn_f64_masked(const double* Q, const double* K, const doubl
     const size_t mn = mask ? mask_elems(B, H, Sq, Sk, mask_sb, mask_sh) : 0;
     if (mask && !mn) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    if (current_mode() == GONN_ATTN_FP64)
+        return f64_exact_fwd(Q, K, V, O, L, B, H, Sq, Sk, d, scale, causal, kv_len, mask, mn,
+                             mask_sb, mask_sh);
     hipStream_t hs = nullptr;
     TRY(host_stream(&hs));
     DevMem mem(hs);
@@ -1082,6 +1213,9 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
     const size_t mn = mask ? mask_elems(B, H, Sq, Sk, mask_sb, mask_sh) : 0;
     if (mask && !mn) return GONN_E_INVALID;
     if (!gonn_hip_available()) return GONN_E_NODEVICE;
+    if (current_mode() == GONN_ATTN_FP64)
+        return f64_exact_bwd(Q, K, V, O, L, dO, dQ, dK, dV, B, H, Sq, Sk, d, scale, causal, kv_len,
+                             mask, mn, mask_sb, mask_sh);
     const int BH = B * H;
     hipStream_t hs = nullptr;
     TRY(host_stream(&hs));
@@ -1139,9 +1273,49 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
     return herr(hipStreamSynchronize(hs));
 }
 
+// Mean ms per call of the f64 mode's forward over `iters` calls (after 5
+// untimed), on zeroed device fp64 buffers, null stream.
+static double bench_f64_exact(int BH, int S, int d, int iters, int causal) {
+    DevMem mem(nullptr);
+    const size_t n = (size_t)BH * S * d;
+    double *q, *k, *v, *o;
+    if (mem.alloc((void**)&q, n * 8) || mem.alloc((void**)&k, n * 8) ||
+        mem.alloc((void**)&v, n * 8) || mem.alloc((void**)&o, n * 8))
+        return (double)GONN_E_NOMEM;
+    if (gonn::launch_fill_zero(q, n * 8, nullptr) || gonn::launch_fill_zero(k, n * 8, nullptr) ||
+        gonn::launch_fill_zero(v, n * 8, nullptr))
+        return -1.0;
+    gonn::F64Params p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.out_o = o;
+    p.B = BH;
+    p.H = 1;
+    p.Sq = p.Sk = S;
+    p.d = d;
+    p.scale = 1.0 / std::sqrt((double)d);
+    p.causal = causal;
+    for (int i = 0; i < 5; i++)
+        if (gonn::launch_f64_fwd(p, nullptr) != hipSuccess) return -1.0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1.0;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
+    (void)hipEventRecord(e0, nullptr);
+    for (int i = 0; i < iters; i++) (void)gonn::launch_f64_fwd(p, nullptr);
+    (void)hipEventRecord(e1, nullptr);
+    (void)hipEventSynchronize(e1);
+    float ms = 0.f;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return (double)ms / iters;
+}
+
 double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal) {
     if (!shim_args_ok(BH, S, d) || iters <= 0) return (double)GONN_E_INVALID;
     if (!gonn_hip_available()) return (double)GONN_E_NODEVICE;
+    if (current_mode() == GONN_ATTN_FP64) return bench_f64_exact(BH, S, d, iters, causal);
     DevMem mem(nullptr);
     const int dp = pad_dim(d);
     const size_t n = (size_t)BH * S * dp;

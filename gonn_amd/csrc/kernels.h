@@ -99,6 +99,30 @@ struct BwdParams {
     long long mask_sb, mask_sh;
 };
 
+// Exact fp64 attention (attn_f64.hip): fp64 (BH, rows, d) buffers.
+struct F64Params {
+    const double* q;      // (BH, Sq, d)
+    const double* k;      // (BH, Sk, d)
+    const double* v;
+    double* out_o;        // forward: O (BH, Sq, d)
+    double* out_lse;      // forward: LSE (BH, Sq), natural log; may be null
+    const double* o;      // backward inputs: O, dO (BH, Sq, d), LSE (BH, Sq)
+    const double* dO;
+    const double* lse;
+    double* delta;        // backward workspace (BH, Sq)
+    double* dq;           // backward outputs
+    double* dk;
+    double* dv;
+    const int* kv_len;    // optional device int[B]: keys >= kv_len[b] are padded
+    const double* mask;   // optional additive mask, element (b, h, i, j) at
+    long long mask_sb, mask_sh;  // b * mask_sb + h * mask_sh + i * Sk + j
+    int B, H, Sq, Sk, d;  // d <= 128
+    double scale;
+    int causal;           // top-left: key j > query i is masked
+};
+hipError_t launch_f64_fwd(const F64Params& p, hipStream_t s);
+hipError_t launch_f64_bwd(const F64Params& p, hipStream_t s);
+
 // Additive mask (WithAttnMask) in the bf16 kernels whose lanes each own one
 // query and whose S^T tiles hold 64 keys (the forwards and the dQ
 // backward): one lane's row of one (b,h) slice, read 4 consecutive keys at a

@@ -27,12 +27,18 @@ import threading
 import numpy as np
 
 from . import _lib
-from ._lib import (GONN_ATTN_BF16_MFMA, GONN_ATTN_FP32_MFMA, GONN_BF16, GONN_F32, GONN_I32,
+from ._lib import (GONN_ATTN_BF16_MFMA, GONN_ATTN_FP32_MFMA, GONN_ATTN_FP64, GONN_BF16,
+                   GONN_F32, GONN_I32,
                    GONN_OP_BWD, GONN_OP_DECODE, GONN_OP_FWD, Buf, BwdArgs, DecodeArgs, FwdArgs,
                    GonnHipError, check)
 
 MODES = {"fp32": GONN_ATTN_FP32_MFMA, "bf16": GONN_ATTN_BF16_MFMA,
          GONN_ATTN_FP32_MFMA: GONN_ATTN_FP32_MFMA, GONN_ATTN_BF16_MFMA: GONN_ATTN_BF16_MFMA}
+# Modes of the f64 entry points: the two MFMA modes, or "f64" (fp64
+# throughout, the precision of the reference's fp64 CUDA seam).
+SHIM_MODES = {**MODES, "f64": GONN_ATTN_FP64, GONN_ATTN_FP64: GONN_ATTN_FP64}
+_SHIM_MODE_NAMES = {GONN_ATTN_FP32_MFMA: "fp32", GONN_ATTN_BF16_MFMA: "bf16",
+                    GONN_ATTN_FP64: "f64"}
 
 _dp = ctypes.POINTER(ctypes.c_double)
 
@@ -51,11 +57,12 @@ def Supports(D: int, Sq: int, Sk: int) -> bool:
 
 
 def SetAttnMode(mode) -> None:
-    check(_lib.load().gonn_hip_set_attn_mode(MODES[mode]), "SetAttnMode")
+    """Mode of the f64 entry points: "fp32", "bf16" or "f64"."""
+    check(_lib.load().gonn_hip_set_attn_mode(SHIM_MODES[mode]), "SetAttnMode")
 
 
 def AttnMode() -> str:
-    return "bf16" if _lib.load().gonn_hip_get_attn_mode() == GONN_ATTN_BF16_MFMA else "fp32"
+    return _SHIM_MODE_NAMES[_lib.load().gonn_hip_get_attn_mode()]
 
 
 def Version() -> str:

@@ -61,10 +61,15 @@ enum {
 typedef enum { GONN_F32 = 0, GONN_BF16 = 1, GONN_F64 = 2, GONN_I32 = 3 } gonn_dtype;
 
 /* The two dense contractions (QK^T and PV, and the five backward products)
- * run on MFMA in one of two modes. Accumulation is fp32 in both.           */
+ * run on MFMA in one of two modes, accumulating in fp32; the f64 entry
+ * points can instead run fp64 kernels throughout (the precision of the
+ * reference's fp64 CUDA seam).                                             */
 typedef enum {
     GONN_ATTN_FP32_MFMA = 0, /* fp32 operands (v_mfma_f32_32x32x2_f32)        */
-    GONN_ATTN_BF16_MFMA = 1  /* bf16 operands (v_mfma_f32_32x32x16_bf16)      */
+    GONN_ATTN_BF16_MFMA = 1, /* bf16 operands (v_mfma_f32_32x32x16_bf16)      */
+    GONN_ATTN_FP64 = 2       /* fp64 throughout, exact to rounding: the f64
+                                entry points only (the device entries take
+                                modes 0 and 1)                              */
 } gonn_attn_mode;
 
 /* A device buffer handle: a device pointer, its size in bytes and the type
@@ -175,8 +180,11 @@ int gonn_hip_available(void);
 int gonn_hip_attn_supports(int D, int Sq, int Sk);
 
 /* Default arithmetic mode used by the f64 compatibility shims. Initialised
- * from the environment variable GONN_HIP_ATTN_MODE ("fp32" or "bf16"),
- * default fp32-MFMA. Returns GONN_E_INVALID for an unknown mode.          */
+ * from the environment variable GONN_HIP_ATTN_MODE ("fp32", "bf16" or
+ * "f64"), default fp32-MFMA. GONN_ATTN_FP64 makes the f64 entries compute
+ * in fp64 (agreeing with an fp64 CPU evaluation to rounding, as the
+ * reference's CUDA seam does); the MFMA modes convert their host fp64 data
+ * to fp32. Returns GONN_E_INVALID for an unknown mode.                     */
 int gonn_hip_set_attn_mode(int mode);
 int gonn_hip_get_attn_mode(void);
 

@@ -58,16 +58,19 @@ def test_version_strerror_modes():
     assert lib.gonn_hip_set_attn_mode(7) == GONN_E_INVALID
     hip.SetAttnMode("bf16")
     assert hip.AttnMode() == "bf16"
+    hip.SetAttnMode("f64")  # the f64 entry points' exact mode
+    assert hip.AttnMode() == "f64" and lib.gonn_hip_get_attn_mode() == 2
     hip.SetAttnMode("fp32")
     assert hip.AttnMode() == "fp32"
 
 
-def test_mode_from_environment():
+@pytest.mark.parametrize("mode", ["bf16", "f64"])
+def test_mode_from_environment(mode):
     code = "from gonn_amd import hip; print(hip.AttnMode())"
-    env = dict(os.environ, GONN_HIP_ATTN_MODE="bf16", PYTHONPATH=ROOT)
+    env = dict(os.environ, GONN_HIP_ATTN_MODE=mode, PYTHONPATH=ROOT)
     out = subprocess.run([sys.executable, "-c", code], env=env, capture_output=True, text=True,
                          check=True)
-    assert out.stdout.strip() == "bf16"
+    assert out.stdout.strip() == mode
 
 
 def test_supports_gate():
@@ -101,6 +104,8 @@ def test_fwd_argument_errors():
     a = _fwd_args(Sq=0)
     assert _fwd(a) == GONN_E_INVALID
     a = _fwd_args(mode=5)
+    assert _fwd(a) == GONN_E_INVALID
+    a = _fwd_args(mode=2)  # the f64 entries' exact mode is not a device-entry mode
     assert _fwd(a) == GONN_E_INVALID
     a = _fwd_args()
     a.q.ptr = None
