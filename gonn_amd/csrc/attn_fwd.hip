@@ -441,10 +441,14 @@ constexpr int kFwdStreamPrio = 1;
 constexpr int kFwdWaves = 4;
 // Resident workgroups per CU the pipelined forward is compiled for (its
 // register budget): two, or one with the additive mask's registers. The
-// kernel is written for any D that is a multiple of 32 and is instantiated
-// for D = 128. At D = 64 it measured slower on C2 than the two-stage kernel
-// (43 against 41 us): its two workgroups per CU run C2's 768 q-blocks in
-// 1.5 rounds, where the two-stage kernel fits three per CU, one round.
+// kernel is written for any D that is a multiple of 32 and runs D = 128 and
+// the unmasked D = 64 calls. At D = 64 it takes 185 VGPRs: two workgroups
+// per CU run C2's 768 q-blocks in 1.5 rounds, where the two-stage kernel fits
+// three per CU in one round, and it is still 3% faster there (leaner softmax:
+// no per-tile row max, no per-tile accumulator seeding). Built for three per
+// CU it spills (112 B/lane) and is 40% slower. The masked D = 64 calls keep
+// the two-stage kernel (two workgroups per CU against the masked pipelined
+// kernel's one).
 constexpr int fwd_pipe_wgs(int D, bool mask) { return mask ? 1 : 2; }
 
 template <int D, bool CAUSAL, typename QT, bool MASK>
@@ -1027,7 +1031,7 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
                       hipStream_t s) {
     FwdParams p = p_in;
     // Query rows per workgroup.
-    const int bm = (mode == 1 && D == 128) ? kFwdWaves * 32 : 128;
+    const int bm = mode == 1 ? kFwdWaves * 32 : 128;  // both bf16 kernels: 128 rows
     p.nqb = (p.Sq + bm - 1) / bm;
     dim3 grid(p.nqb * p.BH);
     // Causal dispatch groups: about two XCDs' worth of workgroup slots
@@ -1047,7 +1051,10 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
         p.hgroup = 2 * slots / p.nqb > 1 ? 2 * slots / p.nqb : 1;
     }
     if (mode == 1) {
-        if (D == 64) {
+        if (D == 64 && !p.mask) {
+            if (causal) launch_bf16_pipe<64, true>(p, q_bf16, grid, s);
+            else launch_bf16_pipe<64, false>(p, q_bf16, grid, s);
+        } else if (D == 64) {
             if (causal) launch_bf16_d<64, true>(p, q_bf16, grid, s);
             else launch_bf16_d<64, false>(p, q_bf16, grid, s);
         } else if (D == 128) {
