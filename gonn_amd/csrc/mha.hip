@@ -246,7 +246,10 @@ int run_forward(gonn_mha* m, const double* xq, const double* xk, const double* x
     a.D = dp;
     a.scale = 1.0 / std::sqrt((double)D);  // nn/attention.go:136
     a.causal = causal;
-    a.mode = gonn_hip_get_attn_mode();
+    // The core runs on the layer's fp32 device intermediates: in the f64
+    // entries' fp64 mode it takes the fp32-MFMA kernels.
+    const int mode = gonn_hip_get_attn_mode();
+    a.mode = mode == GONN_ATTN_FP64 ? GONN_ATTN_FP32_MFMA : mode;
     TRY(gonn_hip_attn_fwd(&a, w + L.aw, L.aw_bytes, s));
     // Merge into Yq's slot (the projections are done with it), then project.
     double* ctx = Y[0];

@@ -184,7 +184,9 @@ int gonn_hip_attn_supports(int D, int Sq, int Sk);
  * "f64"), default fp32-MFMA. GONN_ATTN_FP64 makes the f64 entries compute
  * in fp64 (agreeing with an fp64 CPU evaluation to rounding, as the
  * reference's CUDA seam does); the MFMA modes convert their host fp64 data
- * to fp32. Returns GONN_E_INVALID for an unknown mode.                     */
+ * to fp32. The resident MHA layer (gonn_hip_mha_*) runs its core in this
+ * mode on its fp32 intermediates, fp32-MFMA when the mode is
+ * GONN_ATTN_FP64. Returns GONN_E_INVALID for an unknown mode.              */
 int gonn_hip_set_attn_mode(int mode);
 int gonn_hip_get_attn_mode(void);
 

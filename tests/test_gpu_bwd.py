@@ -171,8 +171,9 @@ def _sample(S, n, seed):
 def test_c5_fwd_bwd_full_size():
     """C5: B=2 H=16 S=8192 D=128 causal, bf16 MFMA, forward + backward.
 
-    The oracle runs the full fp64 forward (O, LSE for every row) and the
-    closed-form backward on sampled query rows (dQ) and key rows (dK, dV). On
+    The oracle runs the full fp64 forward (O, LSE checked on every row) and
+    the closed-form backward on 48+ sampled query rows (dQ) and key rows (dK,
+    dV). On
     the full output: sum_j dV_j = sum_i dO_i (rows of P sum to 1) and
     sum_j dK_j = 0 (sum_j dS_ij = 0), per (b,h) and column; two runs are
     bit-identical (no atomics)."""
@@ -186,9 +187,9 @@ def test_c5_fwd_bwd_full_size():
         assert np.all(np.isfinite(x))
     say("C5 oracle forward")
     ro, rl = oracle.attn_fwd(q, k, v, causal=True)
-    rows = _sample(S, 12, 9)
-    assert_close(o[:, rows], ro[:, rows], mode, "C5 O")
-    assert_close(l[:, rows], rl[:, rows], mode, "C5 LSE")
+    assert_close(o, ro, mode, "C5 O")
+    assert_close(l, rl, mode, "C5 LSE")
+    rows = _sample(S, 48, 9)
     say("C5 oracle backward rows")
     rq, rk, rv = oracle.attn_bwd_rows(q, k, v, ro, rl, g, causal=True, qrows=rows, krows=rows)
     assert_close(dq[:, rows], rq[:, rows], mode, "C5 dQ")

@@ -68,31 +68,23 @@ def test_fwd_scale_variants(mode):
         assert_close(l, rl, mode, f"LSE scale={scale}")
 
 
-def _sample_rows(S, n, seed):
-    rng = np.random.default_rng(seed)
-    fixed = [0, 1, 31, 32, 63, 64, 127, 128, S // 2, S - 2, S - 1]
-    rows = set(r for r in fixed if r < S) | set(rng.integers(0, S, n).tolist())
-    return np.array(sorted(rows), dtype=np.int32)
-
-
 @pytest.mark.parametrize("mode", ["fp32", "bf16"])
 def test_c2_encoder_full_size(mode):
-    """C2: B=8 H=12 S=1024 D=64 non-causal, rows sampled for the oracle."""
+    """C2: B=8 H=12 S=1024 D=64 non-causal, every row against the oracle."""
     B, H, S, D = 8, 12, 1024, 64
     q = randn((B * H, S, D), 21)
     k = randn((B * H, S, D), 22)
     v = randn((B * H, S, D), 23)
     say(f"C2 mode={mode}")
     o, l = _run(q, k, v, False, mode)
-    rows = _sample_rows(S, 24, 1)
-    ro, rl = oracle.attn_fwd(q, k, v, causal=False, rows=rows)
-    assert_close(o[:, rows], ro[:, rows], mode, "C2 O")
-    assert_close(l[:, rows], rl[:, rows], mode, "C2 LSE")
+    ro, rl = oracle.attn_fwd(q, k, v, causal=False)
+    assert_close(o, ro, mode, "C2 O")
+    assert_close(l, rl, mode, "C2 LSE")
 
 
 def test_c3_prefill_full_size():
-    """C3: B=4 H=32 S=4096 D=128 causal, bf16 MFMA; oracle on sampled rows,
-    plus size-independent properties on the full output."""
+    """C3: B=4 H=32 S=4096 D=128 causal, bf16 MFMA; every row against the
+    oracle, plus size-independent properties on the full output."""
     B, H, S, D = 4, 32, 4096, 128
     mode = "bf16"
     q = randn((B * H, S, D), 31)
@@ -101,10 +93,11 @@ def test_c3_prefill_full_size():
     say("C3 parity")
     o, l = _run(q, k, v, True, mode)
     assert np.all(np.isfinite(o)) and np.all(np.isfinite(l))
-    rows = _sample_rows(S, 16, 2)
-    ro, rl = oracle.attn_fwd(q, k, v, causal=True, rows=rows)
-    assert_close(o[:, rows], ro[:, rows], mode, "C3 O")
-    assert_close(l[:, rows], rl[:, rows], mode, "C3 LSE")
+    say("C3 oracle forward (every row)")
+    ro, rl = oracle.attn_fwd(q, k, v, causal=True)
+    assert_close(o, ro, mode, "C3 O")
+    assert_close(l, rl, mode, "C3 LSE")
+    del ro, rl
     # Causal invariance: changing keys/values at positions > p leaves rows <= p
     # bit-identical (masked keys carry exactly zero weight).
     p = 2500

@@ -56,6 +56,8 @@ def test_resident_self_attention_matches_oracle(mode_guard, mode, cfg):
     hip.SetAttnMode(mode)
     mha, p = _layer(E, H, E, E, 1000 + E)
     x = randn((B, Tq, E), 1100 + Tq).astype(np.float64)
+    if name == "C1":
+        x /= math.sqrt(E)  # inputs N(0,1) / sqrt(d_model)
     ref = oracle.mha_fwd(x, x, x, p, H, causal=causal)
     with mha.to_device() as dev:
         got = dev.forward(x, x, x, causal)
@@ -132,3 +134,19 @@ def test_resident_device_buffers_reuse_workspace(mode_guard):
         assert np.array_equal(out.cpu().numpy(), dev.forward_masked(x, x, x, False, key_padding_mask=pad))
         with pytest.raises(Exception):
             dev.dev.forward_dev(xd, xd, xd, ws=ws[:16])
+
+
+def test_resident_layer_in_the_f64_entries_mode(mode_guard):
+    """With the f64 entries' fp64 mode set, the resident layer still runs
+    (its core on fp32-MFMA over its fp32 intermediates)."""
+    hip = mode_guard
+    hip.SetAttnMode("f64")
+    E, H, B, T = 256, 4, 2, 128
+    mha, p = _layer(E, H, E, E, 1256)
+    x = randn((B, T, E), 1257).astype(np.float64) / math.sqrt(E)
+    ref = oracle.mha_fwd(x, x, x, p, H, causal=True)
+    with mha.to_device() as dev:
+        got = dev.forward(x, x, x, True)
+    assert_close(got, ref, "fp32", "resident MHA in f64 mode")
+    # the host-data fused path of the same layer runs the fp64 kernels
+    assert np.max(np.abs(mha.forward_fused(x, x, x, True) - ref)) <= 1e-9
