@@ -27,6 +27,7 @@ GB/s, 1 MI355X".
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -73,18 +74,35 @@ def load_traffic(key: str):
         return None
 
 
+def _prime_queue(torch, ms=20.0):
+    """Queue a bounded spin kernel (~ms at 2 GHz) ahead of a timed loop, so the
+    host enqueues the loop's calls while the GPU spins and the calls then run
+    back to back: a step shorter than its host-side call (C2, decode) is timed
+    as device work rather than as the gaps of a starved queue. The timed span
+    starts after the spin."""
+    torch.cuda._sleep(int(ms * 2e6))
+
+
 def _run_steps(torch, run, steps):
     """Time `steps` back-to-back calls on the current stream with an event
     before each call and one after the last: (mean ms, median ms, wall s).
     The mean is the span of the whole run over `steps`."""
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    t0 = time.perf_counter()
-    for i in range(steps):
-        ev[i].record()
-        run()
-    ev[steps].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    # No garbage-collector pause inside the timed span (host-side only: the
+    # device work is unchanged).
+    gc.collect()
+    gc.disable()
+    try:
+        _prime_queue(torch)
+        t0 = time.perf_counter()
+        for i in range(steps):
+            ev[i].record()
+            run()
+        ev[steps].record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+    finally:
+        gc.enable()
     per = [ev[i].elapsed_time(ev[i + 1]) for i in range(steps)]
     return ev[0].elapsed_time(ev[steps]) / steps, statistics.median(per), wall
 
@@ -106,6 +124,7 @@ def bench_prefill(torch, hip, steps, warmup):
     # per-kernel pass (events recorded by the library around each stage)
     hip.profile_reset()
     hip.profile_enable(True)
+    _prime_queue(torch)
     for _ in range(steps):
         run()
     torch.cuda.synchronize()
@@ -139,6 +158,7 @@ def bench_decode(torch, hip, steps, warmup):
     ms, med, _ = _run_steps(torch, run, steps)
     hip.profile_reset()
     hip.profile_enable(True)
+    _prime_queue(torch)
     for _ in range(steps):
         run()
     torch.cuda.synchronize()
@@ -195,6 +215,7 @@ def bench_incremental(torch, hip, steps, warmup, Ts=(1, 4)):
         ms, med, _ = _run_steps(torch, run, steps)
         hip.profile_reset()
         hip.profile_enable(True)
+        _prime_queue(torch)
         for _ in range(steps):
             run()
         torch.cuda.synchronize()
@@ -230,6 +251,7 @@ def _timed(torch, hip, run, steps, warmup, stages):
     ms, med, _ = _run_steps(torch, run, steps)
     hip.profile_reset()
     hip.profile_enable(True)
+    _prime_queue(torch)
     for _ in range(steps):
         run()
     torch.cuda.synchronize()
