@@ -244,24 +244,28 @@ struct BwdLayout {
     size_t lse2, delta, packed[5], ds, total;
 };
 
-// The bf16 backward stores dS (BH x Skp x Sp bf16, in the blocks of
-// BwdParams::ds) and computes dQ from it in one GEMM when that buffer is at
-// most kDsMaxBytes and one slice of it fits the kernels' 32-bit buffer
-// offsets; otherwise (and with
-// GONN_HIP_BWD_DQ=recompute) the dQ kernel forms S and dP again. The choice
-// depends on the shape only (and the environment), so a workspace sized by
-// gonn_hip_attn_workspace_bytes fits the call that follows.
+// The bf16 backward stores dS (bf16 blocks of 128 keys x 64 queries; for a
+// causal call only the blocks a key block reaches, ds_block_base) and
+// computes dQ from it in one GEMM when that buffer is at most kDsMaxBytes
+// and one slice of it fits the kernels' 32-bit buffer offsets; otherwise (and
+// with GONN_HIP_BWD_DQ=recompute) the dQ kernel forms S and dP again. The
+// choice depends on the shape only (and the environment), so a workspace
+// sized by gonn_hip_attn_workspace_bytes fits the call that follows.
 constexpr double kDsMaxBytes = 16.0 * 1024 * 1024 * 1024;
-bool bwd_use_ds(int mode, size_t BH, int S, int Sk) {
+double ds_slice_bytes(int S, int Sk, int causal) {
+    const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
+    const int Skp = (int)round_up((size_t)Sk, gonn::kBwdPad);
+    return (double)gonn::ds_slice_blocks(Skp / 128, Sp / 64, causal) * gonn::kDsTileElems * 2;
+}
+bool bwd_use_ds(int mode, size_t BH, int S, int Sk, int causal) {
     if (mode != GONN_ATTN_BF16_MFMA) return false;
     const char* e = std::getenv("GONN_HIP_BWD_DQ");
     if (e && std::strcmp(e, "recompute") == 0) return false;
-    const double Sp = (double)round_up((size_t)S, gonn::kBwdPad);
-    const double Skp = (double)round_up((size_t)Sk, gonn::kBwdPad);
-    return Skp * Sp * 2 < 2147483648.0 && (double)BH * Skp * Sp * 2 <= kDsMaxBytes;
+    const double slice = ds_slice_bytes(S, Sk, causal);
+    return slice < 2147483648.0 && (double)BH * slice <= kDsMaxBytes;
 }
 
-BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D) {
+BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal) {
     BwdLayout L{};
     const size_t Sp = round_up((size_t)S, gonn::kBwdPad), Skp = round_up((size_t)Sk, gonn::kBwdPad);
     size_t off = 0;
@@ -276,9 +280,9 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D) {
             L.packed[i] = off;
             off = round_up(off + BH * (keyside[i] ? Skp : Sp) * D * 2, 256);
         }
-        if (bwd_use_ds(mode, BH, S, Sk)) {
+        if (bwd_use_ds(mode, BH, S, Sk, causal)) {
             L.ds = off;
-            off = round_up(off + BH * Skp * Sp * 2, 256);
+            off = round_up(off + BH * (size_t)ds_slice_bytes(S, Sk, causal), 256);
         }
     }
     L.total = off;
@@ -286,7 +290,9 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D) {
 }
 
 size_t bwd_ws(const gonn_attn_bwd_args* a) {
-    return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->D).total + 256;
+    return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->D, a->causal)
+               .total +
+           256;
 }
 
 // ---- helpers for the host shims ----------------------------------------
@@ -783,7 +789,7 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
     const int BH = a->B * a->H, S = a->S, D = a->D;
     const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
     const int mode = bwd_mode(a);
-    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, bwd_keys_of(a), D);
+    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, bwd_keys_of(a), D, a->causal);
     uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
     gonn::BwdParams p{};
     if (a->attn_mask.ptr) {
@@ -857,7 +863,7 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p.k = a->k.ptr;
         p.v = a->v.ptr;
     }
-    const bool use_ds = bwd_use_ds(mode, (size_t)BH, S, p.Sk);
+    const bool use_ds = bwd_use_ds(mode, (size_t)BH, S, p.Sk, a->causal);
     p.ds = use_ds ? (bf16*)(w + L.ds) : nullptr;
     {
         ProfScope ps("bwd_dkdv", s);

@@ -244,9 +244,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     // one of its steps as one contiguous 8 KB. A padded key (kj >= Skv) stores zeros. Without
     // p.ds the resource has no range and every store is dropped.
     const bool store_ds = p.ds != nullptr;
-    const brsrc dsrs = make_rsrc(
-        store_ds ? p.ds + ((size_t)bh * (Skp / BN) + kb) * (size_t)(Sp / BM) * kDsTileElems : p.ds,
-        store_ds ? (uint32_t)(Sp / BM) * kDsTileElems * 2 : 0u);
+    // This key block's blocks (query tiles qb0 .. Sp/64 - 1).
+    const size_t ds0 = (size_t)(bh * ds_slice_blocks(Skp / BN, Sp / BM, CAUSAL) +
+                                ds_block_base(kb, Sp / BM, CAUSAL));
+    const brsrc dsrs = make_rsrc(store_ds ? p.ds + ds0 * kDsTileElems : p.ds,
+                                 store_ds ? (uint32_t)(Sp / BM - qb0) * kDsTileElems * 2 : 0u);
     // Piece (key / 64) * 512 + chunk * 64 + key % 64 of a block, chunk 2e + g
     // for store e.
     const uint32_t dsvo = (uint32_t)(((wave >> 1) * 512 + (wave & 1) * 32 + ln + g * 64) * 16);
@@ -395,7 +397,7 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
                 // kernel re-reads from L2.
                 __builtin_amdgcn_raw_buffer_store_b128(
                     __builtin_bit_cast(i32x4, v), dsrs, dsvo,
-                    (uint32_t)((qb - 1) * kDsTileElems * 2 + es * 2048), 2);
+                    (uint32_t)((qb - 1 - qb0) * kDsTileElems * 2 + es * 2048), 2);
             }
             // Tile loads spread over the first SPAN slots: 1, 1 + DS, ...
             if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA)

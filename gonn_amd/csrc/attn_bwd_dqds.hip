@@ -88,24 +88,30 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
     }
     const bf16* Ktg = (const bf16*)p.kt + (size_t)bh * D * Skp;
     const brsrc krs = make_rsrc(Ktg, (uint32_t)D * Skp * 2);
-    // This slice's stored dS: (Skp/128 key blocks) x (Sp/64 query tiles)
-    // blocks of kDsTileElems. Concurrent workgroups of a head read adjacent
-    // blocks (a query-major order, which makes each workgroup's reads one
-    // stream but puts concurrent workgroups 1 MB apart, measured 10% slower).
+    // This slice's stored dS blocks (placement at ds_block_base): key-block
+    // major, so concurrent workgroups of a head read adjacent blocks (a
+    // query-major order, which makes each workgroup's reads one stream but
+    // puts concurrent workgroups 1 MB apart, measured 10% slower).
     const int nqt = Sp / 64, qt0 = q0 / 64;
-    const brsrc srs = make_rsrc((const bf16*)p.ds + (size_t)bh * (Skp / 128) * nqt * kDsTileElems,
-                                (uint32_t)(Skp / 128) * nqt * kDsTileElems * 2);
+    const long long nblk = ds_slice_blocks(Skp / 128, nqt, CAUSAL);
+    const brsrc srs = make_rsrc((const bf16*)p.ds + (size_t)(bh * nblk) * kDsTileElems,
+                                (uint32_t)(nblk * kDsTileElems * 2));
     const uint32_t kl = lds_addr(sK) + wave * 1024, sl = lds_addr(sS);
     auto load_tile = [&](int t, int slot) {
         for (int i = 0; i < NKI; i++)
             dma16(krs, kl + slot * KTB + i * NT * 16, koff[i], (uint32_t)t * BN * 2);
         // Column c = NW i + wave: query tile qt0 + c / 8, chunk c % 8, the 64
-        // keys of half t % 2 of key block t / 2: lane L loads key L. (Query
-        // tiles past Sp read the next key block's blocks, or zeros past the
-        // slice: only dQ rows past S, which are not written, use them.)
+        // keys of half t % 2 of key block t / 2: lane L loads key L. A query
+        // tile outside the key block's stored range (before its first tile,
+        // causal, or past Sp) is clamped into it: only a wave that skips this
+        // key tile, or dQ rows past S (not written), read that column.
+        const int kb = t / 2, f = ds_first_qt(kb, CAUSAL);
+        const long long kbase = ds_block_base(kb, nqt, CAUSAL);
         for (int i = 0; i < NSC / NW; i++) {
             const int c = NW * i + wave;
-            const uint32_t so = (uint32_t)(((t / 2) * nqt + qt0 + c / 8) * kDsTileElems * 2 +
+            int qt = qt0 + c / 8;
+            qt = qt < f ? f : (qt < nqt ? qt : nqt - 1);
+            const uint32_t so = (uint32_t)((kbase + (qt - f)) * kDsTileElems * 2 +
                                            ((t % 2) * 512 + (c % 8) * 64) * 16);
             dma16_nt(srs, sl + slot * STB + c * SCB, (uint32_t)lane * 16, so);
         }

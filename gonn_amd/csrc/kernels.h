@@ -66,8 +66,11 @@ struct BwdParams {
     const void* v;
     const void* dO;
     const void* kt;   // K^T  bf16 mode only
-    // dS-store path (bf16 mode): dS in blocks of kDsTileElems bf16, block
-    // ((bh * Skp/128 + key block) * Sp/64 + query tile); inside a block,
+    // dS-store path (bf16 mode): dS in blocks of kDsTileElems bf16 (one
+    // 128-key block x one 64-query tile), slice bh at block bh *
+    // ds_slice_blocks(..), key block kb's blocks from ds_block_base(kb, ..)
+    // on, one per query tile from ds_first_qt(kb, causal) (the tiles a causal
+    // key block reaches) to Sp/64; inside a block,
     // 16-byte piece ((key / 64) * 512 + c * 64 + key % 64) (key of the
     // block's 128) holds the key's dS for the 8 queries of
     // chunk c (queries 16 (c/2) + {4(c%2)..+3, 8+4(c%2)..+3}, the vt_pos
@@ -234,6 +237,21 @@ hipError_t launch_bwd_dq_ds(const BwdParams& p, int D, int causal, hipStream_t s
 constexpr int kBwdPad = 128;
 // bf16 elements of one (128-key block, 64-query tile) block of stored dS.
 constexpr int kDsTileElems = 128 * 64;
+// Placement of the stored dS blocks of one (b,h) slice with nqt = Sp/64
+// query tiles. A causal (top-left) key block kb reaches query tiles 2 kb
+// and later only, and only those blocks are stored: key block kb's blocks
+// start after sum_{k<kb} max(0, nqt - 2k) blocks, which for k < ceil(nqt/2)
+// is kb nqt - kb (kb - 1) (key blocks past every query store none).
+__host__ __device__ inline int ds_first_qt(int kb, int causal) { return causal ? 2 * kb : 0; }
+__host__ __device__ inline long long ds_block_base(int kb, int nqt, int causal) {
+    if (!causal) return (long long)kb * nqt;
+    const int half = (nqt + 1) / 2;
+    const long long kc = kb < half ? kb : half;
+    return kc * nqt - kc * (kc - 1);
+}
+__host__ __device__ inline long long ds_slice_blocks(int nkb, int nqt, int causal) {
+    return ds_block_base(nkb, nqt, causal);
+}
 
 // f64 <-> f32/bf16 conversion with optional head-dim padding:
 // dst (rows, dpad) <- src (rows, d); pad columns are zero.
