@@ -237,9 +237,9 @@ int check_bwd(const gonn_attn_bwd_args* a) {
 }
 
 // Backward workspace: lse2 and delta (BH,Sp) f32, then in bf16 mode the
-// packed operands Qb, dOb (BH,Sp,D), Kb, Vb (BH,Skp,D), Qt, dOt (BH,D,Sp)
-// and Kt (BH,D,Skp) bf16, each region 256-byte aligned (Sp, Skp: the query
-// and key counts rounded up to kBwdPad).
+// packed operands Qb, dOb (BH,Sp,D), Kb, Vb (BH,Skp,D) and Kt (BH,D,Skp)
+// bf16, and the stored dS when the dS path is taken, each region 256-byte
+// aligned (Sp, Skp: the query and key counts rounded up to kBwdPad).
 struct BwdLayout {
     size_t lse2, delta, packed[5], ds, total;
 };

@@ -14,21 +14,23 @@
 //   prep  lse2 = L * log2(e) (+inf on pad rows, so padded queries get P = 0)
 //         and D (0 on pad rows), one 16-lane row per query;
 //   dkdv  one workgroup per 128-key block of one (b,h) slice, 32 keys per
-//         wave. K and V of the block stay in VGPRs; Q / dO tiles (and their
-//         transposes in bf16 mode) stream through double-buffered LDS. Per
-//         query tile: S = Q K^T and dP = dO V^T on MFMA with one KEY per lane
-//         (the 16 accumulators of a lane are 16 queries), P and dS in
-//         registers, then dV^T += dO^T P and dK^T += Q^T dS on MFMA straight
-//         from those registers;
-//   dq    one workgroup per 128-query block, 32 queries per wave (the forward
-//         kernel's shape): S^T = K Q^T and dP^T = V dO^T with one QUERY per
-//         lane, so L_i and D_i are lane scalars; dQ^T += K^T dS^T. The bf16
-//         dQ kernel is in attn_bwd_dq.hip (built with other MFMA flags).
+//         wave. K and V of the block stay in VGPRs; Q / dO tiles stream
+//         through LDS rings (bf16 mode reads their transposes from the same
+//         tiles with ds_read_b64_tr_b16). Per query tile: S = Q K^T and
+//         dP = dO V^T on MFMA with one KEY per lane (the 16 accumulators of a
+//         lane are 16 queries), P and dS in registers, then dV^T += dO^T P
+//         and dK^T += Q^T dS on MFMA straight from those registers; bf16 mode
+//         also stores dS for the dQ kernel;
+//   dq    bf16 mode: dQ^T = K^T dS^T from the stored dS (attn_bwd_dqds.hip),
+//         or, past the dS buffer's limits, one workgroup per 128-query block
+//         that forms S^T = K Q^T and dP^T = V dO^T again with one QUERY per
+//         lane (attn_bwd_dq.hip, built with other MFMA flags); fp32 mode: the
+//         latter form, in this file.
 // Causal work skips fully masked tiles and masks only diagonal ones.
 //
 // bf16 mode reads the packed bf16 operands of attn_pack.hip (row-major Qb,
-// dOb, Kb, Vb and the vt_pos-permuted transposes Qt, dOt, Kt, all padded to
-// Sp rows); fp32 mode reads the caller's fp32 (BH,S,D) buffers directly with
+// dOb, Kb, Vb and the vt_pos-permuted transpose Kt, padded to Sp / Skp
+// rows); fp32 mode reads the caller's fp32 (BH,S,D) buffers directly with
 // v_mfma_f32_32x32x2_f32, clamping rows past S (masked or never written).
 #include <type_traits>
 

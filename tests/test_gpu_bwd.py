@@ -116,6 +116,39 @@ def test_bwd_bf16_dq_paths(D, causal, case, monkeypatch):
     assert np.array_equal(got["ds"][2], got["recompute"][2])
 
 
+@pytest.mark.parametrize("shape", [(100, 300), (300, 100), (129, 520)],
+                         ids=lambda s: f"Sq{s[0]}xSk{s[1]}")
+@pytest.mark.parametrize("causal", [False, True])
+def test_bwd_bf16_dq_paths_cross(shape, causal, monkeypatch):
+    """Sq != Sk on both bf16 dQ paths (top-left causal): with Sk > Sq the
+    causal key blocks past every query store no dS blocks and the dQ kernel
+    never reads them; with Sq > Sk every key block reaches the later
+    queries. Both paths against the oracle, dK/dV bitwise equal."""
+    from gonn_amd import hip
+    Sq, Sk = shape
+    B, H, D = 1, 2, 128
+    q = randn((B * H, Sq, D), 4300 + Sq)
+    k, v = (randn((B * H, Sk, D), 4301 + Sk + i) for i in range(2))
+    g = randn((B * H, Sq, D), 4305 + Sq)
+    dev = [torch.from_numpy(x).cuda().reshape(B, H, x.shape[1], D) for x in (q, k, v, g)]
+    o, l = hip.attn_fwd(*dev[:3], causal=causal, mode="bf16")
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal)
+    got = {}
+    for path in ("ds", "recompute"):
+        if path == "recompute":
+            monkeypatch.setenv("GONN_HIP_BWD_DQ", "recompute")
+        else:
+            monkeypatch.delenv("GONN_HIP_BWD_DQ", raising=False)
+        say(f"bwd dq path={path} Sq={Sq} Sk={Sk} causal={causal}")
+        dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=causal, mode="bf16")
+        torch.cuda.synchronize()
+        got[path] = [x.reshape(B * H, -1, D).cpu().numpy() for x in (dq, dk, dv)]
+        for x, ref, n in zip(got[path], (rq, rk, rv), ("dQ", "dK", "dV")):
+            assert_close(x, ref, "bf16", f"{n} path={path}")
+    assert np.array_equal(got["ds"][1], got["recompute"][1])
+    assert np.array_equal(got["ds"][2], got["recompute"][2])
+
+
 def test_bwd_golden_fixtures_via_f64_entry():
     """The committed torch-fp64 fixtures (square cases) through the reference-
     named f64 entry points FlashAttnF64Fwd / FlashAttnF64Bwd (head dims below
