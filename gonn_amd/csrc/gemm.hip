@@ -8,11 +8,19 @@
 // column-major, so the call computes C^T = op(B)^T op(A)^T with the stored
 // row-major column counts as leading dimensions. fp64 runs on the fp64
 // MFMA path of gfx950 inside rocBLAS (a plain library GEMM).
+//
+// Skinny case (batch 1, C = A W^T with W row-major (n, k), m <= 64, k a
+// multiple of 128: the projections of a decoding step, m = B x T rows
+// against E x E weights): a kernel of its own. rocBLAS takes about 445 us
+// for m = 64, k = 4096 whatever n (4096 or 12288; 4.8 and 14 TFLOP/s),
+// the time of a few output tiles walking the whole k range serially; the
+// whole of that GEMM is 2.1 GFLOP (27 us at the 78.6 TFLOP/s fp64 peak).
 #include <hip/hip_runtime.h>
 #include <rocblas/rocblas.h>
 
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 #include <mutex>
 
 #include "../../include/gonn_hip.h"
@@ -68,9 +76,102 @@ __global__ void zero_kernel(double* __restrict__ c, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) c[i] = 0.0;
 }
 
-// Caller holds g_mu and the handle exists.
+// ---- skinny C = A W^T (m <= 64) on v_mfma_f64_16x16x4_f64 ----
+// One workgroup of 4 waves per 16 output columns; wave w takes the k range
+// [w k/4, (w+1) k/4) and all (up to 4) 16-row tiles of A, and the 4 waves'
+// partial tiles are summed through LDS in wave order (deterministic, no
+// global workspace). MFMA k-slots are free to map to any k as long as A and
+// B agree: lane group q = lane / 16 takes 8 consecutive k of each 32-k chunk,
+// so every lane loads 64 contiguous bytes of its A row and its W row (four
+// 16-byte loads each), and the next chunk's loads are issued before the
+// current chunk's 32 MFMAs. A (m x k, 2 MB at m = 64, k = 4096) is re-read
+// from L2 by every workgroup; W streams once.
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
+constexpr int kSkS = 8;             // k-steps of 4 per lane group per chunk
+constexpr int kSkChunk = 4 * kSkS;  // k per chunk
+
+__global__ __launch_bounds__(256, 2) void gemm_f64_skinny_nt(const double* __restrict__ A,
+                                                             const double* __restrict__ W,
+                                                             double* __restrict__ C, int m, int k,
+                                                             int n) {
+    __shared__ double red[4][4 * 4 * 64];  // [wave][(mt, r, lane)]
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * 16, col = n0 + i;
+    const double* wrow = W + (size_t)(col < n ? col : 0) * k;
+    const double* arow[4];
+    bool live[4];
+    for (int mt = 0; mt < 4; mt++) {
+        const int r = 16 * mt + i;
+        live[mt] = r < m;
+        arow[mt] = A + (size_t)(live[mt] ? r : 0) * k;
+    }
+    const bool wlive = col < n;
+    const int kw = k / 4, kb = wave * kw;
+    f64x4 acc[4];
+    for (int mt = 0; mt < 4; mt++) acc[mt] = f64x4{0.0, 0.0, 0.0, 0.0};
+    // Two register buffers (X, Y) of one chunk each; the chunk loop is
+    // unrolled by two so that no buffer is indexed at run time.
+    f64x2 wX[kSkS / 2], aX[4][kSkS / 2], wY[kSkS / 2], aY[4][kSkS / 2];
+    auto load = [&](f64x2* wv, f64x2 (*av)[kSkS / 2], int c0) {
+        const int kk = c0 + q * kSkS;
+        for (int h = 0; h < kSkS / 2; h++)
+            wv[h] = wlive ? *(const f64x2*)(wrow + kk + 2 * h) : f64x2{0.0, 0.0};
+        for (int mt = 0; mt < 4; mt++)
+            for (int h = 0; h < kSkS / 2; h++)
+                av[mt][h] = live[mt] ? *(const f64x2*)(arow[mt] + kk + 2 * h) : f64x2{0.0, 0.0};
+    };
+    auto compute = [&](const f64x2* wv, const f64x2 (*av)[kSkS / 2]) {
+        for (int st = 0; st < kSkS; st++)
+            for (int mt = 0; mt < 4; mt++)
+                if (16 * mt < m)  // uniform: row tiles past m are skipped
+                    acc[mt] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[mt][st >> 1][st & 1],
+                                                                   wv[st >> 1][st & 1], acc[mt],
+                                                                   0, 0, 0);
+    };
+    const int nch = kw / kSkChunk;  // >= 1 (k % 128 == 0)
+    load(wX, aX, kb);
+    for (int c = 0; c < nch; c += 2) {
+        if (c + 1 < nch) load(wY, aY, kb + (c + 1) * kSkChunk);
+        compute(wX, aX);
+        if (c + 1 >= nch) break;
+        if (c + 2 < nch) load(wX, aX, kb + (c + 2) * kSkChunk);
+        compute(wY, aY);
+    }
+    for (int mt = 0; mt < 4; mt++)
+        for (int r = 0; r < 4; r++) red[wave][(mt * 4 + r) * 64 + lane] = acc[mt][r];
+    __syncthreads();
+    // Output element e = (mt, r, lane): row 16 mt + 4 r + lane / 16, column
+    // n0 + lane % 16 (the f64 16x16 accumulator layout, probed on gfx950:
+    // register r of lane l holds row 4 r + l / 16, column l % 16).
+    for (int e = threadIdx.x; e < 4 * 4 * 64; e += 256) {
+        const int mt = e >> 8, r = (e >> 6) & 3, ln = e & 63;
+        const int row = 16 * mt + 4 * r + (ln >> 4), cc = n0 + (ln & 15);
+        if (row < m && cc < n)
+            C[(size_t)row * n + cc] = ((red[0][e] + red[1][e]) + red[2][e]) + red[3][e];
+    }
+}
+
+bool skinny_ok(int batch, int m, int k, int n, int transA, int transB) {
+    return batch == 1 && !transA && transB && m >= 1 && m <= 64 && k >= 128 && k % 128 == 0 &&
+           n >= 1;
+}
+
+int run_skinny(const double* dA, const double* dB, double* dC, int m, int k, int n,
+               hipStream_t s) {
+    hipLaunchKernelGGL(gemm_f64_skinny_nt, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, dA,
+                       dB, dC, m, k, n);
+    return herr(hipGetLastError());
+}
+
+// Caller holds g_mu and the handle exists. GONN_HIP_GEMM=rocblas keeps the
+// skinny shapes on rocBLAS too.
 int run_gemm(const double* dA, const double* dB, double* dC, int batch, int m, int k, int n,
              int transA, int transB, hipStream_t s) {
+    const char* e = std::getenv("GONN_HIP_GEMM");
+    if (skinny_ok(batch, m, k, n, transA, transB) && !(e && std::strcmp(e, "rocblas") == 0))
+        return run_skinny(dA, dB, dC, m, k, n, s);
     if (rocblas_set_stream(g_handle, s) != rocblas_status_success) return GONN_E_BLAS;
     const double alpha = 1.0, beta = 0.0;
     const rocblas_operation opA = transA ? rocblas_operation_transpose : rocblas_operation_none;

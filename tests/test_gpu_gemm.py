@@ -1,5 +1,6 @@
 """GPU checks of the HIP backend's fp64 GEMM (gonn_hip_gemm_f64 /
-gonn_hip_gemm_f64_dev, rocBLAS on gfx950) and of the MHA running its
+gonn_hip_gemm_f64_dev: rocBLAS on gfx950, and a kernel of its own for the
+skinny C = A W^T shapes of a decoding step) and of the MHA running its
 projections through it. Bar: max absolute difference 1e-10, the
 reference's GPU-vs-CPU GEMM bar (tensor/cuda_dispatch_test.go:127-131); the
 CPU side is numpy's fp64 matmul (an independent BLAS), and the small cases
@@ -39,6 +40,47 @@ def test_device_gemm_matches_numpy(shape, ta, tb):
     err = float(np.max(np.abs(got - ref)))
     say(f"[gemm] max abs err {err:.2e}")
     assert err <= 1e-10
+
+
+@pytest.mark.parametrize("shape", [(1, 128, 16), (7, 256, 33), (16, 128, 1), (33, 384, 100),
+                                   (64, 4096, 4096), (64, 4096, 12288), (48, 512, 4100)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_skinny_gemm_path(shape, monkeypatch):
+    """The skinny kernel (C = A W^T, m <= 64, k % 128 == 0: the decoding
+    step's projections) against numpy at the backend's bar, on host and
+    device buffers, and against the rocBLAS path of the same call
+    (GONN_HIP_GEMM=rocblas)."""
+    from gonn_amd import _lib, hip
+    import ctypes
+    m, k, n = shape
+    say(f"[gemm skinny] m={m} k={k} n={n}")
+    rng = np.random.default_rng(m + k + n)
+    A = rng.standard_normal(m * k)
+    W = rng.standard_normal(n * k)
+    ref = _ref(A, W, 1, m, k, n, False, True)
+    got = hip.Gemm(A, W, 1, m, k, n, False, True)
+    err = float(np.max(np.abs(got - ref)))
+    say(f"[gemm skinny] host max abs err {err:.2e}")
+    assert err <= 1e-10
+    dA, dW = (torch.from_numpy(x).cuda() for x in (A, W))
+    out = {}
+    for path in ("skinny", "rocblas"):
+        if path == "rocblas":
+            monkeypatch.setenv("GONN_HIP_GEMM", "rocblas")
+        else:
+            monkeypatch.delenv("GONN_HIP_GEMM", raising=False)
+        C = torch.full((m * n,), float("nan"), dtype=torch.float64, device="cuda")
+        bufs = [_lib.Buf(t.data_ptr(), t.numel() * 8, _lib.GONN_F64) for t in (dA, dW, C)]
+        st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        _lib.check(_lib.load().gonn_hip_gemm_f64_dev(ctypes.byref(bufs[0]), ctypes.byref(bufs[1]),
+                                                     ctypes.byref(bufs[2]), 1, m, k, n, 0, 1, st),
+                   "gemm_f64_dev")
+        torch.cuda.synchronize()
+        out[path] = C.cpu().numpy()
+        assert np.all(np.isfinite(out[path])), path
+        assert float(np.max(np.abs(out[path] - ref))) <= 1e-10, path
+    # two fp64 summation orders: equal to rounding
+    assert float(np.max(np.abs(out["skinny"] - out["rocblas"]))) <= 1e-11
 
 
 def test_device_gemm_dev_buffers():
