@@ -9,9 +9,9 @@
 // row-major column counts as leading dimensions. fp64 runs on the fp64
 // MFMA path of gfx950 inside rocBLAS (a plain library GEMM).
 //
-// Skinny case (batch 1, C = A W^T with W row-major (n, k), m <= 64, k a
-// multiple of 128: the projections of a decoding step, m = B x T rows
-// against E x E weights): a kernel of its own. rocBLAS takes about 445 us
+// Skinny case (batch 1, C = A W^T with W row-major (n, k), m <= 256 as
+// skinny_ok bounds it, k a multiple of 128: the projections of a decoding
+// step, m = B x T rows against E x E weights): a kernel of its own. rocBLAS takes about 445 us
 // for m = 64, k = 4096 whatever n (4096 or 12288; 4.8 and 14 TFLOP/s),
 // the time of a few output tiles walking the whole k range serially; the
 // whole of that GEMM is 2.1 GFLOP (27 us at the 78.6 TFLOP/s fp64 peak).
@@ -76,30 +76,57 @@ __global__ void zero_kernel(double* __restrict__ c, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) c[i] = 0.0;
 }
 
-// ---- skinny C = A W^T (m <= 64) on v_mfma_f64_16x16x4_f64 ----
-// One workgroup of 4 waves per 16 output columns; wave w takes the k range
+// ---- skinny C = A W^T (m <= 256) on v_mfma_f64_16x16x4_f64 ----
+// One workgroup of 4 waves per 16 NW output columns and 64 rows (a row chunk);
+// wave w takes the k range
 // [w k/4, (w+1) k/4) and all (up to 4) 16-row tiles of A, and the 4 waves'
 // partial tiles are summed through LDS in wave order (deterministic, no
 // global workspace). MFMA k-slots are free to map to any k as long as A and
 // B agree: lane group q = lane / 16 takes 8 consecutive k of each 32-k chunk,
 // so every lane loads 64 contiguous bytes of its A row and its W row (four
 // 16-byte loads each), and the next chunk's loads are issued before the
-// current chunk's 32 MFMAs. A (m x k, 2 MB at m = 64, k = 4096) is re-read
-// from L2 by every workgroup; W streams once.
+// current chunk's 32 MFMAs. A variant takes 32 output columns per
+// workgroup (NW = 2) with 16 k per lane group and chunk. A row chunk
+// (64 x k, 2 MB at k = 4096) is re-read from L2 by every workgroup of the
+// chunk. The row chunks of one
+// column tile get block indices 8 apart, so they run on one XCD and read
+// that tile of W from its L2: W streams from HBM once.
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 typedef double f64x2 __attribute__((ext_vector_type(2)));
-constexpr int kSkS = 8;             // k-steps of 4 per lane group per chunk
-constexpr int kSkChunk = 4 * kSkS;  // k per chunk
+constexpr int kSkinnyMaxRows = 256;
 
+template <int NW, int SKS>
 __global__ __launch_bounds__(256, 2) void gemm_f64_skinny_nt(const double* __restrict__ A,
                                                              const double* __restrict__ W,
                                                              double* __restrict__ C, int m, int k,
                                                              int n) {
-    __shared__ double red[4][4 * 4 * 64];  // [wave][(mt, r, lane)]
+    constexpr int CHUNK = 4 * SKS;  // k per chunk
+    constexpr int H = SKS / 2;      // 16-byte loads per row per chunk
+    __shared__ double red[4][NW * 4 * 4 * 64];  // [wave][(j, mt, r, lane)]
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int i = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * 16, col = n0 + i;
-    const double* wrow = W + (size_t)(col < n ? col : 0) * k;
+    // Block -> (column tile, row chunk): with 8 | column tiles, block L runs
+    // on XCD L % 8 and the nm chunks of tile 8 (L / 8 / nm) + L % 8 share it.
+    const int nm = (m + 63) / 64, ntile = (n + 16 * NW - 1) / (16 * NW), L = blockIdx.x;
+    int tile, chunk;
+    if (ntile % 8 == 0) {
+        tile = (L >> 3) / nm * 8 + (L & 7);
+        chunk = (L >> 3) % nm;
+    } else {
+        tile = L / nm;
+        chunk = L % nm;
+    }
+    A += (size_t)chunk * 64 * k;
+    C += (size_t)chunk * 64 * n;
+    m = m - chunk * 64 < 64 ? m - chunk * 64 : 64;
+    const int n0 = tile * 16 * NW;
+    const double* wrow[NW];
+    bool wlive[NW];
+    for (int j = 0; j < NW; j++) {
+        const int col = n0 + 16 * j + i;
+        wlive[j] = col < n;
+        wrow[j] = W + (size_t)(wlive[j] ? col : 0) * k;
+    }
     const double* arow[4];
     bool live[4];
     for (int mt = 0; mt < 4; mt++) {
@@ -107,61 +134,90 @@ __global__ __launch_bounds__(256, 2) void gemm_f64_skinny_nt(const double* __res
         live[mt] = r < m;
         arow[mt] = A + (size_t)(live[mt] ? r : 0) * k;
     }
-    const bool wlive = col < n;
     const int kw = k / 4, kb = wave * kw;
-    f64x4 acc[4];
-    for (int mt = 0; mt < 4; mt++) acc[mt] = f64x4{0.0, 0.0, 0.0, 0.0};
+    f64x4 acc[NW][4];
+    for (int j = 0; j < NW; j++)
+        for (int mt = 0; mt < 4; mt++) acc[j][mt] = f64x4{0.0, 0.0, 0.0, 0.0};
     // Two register buffers (X, Y) of one chunk each; the chunk loop is
     // unrolled by two so that no buffer is indexed at run time.
-    f64x2 wX[kSkS / 2], aX[4][kSkS / 2], wY[kSkS / 2], aY[4][kSkS / 2];
-    auto load = [&](f64x2* wv, f64x2 (*av)[kSkS / 2], int c0) {
-        const int kk = c0 + q * kSkS;
-        for (int h = 0; h < kSkS / 2; h++)
-            wv[h] = wlive ? *(const f64x2*)(wrow + kk + 2 * h) : f64x2{0.0, 0.0};
+    f64x2 wX[NW][H], aX[4][H], wY[NW][H], aY[4][H];
+    auto load = [&](f64x2 (*wv)[H], f64x2 (*av)[H], int c0) {
+        const int kk = c0 + q * SKS;
+        for (int j = 0; j < NW; j++)
+            for (int h = 0; h < H; h++)
+                wv[j][h] = wlive[j] ? *(const f64x2*)(wrow[j] + kk + 2 * h) : f64x2{0.0, 0.0};
         for (int mt = 0; mt < 4; mt++)
-            for (int h = 0; h < kSkS / 2; h++)
+            for (int h = 0; h < H; h++)
                 av[mt][h] = live[mt] ? *(const f64x2*)(arow[mt] + kk + 2 * h) : f64x2{0.0, 0.0};
     };
-    auto compute = [&](const f64x2* wv, const f64x2 (*av)[kSkS / 2]) {
-        for (int st = 0; st < kSkS; st++)
-            for (int mt = 0; mt < 4; mt++)
-                if (16 * mt < m)  // uniform: row tiles past m are skipped
-                    acc[mt] = __builtin_amdgcn_mfma_f64_16x16x4f64(av[mt][st >> 1][st & 1],
-                                                                   wv[st >> 1][st & 1], acc[mt],
-                                                                   0, 0, 0);
+    auto compute = [&](const f64x2 (*wv)[H], const f64x2 (*av)[H]) {
+        for (int st = 0; st < SKS; st++)
+            for (int j = 0; j < NW; j++)
+                for (int mt = 0; mt < 4; mt++)
+                    if (16 * mt < m)  // uniform: row tiles past m are skipped
+                        acc[j][mt] = __builtin_amdgcn_mfma_f64_16x16x4f64(
+                            av[mt][st >> 1][st & 1], wv[j][st >> 1][st & 1], acc[j][mt], 0, 0, 0);
     };
-    const int nch = kw / kSkChunk;  // >= 1 (k % 128 == 0)
+    const int nch = kw / CHUNK;  // >= 1 (k % 128 == 0)
     load(wX, aX, kb);
     for (int c = 0; c < nch; c += 2) {
-        if (c + 1 < nch) load(wY, aY, kb + (c + 1) * kSkChunk);
+        if (c + 1 < nch) load(wY, aY, kb + (c + 1) * CHUNK);
         compute(wX, aX);
         if (c + 1 >= nch) break;
-        if (c + 2 < nch) load(wX, aX, kb + (c + 2) * kSkChunk);
+        if (c + 2 < nch) load(wX, aX, kb + (c + 2) * CHUNK);
         compute(wY, aY);
     }
-    for (int mt = 0; mt < 4; mt++)
-        for (int r = 0; r < 4; r++) red[wave][(mt * 4 + r) * 64 + lane] = acc[mt][r];
+    for (int j = 0; j < NW; j++)
+        for (int mt = 0; mt < 4; mt++)
+            for (int r = 0; r < 4; r++)
+                red[wave][((j * 4 + mt) * 4 + r) * 64 + lane] = acc[j][mt][r];
     __syncthreads();
-    // Output element e = (mt, r, lane): row 16 mt + 4 r + lane / 16, column
-    // n0 + lane % 16 (the f64 16x16 accumulator layout, probed on gfx950:
-    // register r of lane l holds row 4 r + l / 16, column l % 16).
-    for (int e = threadIdx.x; e < 4 * 4 * 64; e += 256) {
-        const int mt = e >> 8, r = (e >> 6) & 3, ln = e & 63;
-        const int row = 16 * mt + 4 * r + (ln >> 4), cc = n0 + (ln & 15);
+    // Output element e = (j, mt, r, lane): row 16 mt + 4 r + lane / 16,
+    // column n0 + 16 j + lane % 16 (the f64 16x16 accumulator layout, probed
+    // on gfx950: register r of lane l holds row 4 r + l / 16, column l % 16).
+    for (int e = threadIdx.x; e < NW * 4 * 4 * 64; e += 256) {
+        const int j = e >> 10, mt = (e >> 8) & 3, r = (e >> 6) & 3, ln = e & 63;
+        const int row = 16 * mt + 4 * r + (ln >> 4), cc = n0 + 16 * j + (ln & 15);
         if (row < m && cc < n)
             C[(size_t)row * n + cc] = ((red[0][e] + red[1][e]) + red[2][e]) + red[3][e];
     }
 }
 
+// Shapes the skinny kernel takes: every m <= 64 (rocBLAS spends ~445 us on
+// any such call at k = 4096, the skinny kernel 27-32 TFLOP/s), and m <= 256
+// while the product is at most 16 GFLOP (the skinny kernel's 35-47 TFLOP/s
+// against rocBLAS's ~445 us floor and 57 TFLOP/s beyond it, measured at
+// k = 4096 on one MI355X: 128 x 12288 382 against 448 us, 256 x 4096 184
+// against 443 us, 256 x 12288 566 against 452 us).
 bool skinny_ok(int batch, int m, int k, int n, int transA, int transB) {
-    return batch == 1 && !transA && transB && m >= 1 && m <= 64 && k >= 128 && k % 128 == 0 &&
-           n >= 1;
+    if (batch != 1 || transA || !transB || m < 1 || k < 128 || k % 128 != 0 || n < 1) return false;
+    return m <= 64 || (m <= kSkinnyMaxRows && 2.0 * m * n * k <= 1.6e10);
+}
+
+int device_cus() {
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev] &&
+        hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus[dev] = 256;
+    return cus[dev];
 }
 
 int run_skinny(const double* dA, const double* dB, double* dC, int m, int k, int n,
                hipStream_t s) {
-    hipLaunchKernelGGL(gemm_f64_skinny_nt, dim3((unsigned)((n + 15) / 16)), dim3(256), 0, s, dA,
-                       dB, dC, m, k, n);
+    // 32 columns per workgroup halve the re-reads of A where that still
+    // leaves a workgroup per CU (128 x 4096: 111 against 154 us; 64 x 4096,
+    // 128 workgroups: 106 against 78 us).
+    const long long wide = (long long)((n + 31) / 32) * ((m + 63) / 64);
+    const int nw = wide >= device_cus() ? 2 : 1;
+    const unsigned blocks = (unsigned)((n + 16 * nw - 1) / (16 * nw)) * (unsigned)((m + 63) / 64);
+    if (nw == 2)
+        hipLaunchKernelGGL((gemm_f64_skinny_nt<2, 4>), dim3(blocks), dim3(256), 0, s, dA, dB, dC, m,
+                           k, n);
+    else
+        hipLaunchKernelGGL((gemm_f64_skinny_nt<1, 8>), dim3(blocks), dim3(256), 0, s, dA, dB, dC, m,
+                           k, n);
     return herr(hipGetLastError());
 }
 

@@ -43,11 +43,15 @@ def test_device_gemm_matches_numpy(shape, ta, tb):
 
 
 @pytest.mark.parametrize("shape", [(1, 128, 16), (7, 256, 33), (16, 128, 1), (33, 384, 100),
-                                   (64, 4096, 4096), (64, 4096, 12288), (48, 512, 4100)],
+                                   (64, 4096, 4096), (64, 4096, 12288), (48, 512, 4100),
+                                   (65, 128, 48), (100, 256, 200), (256, 4096, 4096),
+                                   (128, 4096, 12288), (200, 384, 136), (200, 256, 4100),
+                                   (130, 128, 8200)],
                          ids=lambda s: "x".join(map(str, s)))
 def test_skinny_gemm_path(shape, monkeypatch):
-    """The skinny kernel (C = A W^T, m <= 64, k % 128 == 0: the decoding
-    step's projections) against numpy at the backend's bar, on host and
+    """The skinny kernel (C = A W^T, m <= 256, k % 128 == 0: the decoding
+    step's projections; row chunks of 64, 16 and 32 columns per workgroup,
+    column tile counts with and without the XCD grouping) against numpy at the backend's bar, on host and
     device buffers, and against the rocBLAS path of the same call
     (GONN_HIP_GEMM=rocblas)."""
     from gonn_amd import _lib, hip
