@@ -628,7 +628,13 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     // S^T chains behind their LDS reads). MFMA order per 16-key PV k-step j:
     // PV(j, dt = 0..3), then S^T k-steps 2j and 2j+1 (mt = 0, 1), so six
     // accumulator chains interleave.
-    auto step = [&](int t, f32x16* sA, f32x16* sB) __attribute__((always_inline)) {
+    // TAIL: 0 a full step; 1 the block's next-to-last step (no S^T(t+2) and
+    // no K load: that tile is past the block); 2 its last step (no P(t+1)
+    // and no tile loads either, and a wave whose rows all precede tile t's
+    // first key skips its PV MFMAs: P(t) is zero there).
+    auto step = [&](int t, f32x16* sA, f32x16* sB, auto TAILC) __attribute__((always_inline)) {
+        constexpr int TAIL = decltype(TAILC)::value;
+        const bool pv_dead = CAUSAL && TAIL == 2 && t * BN > qw + 31;
         const int kslot = (t + KLEAD) & (KSLOTS - 1);
         const int vslot = (t + 1) & 1;
         // Tiles past the last one are clamped to it: such a load refills a
@@ -637,8 +643,9 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         const int vload = t + VLEAD < ntiles ? t + VLEAD : ntiles - 1;
         // Diagonal / key-end tiles only (a wave-uniform branch ahead of the
         // step's MFMA stream).
-        if (needs_mask(t + 1)) mask(t + 1, sB);
-        if constexpr (MASK) mrow.load(t + 2 < ntiles ? t + 2 : ntiles - 1, g, mreg);
+        if constexpr (TAIL < 2)
+            if (needs_mask(t + 1)) mask(t + 1, sB);
+        if constexpr (MASK && TAIL == 0) mrow.load(t + 2 < ntiles ? t + 2 : ntiles - 1, g, mreg);
         const uint32_t vb = (uint32_t)(t & 1) * VTB;
         const uint32_t kb = (uint32_t)((t + 2) & (KSLOTS - 1)) * KTB;
 
@@ -657,13 +664,15 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         auto fetch = [&](auto E) {
             constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
             if constexpr (w < NDT) opr[e & 3] = vfrag(vb, j, w);
-            else opr[e & 3] = kfrag(kb, SKS * j + ((w - NDT) >> 1), (w - NDT) & 1);
+            else if constexpr (TAIL == 0)
+                opr[e & 3] = kfrag(kb, SKS * j + ((w - NDT) >> 1), (w - NDT) & 1);
         };
         auto issue = [&](auto E) {
             constexpr int e = decltype(E)::value, j = e / GW, w = e % GW;
             if constexpr (w < NDT) {
-                oacc[w] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pp[j]), oacc[w]);
-            } else {
+                if (TAIL < 2 || !pv_dead)
+                    oacc[w] = mfma_bf16(opr[e & 3], __builtin_bit_cast(bf16x8, pp[j]), oacc[w]);
+            } else if constexpr (TAIL == 0) {
                 constexpr int kk = SKS * j + ((w - NDT) >> 1), mt = (w - NDT) & 1;
                 sA[mt] = mfma_bf16(opr[e & 3], qf[kk], kk == 0 ? nmc : sA[mt]);
             }
@@ -672,13 +681,16 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         // the V(t+1) loads. Its M0 is written at the slot before.
         auto dma_slot = [&](auto E) {
             constexpr int e = decltype(E)::value;
-            if constexpr (e % DS == 0 && e / DS < NDMA) {
+            // Tail steps load no K tile (TAIL >= 1) and no V tile (TAIL 2).
+            constexpr int d0 = TAIL == 0 ? 0 : (TAIL == 1 ? NKI : NDMA);
+            if constexpr (e % DS == 0 && e / DS < NDMA && e / DS >= d0) {
                 constexpr int d = e / DS;
                 const uint32_t lds = d < NKI ? kl + kslot * KTB + d * NT * 16
                                              : vl + vslot * VTB + (d - NKI) * NT * 16;
                 dma_set_m0(lds);
             }
-            if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA) {
+            if constexpr (e >= 1 && (e - 1) % DS == 0 && (e - 1) / DS < NDMA &&
+                          (e - 1) / DS >= d0) {
                 constexpr int d = (e - 1) / DS;
                 if constexpr (d < NKI) dma16_m0(krs, koff[d], kload * BN * D * 2);
                 else dma16_m0(vrs, voff[d - NKI], vload * BN * 2);
@@ -717,6 +729,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         // uslot(k) - 2 + 2 st); e = NM runs everything past the stream's end.
         auto uops_at = [&](auto E) {
             constexpr int e = decltype(E)::value;
+            if constexpr (TAIL == 2) return;  // P(t+1) is past the block
             static_for<2>([&](auto S) {
                 static_for<NU>([&](auto U) {
                     constexpr int at = uslot(decltype(U)::value) - 2 + 2 * decltype(S)::value;
@@ -751,7 +764,8 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
             // every earlier key blocked or -inf), so the offset follows the
             // first tile with a finite score instead of staying at a level
             // below which the tile's P would underflow.
-            if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound) || l == 0.f)) {
+            // (Not in the last step: no P(t+1) there, and sB is not a tile.)
+            if (TAIL < 2 && __builtin_amdgcn_ballot_w64(!(ts <= kSumBound) || l == 0.f)) {
                 const float mx = tile_max(sB);
                 const bool empty = pair_sum32(l) == 0.f;
                 const float mn =
@@ -760,7 +774,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
                 mc = mn;
                 ts = p_tile(sB, pp, -mc);
             }
-        } else if (__builtin_amdgcn_ballot_w64(!(ts <= kSumBound))) {
+        } else if (TAIL < 2 && __builtin_amdgcn_ballot_w64(!(ts <= kSumBound))) {
             const float mx = tile_max(sB);  // relative to mc
             const float dlt = mx > kLazyLog2 ? -mx : 0.f;
             alpha = fast_exp2(dlt);
@@ -774,7 +788,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         // K(t+3) and V(t+1), which step t+1 reads, have landed.
         GONN_VMCNT(0);
         __syncthreads();
-        if constexpr (MASK) MaskRow::add(mreg, sA);
+        if constexpr (MASK && TAIL == 0) MaskRow::add(mreg, sA);
         if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
             for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
     };
@@ -826,12 +840,30 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     __syncthreads();
 
     {
+        // S^T(k) lives in s[k & 1]. Full steps up to the block's last two,
+        // then the tail steps: 1 reads S^T(ntiles - 1) as sB, 2 reads only
+        // P(ntiles - 1) (no S^T tile). One copy of each tail step: when the
+        // next-to-last index is odd, s0 and s1 trade contents first.
+        const std::integral_constant<int, 0> full;
+        const std::integral_constant<int, 1> tail1;
+        const std::integral_constant<int, 2> tail2;
+        const int nfull = ntiles - 2;
         int t = 0;
-        for (; t + 1 < ntiles; t += 2) {
-            step(t, s0, s1);
-            step(t + 1, s1, s0);
+        for (; t + 1 < nfull; t += 2) {
+            step(t, s0, s1, full);
+            step(t + 1, s1, s0, full);
         }
-        if (t < ntiles) step(t, s0, s1);
+        if (t < nfull) step(t++, s0, s1, full);
+        if (ntiles >= 2) {
+            if (t & 1)
+                for (int mt = 0; mt < 2; mt++) {
+                    const f32x16 x = s0[mt];
+                    s0[mt] = s1[mt];
+                    s1[mt] = x;
+                }
+            step(t, s0, s1, tail1);
+        }
+        step(ntiles - 1, s1, s0, tail2);
     }
     // The last steps leave V loads in flight; they write this workgroup's
     // LDS, so they land before the waves exit.
