@@ -816,6 +816,9 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
     GONN_VMCNT(0);
     __syncthreads();
     qk_tile(sVc + VTB, s0, f32x16{});
+    // K(1), or for a one-tile block a masked copy of K(0): issued before the
+    // VALU of tile 0 so the two overlap; -mc is added once mc is known.
+    qk_tile(sKc + KTB, s1, f32x16{});
     if constexpr (MASK) {
         mrow.load(0, g, mreg);
         MaskRow::add(mreg, s0);
@@ -829,9 +832,9 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK)) void fwd_bf16_pipe_kern
         if (!(mc > -INFINITY)) mc = 0.f;  // a first tile of -inf: no offset yet
     } else {
         nmc = f32x16{} - mc;
+        for (int mt = 0; mt < 2; mt++) s1[mt] += nmc;
     }
     l = p_tile(s0, pp, -mc);
-    qk_tile(sKc + KTB, s1, nmc);  // K(1), or for a one-tile block a masked copy of K(0)
     if constexpr (MASK) {
         mrow.load(last(1), g, mreg);
         MaskRow::add(mreg, s1);
