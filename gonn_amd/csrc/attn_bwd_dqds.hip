@@ -97,9 +97,16 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
     const brsrc srs = make_rsrc((const bf16*)p.ds + (size_t)(bh * nblk) * kDsTileElems,
                                 (uint32_t)(nblk * kDsTileElems * 2));
     const uint32_t kl = lds_addr(sK) + wave * 1024, sl = lds_addr(sS);
-    auto load_tile = [&](int t, int slot) {
+    // A load no step reads (a tile past the last, or a dS column whose
+    // waves skip this key tile) still issues, so every wave's vmcnt counts
+    // match, but against a zero-size buffer: it moves no bytes.
+    const brsrc nul = make_rsrc(p.ds, 0u);
+    auto load_tile = [&](int t0, int slot) {
+        const bool real = t0 < ntiles;
+        const int t = real ? t0 : ntiles - 1;
+        const brsrc kr = real ? krs : nul;
         for (int i = 0; i < NKI; i++)
-            dma16(krs, kl + slot * KTB + i * NT * 16, koff[i], (uint32_t)t * BN * 2);
+            dma16(kr, kl + slot * KTB + i * NT * 16, koff[i], (uint32_t)t * BN * 2);
         // Column c = NW i + wave: query tile qt0 + c / 8, chunk c % 8, the 64
         // keys of half t % 2 of key block t / 2: lane L loads key L. A query
         // tile outside the key block's stored range (before its first tile,
@@ -113,7 +120,9 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
             qt = qt < f ? f : (qt < nqt ? qt : nqt - 1);
             const uint32_t so = (uint32_t)((kbase + (qt - f)) * kDsTileElems * 2 +
                                            ((t % 2) * 512 + (c % 8) * 64) * 16);
-            dma16_nt(srs, sl + slot * STB + c * SCB, (uint32_t)lane * 16, so);
+            // Column c is read by the waves of query tile qt0 + c / 8.
+            const bool need = real && (!CAUSAL || t <= qt0 + c / 8);
+            dma16_nt(need ? srs : nul, sl + slot * STB + c * SCB, (uint32_t)lane * 16, so);
         }
     };
 
@@ -140,16 +149,16 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
 
     f32x16 acc[NDT];
     for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x16{};
-    // Tiles past the last are clamped to it (a redundant load into a slot
-    // no step reads), so every step issues NLD loads and the wait for tile
-    // t+1 at the end of step t is always "all but the newest PF-1 tiles".
+    // Tiles past the last are loads of no bytes into a slot no step reads,
+    // so every step issues NLD loads and the wait for tile t+1 at the end of
+    // step t is always "all but the newest PF-1 tiles".
     if (ntiles > 0) {
-        for (int j = 0; j < PF; j++) load_tile(j < ntiles ? j : ntiles - 1, j);
+        for (int j = 0; j < PF; j++) load_tile(j, j);
         GONN_VMCNT((PF - 1) * NLD);
         __syncthreads();
         for (int t = 0; t < ntiles; t++) {
             const int cur = t % NSLOT;
-            load_tile(t + PF < ntiles ? t + PF : ntiles - 1, (t + PF) % NSLOT);
+            load_tile(t + PF, (t + PF) % NSLOT);
             const char* kbase = (const char*)sK + cur * KTB;
             const uint32_t sbase = cur * STB + sb;
             // Causal: this wave's 32 queries lie in query tile qt0 + wave/2,
