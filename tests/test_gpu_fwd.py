@@ -3,7 +3,8 @@
 Configs: small ragged shapes for both modes, D in {64, 128}, causal and not,
 Sq != Sk (top-left causal); BASELINE configs C2 (encoder) and C3 (causal
 prefill) at full size on sampled query rows, plus size-independent properties
-at full size (causal invariance, Q = 0 prefix means, determinism).
+at full size (causal invariance, Q = 0 prefix means, determinism); bfloat16
+inputs against their float32 widening (bit-identical outputs).
 """
 import math
 
@@ -144,3 +145,43 @@ def test_ref_shape_refattn_protocol():
                               scale, causal)
         # the fused fp64 kernel met 1e-9; fp32-MFMA meets the fp32 bar
         assert_close(O.reshape(BH, S, d), ref, "fp32", f"refAttn causal={causal}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("shape", [(2, 64, 64), (2, 129, 129), (1, 200, 200), (2, 130, 300),
+                                   (2, 1000, 1000)], ids=lambda s: "x".join(map(str, s)))
+def test_fwd_bf16_inputs_match_f32_inputs(D, causal, shape):
+    """bf16-mode forward on bfloat16 Q/K/V against the same call on their
+    float32 widening: the kernels round the same products (Q * sign * c2 and
+    the packed K/V) to bf16, so O and LSE must agree bit for bit; the float32
+    path is the one pinned to the oracle above. Covers the QT = bf16 kernel
+    instantiations and the bf16 pack, with ragged and multi-tile blocks."""
+    from gonn_amd import hip
+    BH, Sq, Sk = shape
+    say(f"[fwd bf16 inputs] D={D} causal={causal} shape={shape}")
+    g = torch.Generator(device="cuda").manual_seed(Sq * 31 + Sk + D + int(causal))
+    qb, kb, vb = (torch.randn((BH, S, D), generator=g, device="cuda").to(torch.bfloat16)
+                  for S in (Sq, Sk, Sk))
+    o16, l16 = hip.attn_fwd(qb, kb, vb, causal=causal, mode="bf16")
+    o32, l32 = hip.attn_fwd(qb.float(), kb.float(), vb.float(), causal=causal, mode="bf16")
+    torch.cuda.synchronize()
+    assert torch.equal(o16, o32), float((o16 - o32).abs().max())
+    assert torch.equal(l16, l32), float((l16 - l32).abs().max())
+
+
+def test_fwd_bf16_inputs_masked_and_kv_len():
+    """The same equality through the additive-mask (D = 64) and kv_len paths."""
+    from gonn_amd import hip
+    B, H, S, D = 2, 3, 150, 64
+    g = torch.Generator(device="cuda").manual_seed(77)
+    qb, kb, vb = (torch.randn((B, H, S, D), generator=g, device="cuda").to(torch.bfloat16)
+                  for _ in range(3))
+    mask = torch.randn((B, S, S), generator=g, device="cuda")
+    kv_len = torch.tensor([150, 97], dtype=torch.int32, device="cuda")
+    for kw in ({"attn_mask": mask}, {"kv_len": kv_len, "causal": True}):
+        o16, l16 = hip.attn_fwd(qb, kb, vb, mode="bf16", **kw)
+        o32, l32 = hip.attn_fwd(qb.float(), kb.float(), vb.float(), mode="bf16", **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(o16, o32), (list(kw), float((o16 - o32).abs().max()))
+        assert torch.equal(l16, l32), list(kw)
