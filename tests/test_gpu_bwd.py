@@ -149,6 +149,31 @@ def test_bwd_bf16_dq_paths_cross(shape, causal, monkeypatch):
     assert np.array_equal(got["ds"][2], got["recompute"][2])
 
 
+@pytest.mark.parametrize("path", ["ds", "recompute"])
+def test_bwd_bf16_full_rows_many_key_blocks(path, monkeypatch):
+    """B=1 H=2 S=4096 D=128 causal, bf16 MFMA: every row of dQ, dK and dV
+    against the oracle's autograd chain. 32 key blocks of 128 keys reach
+    2 to 64 query tiles each, so the compact causal dS placement
+    (ds_block_base) is checked on every block, not on sampled rows, on
+    both dQ paths."""
+    from gonn_amd import hip
+    B, H, S, D = 1, 2, 4096, 128
+    q, k, v, g = (randn((B * H, S, D), 4400 + i) for i in range(4))
+    dev = [torch.from_numpy(x).cuda() for x in (q, k, v, g)]
+    if path == "recompute":
+        monkeypatch.setenv("GONN_HIP_BWD_DQ", "recompute")
+    else:
+        monkeypatch.delenv("GONN_HIP_BWD_DQ", raising=False)
+    say(f"bwd full rows S={S} path={path}")
+    o, l = hip.attn_fwd(*dev[:3], causal=True, mode="bf16")
+    dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=True, mode="bf16")
+    torch.cuda.synchronize()
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=True)
+    assert_close(dq.cpu().numpy(), rq, "bf16", f"dQ path={path}")
+    assert_close(dk.cpu().numpy(), rk, "bf16", f"dK path={path}")
+    assert_close(dv.cpu().numpy(), rv, "bf16", f"dV path={path}")
+
+
 def test_bwd_golden_fixtures_via_f64_entry():
     """The committed torch-fp64 fixtures (square cases) through the reference-
     named f64 entry points FlashAttnF64Fwd / FlashAttnF64Bwd (head dims below

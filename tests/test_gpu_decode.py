@@ -88,8 +88,8 @@ def test_c4_decode_full_size():
     """C4: B=64 H=32 D=128, cache of 8192 positions, lens ~ U[512, 8192].
 
     The caches are drawn on the device (torch's seeded generator, bf16); the
-    oracle checks a sample of (b, h) slices, including the longest and the
-    shortest sequence."""
+    oracle checks every one of the 2048 (b, h) slices, one sequence (32
+    slices) per oracle call, on the bf16 cache contents the kernel read."""
     from gonn_amd import hip
     B, H, Lmax, D = 64, 32, 8192, 128
     lens = np.random.default_rng(4).integers(512, 8193, B).astype(np.int32)
@@ -105,13 +105,12 @@ def test_c4_decode_full_size():
     torch.cuda.synchronize()
     o = o.cpu().numpy()
     assert np.all(np.isfinite(o))
-    rng = np.random.default_rng(5)
-    pairs = {(int(np.argmax(lens)), 0), (int(np.argmin(lens)), H - 1)}
-    pairs |= {(int(b), int(h)) for b, h in zip(rng.integers(0, B, 14), rng.integers(0, H, 14))}
     qn = q.float().cpu().numpy()
-    for b, h in sorted(pairs):
+    worst = 0.0
+    for b in range(B):
         n = int(lens[b])
-        ks = kc[b, h, :n].float().cpu().numpy()[None]
-        vs = vc[b, h, :n].float().cpu().numpy()[None]
-        ro, _ = oracle.attn_fwd(qn[b, h][None, None], ks, vs, causal=False)
-        assert_close(o[b, h], ro[0, 0], "fp32", f"C4 O b={b} h={h} len={n}")
+        ks = kc[b, :, :n].float().cpu().numpy()
+        vs = vc[b, :, :n].float().cpu().numpy()
+        ro, _ = oracle.attn_fwd(qn[b][:, None, :], ks, vs, causal=False)
+        worst = max(worst, assert_close(o[b], ro[:, 0], "fp32", f"C4 O b={b} len={n}"))
+    say(f"C4: all {B * H} slices within the fp32 bar, worst max-abs {worst:.3e}")

@@ -106,3 +106,41 @@ def test_noalloc_decode_full_size_c4_slice():
     assert np.array_equal(got, ref)
     del dev
     torch.cuda.empty_cache()
+
+
+def test_noalloc_decode_allocates_nothing(monkeypatch):
+    """The entry point's contract: no allocation. (1) With GONN_HIP_FAIL_ALLOC=1
+    every allocation helper of the library fails (GONN_E_INJECTED), yet the
+    call still succeeds with the same output. (2) It records into a graph
+    under global stream capture, where a device allocation, a memset or a
+    synchronisation would fail the capture; each replay, with eager work of
+    the workspace entry between replays, reproduces the eager output bit for
+    bit."""
+    from gonn_amd import _lib, hip
+    B, H, Lmax, D = 4, 3, 900, 128
+    q, kc, vc, lens, dev = _inputs(B, H, Lmax, D, [5, 300, 900, 64], 31)
+    ref = _noalloc(dev)  # warm-up: the per-device scratch lookup happens here
+    assert_close(ref, _oracle(q, kc, vc, lens), "fp32", "noalloc decode O")
+    monkeypatch.setenv("GONN_HIP_FAIL_ALLOC", "1")
+    say("noalloc decode with allocation failures injected")
+    assert np.array_equal(_noalloc(dev), ref)
+    monkeypatch.delenv("GONN_HIP_FAIL_ALLOC")
+
+    out = torch.full((B, H, D), float("nan"), dtype=torch.float32, device="cuda")
+    a = _lib.DecodeArgs(hip.buf(dev["q"]), hip.buf(dev["kc"]), hip.buf(dev["vc"]),
+                        hip.buf(dev["kv_len"]), hip.buf(out), B, H, Lmax, D,
+                        1.0 / math.sqrt(D), 0)
+    lib = _lib.load()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    say("noalloc decode under graph capture")
+    with torch.cuda.graph(graph, stream=side, capture_error_mode="global"):
+        rc = lib.gonn_hip_attn_decode_noalloc(
+            ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, _lib.strerror(rc)
+    for i in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), ref), f"replay {i}"
+        assert np.array_equal(_with_ws(dev), ref)
