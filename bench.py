@@ -132,11 +132,54 @@ def bench_prefill(torch, hip, steps, warmup):
     kt, kn = hip.profile_read("fwd_bf16")
     pt, pn = hip.profile_read("pack_kv")
     hip.profile_reset()
+    # Shader clock over the same run of steps: a one-wave probe on a side
+    # stream starts when the spin ahead of the steps ends and reads the
+    # clock for 90% of their measured span.
+    side = torch.cuda.Stream()
+    _prime_queue(torch)
+    start = torch.cuda.Event()
+    start.record()
+    side.wait_event(start)
+    hip.calib_clock_start(0.9 * ms * steps, stream=side)
+    for _ in range(steps):
+        run()
+    torch.cuda.synchronize()
+    sclk = hip.calib_clock_read()
     # Per-launch time of each stage and the launches per step (one pack and
     # one attention kernel per gonn_hip_attn_fwd call).
     return dict(B=B, H=H, S=S, D=D, flop=flop, ms=ms, median_ms=med, wall_s=wall,
                 kernel_ms=kt / max(kn, 1), pack_ms=pt / max(pn, 1),
-                launches=max(kn, 1) / steps, q=q, k=k, v=v)
+                launches=max(kn, 1) / steps, sclk_ghz=sclk, q=q, k=k, v=v)
+
+
+def calibration(torch, hip, sclk_ghz):
+    """Figures of the box itself, measured in the same process, so a slow box
+    can be told from a slow kernel: the rate of a fixed MFMA loop on constant
+    operands, the bandwidth of a 1 GiB device copy (bytes read + written per
+    second), and the shader clock during the C3 steps (nominal 2.4 GHz)."""
+    mfma = hip.calib_mfma()
+    n = 1 << 28
+    x = torch.ones(n, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(2):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        y.copy_(x)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 5 * 2 * 4 * n / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del x, y
+    return {"mfma_const_TFLOPs": round(mfma, 1),
+            "mfma_const_frac": round(mfma / PEAK_BF16_TFLOPS, 4),
+            "copy_1GiB_GBps": round(copy_gbs, 1),
+            "copy_frac": round(copy_gbs / PEAK_HBM_GBS, 4),
+            "sclk_GHz_during_c3": round(sclk_ghz, 3),
+            "note": "mfma_const: v_mfma_f32_32x32x16_bf16 loop on constant operands, two "
+                    "waves per SIMD; copy: torch copy_ of 2^28 floats, read + write bytes; "
+                    "sclk: s_memtime against the 100 MHz s_memrealtime over the C3 steps"}
 
 
 def bench_decode(torch, hip, steps, warmup):
@@ -429,7 +472,8 @@ def cpu_baseline(pre, seconds):
     n, dt = timed(lambda q, k, v: oracle.attn_fwd_goflow(q, k, v, causal=True), 2)
     n2, dt2 = timed(lambda q, k, v: oracle.attn_fwd(q, k, v, causal=True), BH)
     return {"value": flop1 * n / dt / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": f"{n} of {BH} (b,h) slices of C3 (S={S}, D={D}, causal), fp64, GoNN's "
+            "sample": f"{n} of {BH} (b,h) slices of C3 (S={S}, D={D}, causal), extrapolated to "
+                      f"the whole workload (every slice does equal work), fp64, GoNN's "
                       f"op sequence and pass structure (MatMul, MulScalar, Add mask, Softmax as "
                       f"MaxAxis/Sub/Exp/SumAxis/Div, MatMul; broadcasts materialised), the two "
                       f"GEMMs threaded over {threads} threads, the elementwise passes and "
@@ -437,7 +481,8 @@ def cpu_baseline(pre, seconds):
                       f"same FLOP convention as value",
             "seconds": dt,
             "threaded": {"value": flop1 * n2 / dt2 / 1e12, "cores": threads,
-                         "sample": f"{n2} slices, fused per-row oracle with scores, softmax and "
+                         "sample": f"{n2} slices (extrapolated), fused per-row oracle with "
+                                   f"scores, softmax and "
                                    f"P.V rows all threaded ({dt2:.1f} s); faster than GoNN's "
                                    f"CPU path"}}
 
@@ -532,6 +577,8 @@ def main():
                      "launches_per_step": pre["launches"],
                      "pack_kv_ms": round(pre["pack_ms"], 5)},
     }
+    log("[bench] calibration")
+    line["calibration"] = calibration(torch, hip, pre["sclk_ghz"])
     if not args.no_decode:
         log("[bench] decode C4")
         dec = bench_decode(torch, hip, args.steps, args.warmup)

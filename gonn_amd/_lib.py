@@ -52,6 +52,7 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_attn_decode_noalloc",
     "gonn_hip_kvcache_attend_causal_workspace_bytes", "gonn_hip_kvcache_attend_causal",
     "gonn_hip_mha_incremental_workspace_bytes", "gonn_hip_mha_forward_incremental_dev",
+    "gonn_hip_calib_mfma", "gonn_hip_calib_clock_start", "gonn_hip_calib_clock_read",
 )
 
 # Size of the library-owned scratch array of gonn_hip_attn_decode_noalloc
@@ -141,6 +142,9 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_selftest_mfma.restype = i
     lib.gonn_hip_profile_enable.argtypes = [i]
     lib.gonn_hip_profile_read.argtypes = [ctypes.c_char_p, dp, ctypes.POINTER(i)]
+    lib.gonn_hip_calib_mfma.argtypes = [dp]
+    lib.gonn_hip_calib_clock_start.argtypes = [ctypes.c_double, vp]
+    lib.gonn_hip_calib_clock_read.argtypes = [dp]
     ip = ctypes.POINTER(i)
     lib.gonn_hip_kvcache_create.argtypes = [ctypes.POINTER(vp), i, i, i, i]
     lib.gonn_hip_kvcache_free.argtypes = [vp]

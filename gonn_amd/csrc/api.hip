@@ -306,17 +306,28 @@ size_t bwd_ws(const gonn_attn_bwd_args* a) {
 // The host (fp64) entry points run on a stream of the calling thread, not on
 // the legacy null stream, and wait for that stream only: GoNN runs Backward
 // calls concurrently (tensor/autograd.go:10-32), and such callers must not
-// serialise on each other's device work. One non-blocking stream (default
-// priority) per thread and device, created on first use and kept for the
-// thread's life.
+// serialise on each other's device work. Each device has a fixed pool of
+// kHostStreams non-blocking streams (default priority), created on first use
+// and kept for the process; a thread draws one slot of the pool the first
+// time it calls in and keeps it. cgo spreads calls over many OS threads, so
+// the pool bounds the streams: threads beyond kHostStreams share slots,
+// which only orders their device work (each call still waits for its own
+// stream before returning).
 constexpr int kMaxDevices = 64;
+constexpr int kHostStreams = 16;
 int host_stream(hipStream_t* out) {
-    thread_local hipStream_t streams[kMaxDevices] = {};
+    static std::mutex mu;
+    static hipStream_t pool[kMaxDevices][kHostStreams] = {};
+    static std::atomic<unsigned> next_slot{0};
+    thread_local int slot = -1;
+    if (slot < 0) slot = (int)(next_slot.fetch_add(1, std::memory_order_relaxed) % kHostStreams);
     int dev = 0;
     TRYH_EARLY(hipGetDevice(&dev));
     if (dev < 0 || dev >= kMaxDevices) return GONN_E_UNSUPPORTED;
-    if (!streams[dev]) TRYH_EARLY(hipStreamCreateWithFlags(&streams[dev], hipStreamNonBlocking));
-    *out = streams[dev];
+    std::lock_guard<std::mutex> lock(mu);
+    hipStream_t& st = pool[dev][slot];
+    if (!st) TRYH_EARLY(hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+    *out = st;
     return GONN_OK;
 }
 
@@ -512,6 +523,10 @@ struct gonn_kvcache {
     size_t ws_bytes = 0;
     std::vector<int> h_len;  // host copy of the lengths (authoritative)
     std::vector<int> h_pc;
+    // Set when a failed call left the device lengths advanced past h_len and
+    // putting them back failed too: every call that reads them then returns
+    // GONN_E_INVALID until gonn_hip_kvcache_reset succeeds.
+    bool stale = false;
 };
 
 namespace {
@@ -541,7 +556,7 @@ gonn_attn_decode_args kv_decode_args(const gonn_kvcache* c) {
 // Checks an append of T rows per sequence (counts: host int[B] or null = T);
 // fills c->h_pc with (positions, counts).
 int kv_check_append(gonn_kvcache* c, int T, const int* counts) {
-    if (T <= 0) return GONN_E_INVALID;
+    if (T <= 0 || c->stale) return GONN_E_INVALID;
     c->h_pc.assign(2 * (size_t)c->B, 0);
     for (int b = 0; b < c->B; b++) {
         const int n = counts ? counts[b] : T;
@@ -568,7 +583,13 @@ int kv_append_dev(gonn_kvcache* c, const void* k, const void* v, int src_bf16, i
     for (int b = 0; b < c->B; b++) len[b] += c->h_pc[c->B + b];
     TRYH(hipMemcpyAsync(c->d_len, len.data(), (size_t)c->B * sizeof(int), hipMemcpyHostToDevice,
                         s));
-    TRYH(hipStreamSynchronize(s));
+    const hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        // The upload of the new lengths may have run: put the committed ones
+        // back (a failure there marks the handle stale).
+        (void)gonn::kvcache_restore(c);
+        return herr(e);
+    }
     c->h_len.swap(len);
     return GONN_OK;
 }
@@ -608,9 +629,14 @@ int kvcache_append_pending(gonn_kvcache* c, const float* k, const float* v, int 
 
 void kvcache_commit(gonn_kvcache* c, std::vector<int>* new_len) { c->h_len.swap(*new_len); }
 
-void kvcache_restore(gonn_kvcache* c) {
-    (void)hipMemcpy(c->d_len, c->h_len.data(), (size_t)c->B * sizeof(int), hipMemcpyHostToDevice);
+int kvcache_restore(gonn_kvcache* c) {
+    const hipError_t e =
+        hipMemcpy(c->d_len, c->h_len.data(), (size_t)c->B * sizeof(int), hipMemcpyHostToDevice);
+    c->stale = e != hipSuccess;
+    return herr(e);
 }
+
+bool kvcache_usable(const gonn_kvcache* c) { return c && !c->stale; }
 
 size_t kvcache_attend_causal_ws(const gonn_kvcache* c, int T) {
     if (!c || T <= 0) return 0;
@@ -1454,6 +1480,7 @@ int gonn_hip_kvcache_reset(gonn_kvcache* c) {
     if (!c) return GONN_E_INVALID;
     std::fill(c->h_len.begin(), c->h_len.end(), 0);
     TRYH(hipMemcpy(c->d_len, c->h_len.data(), (size_t)c->B * 4, hipMemcpyHostToDevice));
+    c->stale = false;  // host and device lengths agree again
     return GONN_OK;
 }
 
@@ -1493,7 +1520,7 @@ int gonn_hip_kvcache_append_f64(gonn_kvcache* c, const double* k, const double* 
 
 int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, double scale,
                             void* stream) {
-    if (!c || !q || !o) return GONN_E_INVALID;
+    if (!c || !q || !o || c->stale) return GONN_E_INVALID;
     gonn_attn_decode_args a = kv_decode_args(c);
     a.q = *q;
     a.o = *o;
@@ -1502,7 +1529,7 @@ int gonn_hip_kvcache_attend(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, dou
 }
 
 int gonn_hip_kvcache_attend_f64(gonn_kvcache* c, const double* q, double* o, double scale) {
-    if (!c || !q || !o) return GONN_E_INVALID;
+    if (!c || !q || !o || c->stale) return GONN_E_INVALID;
     const size_t rows = (size_t)c->B * c->H;
     hipStream_t hs = nullptr;
     TRY(host_stream(&hs));
@@ -1524,7 +1551,7 @@ size_t gonn_hip_kvcache_attend_causal_workspace_bytes(const gonn_kvcache* c, int
 
 int gonn_hip_kvcache_attend_causal(gonn_kvcache* c, const gonn_buf* q, gonn_buf* o, int T,
                                    double scale, void* ws, size_t ws_bytes, void* stream) {
-    if (!c || !q || !o || T <= 0 || !std::isfinite(scale)) return GONN_E_INVALID;
+    if (!c || !q || !o || T <= 0 || !std::isfinite(scale) || c->stale) return GONN_E_INVALID;
     const size_t n = (size_t)c->B * c->H * T * c->D;
     if (!buf_ok(*q, n, GONN_F32) || !buf_ok(*o, n, GONN_F32)) return GONN_E_INVALID;
     // The T queries' own positions are the last T cached ones.

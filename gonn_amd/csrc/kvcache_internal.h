@@ -20,8 +20,13 @@ void kvcache_dims(const gonn_kvcache* c, int* B, int* H, int* Lmax, int* D);
 int kvcache_append_pending(gonn_kvcache* c, const float* k, const float* v, int T, hipStream_t s,
                            std::vector<int>* new_len);
 void kvcache_commit(gonn_kvcache* c, std::vector<int>* new_len);
-// Puts the committed lengths back on the device (after a failed call).
-void kvcache_restore(gonn_kvcache* c);
+// Puts the committed lengths back on the device (after a failed call). If
+// that copy fails too, the handle is marked stale: every later call that
+// reads the device lengths returns GONN_E_INVALID until a successful
+// gonn_hip_kvcache_reset. Returns the copy's status.
+int kvcache_restore(gonn_kvcache* c);
+// False for a stale handle (see kvcache_restore).
+bool kvcache_usable(const gonn_kvcache* c);
 // Workspace of the causal multi-token attend of T queries per (b,h).
 size_t kvcache_attend_causal_ws(const gonn_kvcache* c, int T);
 // Enqueues the causal multi-token attend: q, o f32 device (B,H,T,D); query t

@@ -302,6 +302,7 @@ bool inc_ok(const gonn_mha* m, const gonn_kvcache* c, int T, int* B) {
 // Incremental self-attention on device data: x, out fp64 (B, T, E).
 int run_incremental(gonn_mha* m, gonn_kvcache* c, const double* x, double* out, int B, int T,
                     uint8_t* w, const IncLayout& L, hipStream_t s) {
+    if (!gonn::kvcache_usable(c)) return GONN_E_INVALID;
     const int E = m->E, H = m->H, D = m->D, dp = m->dp;
     const size_t n = (size_t)B * T;
     double* Y = (double*)(w + L.y);
@@ -343,8 +344,13 @@ int run_incremental(gonn_mha* m, gonn_kvcache* c, const double* x, double* out, 
     if (rc == GONN_OK) {
         gonn::kvcache_commit(c, &new_len);
     } else {
+        // The enqueued upload may have advanced the device lengths: put the
+        // committed ones back. The call's own error is returned; if the
+        // restore fails as well, the handle is marked stale, so later calls
+        // fail instead of attending positions that were never committed.
         (void)hipStreamSynchronize(s);
-        gonn::kvcache_restore(c);
+        const int rr = gonn::kvcache_restore(c);
+        (void)rr;
     }
     return rc;
 }

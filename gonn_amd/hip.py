@@ -90,6 +90,25 @@ def profile_read(kernel: str):
     return tot.value, n.value
 
 
+def calib_mfma() -> float:
+    """TFLOP/s of a fixed bf16 MFMA loop on constant operands (whole device)."""
+    t = ctypes.c_double(0.0)
+    check(_lib.load().gonn_hip_calib_mfma(ctypes.byref(t)), "calib_mfma")
+    return t.value
+
+
+def calib_clock_start(ms: float, stream=None) -> None:
+    """Enqueue the shader-clock probe (about `ms` milliseconds) on `stream`."""
+    check(_lib.load().gonn_hip_calib_clock_start(float(ms), _stream(stream)), "calib_clock")
+
+
+def calib_clock_read() -> float:
+    """Shader clock (GHz) the last probe saw; after its stream has finished."""
+    g = ctypes.c_double(0.0)
+    check(_lib.load().gonn_hip_calib_clock_read(ctypes.byref(g)), "calib_clock_read")
+    return g.value
+
+
 # ---------------------------------------------------------------------------
 # reference-named f64 entry points
 # ---------------------------------------------------------------------------

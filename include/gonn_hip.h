@@ -235,7 +235,11 @@ int gonn_hip_attn_decode_noalloc(const gonn_attn_decode_args* a, void* stream);
  * mask (nn/attention.go:305-341, :261-272) on the post-projection core; a
  * sequence with no cached position gets o = 0. Calls on one handle are not
  * reentrant; different handles are independent. For callers that cannot
- * hold device pointers (cgo), the _f64 variants take host arrays.        */
+ * hold device pointers (cgo), the _f64 variants take host arrays.
+ * A failed call leaves the lengths as they were. If putting the device copy
+ * of the lengths back fails as well, the handle is stale: every append and
+ * attend on it (and the incremental MHA forward) returns GONN_E_INVALID
+ * until gonn_hip_kvcache_reset succeeds.                                 */
 typedef struct gonn_kvcache gonn_kvcache;
 
 /* D must be 64 or 128 (GONN_E_UNSUPPORTED otherwise); GONN_E_NODEVICE
@@ -243,7 +247,7 @@ typedef struct gonn_kvcache gonn_kvcache;
 int gonn_hip_kvcache_create(gonn_kvcache** out, int B, int H, int Lmax, int D);
 /* Frees the handle and its device memory (NULL is allowed).              */
 int gonn_hip_kvcache_free(gonn_kvcache* c);
-/* Drops every cached position (lengths back to 0).                       */
+/* Drops every cached position (lengths back to 0); clears a stale handle. */
 int gonn_hip_kvcache_reset(gonn_kvcache* c);
 /* Copies the B current lengths into len[B].                              */
 int gonn_hip_kvcache_lengths(const gonn_kvcache* c, int* len);
@@ -440,6 +444,20 @@ double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal
 int gonn_hip_profile_enable(int on);
 int gonn_hip_profile_reset(void);
 int gonn_hip_profile_read(const char* kernel, double* total_ms, int* count);
+
+/* Box calibration for benchmarks (no reference counterpart: GoNN's
+ * benchmark reports raw times, backend/cuda/gonn_cuda.cu:532-560).
+ * calib_mfma: TFLOP/s of a fixed loop of v_mfma_f32_32x32x16_bf16 on
+ * constant operands over the whole device (two waves per SIMD, eight
+ * independent chains each, no memory traffic); synchronous.
+ * calib_clock_start: enqueues on `stream` a one-wave probe that reads the
+ * shader clock against the fixed 100 MHz counter for `ms` milliseconds
+ * (0 < ms <= 60000), for running beside other work on another stream.
+ * calib_clock_read: the probe's shader clock in GHz; call it after that
+ * stream has been synchronised.                                          */
+int gonn_hip_calib_mfma(double* tflops);
+int gonn_hip_calib_clock_start(double ms, void* stream);
+int gonn_hip_calib_clock_read(double* ghz);
 
 /* Runs one v_mfma_f32_32x32x16_bf16 and one v_mfma_f32_32x32x2_f32 on known
  * inputs and compares every output element with a host matrix product; the
