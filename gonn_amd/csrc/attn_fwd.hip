@@ -27,6 +27,7 @@
 //        is one 16-byte read. Skp = Sk rounded up to 64; the pad is zero and
 //        masked.
 //  fp32: v_mfma_f32_32x32x2_f32 straight from the fp32 K/V (no pack).
+#include <atomic>
 #include <type_traits>
 
 #include "common.h"
@@ -1087,6 +1088,21 @@ static void launch_bf16_pipe(const FwdParams& p, int q_bf16, dim3 grid, hipStrea
     }
 }
 
+// Compute units of the current device, looked up once per device (the
+// lookup is idempotent, so concurrent first calls may both run it).
+static int device_cus() {
+    constexpr int kMaxDev = 64;
+    static std::atomic<int> cache[kMaxDev];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 256;
+    int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+        c = 256;
+    cache[dev].store(c, std::memory_order_relaxed);
+    return c;
+}
+
 hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_bf16,
                       hipStream_t s) {
     FwdParams p = p_in;
@@ -1098,16 +1114,9 @@ hipError_t launch_fwd(const FwdParams& p_in, int mode, int D, int causal, int q_
     // (2 x CUs / 8 XCDs x 2 resident workgroups) of q-blocks per group.
     p.hgroup = 1;
     if (causal && mode == 1 && D == 128) {
-        static int cus = 0;
-        if (!cus) {
-            int dev = 0;
-            if (hipGetDevice(&dev) != hipSuccess ||
-                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-                cus = 256;
-        }
         // Two XCDs' worth measured 1% faster on C3 than one (interleaved
         // runs), and the same on C5.
-        const int slots = cus / 8 * (8 / kFwdWaves);
+        const int slots = device_cus() / 8 * (8 / kFwdWaves);
         p.hgroup = 2 * slots / p.nqb > 1 ? 2 * slots / p.nqb : 1;
     }
     if (mode == 1) {
