@@ -433,6 +433,42 @@ def bench_mha(torch, hip, steps, warmup):
             "resident_device_buffers": {"ms": r(dev_ms), "median_ms": r(dev_med)}}
 
 
+# GoNN's published fused-forward numbers (fp64, head_dim 64, RTX 3060,
+# benchmark/results/gonn_flash.json:7-82): GFLOP/s by (BH, S, causal).
+REF_F64_GFLOPS = {(64, 512, False): 85.06, (32, 1024, False): 86.13, (16, 2048, False): 85.64,
+                  (64, 512, True): 77.78, (32, 1024, True): 80.31, (16, 2048, True): 80.10}
+PEAK_FP64_TFLOPS = 78.6  # MI355X dense fp64 (vector and matrix)
+
+
+def bench_f64_reference(hip, iters=30):
+    """The reference-named BenchFlashAttnF64 entry (gonn_cuda.cu:532-560's
+    protocol: zero-filled device inputs, 5 warm-ups, one event pair around
+    `iters` launches, mean ms) at the shapes GoNN publishes, d = 64, in the
+    f64 entries' exact fp64 mode and in their default fp32-MFMA mode; FLOP
+    by the reference's convention (4 BH S^2 d, halved when causal)."""
+    prev = hip.AttnMode()
+    rows = []
+    try:
+        for mode, peak in (("f64", PEAK_FP64_TFLOPS), ("fp32", PEAK_FP32_TFLOPS)):
+            hip.SetAttnMode(mode)
+            for (BH, S, causal), ref in REF_F64_GFLOPS.items():
+                ms = hip.BenchFlashAttnF64(BH, S, 64, iters, causal)
+                flop = 4.0 * BH * S * S * 64 * (0.5 if causal else 1.0)
+                gf = flop / (ms * 1e-3) / 1e9
+                rows.append({"mode": mode, "BH": BH, "S": S, "d": 64, "causal": causal,
+                             "ms": round(ms, 5), "GFLOPs": round(gf, 1),
+                             "frac": round(gf / 1e3 / peak, 4),
+                             "reference_GFLOPs": ref, "vs_reference": round(gf / ref, 1)})
+    finally:
+        hip.SetAttnMode(prev)
+    return {"metric": "fused forward GFLOP/s at GoNN's published shapes",
+            "unit": "GFLOP/s",
+            "note": "reference: GoNN's fp64 CUDA kernel on an RTX 3060 "
+                    "(benchmark/results/gonn_flash.json); frac against the MI355X peak of the "
+                    "mode (fp64 78.6 TFLOP/s, fp32 MFMA 157.3 TFLOP/s)",
+            "rows": rows}
+
+
 def cpu_baseline(pre, seconds):
     """Time GoNN's CPU attention core on a bounded sample of the prefill
     workload (whole (b,h) slices), two ways:
@@ -501,6 +537,8 @@ def main():
     ap.add_argument("--no-incremental", action="store_true",
                     help="skip the resident incremental-decoding leg")
     ap.add_argument("--no-wide", action="store_true", help="skip the masked / cross legs")
+    ap.add_argument("--no-f64", action="store_true",
+                    help="skip the f64 entries at the reference's published shapes")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the headline leg (profiling runs of the other legs only)")
     ap.add_argument("--copy-calib", action="store_true",
@@ -644,6 +682,9 @@ def main():
             log(f"[bench] wide gate {kind}")
             line["wide_gate"][kind] = bench_wide_gate(torch, hip, max(args.steps // 5, 3),
                                                       max(args.warmup // 2, 1), kind)
+    if not args.no_f64:
+        log("[bench] f64 entries at the reference's shapes")
+        line["f64_reference_shapes"] = bench_f64_reference(hip)
     if not args.no_mha:
         log("[bench] MHA C1")
         line["mha"] = bench_mha(torch, hip, args.steps, args.warmup)

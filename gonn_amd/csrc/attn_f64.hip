@@ -32,6 +32,7 @@
 // The two backward kernels each own their outputs: no atomics,
 // deterministic.
 #include <cmath>
+#include <cstdlib>
 
 #include "common.h"
 #include "kernels.h"
@@ -139,6 +140,186 @@ __global__ __launch_bounds__(256) void fwd_f64_kernel(F64Params p) {
             if (c < d) orow[c] = od[t] * inv;
         }
         if (p.out_lse && u == 0) p.out_lse[(size_t)bh * Sq + i] = l > 0.0 ? m + log(l) : -INFINITY;
+    }
+}
+
+// Forward on v_mfma_f64_16x16x4f64 (fp64 in, fp64 accumulate). Layout of
+// that instruction (probed on gfx950, as in gemm.hip): the A operand (16 x 4)
+// is element (l % 16, l / 16) of lane l, B (4 x 16) element (l / 16, l % 16),
+// and register r of the 16 x 16 result holds row 4 r + l / 16, column l % 16.
+//
+// A wave owns 16 queries (workgroup: 4 waves, 64 queries). Per 16-key tile
+// it forms S^T = K Q^T (rows: keys, columns: queries; Q^T is the B operand,
+// kept in registers), so register r of a lane holds the score of key
+// 4 r + l / 16 for query l % 16. That is exactly the B operand of the PV
+// product's k-step r: O^T (d x queries) += V^T (d x keys) P^T, with k-slot
+// l / 16 of step r standing for key 4 r + l / 16. P goes from the score
+// registers into the PV MFMAs without moving, and the exponential of every
+// score is taken once (the VALU kernel above takes it on all 8 lanes of a
+// team). A query's scores sit in the 4 lanes l % 16 = c; its row max and
+// sum are in-lane plus two cross-lane steps.
+//
+// K and V stages (32 keys, 16 at d = 128) are staged through registers into
+// LDS in the order the A operands are read, so every MFMA operand read is 64
+// doubles in lane order:
+//   sK[t][s][j][q] = K[16 t + j][4 s + q]               (S^T k-step s)
+//   sV[t][r][dt][q][j] = V[16 t + 4 r + q][16 dt + j]   (PV k-step r, d tile dt)
+// Causal grids put the longest q-blocks first.
+typedef double f64x4_t __attribute__((ext_vector_type(4)));
+typedef double f64x2_t __attribute__((ext_vector_type(2)));
+constexpr int kMWaveQ = 16;                   // queries per wave
+constexpr int kMRows = 4 * kMWaveQ;           // queries per workgroup
+// Keys per LDS stage: 32 at d <= 64; 16 at d = 128, where the register
+// staging of a 32-key stage would not fit beside the Q fragment and O.
+constexpr int mstage(int DP) { return DP <= 64 ? 32 : 16; }
+
+__device__ __forceinline__ f64x4_t mfma_f64(double a, double b, f64x4_t c) {
+    return __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, c, 0, 0, 0);
+}
+
+// Value of lane l combined with lanes l ^ 16 and l ^ 32 (the 4 lanes that
+// hold one query's keys).
+__device__ __forceinline__ double quad_max(double x) {
+    x = fmax(x, __shfl_xor(x, 16));
+    return fmax(x, __shfl_xor(x, 32));
+}
+__device__ __forceinline__ double quad_sum(double x) {
+    x += __shfl_xor(x, 16);
+    return x + __shfl_xor(x, 32);
+}
+
+template <int DP>
+__global__ __launch_bounds__(256, 2) void fwd_f64_mfma_kernel(F64Params p) {
+    constexpr int NS = DP / 4;    // S^T k-steps (d)
+    constexpr int NDT = DP / 16;  // 16-row d tiles of O^T
+    constexpr int kMStage = mstage(DP), kMTiles = kMStage / 16;
+    constexpr int NCH = kMStage * DP / 2 / 256;  // 16-byte chunks per thread per stage (K, V each)
+    static_assert(NCH * 256 * 2 == kMStage * DP, "whole chunks per stage");
+    __shared__ double sK[kMTiles * NS * 64];
+    __shared__ double sV[kMTiles * 4 * NDT * 64];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, quad = lane >> 4;
+    const int Sq = p.Sq, Sk = p.Sk, d = p.d;
+    const int nqb = (Sq + kMRows - 1) / kMRows, BH = p.B * p.H;
+    const int rank = blockIdx.x / BH;
+    const int bh = blockIdx.x - rank * BH;
+    const int qb = p.causal ? nqb - 1 - rank : rank;
+    const int q0 = qb * kMRows, qw = q0 + wave * kMWaveQ, qi = qw + col;
+    const int kend_b = keys_of(p, bh);
+    int kend = kend_b;
+    if (p.causal && q0 + kMRows < kend) kend = q0 + kMRows;
+
+    // Q^T fragment: qf[s] = Q[qi][4 s + quad].
+    double qf[NS];
+    {
+        const double* qrow = p.q + ((size_t)bh * Sq + (qi < Sq ? qi : 0)) * d;
+        for (int s = 0; s < NS; s++) {
+            const int c = 4 * s + quad;
+            qf[s] = (qi < Sq && c < d) ? qrow[c] : 0.0;
+        }
+    }
+    f64x4_t oacc[NDT];
+    for (int t = 0; t < NDT; t++) oacc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+    double m = -INFINITY, l = 0.0;
+
+    const double* kg = p.k + (size_t)bh * Sk * d;
+    const double* vg = p.v + (size_t)bh * Sk * d;
+    // Chunk i of thread tid: key (i*256 + tid) / (DP/2), columns 2 ((i*256 +
+    // tid) % (DP/2)) and the next (coalesced rows).
+    f64x2_t kst[NCH], vst[NCH];
+    auto load_stage = [&](int j0) {
+        for (int i = 0; i < NCH; i++) {
+            const int c = i * 256 + tid, key = j0 + c / (DP / 2), dd = 2 * (c % (DP / 2));
+            const bool in = key < Sk && dd < d;  // d even or dd + 1 < d handled below
+            f64x2_t kv{0.0, 0.0}, vv{0.0, 0.0};
+            if (in) {
+                const size_t off = (size_t)key * d + dd;
+                kv[0] = kg[off];
+                vv[0] = vg[off];
+                if (dd + 1 < d) {
+                    kv[1] = kg[off + 1];
+                    vv[1] = vg[off + 1];
+                }
+            }
+            kst[i] = kv;
+            vst[i] = vv;
+        }
+    };
+    auto store_stage = [&]() {
+        for (int i = 0; i < NCH; i++) {
+            const int c = i * 256 + tid, kr = c / (DP / 2), dd = 2 * (c % (DP / 2));
+            const int t = kr >> 4, j = kr & 15;
+            // K: (t, s = dd / 4, j, q = dd % 4 and + 1)
+            *(f64x2_t*)&sK[((t * NS + (dd >> 2)) * 16 + j) * 4 + (dd & 3)] = kst[i];
+            // V: (t, r = j / 4, dt = dd / 16, q = j % 4, jj = dd % 16 and + 1)
+            *(f64x2_t*)&sV[(((t * 4 + (j >> 2)) * NDT + (dd >> 4)) * 4 + (j & 3)) * 16 + (dd & 15)] =
+                vst[i];
+        }
+    };
+
+    if (kend > 0) load_stage(0);
+    for (int j0 = 0; j0 < kend; j0 += kMStage) {
+        __syncthreads();  // the previous stage is consumed
+        store_stage();
+        __syncthreads();
+        if (j0 + kMStage < kend) load_stage(j0 + kMStage);  // lands during this stage
+        // Tiles of this stage this wave sees at all (causal: keys <= its last query).
+        f64x4_t sacc[kMTiles];
+        double smax = -INFINITY;
+        for (int t = 0; t < kMTiles; t++) {
+            const int kt0 = j0 + 16 * t;
+            sacc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+            if (kt0 >= kend || (p.causal && kt0 > qw + kMWaveQ - 1)) {
+                sacc[t] = f64x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+                continue;
+            }
+            for (int s = 0; s < NS; s++)
+                sacc[t] = mfma_f64(sK[((t * NS + s) * 16 + col) * 4 + quad], qf[s], sacc[t]);
+            for (int r = 0; r < 4; r++) {
+                const int key = kt0 + 4 * r + quad;
+                const bool off = key >= kend_b || qi >= Sq || (p.causal && key > qi);
+                const double sc = off ? -INFINITY
+                                      : p.scale * sacc[t][r] +
+                                            mask_at(p, bh, qi < Sq ? qi : 0, key < Sk ? key : 0);
+                sacc[t][r] = sc;
+                smax = fmax(smax, sc);
+            }
+        }
+        smax = quad_max(smax);
+        // No branch on a query column's state around the MFMAs (they read
+        // operands from every lane): a column that has seen no key yet keeps
+        // m = -inf, gets offset 0 (so P = exp(-inf) = 0) and alpha = 0.
+        const double mnew = fmax(m, smax);
+        const double mref = mnew == -INFINITY ? 0.0 : mnew;
+        const double alpha = m == -INFINITY ? 0.0 : exp(m - mref);
+        l *= alpha;
+        for (int t = 0; t < NDT; t++) oacc[t] *= alpha;
+        m = mnew;
+        for (int t = 0; t < kMTiles; t++) {
+            const int kt0 = j0 + 16 * t;
+            if (kt0 >= kend || (p.causal && kt0 > qw + kMWaveQ - 1)) continue;  // wave-uniform
+            for (int r = 0; r < 4; r++) {
+                const double pr = exp(sacc[t][r] - mref);  // once per score
+                l += pr;
+                for (int dt = 0; dt < NDT; dt++)
+                    oacc[dt] = mfma_f64(sV[(((t * 4 + r) * NDT + dt) * 4 + quad) * 16 + col], pr,
+                                        oacc[dt]);
+            }
+        }
+    }
+    const double lt = quad_sum(l);
+    if (qi < Sq) {
+        double* orow = p.out_o + ((size_t)bh * Sq + qi) * d;
+        const double inv = lt > 0.0 ? 1.0 / lt : 0.0;
+        for (int dt = 0; dt < NDT; dt++)
+            for (int r = 0; r < 4; r++) {
+                const int c = 16 * dt + 4 * r + quad;
+                if (c < d) orow[c] = oacc[dt][r] * inv;
+            }
+        if (p.out_lse && quad == 0)
+            p.out_lse[(size_t)bh * Sq + qi] = lt > 0.0 ? m + log(lt) : -INFINITY;
     }
 }
 
@@ -296,6 +477,16 @@ bool f64_args_ok(const F64Params& p) {
 
 hipError_t launch_f64_fwd(const F64Params& p, hipStream_t s) {
     if (!f64_args_ok(p) || !p.out_o) return hipErrorInvalidValue;
+    const char* e = std::getenv("GONN_HIP_F64_FWD");
+    if (!(e && e[0] == 'v')) {  // "valu": the team kernel (kept for comparison)
+        const dim3 grid(((p.Sq + kMRows - 1) / kMRows) * p.B * p.H);
+        switch (dp_of(p.d)) {
+        case 32:
+        case 64: fwd_f64_mfma_kernel<64><<<grid, 256, 0, s>>>(p); break;
+        default: fwd_f64_mfma_kernel<128><<<grid, 256, 0, s>>>(p); break;
+        }
+        return hipGetLastError();
+    }
     const dim3 grid((p.Sq + kRowsWG - 1) / kRowsWG, p.B * p.H);
     switch (dp_of(p.d)) {
     case 32: fwd_f64_kernel<32><<<grid, 256, 0, s>>>(p); break;
