@@ -322,12 +322,24 @@ def bench_fwd_bwd(torch, hip, steps, warmup):
     def run():
         hip.attn_fwd(q, k, v, causal=True, mode="bf16", out=o, lse_out=lse)
         hip.attn_bwd(q, k, v, o, lse, do, causal=True, mode="bf16", out=grads)
-    (ms, med), per, nl = _timed(torch, hip, run, steps, warmup,
-                         ("pack_kv", "fwd_bf16", "bwd_prep", "bwd_pack", "bwd_dkdv", "bwd_dq"))
+    stages = ("pack_kv", "fwd_bf16", "bwd_prep", "bwd_pack", "bwd_dkdv", "bwd_dq")
+    (ms, med), per, nl = _timed(torch, hip, run, steps, warmup, stages)
     # stage times per step (a stage may be several launches)
     per = {k: v * nl[k] for k, v in per.items()}
+    # The other dQ path (S and dP formed again instead of the stored dS),
+    # timed in the same run so the measuring box shows which default wins.
+    prev = os.environ.get("GONN_HIP_BWD_DQ")
+    os.environ["GONN_HIP_BWD_DQ"] = "recompute"
+    try:
+        (ms_rc, _), per_rc, nl_rc = _timed(torch, hip, run, steps, max(warmup // 2, 1), stages)
+    finally:
+        if prev is None:
+            del os.environ["GONN_HIP_BWD_DQ"]
+        else:
+            os.environ["GONN_HIP_BWD_DQ"] = prev
+    per_rc = {k: v * nl_rc[k] for k, v in per_rc.items()}
     return dict(B=B, H=H, S=S, D=D, fwd_flop=fwd_flop, bwd_flop=bwd_flop, ms=ms, median_ms=med,
-                per=per)
+                per=per, ms_recompute=ms_rc, per_recompute=per_rc)
 
 
 def bench_encoder(torch, hip, steps, warmup, mode):
@@ -459,6 +471,17 @@ def bench_f64_reference(hip, iters=30):
                              "ms": round(ms, 5), "GFLOPs": round(gf, 1),
                              "frac": round(gf / 1e3 / peak, 4),
                              "reference_GFLOPs": ref, "vs_reference": round(gf / ref, 1)})
+        # The exact-mode backward at the same shapes (no reference figure:
+        # GoNN publishes no backward timing). FLOP: the five S^2 d products
+        # (S, dP, dV, dK, dQ), 10 BH S^2 d, halved when causal.
+        hip.SetAttnMode("f64")
+        bwd = []
+        for (BH, S, causal) in REF_F64_GFLOPS:
+            ms = hip.BenchFlashAttnF64Bwd(BH, S, 64, iters, causal)
+            gf = 10.0 * BH * S * S * 64 * (0.5 if causal else 1.0) / (ms * 1e-3) / 1e9
+            bwd.append({"mode": "f64", "BH": BH, "S": S, "d": 64, "causal": causal,
+                        "ms": round(ms, 5), "GFLOPs": round(gf, 1),
+                        "frac": round(gf / 1e3 / PEAK_FP64_TFLOPS, 4)})
     finally:
         hip.SetAttnMode(prev)
     return {"metric": "fused forward GFLOP/s at GoNN's published shapes",
@@ -466,7 +489,7 @@ def bench_f64_reference(hip, iters=30):
             "note": "reference: GoNN's fp64 CUDA kernel on an RTX 3060 "
                     "(benchmark/results/gonn_flash.json); frac against the MI355X peak of the "
                     "mode (fp64 78.6 TFLOP/s, fp32 MFMA 157.3 TFLOP/s)",
-            "rows": rows}
+            "rows": rows, "bwd_rows": bwd}
 
 
 def cpu_baseline(pre, seconds):
@@ -651,6 +674,14 @@ def main():
                        "fwd_flop": fb["fwd_flop"], "bwd_flop": fb["bwd_flop"]},
             "bwd_TFLOPs": round(fb["bwd_flop"] / (bwd_ms * 1e-3) / 1e12, 3),
             "stage_ms": {k: round(v, 5) for k, v in per.items()},
+            "dq_paths": {
+                "default": "stored dS (one GEMM)", "stored_ds_dq_ms": round(per["bwd_dq"], 5),
+                "stored_ds_dkdv_ms": round(per["bwd_dkdv"], 5),
+                "recompute_dq_ms": round(fb["per_recompute"]["bwd_dq"], 5),
+                "recompute_dkdv_ms": round(fb["per_recompute"]["bwd_dkdv"], 5),
+                "recompute_step_ms": round(fb["ms_recompute"], 4),
+                "note": "GONN_HIP_BWD_DQ=recompute: dK/dV stores no dS and the dQ kernel forms "
+                        "S and dP again; both paths timed in this run"},
             "roofline": {"bound": "mfma", "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                          "kernel": "bwd_dkdv + bwd_dq",
                          "traffic": (load_traffic("bwd_dkdv:C5") or 0) + (load_traffic("bwd_dq:C5") or 0)

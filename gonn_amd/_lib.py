@@ -39,8 +39,8 @@ EXPORTED_SYMBOLS = (
     "gonn_hip_free", "gonn_hip_upload_from_f64", "gonn_hip_download_to_f64",
     "gonn_hip_memcpy_h2d", "gonn_hip_memcpy_d2h", "gonn_hip_stream_sync",
     "gonn_hip_flash_attn_f64", "gonn_hip_flash_attn_f64_fwd", "gonn_hip_flash_attn_f64_bwd",
-    "gonn_hip_bench_flash_attn_f64", "gonn_hip_profile_enable", "gonn_hip_profile_reset",
-    "gonn_hip_profile_read", "gonn_hip_selftest_mfma",
+    "gonn_hip_bench_flash_attn_f64", "gonn_hip_bench_flash_attn_f64_bwd",
+    "gonn_hip_profile_enable", "gonn_hip_profile_reset", "gonn_hip_profile_read", "gonn_hip_selftest_mfma",
     "gonn_hip_kvcache_create", "gonn_hip_kvcache_free", "gonn_hip_kvcache_reset",
     "gonn_hip_kvcache_lengths", "gonn_hip_kvcache_append", "gonn_hip_kvcache_append_f64",
     "gonn_hip_kvcache_attend", "gonn_hip_kvcache_attend_f64", "gonn_hip_flash_attn_f64_ex",
@@ -139,6 +139,8 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_flash_attn_f64_bwd.argtypes = [dp] * 9 + [i, i, i, ctypes.c_double, i]
     lib.gonn_hip_bench_flash_attn_f64.restype = ctypes.c_double
     lib.gonn_hip_bench_flash_attn_f64.argtypes = [i, i, i, i, i]
+    lib.gonn_hip_bench_flash_attn_f64_bwd.restype = ctypes.c_double
+    lib.gonn_hip_bench_flash_attn_f64_bwd.argtypes = [i, i, i, i, i]
     lib.gonn_hip_selftest_mfma.restype = i
     lib.gonn_hip_profile_enable.argtypes = [i]
     lib.gonn_hip_profile_read.argtypes = [ctypes.c_char_p, dp, ctypes.POINTER(i)]

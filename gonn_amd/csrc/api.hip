@@ -249,8 +249,11 @@ struct BwdLayout {
 // computes dQ from it in one GEMM when that buffer is at most kDsMaxBytes
 // and one slice of it fits the kernels' 32-bit buffer offsets; otherwise (and
 // with GONN_HIP_BWD_DQ=recompute) the dQ kernel forms S and dP again. The
-// choice depends on the shape only (and the environment), so a workspace
-// sized by gonn_hip_attn_workspace_bytes fits the call that follows.
+// choice depends on the shape and the environment. A call reads the
+// variable once and sizes, checks and lays out its workspace for that one
+// choice, so a workspace sized by gonn_hip_attn_workspace_bytes under the
+// same setting fits, and one sized under the other setting is either big
+// enough or refused with GONN_E_WORKSPACE before any work is queued.
 constexpr double kDsMaxBytes = 16.0 * 1024 * 1024 * 1024;
 double ds_slice_bytes(int S, int Sk, int causal) {
     const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
@@ -265,7 +268,7 @@ bool bwd_use_ds(int mode, size_t BH, int S, int Sk, int causal) {
     return slice < 2147483648.0 && (double)BH * slice <= kDsMaxBytes;
 }
 
-BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal) {
+BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal, bool use_ds) {
     BwdLayout L{};
     const size_t Sp = round_up((size_t)S, gonn::kBwdPad), Skp = round_up((size_t)Sk, gonn::kBwdPad);
     size_t off = 0;
@@ -280,7 +283,7 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal) {
             L.packed[i] = off;
             off = round_up(off + BH * (keyside[i] ? Skp : Sp) * D * 2, 256);
         }
-        if (bwd_use_ds(mode, BH, S, Sk, causal)) {
+        if (use_ds) {
             L.ds = off;
             off = round_up(off + BH * (size_t)ds_slice_bytes(S, Sk, causal), 256);
         }
@@ -289,10 +292,14 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal) {
     return L;
 }
 
-size_t bwd_ws(const gonn_attn_bwd_args* a) {
-    return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->D, a->causal)
+size_t bwd_ws(const gonn_attn_bwd_args* a, bool use_ds) {
+    return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->D, a->causal,
+                      use_ds)
                .total +
            256;
+}
+bool bwd_use_ds(const gonn_attn_bwd_args* a) {
+    return bwd_use_ds(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->causal);
 }
 
 // ---- helpers for the host shims ----------------------------------------
@@ -740,7 +747,7 @@ size_t gonn_hip_attn_workspace_bytes(int op, const void* args) {
         case GONN_OP_BWD: {
             const auto* a = (const gonn_attn_bwd_args*)args;
             if (a->B <= 0 || a->H <= 0 || a->S <= 0 || !head_dim_ok(a->D)) return 0;
-            return bwd_ws(a);
+            return bwd_ws(a, bwd_use_ds(a));
         }
         case GONN_OP_DECODE: {
             const auto* a = (const gonn_attn_decode_args*)args;
@@ -809,13 +816,14 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
 
 int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, void* stream) {
     TRY(check_bwd(a));
-    const size_t need = bwd_ws(a);
+    const bool use_ds = bwd_use_ds(a);  // the dQ path of this call, read once
+    const size_t need = bwd_ws(a, use_ds);
     if (!ws || ws_bytes < need) return GONN_E_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
     const int BH = a->B * a->H, S = a->S, D = a->D;
     const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
     const int mode = bwd_mode(a);
-    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, bwd_keys_of(a), D, a->causal);
+    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, bwd_keys_of(a), D, a->causal, use_ds);
     uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
     gonn::BwdParams p{};
     if (a->attn_mask.ptr) {
@@ -889,7 +897,6 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p.k = a->k.ptr;
         p.v = a->v.ptr;
     }
-    const bool use_ds = bwd_use_ds(mode, (size_t)BH, S, p.Sk, a->causal);
     p.ds = use_ds ? (bf16*)(w + L.ds) : nullptr;
     {
         ProfScope ps("bwd_dkdv", s);
@@ -1342,6 +1349,62 @@ static double bench_f64_exact(int BH, int S, int d, int iters, int causal) {
     (void)hipEventDestroy(e0);
     (void)hipEventDestroy(e1);
     return (double)ms / iters;
+}
+
+// Mean ms per call of the f64 mode's backward (D = rowsum(dO * O), dQ,
+// dK/dV) over `iters` calls (after 5 untimed), on zeroed device fp64
+// buffers (LSE 0: every key live), null stream.
+static double bench_f64_exact_bwd(int BH, int S, int d, int iters, int causal) {
+    DevMem mem(nullptr);
+    const size_t n = (size_t)BH * S * d, nr = (size_t)BH * S;
+    double *q, *k, *v, *o, *g, *l, *dl, *dq, *dk, *dv;
+    if (mem.alloc((void**)&q, n * 8) || mem.alloc((void**)&k, n * 8) ||
+        mem.alloc((void**)&v, n * 8) || mem.alloc((void**)&o, n * 8) ||
+        mem.alloc((void**)&g, n * 8) || mem.alloc((void**)&l, nr * 8) ||
+        mem.alloc((void**)&dl, nr * 8) || mem.alloc((void**)&dq, n * 8) ||
+        mem.alloc((void**)&dk, n * 8) || mem.alloc((void**)&dv, n * 8))
+        return (double)GONN_E_NOMEM;
+    for (double* x : {q, k, v, o, g})
+        if (gonn::launch_fill_zero(x, n * 8, nullptr)) return -1.0;
+    if (gonn::launch_fill_zero(l, nr * 8, nullptr)) return -1.0;
+    gonn::F64Params p{};
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.o = o;
+    p.dO = g;
+    p.lse = l;
+    p.delta = dl;
+    p.dq = dq;
+    p.dk = dk;
+    p.dv = dv;
+    p.B = BH;
+    p.H = 1;
+    p.Sq = p.Sk = S;
+    p.d = d;
+    p.scale = 1.0 / std::sqrt((double)d);
+    p.causal = causal;
+    for (int i = 0; i < 5; i++)
+        if (gonn::launch_f64_bwd(p, nullptr) != hipSuccess) return -1.0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1.0;
+    hipEvent_t e0, e1;
+    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
+    (void)hipEventRecord(e0, nullptr);
+    for (int i = 0; i < iters; i++) (void)gonn::launch_f64_bwd(p, nullptr);
+    (void)hipEventRecord(e1, nullptr);
+    (void)hipEventSynchronize(e1);
+    float ms = 0.f;
+    (void)hipEventElapsedTime(&ms, e0, e1);
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return (double)ms / iters;
+}
+
+double gonn_hip_bench_flash_attn_f64_bwd(int BH, int S, int d, int iters, int causal) {
+    if (!shim_args_ok(BH, S, d) || iters <= 0) return (double)GONN_E_INVALID;
+    if (!gonn_hip_available()) return (double)GONN_E_NODEVICE;
+    if (current_mode() != GONN_ATTN_FP64) return (double)GONN_E_INVALID;
+    return bench_f64_exact_bwd(BH, S, d, iters, causal);
 }
 
 double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal) {

@@ -323,6 +323,221 @@ __global__ __launch_bounds__(256, 2) void fwd_f64_mfma_kernel(F64Params p) {
     }
 }
 
+// Backward on v_mfma_f64_16x16x4f64, the forward's layout applied to the
+// backward identities (P = exp(s - L), dS = P (dP - D) scale):
+//  dQ: a wave owns 16 queries; per 16-key tile S^T = K Q^T and dP^T = V dO^T
+//      (Q^T, dO^T fragments in registers), then dQ^T (d x queries) += K^T
+//      dS^T with dS^T straight from the score registers (register r = key
+//      4 r + l / 16, the k-slot of step r).
+//  dK/dV: a wave owns 16 keys; per 16-query tile S = Q K^T and dP = dO V^T
+//      (K^T, V^T fragments in registers; register r = query 4 r + l / 16),
+//      then dV^T += dO^T P and dK^T += Q^T dS from those registers.
+// The streamed rows go into LDS in both operand orders they are read in:
+//   "rows"  X[t][s][j][q] = X[16 t + j][4 s + q]   (A of S, dP: rows x d)
+//   "cols"  X[t][r][dt][q][j] = X[16 t + 4 r + q][16 dt + j]  (A of the
+//           output products: d x rows)
+// Each kernel owns its outputs (no atomics), so results are deterministic.
+// d = 128 runs one wave per SIMD (the four register fragments and
+// accumulators need more than half the register file).
+constexpr int mb_waves(int DP) { return DP <= 64 ? 2 : 1; }  // workgroups per CU
+
+// Stage `srcA` (and `srcB`) rows [r0, r0 + ROWS) of a (nrows, d) slice into
+// LDS in the rows order (la, lb) and the cols order (ta, tb); rows past
+// nrows and columns past d are zero. Chunk i of thread tid is row (i*256 +
+// tid) / (DP/2), columns 2 ((i*256 + tid) % (DP/2)) and the next.
+template <int DP, int ROWS>
+struct F64Stage {
+    static constexpr int NS = DP / 4, NDT = DP / 16;
+    static constexpr int NCH = ROWS * DP / 2 / 256;
+    static_assert(NCH * 512 == ROWS * DP, "whole chunks per stage");
+    f64x2_t a[NCH], b[NCH];
+    __device__ __forceinline__ void load(const double* srcA, const double* srcB, int r0, int nrows,
+                                         int d) {
+        for (int i = 0; i < NCH; i++) {
+            const int c = i * 256 + threadIdx.x, row = r0 + c / (DP / 2), dd = 2 * (c % (DP / 2));
+            f64x2_t va{0.0, 0.0}, vb{0.0, 0.0};
+            if (row < nrows && dd < d) {
+                const size_t off = (size_t)row * d + dd;
+                va[0] = srcA[off];
+                vb[0] = srcB[off];
+                if (dd + 1 < d) {
+                    va[1] = srcA[off + 1];
+                    vb[1] = srcB[off + 1];
+                }
+            }
+            a[i] = va;
+            b[i] = vb;
+        }
+    }
+    // la/lb: rows order (or null), ta/tb: cols order (or null).
+    __device__ __forceinline__ void store(double* la, double* lb, double* ta, double* tb) const {
+        for (int i = 0; i < NCH; i++) {
+            const int c = i * 256 + threadIdx.x, kr = c / (DP / 2), dd = 2 * (c % (DP / 2));
+            const int t = kr >> 4, j = kr & 15;
+            const int ro = ((t * NS + (dd >> 2)) * 16 + j) * 4 + (dd & 3);
+            const int co = (((t * 4 + (j >> 2)) * NDT + (dd >> 4)) * 4 + (j & 3)) * 16 + (dd & 15);
+            if (la) *(f64x2_t*)&la[ro] = a[i];
+            if (lb) *(f64x2_t*)&lb[ro] = b[i];
+            if (ta) *(f64x2_t*)&ta[co] = a[i];
+            if (tb) *(f64x2_t*)&tb[co] = b[i];
+        }
+    }
+};
+
+template <int DP>
+__global__ __launch_bounds__(256, mb_waves(DP)) void dq_f64_mfma_kernel(F64Params p) {
+    constexpr int NS = DP / 4, NDT = DP / 16;
+    constexpr int STG = mstage(DP), NT16 = STG / 16;
+    __shared__ double sK[NT16 * NS * 64];             // K, rows order (A of S^T)
+    __shared__ double sV[NT16 * NS * 64];             // V, rows order (A of dP^T)
+    __shared__ double sKt[NT16 * 4 * NDT * 64];       // K, cols order (A of dQ^T)
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, quad = lane >> 4;
+    const int Sq = p.Sq, Sk = p.Sk, d = p.d;
+    const int nqb = (Sq + kMRows - 1) / kMRows, BH = p.B * p.H;
+    const int rank = blockIdx.x / BH, bh = blockIdx.x - rank * BH;
+    const int qb = p.causal ? nqb - 1 - rank : rank;
+    const int q0 = qb * kMRows, qw = q0 + wave * kMWaveQ, qi = qw + col;
+    const int kend_b = keys_of(p, bh);
+    int kend = kend_b;
+    if (p.causal && q0 + kMRows < kend) kend = q0 + kMRows;
+    const int ic = qi < Sq ? qi : 0;
+    const size_t row = ((size_t)bh * Sq + ic) * d;
+    double qf[NS], gf[NS];
+    for (int s = 0; s < NS; s++) {
+        const int c = 4 * s + quad;
+        qf[s] = (qi < Sq && c < d) ? p.q[row + c] : 0.0;
+        gf[s] = (qi < Sq && c < d) ? p.dO[row + c] : 0.0;
+    }
+    const double L = p.lse[(size_t)bh * Sq + ic];
+    const double Di = p.delta[(size_t)bh * Sq + ic];
+    const bool live = qi < Sq && L != -INFINITY;
+    f64x4_t dqacc[NDT];
+    for (int t = 0; t < NDT; t++) dqacc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+    const double* kg = p.k + (size_t)bh * Sk * d;
+    const double* vg = p.v + (size_t)bh * Sk * d;
+    F64Stage<DP, STG> st;
+    if (kend > 0) st.load(kg, vg, 0, Sk, d);
+    for (int j0 = 0; j0 < kend; j0 += STG) {
+        __syncthreads();
+        st.store(sK, sV, sKt, nullptr);
+        __syncthreads();
+        if (j0 + STG < kend) st.load(kg, vg, j0 + STG, Sk, d);
+        for (int t = 0; t < NT16; t++) {
+            const int kt0 = j0 + 16 * t;
+            if (kt0 >= kend || (p.causal && kt0 > qw + kMWaveQ - 1)) continue;  // wave-uniform
+            f64x4_t sacc{0.0, 0.0, 0.0, 0.0}, pacc{0.0, 0.0, 0.0, 0.0};
+            for (int s2 = 0; s2 < NS; s2++) {
+                const int a = ((t * NS + s2) * 16 + col) * 4 + quad;
+                sacc = mfma_f64(sK[a], qf[s2], sacc);
+                pacc = mfma_f64(sV[a], gf[s2], pacc);
+            }
+            for (int r = 0; r < 4; r++) {
+                const int key = kt0 + 4 * r + quad;
+                const bool on = live && key < kend_b && !(p.causal && key > qi);
+                const double sc = p.scale * sacc[r] + mask_at(p, bh, ic, key < Sk ? key : 0);
+                const double ds = on ? exp(sc - L) * (pacc[r] - Di) * p.scale : 0.0;
+                for (int dt = 0; dt < NDT; dt++)
+                    dqacc[dt] = mfma_f64(sKt[(((t * 4 + r) * NDT + dt) * 4 + quad) * 16 + col], ds,
+                                         dqacc[dt]);
+            }
+        }
+    }
+    if (qi < Sq) {
+        double* dqr = p.dq + row;
+        for (int dt = 0; dt < NDT; dt++)
+            for (int r = 0; r < 4; r++) {
+                const int c = 16 * dt + 4 * r + quad;
+                if (c < d) dqr[c] = dqacc[dt][r];
+            }
+    }
+}
+
+template <int DP>
+__global__ __launch_bounds__(256, mb_waves(DP)) void dkdv_f64_mfma_kernel(F64Params p) {
+    constexpr int NS = DP / 4, NDT = DP / 16;
+    constexpr int STG = mstage(DP), NT16 = STG / 16;
+    __shared__ double sQ[NT16 * NS * 64];        // Q, rows order (A of S)
+    __shared__ double sG[NT16 * NS * 64];        // dO, rows order (A of dP)
+    __shared__ double sQt[NT16 * 4 * NDT * 64];  // Q, cols order (A of dK^T)
+    __shared__ double sGt[NT16 * 4 * NDT * 64];  // dO, cols order (A of dV^T)
+    __shared__ double sL[STG], sD[STG];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int col = lane & 15, quad = lane >> 4;
+    const int Sq = p.Sq, Sk = p.Sk, d = p.d;
+    const int nkb = (Sk + kMRows - 1) / kMRows, BH = p.B * p.H;
+    const int rank = blockIdx.x / BH, bh = blockIdx.x - rank * BH;
+    // Causal key blocks see queries from their first key on: the first
+    // blocks are the longest.
+    const int kb = rank;
+    const int k0 = kb * kMRows, kw = k0 + wave * kMWaveQ, kj = kw + col;
+    const int kend_b = keys_of(p, bh);
+    const int jc = kj < Sk ? kj : 0;
+    const size_t row = ((size_t)bh * Sk + jc) * d;
+    double kf[NS], vf[NS];
+    for (int s = 0; s < NS; s++) {
+        const int c = 4 * s + quad;
+        kf[s] = (kj < Sk && c < d) ? p.k[row + c] : 0.0;
+        vf[s] = (kj < Sk && c < d) ? p.v[row + c] : 0.0;
+    }
+    const bool klive = kj < kend_b;
+    f64x4_t dkacc[NDT], dvacc[NDT];
+    for (int t = 0; t < NDT; t++) dkacc[t] = dvacc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
+    const int i_start = (p.causal ? k0 : 0) / STG * STG;
+    const double* qg = p.q + (size_t)bh * Sq * d;
+    const double* gg = p.dO + (size_t)bh * Sq * d;
+    F64Stage<DP, STG> st;
+    if (k0 < kend_b && i_start < Sq) st.load(qg, gg, i_start, Sq, d);
+    for (int i0 = i_start; k0 < kend_b && i0 < Sq; i0 += STG) {
+        __syncthreads();
+        st.store(sQ, sG, sQt, sGt);
+        if (tid < STG) {
+            const int ii = i0 + tid;
+            sL[tid] = ii < Sq ? p.lse[(size_t)bh * Sq + ii] : -INFINITY;
+            sD[tid] = ii < Sq ? p.delta[(size_t)bh * Sq + ii] : 0.0;
+        }
+        __syncthreads();
+        if (i0 + STG < Sq) st.load(qg, gg, i0 + STG, Sq, d);
+        for (int t = 0; t < NT16; t++) {
+            const int it0 = i0 + 16 * t;
+            if (it0 >= Sq || (p.causal && it0 + 15 < kw)) continue;  // wave-uniform
+            f64x4_t sacc{0.0, 0.0, 0.0, 0.0}, pacc{0.0, 0.0, 0.0, 0.0};
+            for (int s2 = 0; s2 < NS; s2++) {
+                const int a = ((t * NS + s2) * 16 + col) * 4 + quad;
+                sacc = mfma_f64(sQ[a], kf[s2], sacc);
+                pacc = mfma_f64(sG[a], vf[s2], pacc);
+            }
+            for (int r = 0; r < 4; r++) {
+                const int qr = 16 * t + 4 * r + quad, i = i0 + qr;
+                const double Li = sL[qr];
+                const bool on = klive && i < Sq && Li != -INFINITY && !(p.causal && kj > i);
+                const double sc = p.scale * sacc[r] + mask_at(p, bh, i < Sq ? i : 0, jc);
+                const double pr = on ? exp(sc - Li) : 0.0;
+                const double ds = pr * (pacc[r] - sD[qr]) * p.scale;
+                for (int dt = 0; dt < NDT; dt++) {
+                    const int a = (((t * 4 + r) * NDT + dt) * 4 + quad) * 16 + col;
+                    dvacc[dt] = mfma_f64(sGt[a], pr, dvacc[dt]);
+                    dkacc[dt] = mfma_f64(sQt[a], ds, dkacc[dt]);
+                }
+            }
+        }
+    }
+    if (kj < Sk) {
+        double* dkr = p.dk + row;
+        double* dvr = p.dv + row;
+        for (int dt = 0; dt < NDT; dt++)
+            for (int r = 0; r < 4; r++) {
+                const int c = 16 * dt + 4 * r + quad;
+                if (c < d) {
+                    dkr[c] = dkacc[dt][r];
+                    dvr[c] = dvacc[dt][r];
+                }
+            }
+    }
+}
+
 // D_i = dO_i . O_i, one team per row.
 template <int DP>
 __global__ __launch_bounds__(256) void prep_f64_kernel(F64Params p) {
@@ -499,6 +714,22 @@ hipError_t launch_f64_fwd(const F64Params& p, hipStream_t s) {
 hipError_t launch_f64_bwd(const F64Params& p, hipStream_t s) {
     if (!f64_args_ok(p) || !p.o || !p.dO || !p.lse || !p.delta || !p.dq || !p.dk || !p.dv)
         return hipErrorInvalidValue;
+    const char* e = std::getenv("GONN_HIP_F64_BWD");
+    if (!(e && e[0] == 'v')) {  // "valu": the team kernels (kept for comparison)
+        const dim3 gp((p.Sq + kRowsWG - 1) / kRowsWG, p.B * p.H);
+        const dim3 gq(((p.Sq + kMRows - 1) / kMRows) * p.B * p.H);
+        const dim3 gk(((p.Sk + kMRows - 1) / kMRows) * p.B * p.H);
+        if (dp_of(p.d) <= 64) {
+            prep_f64_kernel<64><<<gp, 256, 0, s>>>(p);
+            dq_f64_mfma_kernel<64><<<gq, 256, 0, s>>>(p);
+            dkdv_f64_mfma_kernel<64><<<gk, 256, 0, s>>>(p);
+        } else {
+            prep_f64_kernel<128><<<gp, 256, 0, s>>>(p);
+            dq_f64_mfma_kernel<128><<<gq, 256, 0, s>>>(p);
+            dkdv_f64_mfma_kernel<128><<<gk, 256, 0, s>>>(p);
+        }
+        return hipGetLastError();
+    }
     const dim3 gq((p.Sq + kRowsWG - 1) / kRowsWG, p.B * p.H);
     const dim3 gk((p.Sk + kRowsWG - 1) / kRowsWG, p.B * p.H);
     switch (dp_of(p.d)) {

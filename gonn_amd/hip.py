@@ -274,6 +274,16 @@ def BenchFlashAttnF64(BH: int, S: int, d: int, iters: int, causal: bool) -> floa
     return ms
 
 
+def BenchFlashAttnF64Bwd(BH: int, S: int, d: int, iters: int, causal: bool) -> float:
+    """New (the reference times no backward): the exact-mode (SetAttnMode
+    "f64") backward, device-resident and event-timed like BenchFlashAttnF64;
+    mean ms per call. Raises GonnHipError in any other mode."""
+    ms = float(_lib.load().gonn_hip_bench_flash_attn_f64_bwd(BH, S, d, iters, int(bool(causal))))
+    if ms < 0:
+        raise GonnHipError(int(ms), "BenchFlashAttnF64Bwd")
+    return ms
+
+
 # ---------------------------------------------------------------------------
 # device-resident API on torch tensors
 # ---------------------------------------------------------------------------
@@ -731,5 +741,5 @@ __all__ = ["Available", "Supports", "SetAttnMode", "AttnMode", "Version", "Selft
            "FlashAttnF64", "FlashAttnF64Fwd", "FlashAttnF64Bwd", "FlashAttnF64Ex",
            "FlashAttnF64BwdEx", "mask_strides", "Gemm",
            "Unary", "Binary",
-           "BenchFlashAttnF64", "attn_fwd", "attn_bwd", "attn_decode", "KVCache", "DeviceMHA", "buf",
-           "GonnHipError"]
+           "BenchFlashAttnF64", "BenchFlashAttnF64Bwd", "attn_fwd", "attn_bwd", "attn_decode",
+           "KVCache", "DeviceMHA", "buf", "GonnHipError"]

@@ -431,6 +431,12 @@ int gonn_hip_flash_attn_f64_ex(const double* Q, const double* K, const double* V
  * event-timed forward; returns mean ms per launch, or a negative value on
  * error. Inputs are zero-filled like the reference's benchmark.           */
 double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal);
+/* New (the reference times no backward: benchmark/flashbwd/main.go only
+ * gradchecks FlashAttnF64Bwd): the exact-mode backward timed like the
+ * forward above (zero-filled device fp64 inputs, 5 warm-ups, one event pair
+ * around `iters` calls, mean ms per call). Only in mode GONN_ATTN_FP64;
+ * other modes return GONN_E_INVALID (their backward is gonn_hip_attn_bwd).*/
+double gonn_hip_bench_flash_attn_f64_bwd(int BH, int S, int d, int iters, int causal);
 
 /* ---- diagnostics ---------------------------------------------------------- */
 

@@ -282,6 +282,7 @@ def test_shim_argument_errors():
     assert lib.gonn_hip_flash_attn_f64(p, p, p, p, 0, 2, 8, 0.1, 0) == GONN_E_INVALID
     assert lib.gonn_hip_flash_attn_f64(None, p, p, p, 1, 2, 8, 0.1, 0) == GONN_E_INVALID
     assert lib.gonn_hip_bench_flash_attn_f64(1, 2, 8, 0, 0) < 0
+    assert lib.gonn_hip_bench_flash_attn_f64_bwd(1, 2, 8, 0, 0) < 0
 
 
 def test_injected_allocation_failure():

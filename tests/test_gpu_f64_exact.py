@@ -156,6 +156,39 @@ def test_masked_cross_kv_len(f64_mode, d, causal):
             _close(np.reshape(got, ref.shape), ref, x)
 
 
+@pytest.mark.parametrize("kernels", ["mfma", "valu"])
+@pytest.mark.parametrize("d", [64, 100, 128])
+@pytest.mark.parametrize("causal", [False, True])
+def test_many_blocks_both_kernel_families(f64_mode, monkeypatch, kernels, d, causal):
+    """Rows spanning several 64-row blocks and LDS stages, a ragged last
+    block and key padding, through the MFMA kernels (default) and the team
+    kernels (GONN_HIP_F64_FWD / GONN_HIP_F64_BWD = "valu"), forward and
+    backward, against the oracle at the fp64 bar."""
+    hip = f64_mode
+    if kernels == "valu":
+        monkeypatch.setenv("GONN_HIP_F64_FWD", "valu")
+        monkeypatch.setenv("GONN_HIP_F64_BWD", "valu")
+    B, H = 2, 2
+    for Sq, Sk in ((333, 333), (150, 397)):
+        lens = np.array([Sk, Sk // 2 + 7], dtype=np.int32)
+        rng = np.random.default_rng(960 + d + Sq + int(causal))
+        q, k, v, g = (rng.standard_normal((B * H, n, d)) for n in (Sq, Sk, Sk, Sq))
+        scale = 1.0 / math.sqrt(d)
+        say(f"f64 {kernels} d={d} causal={causal} Sq={Sq} Sk={Sk}")
+        O, L = hip.FlashAttnF64Ex(q, k, v, B, H, Sq, Sk, d, scale, causal, kv_len=lens, lse=True)
+        ro, rl = oracle.attn_fwd(q, k, v, scale, causal, kv_len=lens, H=H)
+        _close(O.reshape(ro.shape), ro, "O")
+        live = np.isfinite(rl)
+        assert np.array_equal(np.isfinite(L.reshape(rl.shape)), live)
+        _close(L.reshape(rl.shape)[live], rl[live], "LSE")
+        dQ, dK, dV = hip.FlashAttnF64BwdEx(q, k, v, O, L, g, B, H, Sq, d, scale, causal,
+                                           kv_len=lens, Sk=Sk)
+        rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, scale=scale, causal=causal,
+                                              kv_len=lens, H=H)
+        for x, got, ref in (("dQ", dQ, rq), ("dK", dK, rk), ("dV", dV, rv)):
+            _close(np.reshape(got, ref.shape), ref, x)
+
+
 def test_mha_fused_protocol(f64_mode):
     """benchmark/mha: ForwardFused against the unfused Forward at <= 1e-9
     (the oracle's op sequence stands in for GoNN's CPU Forward)."""
