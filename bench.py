@@ -154,10 +154,13 @@ def bench_prefill(torch, hip, steps, warmup):
 
 def calibration(torch, hip, sclk_ghz):
     """Figures of the box itself, measured in the same process, so a slow box
-    can be told from a slow kernel: the rate of a fixed MFMA loop on constant
-    operands, the bandwidth of a 1 GiB device copy (bytes read + written per
-    second), and the shader clock during the C3 steps (nominal 2.4 GHz)."""
-    mfma = hip.calib_mfma()
+    can be told from a slow kernel: the rate and clock of a fixed MFMA loop on
+    constant operands and on random ones (real data's switching, under which
+    the power limit lowers the clock: the rate no bf16 MFMA kernel can pass
+    on this box), the bandwidth of a 1 GiB device copy (bytes read + written
+    per second), and the shader clock during the C3 steps (nominal 2.4 GHz)."""
+    mfma, mfma_ghz = hip.calib_mfma(False)
+    mfma_r, mfma_r_ghz = hip.calib_mfma(True)
     n = 1 << 28
     x = torch.ones(n, device="cuda")
     y = torch.empty_like(x)
@@ -174,11 +177,16 @@ def calibration(torch, hip, sclk_ghz):
     del x, y
     return {"mfma_const_TFLOPs": round(mfma, 1),
             "mfma_const_frac": round(mfma / PEAK_BF16_TFLOPS, 4),
+            "mfma_const_GHz": round(mfma_ghz, 3),
+            "mfma_random_TFLOPs": round(mfma_r, 1),
+            "mfma_random_frac": round(mfma_r / PEAK_BF16_TFLOPS, 4),
+            "mfma_random_GHz": round(mfma_r_ghz, 3),
             "copy_1GiB_GBps": round(copy_gbs, 1),
             "copy_frac": round(copy_gbs / PEAK_HBM_GBS, 4),
             "sclk_GHz_during_c3": round(sclk_ghz, 3),
-            "note": "mfma_const: v_mfma_f32_32x32x16_bf16 loop on constant operands, two "
-                    "waves per SIMD; copy: torch copy_ of 2^28 floats, read + write bytes; "
+            "note": "mfma_const / mfma_random: v_mfma_f32_32x32x16_bf16 loop on constant / "
+                    "uniform random operands, two waves per SIMD, clock over the loop; copy: "
+                    "torch copy_ of 2^28 floats, read + write bytes; "
                     "sclk: s_memtime against the 100 MHz s_memrealtime over the C3 steps"}
 
 
@@ -640,6 +648,9 @@ def main():
     }
     log("[bench] calibration")
     line["calibration"] = calibration(torch, hip, pre["sclk_ghz"])
+    # The kernel against the MFMA rate this box sustains on random operands.
+    line["roofline"]["frac_of_mfma_random"] = round(
+        ach / line["calibration"]["mfma_random_TFLOPs"], 4)
     if not args.no_decode:
         log("[bench] decode C4")
         dec = bench_decode(torch, hip, args.steps, args.warmup)

@@ -144,7 +144,7 @@ def load() -> ctypes.CDLL:
     lib.gonn_hip_selftest_mfma.restype = i
     lib.gonn_hip_profile_enable.argtypes = [i]
     lib.gonn_hip_profile_read.argtypes = [ctypes.c_char_p, dp, ctypes.POINTER(i)]
-    lib.gonn_hip_calib_mfma.argtypes = [dp]
+    lib.gonn_hip_calib_mfma.argtypes = [i, dp, dp]
     lib.gonn_hip_calib_clock_start.argtypes = [ctypes.c_double, vp]
     lib.gonn_hip_calib_clock_read.argtypes = [dp]
     ip = ctypes.POINTER(i)

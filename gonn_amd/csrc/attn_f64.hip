@@ -24,13 +24,20 @@
 //   dQ_i = scale sum_j dS_ij k_j (backend/cuda/gonn_cuda.cu:333-340).
 //
 // Layout: fp64 (BH, rows, d) row-major, as the f64 entries receive them.
-// A row (query or key) is owned by a team of 8 lanes; lane u of the team
-// holds elements 8t + u (t < DP/8) of the row's vectors, so a team reads 64
-// contiguous bytes per t and dot products end in a 3-step lane reduction.
-// The streamed rows (K/V for the forward and dQ, Q/dO for dK/dV) sit in LDS
-// tiles of 32 rows that every team reads in the same order (broadcasts).
-// The two backward kernels each own their outputs: no atomics,
-// deterministic.
+// Two kernel families:
+//  * the default, on v_mfma_f64_16x16x4f64 (fwd_f64_mfma_kernel,
+//    dq_f64_mfma_kernel, dkdv_f64_mfma_kernel): a wave owns 16 rows, and
+//    the score tiles are formed in the orientation whose register layout is
+//    the next product's operand layout, so P and dS feed the MFMAs from
+//    registers and each score's exp is computed once (the kernels' own
+//    comments give the layouts);
+//  * the team kernels (GONN_HIP_F64_FWD / GONN_HIP_F64_BWD = "valu"): a row
+//    (query or key) is owned by a team of 8 lanes; lane u of the team holds
+//    elements 8t + u (t < DP/8) of the row's vectors, so a team reads 64
+//    contiguous bytes per t and dot products end in a 3-step lane
+//    reduction; the streamed rows sit in LDS tiles of 32 rows that every
+//    team reads in the same order (broadcasts).
+// Every backward kernel owns its outputs: no atomics, deterministic.
 #include <cmath>
 #include <cstdlib>
 

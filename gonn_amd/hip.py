@@ -90,11 +90,13 @@ def profile_read(kernel: str):
     return tot.value, n.value
 
 
-def calib_mfma() -> float:
-    """TFLOP/s of a fixed bf16 MFMA loop on constant operands (whole device)."""
-    t = ctypes.c_double(0.0)
-    check(_lib.load().gonn_hip_calib_mfma(ctypes.byref(t)), "calib_mfma")
-    return t.value
+def calib_mfma(random: bool = False):
+    """(TFLOP/s, shader GHz) of a fixed bf16 MFMA loop over the whole device,
+    on constant operands or (random) distinct uniform values per lane."""
+    t, g = ctypes.c_double(0.0), ctypes.c_double(0.0)
+    check(_lib.load().gonn_hip_calib_mfma(int(bool(random)), ctypes.byref(t), ctypes.byref(g)),
+          "calib_mfma")
+    return t.value, g.value
 
 
 def calib_clock_start(ms: float, stream=None) -> None:

@@ -453,15 +453,18 @@ int gonn_hip_profile_read(const char* kernel, double* total_ms, int* count);
 
 /* Box calibration for benchmarks (no reference counterpart: GoNN's
  * benchmark reports raw times, backend/cuda/gonn_cuda.cu:532-560).
- * calib_mfma: TFLOP/s of a fixed loop of v_mfma_f32_32x32x16_bf16 on
- * constant operands over the whole device (two waves per SIMD, eight
- * independent chains each, no memory traffic); synchronous.
+ * calib_mfma: TFLOP/s of a fixed loop of v_mfma_f32_32x32x16_bf16 over
+ * the whole device (two waves per SIMD, eight independent chains each, no
+ * memory traffic), and the mean shader clock (GHz) over the loop; operands
+ * constant (random = 0) or distinct uniform [-1, 1) values per lane and
+ * chain (random = 1: the switching of real data, whose power sets the
+ * clock); synchronous.
  * calib_clock_start: enqueues on `stream` a one-wave probe that reads the
  * shader clock against the fixed 100 MHz counter for `ms` milliseconds
  * (0 < ms <= 60000), for running beside other work on another stream.
  * calib_clock_read: the probe's shader clock in GHz; call it after that
  * stream has been synchronised.                                          */
-int gonn_hip_calib_mfma(double* tflops);
+int gonn_hip_calib_mfma(int random, double* tflops, double* ghz);
 int gonn_hip_calib_clock_start(double ms, void* stream);
 int gonn_hip_calib_clock_read(double* ghz);
 
