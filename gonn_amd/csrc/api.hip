@@ -1312,6 +1312,25 @@ int gonn_hip_flash_attn_f64_bwd_masked(const double* Q, const double* K, const d
     return herr(hipStreamSynchronize(hs));
 }
 
+// Mean ms per call of `call` over `iters` calls on the null stream (after
+// five untimed ones), from one event pair; -1 if a call or an event fails.
+extern "C++" template <typename F>
+static double time_calls(F call, int iters) {
+    for (int i = 0; i < 5; i++)
+        if (!call()) return -1.0;
+    if (hipDeviceSynchronize() != hipSuccess) return -1.0;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    bool ok = hipEventCreate(&e0) == hipSuccess && hipEventCreate(&e1) == hipSuccess &&
+              hipEventRecord(e0, nullptr) == hipSuccess;
+    for (int i = 0; ok && i < iters; i++) ok = call();
+    ok = ok && hipEventRecord(e1, nullptr) == hipSuccess && hipEventSynchronize(e1) == hipSuccess;
+    float ms = 0.f;
+    ok = ok && hipEventElapsedTime(&ms, e0, e1) == hipSuccess;
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    return ok ? (double)ms / iters : -1.0;
+}
+
 // Mean ms per call of the f64 mode's forward over `iters` calls (after 5
 // untimed), on zeroed device fp64 buffers, null stream.
 static double bench_f64_exact(int BH, int S, int d, int iters, int causal) {
@@ -1335,20 +1354,7 @@ static double bench_f64_exact(int BH, int S, int d, int iters, int causal) {
     p.d = d;
     p.scale = 1.0 / std::sqrt((double)d);
     p.causal = causal;
-    for (int i = 0; i < 5; i++)
-        if (gonn::launch_f64_fwd(p, nullptr) != hipSuccess) return -1.0;
-    if (hipDeviceSynchronize() != hipSuccess) return -1.0;
-    hipEvent_t e0, e1;
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
-    (void)hipEventRecord(e0, nullptr);
-    for (int i = 0; i < iters; i++) (void)gonn::launch_f64_fwd(p, nullptr);
-    (void)hipEventRecord(e1, nullptr);
-    (void)hipEventSynchronize(e1);
-    float ms = 0.f;
-    (void)hipEventElapsedTime(&ms, e0, e1);
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    return (double)ms / iters;
+    return time_calls([&] { return gonn::launch_f64_fwd(p, nullptr) == hipSuccess; }, iters);
 }
 
 // Mean ms per call of the f64 mode's backward (D = rowsum(dO * O), dQ,
@@ -1384,20 +1390,7 @@ static double bench_f64_exact_bwd(int BH, int S, int d, int iters, int causal) {
     p.d = d;
     p.scale = 1.0 / std::sqrt((double)d);
     p.causal = causal;
-    for (int i = 0; i < 5; i++)
-        if (gonn::launch_f64_bwd(p, nullptr) != hipSuccess) return -1.0;
-    if (hipDeviceSynchronize() != hipSuccess) return -1.0;
-    hipEvent_t e0, e1;
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
-    (void)hipEventRecord(e0, nullptr);
-    for (int i = 0; i < iters; i++) (void)gonn::launch_f64_bwd(p, nullptr);
-    (void)hipEventRecord(e1, nullptr);
-    (void)hipEventSynchronize(e1);
-    float ms = 0.f;
-    (void)hipEventElapsedTime(&ms, e0, e1);
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    return (double)ms / iters;
+    return time_calls([&] { return gonn::launch_f64_bwd(p, nullptr) == hipSuccess; }, iters);
 }
 
 double gonn_hip_bench_flash_attn_f64_bwd(int BH, int S, int d, int iters, int causal) {
@@ -1437,20 +1430,7 @@ double gonn_hip_bench_flash_attn_f64(int BH, int S, int d, int iters, int causal
     const size_t wsb = gonn_hip_attn_workspace_bytes(GONN_OP_FWD, &a);
     void* ws = nullptr;
     if (wsb && mem.alloc(&ws, wsb)) return (double)GONN_E_NOMEM;
-    for (int i = 0; i < 5; i++)
-        if (gonn_hip_attn_fwd(&a, ws, wsb, nullptr)) return -1.0;
-    if (hipDeviceSynchronize() != hipSuccess) return -1.0;
-    hipEvent_t e0, e1;
-    if (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess) return -1.0;
-    (void)hipEventRecord(e0, nullptr);
-    for (int i = 0; i < iters; i++) (void)gonn_hip_attn_fwd(&a, ws, wsb, nullptr);
-    (void)hipEventRecord(e1, nullptr);
-    (void)hipEventSynchronize(e1);
-    float ms = 0.f;
-    (void)hipEventElapsedTime(&ms, e0, e1);
-    (void)hipEventDestroy(e0);
-    (void)hipEventDestroy(e1);
-    return (double)ms / iters;
+    return time_calls([&] { return gonn_hip_attn_fwd(&a, ws, wsb, nullptr) == GONN_OK; }, iters);
 }
 
 int gonn_hip_profile_enable(int on) {
