@@ -268,13 +268,18 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK, CAUSAL)) void fwd_bf16_p
     float mc = 0.f, l = 0.f, alpha = 1.f;
     f32x16 nmc = f32x16{};
 
+    // Key kt * BN + 4g + c of register (mt, r), c = 32 mt + 8 (r / 4) + r % 4,
+    // is masked when past the key end or (causal) past this lane's query,
+    // i.e. when c exceeds one per-lane threshold: a compare against a
+    // constant and a select per score.
     auto mask = [&](int kt, f32x16* s) {
-        const int kb = kt * BN + 4 * g;
+        int lim = Sk - 1;
+        if (CAUSAL) lim = qi < lim ? qi : lim;
+        const int thr = lim - (kt * BN + 4 * g);
         for (int mt = 0; mt < 2; mt++)
             for (int r = 0; r < 16; r++) {
-                const int key = kb + mt * 32 + 8 * (r >> 2) + (r & 3);
-                const bool off = key >= Sk || (CAUSAL && key > qi);
-                s[mt][r] = off ? -INFINITY : s[mt][r];
+                const int c = mt * 32 + 8 * (r >> 2) + (r & 3);
+                s[mt][r] = c > thr ? -INFINITY : s[mt][r];
             }
     };
     auto needs_mask = [&](int kt) {
