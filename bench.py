@@ -649,8 +649,8 @@ def main():
     log("[bench] calibration")
     line["calibration"] = calibration(torch, hip, pre["sclk_ghz"])
     # The kernel against the MFMA rate this box sustains on random operands.
-    line["roofline"]["frac_of_mfma_random"] = round(
-        ach / line["calibration"]["mfma_random_TFLOPs"], 4)
+    rnd = line["calibration"]["mfma_random_TFLOPs"]
+    line["roofline"]["frac_of_mfma_random"] = round(ach / rnd, 4) if rnd > 0 else None
     if not args.no_decode:
         log("[bench] decode C4")
         dec = bench_decode(torch, hip, args.steps, args.warmup)
