@@ -8,9 +8,10 @@ pinned in test_oracle.py. O and LSE fed to the GPU backward come from the GPU
 forward of the same mode, as in a training step.
 
 Cases: small ragged shapes for both modes, D in {64, 128}, causal and not;
-signed and zero scales; the golden fixtures and the reference's flashbwd shape
-through the f64 entry point; BASELINE config C5 (B=2 H=16 S=8192 D=128 causal,
-bf16) on sampled rows plus size-independent identities on the full output.
+signed and zero scales; many queries against a handful of keys; the golden
+fixtures and the reference's flashbwd shape through the f64 entry point;
+BASELINE config C5 (B=2 H=16 S=8192 D=128 causal, bf16) on sampled rows plus
+size-independent identities on the full output.
 """
 import math
 
@@ -172,6 +173,65 @@ def test_bwd_bf16_full_rows_many_key_blocks(path, monkeypatch):
     assert_close(dq.cpu().numpy(), rq, "bf16", f"dQ path={path}")
     assert_close(dk.cpu().numpy(), rk, "bf16", f"dK path={path}")
     assert_close(dv.cpu().numpy(), rv, "bf16", f"dV path={path}")
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("shape", [(592, 3, True), (1200, 8, False), (2400, 3, True)],
+                         ids=lambda s: f"{s[0]}x{s[1]}{'c' if s[2] else ''}")
+def test_bwd_long_query_few_keys(D, shape):
+    """Cross-attention with many queries and a handful of keys (Sq >> Sk):
+    each dK and dV row sums about Sq products of order 1, so it reaches 17 to
+    90 while single entries of the same row can sit near 0. The bf16 bar
+    (2e-2 + 1e-2 |ref| per entry) is stated for the N(0,1) self-attention
+    configs; here the rounding of the inputs alone breaks it: the fp64
+    oracle on bf16-rounded operands (Q * scale * log2(e), K, V, dO, as the
+    kernels read them) differs from the oracle on the inputs by up to 0.14
+    in dK and dV.
+
+    The same holds for fp32 sums: 2400 terms of order 1 leave about 4e-6 of
+    a row's size (1.3e-4 on an entry of 33), past the fp32-mode 1e-4.
+    So both bars are taken per row here (the row's largest |ref| in place of
+    the entry's own |ref|). Checks, per case:
+    - fp32 mode, the same inputs: every entry within
+      1e-4 + 1e-5 * (largest |ref| of its row), so the kernels' blocking,
+      causal limits and key tails are right at this shape;
+    - bf16 mode against the oracle on the rounded operands (the kernels' own
+      rounding: bf16 P and dS, fp32 sums): every entry within
+      2e-2 + 1e-2 * (largest |ref| of its row);
+    - bf16 mode against the oracle on the inputs: the worst entry at most
+      twice the worst difference the input rounding alone makes, plus 2e-2.
+    A query block left out of a dK or dV sum moves its rows by 64/Sq of
+    their size (3% to 11% here) and fails the row bar."""
+    from tests._util import bf16_round
+    Sq, Sk, causal = shape
+    BH = 4
+    seed = 4700 + Sq + Sk + D
+    q, g = (randn((BH, Sq, D), seed + i) for i in range(2))
+    k, v = (randn((BH, Sk, D), seed + 2 + i) for i in range(2))
+    sc = 1.0 / math.sqrt(D)
+    say(f"bwd long-query few-key D={D} Sq={Sq} Sk={Sk} causal={causal}")
+    def row_bar(got, ref, atol, rtol, what):
+        err = np.abs(got.astype(np.float64) - ref)
+        bound = atol + rtol * np.abs(ref).max(axis=-1, keepdims=True)
+        worst = np.unravel_index(int(np.argmax(err - bound)), err.shape)
+        say(f"[{what}] max_abs={err.max():.3e} row bar ok: {bool(np.all(err <= bound))}")
+        assert np.all(err <= bound), (what, worst, got[worst], ref[worst])
+
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, sc, causal)
+    _, _, dq, dk, dv = _fwd_bwd(q, k, v, g, causal, "fp32")
+    for got, ref, n in ((dq, rq, "dQ"), (dk, rk, "dK"), (dv, rv, "dV")):
+        row_bar(got, ref, 1e-4, 1e-5, f"{n} fp32")
+    c2 = np.float32(sc * math.log2(math.e))
+    qr = bf16_round(q * c2).astype(np.float64) / np.float64(c2)
+    bq, bk, bv = oracle.attn_bwd_autograd(qr, bf16_round(k), bf16_round(v), bf16_round(g),
+                                          sc, causal)
+    _, _, dq, dk, dv = _fwd_bwd(q, k, v, g, causal, "bf16")
+    for got, ref, bref, n in ((dq, rq, bq, "dQ"), (dk, rk, bk, "dK"), (dv, rv, bv, "dV")):
+        row_bar(got, bref, 2e-2, 1e-2, f"{n} bf16 vs rounded operands")
+        inputs = np.abs(bref - ref).max()
+        err = np.abs(got.astype(np.float64) - ref).max()
+        say(f"[{n} bf16] vs inputs {err:.3e}, input rounding alone {inputs:.3e}")
+        assert err <= 2 * inputs + 2e-2, n
 
 
 def test_bwd_golden_fixtures_via_f64_entry():
