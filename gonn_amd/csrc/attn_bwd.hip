@@ -257,32 +257,29 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     const bool ds_live = kj < Skv;
 
     typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    // Causal mask (key > query) of S(i): only the first two query tiles of a
+    // key block cross the diagonal. Applied between steps, once S(i) is
+    // complete and before the step that exponentiates it reads it. The
+    // exponent scale c2b is positive (a negative scale is folded into the
+    // packed Q), so a masked score of -inf gives P = 0 and dS = 0.
+    auto causal_mask = [&](int i, f32x16* s) {
+        const int kq = kj - (qb0 + i) * BM - 4 * g;  // key minus the lane group's base query
+        for (int mt = 0; mt < 2; mt++)
+            for (int r = 0; r < 16; r++)
+                s[mt][r] = kq > mt * 32 + 8 * (r >> 2) + (r & 3) ? -INFINITY : s[mt][r];
+    };
     // One pipeline step. sA <- S(i+1), dA <- dP(i+1); sB, dB = S(i), dP(i).
-    auto step = [&](auto ha_tag, auto hb_tag, auto hc_tag, auto mk_tag, int i, f32x16* sA,
+    auto step = [&](auto ha_tag, auto hb_tag, auto hc_tag, int i, f32x16* sA,
                     f32x16* dA, f32x16* sB, f32x16* dB) __attribute__((always_inline)) {
         constexpr bool HA = decltype(ha_tag)::value;  // S/dP of tile i+1
         constexpr bool HB = decltype(hb_tag)::value;  // P/dS of tile i
         constexpr bool HC = decltype(hc_tag)::value;  // dV/dK of tile i-1
-        constexpr bool MK = decltype(mk_tag)::value;  // tile i may need the causal mask
         const int qb = qb0 + i;
         if constexpr (MASK && HA) mcol.load(qb + 1, g, mreg);
         // Loads for the next steps: row tiles i+2, L/D i+1.
         const uint32_t dr = HA && i + 2 < nq;
         const bool dl = HA;
         if (dl) dma_ld(qb + 1, (i + 1) & 1);
-        // Causal mask (key > query), only on the first two tiles (steps with
-        // MK set; kept out of the other steps, where the selects would pull
-        // every score out of its accumulator registers). The exponent scale
-        // c2b is positive (a negative scale is folded into the packed Q), so
-        // a masked score of -inf gives P = 0 and dS = 0.
-        if constexpr (HB && MK) {
-            if (i < 2) {
-                const int kq = kj - qb * BM - 4 * g;  // key minus the lane group's base query
-                for (int mt = 0; mt < 2; mt++)
-                    for (int r = 0; r < 16; r++)
-                        sB[mt][r] = kq > mt * 32 + 8 * (r >> 2) + (r & 3) ? -INFINITY : sB[mt][r];
-            }
-        }
         const uint32_t rsl = (uint32_t)((i + 1) & 3) * RTB;   // row tile i+1 (S, dP)
         const uint32_t tsl = (uint32_t)((i + 3) & 3) * RTB;   // row tile i-1 (dV, dK)
         const uint32_t nsl = (uint32_t)((i + 2) & 3);     // slot of row tile i+2
@@ -439,34 +436,33 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     }
 
     // Steps 0 .. nq: step i has S/dP(i+1) while i+1 < nq, P/dS(i) while
-    // i < nq, dV/dK(i-1) from i = 1.
-    // Even steps write S/dP into sY/dY and read sX/dX, odd steps the reverse.
-    // Steps 0 and 1 carry the causal mask; the loop starts at step 2.
-    using Mk = std::integral_constant<bool, CAUSAL>;
+    // i < nq, dV/dK(i-1) from i = 1. Step i writes S/dP(i+1) into the
+    // register set the next step reads as S/dP(i): the full steps
+    // 1 .. nq-2 run in pairs (sX, sY), then (sY, sX); an odd count peels
+    // step 1 and copies its S/dP(2) into sY, so one copy of each tail step
+    // (the next-to-last reads sY) follows the loop.
+    if constexpr (CAUSAL) causal_mask(0, sX);
     if (nq == 1) {
-        step(No{}, Yes{}, No{}, Mk{}, 0, sY, dY, sX, dX);
-        step(No{}, No{}, Yes{}, No{}, 1, sX, dX, sY, dY);
-    } else if (nq == 2) {
-        step(Yes{}, Yes{}, No{}, Mk{}, 0, sY, dY, sX, dX);
-        step(No{}, Yes{}, Yes{}, Mk{}, 1, sX, dX, sY, dY);
-        step(No{}, No{}, Yes{}, No{}, 2, sY, dY, sX, dX);
+        step(No{}, Yes{}, No{}, 0, sY, dY, sX, dX);
+        step(No{}, No{}, Yes{}, 1, sX, dX, sY, dY);
     } else {
-        step(Yes{}, Yes{}, No{}, Mk{}, 0, sY, dY, sX, dX);
-        step(Yes{}, Yes{}, Yes{}, Mk{}, 1, sX, dX, sY, dY);
-        int i = 2;
-        for (; i + 2 < nq; i += 2) {
-            step(Yes{}, Yes{}, Yes{}, No{}, i, sY, dY, sX, dX);
-            step(Yes{}, Yes{}, Yes{}, No{}, i + 1, sX, dX, sY, dY);
+        step(Yes{}, Yes{}, No{}, 0, sY, dY, sX, dX);
+        if constexpr (CAUSAL) causal_mask(1, sY);
+        int i = 1;
+        if ((nq - 2) & 1) {
+            step(Yes{}, Yes{}, Yes{}, 1, sX, dX, sY, dY);
+            for (int mt = 0; mt < 2; mt++) {
+                sY[mt] = sX[mt];
+                dY[mt] = dX[mt];
+            }
+            i = 2;
         }
-        // i = nq-2 or nq-1 remain (then the final dV/dK step)
-        if (i + 1 < nq) {
-            step(Yes{}, Yes{}, Yes{}, No{}, i, sY, dY, sX, dX);
-            step(No{}, Yes{}, Yes{}, No{}, i + 1, sX, dX, sY, dY);
-            step(No{}, No{}, Yes{}, No{}, i + 2, sY, dY, sX, dX);
-        } else {
-            step(No{}, Yes{}, Yes{}, No{}, i, sY, dY, sX, dX);
-            step(No{}, No{}, Yes{}, No{}, i + 1, sX, dX, sY, dY);
+        for (; i < nq - 1; i += 2) {
+            step(Yes{}, Yes{}, Yes{}, i, sX, dX, sY, dY);
+            step(Yes{}, Yes{}, Yes{}, i + 1, sY, dY, sX, dX);
         }
+        step(No{}, Yes{}, Yes{}, nq - 1, sX, dX, sY, dY);
+        step(No{}, No{}, Yes{}, nq, sY, dY, sX, dX);
     }
 
     if (kj < Sk) {
