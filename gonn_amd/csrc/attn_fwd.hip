@@ -152,6 +152,9 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK, CAUSAL)) void fwd_bf16_p
     constexpr int KLEAD = 3, VLEAD = 1;
     __shared__ __attribute__((aligned(16))) bf16 sKb[KSLOTS * BN * D];
     __shared__ __attribute__((aligned(16))) bf16 sVb[VSLOTS * D * BN];
+    // Additive mask (MASK variant): one 64-key tile of this wave's 32 rows,
+    // 8 KB per wave, written and read by that wave only.
+    __shared__ __attribute__((aligned(16))) float sMk[MASK ? NW * 32 * BN : 4];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -171,12 +174,41 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK, CAUSAL)) void fwd_bf16_p
         if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
         ntiles = (kend + BN - 1) / BN;
     }
-    // Additive mask (MASK variant, one workgroup per CU for the registers):
-    // the values of S^T(t+2) are loaded at the start of step t and added when
-    // that tile is complete, at the step's end.
+    // Additive mask (MASK variant): the values of S^T(t+2) are loaded at the
+    // start of step t and added when that tile is complete, at the step's
+    // end. A lane's own scores are 4-key runs of its query's row, 32 bytes of
+    // it per load instruction: loaded straight into registers, one
+    // instruction touches 32 rows' cache lines for 32 bytes of each, and the
+    // mask stream cost the D = 64 forward 30 of its 74 us. So each wave
+    // stages its 32 rows of the tile in its own LDS slot instead, each load
+    // instruction filling 4 whole 256-byte rows (16-byte chunk c of row r at
+    // chunk slot c ^ (r % 16), which keeps the lanes' reads conflict-free),
+    // and reads its values back after the step's closing wait. The prologue's
+    // two tiles go straight to registers.
     MaskRow mrow{};
     f32x4 mreg[8];
-    if constexpr (MASK) mrow.init(p.mask, p.mask_sb, p.mask_sh, p.H, p.Sq, p.Sk, bh, qi);
+    uint32_t moff[MASK ? 8 : 1];
+    if constexpr (MASK) {
+        mrow.init(p.mask, p.mask_sb, p.mask_sh, p.H, p.Sq, p.Sk, bh, qi);
+        for (int i = 0; i < 8; i++) {
+            const int r = 4 * i + (lane >> 4), q = qw + r < Sq ? qw + r : Sq - 1;
+            moff[i] = (uint32_t)(q * p.Sk) * 4u + (uint32_t)(((lane & 15) ^ (r & 15)) * 16);
+        }
+    }
+    const uint32_t mkl = lds_addr(sMk) + wave * 32 * BN * 4;
+    auto mask_dma = [&](int kt) {
+        for (int i = 0; i < 8; i++) dma16(mrow.rs, mkl + i * 1024, moff[i], (uint32_t)kt * BN * 4);
+    };
+    auto mask_add_lds = [&](f32x16* s) {
+        const char* base = (const char*)sMk + wave * 32 * BN * 4 + ln * BN * 4;
+        for (int mt = 0; mt < 2; mt++)
+            for (int j = 0; j < 4; j++) {
+                const int c = 8 * mt + 2 * j + g;
+                const f32x4 m = *(const f32x4*)(base + ((c ^ (ln & 15)) << 4));
+                for (int e = 0; e < 4; e++)
+                    s[mt][4 * j + e] = __builtin_fmaf(m[e], kLog2e, s[mt][4 * j + e]);
+            }
+    };
 
     // Q fragment: qf[ks] = Q[qi][16ks + 8g .. +7] * sign(scale) * c2, in bf16.
     // Loaded in the prologue after the first tile loads are issued, so the
@@ -340,7 +372,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK, CAUSAL)) void fwd_bf16_p
         // step's MFMA stream).
         if constexpr (TAIL < 2)
             if (needs_mask(t + 1)) mask(t + 1, sB);
-        if constexpr (MASK && TAIL == 0) mrow.load(t + 2 < ntiles ? t + 2 : ntiles - 1, g, mreg);
+        if constexpr (MASK && TAIL == 0) mask_dma(t + 2 < ntiles ? t + 2 : ntiles - 1);
         const uint32_t vb = (uint32_t)(t & 1) * VTB;
         const uint32_t kb = (uint32_t)((t + 2) & (KSLOTS - 1)) * KTB;
 
@@ -483,7 +515,7 @@ __global__ __launch_bounds__(256, fwd_pipe_wgs(D, MASK, CAUSAL)) void fwd_bf16_p
         // K(t+3) and V(t+1), which step t+1 reads, have landed.
         GONN_VMCNT(0);
         __syncthreads();
-        if constexpr (MASK && TAIL == 0) MaskRow::add(mreg, sA);
+        if constexpr (MASK && TAIL == 0) mask_add_lds(sA);
         if (__builtin_amdgcn_ballot_w64(alpha != 1.f))
             for (int dt = 0; dt < NDT; dt++) oacc[dt] *= alpha;
     };
