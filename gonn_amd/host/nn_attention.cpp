@@ -236,14 +236,23 @@ Tensor MultiHeadAttention::fusedGeneral(const Tensor& q, const Tensor& k, const 
     return OutProj.Forward(ctx);
 }
 
-// A query row whose best in-window additive mask value is at or below this
-// has no unblocked key. GoNN then returns a uniform average (every score is
-// absorbed into the -1e30 constants, nn/attention.go:185-196, :261-272); the
-// fused core does not define such rows and refuses them.
+// A query row whose best in-window additive mask value is at or below
+// kNoKeyLevel has no unblocked key. GoNN adds its masks as fp64 -1e30
+// constants (nn/attention.go:185-196, :261-272), which absorb the scores, so
+// such a row is a uniform average over the keys whose summed mask is the
+// row's maximum, future keys included (their causal -1e30). The fused core
+// reproduces it when that maximum is at or below kUniformLevel: the scores
+// vanish next to it in fp32 as in fp64, so the row is passed unshifted. A
+// blocked row between the two levels (fp64 keeps part of the score there,
+// fp32 does not) or of -inf keys only (NaN in GoNN) is refused.
 constexpr double kNoKeyLevel = -1e15;
+constexpr double kUniformLevel = -1e25;
 static const char* kNoKeyMsg =
     "nn: a query row has no unblocked key (every key it may attend is padded or masked); "
     "the fused core does not define such rows";
+static const char* kBlockedMsg =
+    "nn: a query row has no unblocked key and its best mask value lies between -1e25 and "
+    "-1e15 (or is -inf); the fused core does not define such rows";
 
 // keyPaddingMaskAdd's shape check (nn/attention.go:262-264) and the mask's
 // form: kvLen (B entries) when every row's padded keys (nonzero = ignore) are
@@ -299,14 +308,20 @@ static std::vector<int> kv_len_from_mask(const Tensor& keyPad, int B, int Tk) {
 // padded keys); any other is added as keyPaddingMaskAdd's -1e30. Each row of
 // the additive mask is shifted by its maximum over the keys the row attends
 // (causal window, kvLen): softmax is unchanged, and the fp32 scores the
-// kernels form keep full precision under a large common offset. A row with
-// no unblocked key throws.
+// kernels form keep full precision under a large common offset.
+//
+// When some row has no unblocked key, the call takes the whole-row form: the
+// causal mask and the key padding become GoNN's -1e30 terms, added in its
+// order (causal, attn mask, key padding) over every key; `causal` is cleared
+// and kvLen emptied; rows with an unblocked key are shifted by their maximum
+// and blocked rows stay as they are (kUniformLevel). Blocked rows the core
+// cannot reproduce throw.
 static void core_masks(const Tensor& keyPad, const Tensor& attnMask, int B, int H, int Tq,
-                       int Tk, bool causal, std::vector<int>& kvLen, Tensor& mask) {
+                       int Tk, bool& causal, std::vector<int>& kvLen, Tensor& mask) {
     std::vector<double> kpAdd;
     key_padding(keyPad, B, Tk, kvLen, kpAdd);
     mask = Tensor{};
-    if (attnMask.Data.empty() && kpAdd.empty()) return;
+    if (attnMask.Data.empty() && kpAdd.empty()) return;  // a suffix kvLen leaves every row a key
     int Bu = 1, Hu = 1;
     if (!attnMask.Data.empty()) {
         const auto st = maskStrides(attnMask.Shape, B, H, Tq, Tk);  // expandAttnMask's check
@@ -314,15 +329,17 @@ static void core_masks(const Tensor& keyPad, const Tensor& attnMask, int B, int 
         Hu = st[1] ? H : 1;
     }
     const size_t QK = (size_t)Tq * Tk;
+    auto user = [&](int b, int h, int i) {
+        return attnMask.Data.empty()
+                   ? nullptr
+                   : &attnMask.Data[((size_t)(b % Bu) * Hu + h) * QK + (size_t)i * Tk];
+    };
     std::vector<double> full((size_t)B * Hu * QK);
-    bool shifted = !kpAdd.empty();
-    for (int b = 0; b < B; b++)
-        for (int h = 0; h < Hu; h++)
+    bool shifted = !kpAdd.empty(), blocked = false;
+    for (int b = 0; b < B && !blocked; b++)
+        for (int h = 0; h < Hu && !blocked; h++)
             for (int i = 0; i < Tq; i++) {
-                const double* src =
-                    attnMask.Data.empty()
-                        ? nullptr
-                        : &attnMask.Data[((size_t)(b % Bu) * Hu + h) * QK + (size_t)i * Tk];
+                const double* src = user(b, h, i);
                 double* dst = &full[((size_t)b * Hu + h) * QK + (size_t)i * Tk];
                 for (int j = 0; j < Tk; j++)
                     dst[j] = (src ? src[j] : 0.0) + (kpAdd.empty() ? 0.0 : kpAdd[(size_t)b * Tk + j]);
@@ -330,16 +347,48 @@ static void core_masks(const Tensor& keyPad, const Tensor& attnMask, int B, int 
                 if (causal && i + 1 < n) n = i + 1;
                 double mx = -INFINITY;
                 for (int j = 0; j < n; j++) mx = std::max(mx, dst[j]);
-                if (!(mx > kNoKeyLevel)) throw std::invalid_argument(kNoKeyMsg);
+                if (!(mx > kNoKeyLevel)) {
+                    blocked = true;
+                    break;
+                }
                 if (mx != 0) {
                     shifted = true;
                     for (int j = 0; j < Tk; j++) dst[j] -= mx;
                 }
             }
-    if (!shifted) {
-        mask = attnMask;
+    if (!blocked) {
+        if (!shifted) {
+            mask = attnMask;
+            return;
+        }
+        mask = Hu == 1 ? Tensor::New(std::move(full), {B, Tq, Tk})
+                       : Tensor::New(std::move(full), {B, H, Tq, Tk});
         return;
     }
+    // whole-row form, in GoNN's order of additions
+    for (int b = 0; b < B; b++)
+        for (int h = 0; h < Hu; h++)
+            for (int i = 0; i < Tq; i++) {
+                const double* src = user(b, h, i);
+                double* dst = &full[((size_t)b * Hu + h) * QK + (size_t)i * Tk];
+                for (int j = 0; j < Tk; j++) {
+                    double x = 0.0;
+                    if (causal) x = x + (j > i ? -1e30 : 0.0);
+                    x = x + (src ? src[j] : 0.0);
+                    if (!kvLen.empty()) x = x + (j >= kvLen[b] ? -1e30 : 0.0);
+                    if (!kpAdd.empty()) x = x + kpAdd[(size_t)b * Tk + j];
+                    dst[j] = x;
+                }
+                double mx = -INFINITY;
+                for (int j = 0; j < Tk; j++) mx = std::max(mx, dst[j]);
+                if (mx > kNoKeyLevel) {
+                    for (int j = 0; j < Tk; j++) dst[j] -= mx;
+                } else if (!(mx <= kUniformLevel && mx > -INFINITY)) {
+                    throw std::invalid_argument(kBlockedMsg);
+                }
+            }
+    causal = false;
+    kvLen.clear();
     mask = Hu == 1 ? Tensor::New(std::move(full), {B, Tq, Tk})
                    : Tensor::New(std::move(full), {B, H, Tq, Tk});
 }

@@ -112,12 +112,21 @@ class Linear:
 
 
 # A row of the core whose best in-window additive mask value is at or below
-# this has no unblocked key. The reference then returns a uniform average
-# (every score absorbed into the -1e30 constants, nn/attention.go:185-196,
-# :261-272), which the fused core does not define; such calls are refused.
+# NO_KEY_LEVEL has no unblocked key. GoNN adds its masks as -1e30 constants
+# (nn/attention.go:185-196, :261-272) in fp64, where they absorb the scores,
+# so such a row's softmax depends on the mask sums alone: a uniform average
+# over the keys whose summed mask is the row's maximum. Future keys count too,
+# with their causal -1e30. The fused core reproduces it when the row's maximum
+# is at or below UNIFORM_LEVEL: the scores vanish next to it in fp32 as in
+# fp64, so the row is passed unshifted. A blocked row whose maximum lies
+# between the two levels (fp64 keeps part of the score there, fp32 does not)
+# is refused, and so is a row whose every key is -inf (NaN in the reference).
 NO_KEY_LEVEL = -1e15
+UNIFORM_LEVEL = -1e25
 _NO_KEY_MSG = ("nn: a query row has no unblocked key (every key it may attend is padded or "
                "masked); the fused core does not define such rows")
+_BLOCKED_MSG = ("nn: a query row has no unblocked key and its best mask value lies between "
+                "-1e25 and -1e15 (or is -inf); the fused core does not define such rows")
 
 
 def _kv_len_from_mask(key_padding_mask, B: int, Tk: int):
@@ -153,39 +162,59 @@ def _key_padding(key_padding_mask, B: int, Tk: int):
 
 def _core_masks(key_padding_mask, attn_mask, B: int, H: int, Tq: int, Tk: int, causal: bool):
     """ForwardMasked's masks (nn/attention.go:318-330) in the form the fused
-    core takes them: (kv_len or None, additive mask or None).
+    core takes them: (kv_len or None, additive mask or None, causal).
 
     A suffix-form padding mask becomes kv_len (the kernels skip the padded
     keys); any other is added as keyPaddingMaskAdd's 0 / -1e30 values. Each
     row of the additive mask is shifted by its maximum over the keys the row
     attends (causal window, kv_len): softmax is unchanged, and the fp32
     scores the kernels form keep full precision under a large common offset.
-    A row with no unblocked key (that maximum at or below NO_KEY_LEVEL, or no
-    key at all) raises ValueError."""
+
+    When some row has no unblocked key (that maximum at or below
+    NO_KEY_LEVEL), the call takes the whole-row form instead: the causal mask
+    and the key padding become the reference's -1e30 terms, added in its
+    order (causal, attn_mask, key padding) over every key, the call runs
+    non-causal and without kv_len, each row with an unblocked key is shifted
+    by its maximum, and each blocked row stays as it is (see UNIFORM_LEVEL).
+    Blocked rows the core cannot reproduce raise ValueError."""
     kv_len, kp_add = _key_padding(key_padding_mask, B, Tk)
     if attn_mask is None and kp_add is None:
-        return kv_len, None
+        return kv_len, None, causal  # a suffix-form kv_len leaves every row a key
     if attn_mask is not None:
         sb, sh = hip.mask_strides(np.shape(attn_mask), B, H, Tq, Tk)  # expandAttnMask's check
         Hu = H if sh else 1
-        full = np.asarray(attn_mask, dtype=np.float64).reshape(B if sb else 1, Hu, Tq, Tk)
-        full = np.broadcast_to(full, (B, Hu, Tq, Tk))
+        user = np.asarray(attn_mask, dtype=np.float64).reshape(B if sb else 1, Hu, Tq, Tk)
+        user = np.broadcast_to(user, (B, Hu, Tq, Tk))
     else:
-        full = np.zeros((B, 1, Tq, Tk))
-    if kp_add is not None:
-        full = full + kp_add[:, None, None, :]
+        Hu, user = 1, np.zeros((B, 1, Tq, Tk))
+    full = user if kp_add is None else user + kp_add[:, None, None, :]
     win = np.ones((B, 1, Tq, Tk), dtype=bool)
     if kv_len is not None:
         win &= (np.arange(Tk)[None, :] < kv_len[:, None])[:, None, None, :]
     if causal:
         win &= (np.arange(Tk)[None, :] <= np.arange(Tq)[:, None])[None, None]
     wmax = np.where(win, full, -np.inf).max(axis=-1)
-    if not (wmax > NO_KEY_LEVEL).all():
-        raise ValueError(_NO_KEY_MSG)
-    if kp_add is None and not wmax.any():
-        return kv_len, attn_mask
-    out = np.ascontiguousarray(full - wmax[..., None])
-    return kv_len, (out[:, 0] if out.shape[1] == 1 else out)
+    if (wmax > NO_KEY_LEVEL).all():
+        if kp_add is None and not wmax.any():
+            return kv_len, attn_mask, causal
+        out = np.ascontiguousarray(full - wmax[..., None])
+        return kv_len, (out[:, 0] if out.shape[1] == 1 else out), causal
+    # whole-row form, in the reference's order of additions
+    whole = np.zeros((B, Hu, Tq, Tk))
+    if causal:
+        whole = whole + np.where(np.arange(Tk)[None, :] > np.arange(Tq)[:, None], -1e30, 0.0)
+    whole = whole + user
+    pad = kp_add
+    if kv_len is not None:
+        pad = np.where(np.arange(Tk)[None, :] >= kv_len[:, None], -1e30, 0.0)
+    if pad is not None:
+        whole = whole + pad[:, None, None, :]
+    rmax = whole.max(axis=-1)
+    blocked = ~(rmax > NO_KEY_LEVEL)
+    if not (np.isfinite(rmax[blocked]).all() and (rmax[blocked] <= UNIFORM_LEVEL).all()):
+        raise ValueError(_BLOCKED_MSG)
+    out = np.ascontiguousarray(whole - np.where(blocked, 0.0, rmax)[..., None])
+    return None, (out[:, 0] if Hu == 1 else out), False
 
 
 class MultiHeadAttention:
@@ -286,8 +315,8 @@ class MultiHeadAttention:
         self._check(q, k, v)
         if not fused_attn_available():
             raise RuntimeError("nn: fused attention requires the HIP library and a gfx950 device")
-        kv_len, attn_mask = _core_masks(key_padding_mask, attn_mask, q.shape[0], self.NumHeads,
-                                        q.shape[1], k.shape[1], causal)
+        kv_len, attn_mask, causal = _core_masks(key_padding_mask, attn_mask, q.shape[0],
+                                                self.NumHeads, q.shape[1], k.shape[1], causal)
         return self._fused(q, k, v, causal, kv_len, attn_mask)
 
     # ---- device-resident forward (new: weights and intermediates in HBM) ----

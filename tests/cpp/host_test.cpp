@@ -712,16 +712,31 @@ static void test_gpu() {
         CHECK(close(m.ForwardMasked(q, mem, mem, causal, holes).Data,
                     oracle_mha(m, q, mem, mem, causal, {}, kpAdd), 1e-4, 0.0,
                     ("ForwardMasked holes" + tag).c_str()), "ForwardMasked holes%s", tag.c_str());
-        // a row with no unblocked key is refused
+        // rows with no unblocked key: GoNN's -1e30 terms absorb their
+        // scores (a uniform average over the keys of the row's maximum
+        // summed mask, future keys included); the whole-row form
         Tensor full = pad;
         for (int t = 0; t < Tk; t++) full.Data[(size_t)1 * Tk + t] = 1.0;
-        CHECK(throws_invalid([&] { m.ForwardMasked(q, mem, mem, causal, full); }),
-              "fully padded row rejected");
-        if (causal) {  // row 0 attends key 0 only: blocking it leaves no key
+        CHECK(close(m.ForwardMasked(q, mem, mem, causal, full).Data,
+                    oracle_mha(m, q, mem, mem, causal, {Tk, 0, 7}), 1e-4, 0.0,
+                    ("ForwardMasked fully padded" + tag).c_str()),
+              "ForwardMasked fully padded%s", tag.c_str());
+        {  // row 0 attends key 0 only under causal: blocking it leaves no key
             Tensor am = Tensor::Zeros({Tq, Tk});
             am.Data[0] = -1e30;
-            CHECK(throws_invalid([&] { m.ForwardMasked(q, mem, mem, true, Tensor{}, am); }),
-                  "causal row with its window blocked rejected");
+            for (int t = 0; t < Tk; t++) am.Data[(size_t)9 * Tk + t] = -1e30;  // row 9 blocked
+            std::vector<double> amB((size_t)B * Tq * Tk);
+            for (int b = 0; b < B; b++)
+                std::copy(am.Data.begin(), am.Data.end(), amB.begin() + (size_t)b * Tq * Tk);
+            CHECK(close(m.ForwardMasked(q, mem, mem, causal, Tensor{}, am).Data,
+                        oracle_mha(m, q, mem, mem, causal, {}, amB), 1e-4, 0.0,
+                        ("ForwardMasked blocked rows" + tag).c_str()),
+                  "ForwardMasked blocked rows%s", tag.c_str());
+            // refused: a blocked row whose best value keeps part of the score in fp64
+            Tensor mid = Tensor::Zeros({Tq, Tk});
+            for (int t = 0; t < Tk; t++) mid.Data[(size_t)4 * Tk + t] = -1e20;
+            CHECK(throws_invalid([&] { m.ForwardMasked(q, mem, mem, causal, Tensor{}, mid); }),
+                  "blocked row between the levels rejected");
         }
     }
     // Incremental decoding: ForwardIncremental over a KV cache in two chunks

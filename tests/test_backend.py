@@ -219,29 +219,28 @@ def test_key_padding_mask_to_kv_len():
 def test_core_masks_forms():
     """ForwardMasked's masks as the fused core takes them (nn._core_masks):
     suffix padding -> kv_len; holes -> keyPaddingMaskAdd's -1e30 added to the
-    additive mask; rows shifted by their in-window maximum; rows with no
-    unblocked key refused. Checked against a direct restatement on small
-    cases, and by softmax invariance: the shifted mask gives the same
-    probabilities as GoNN's scores + mask in fp64."""
+    additive mask; rows shifted by their in-window maximum. Checked against a
+    direct restatement on small cases, and by softmax invariance: the shifted
+    mask gives the same probabilities as GoNN's scores + mask in fp64."""
     from gonn_amd import nn
     B, H, Tq, Tk = 2, 3, 5, 7
     r = np.random.default_rng(3)
     pad = np.zeros((B, Tk))
     pad[1, 5:] = 1
-    kv, am = nn._core_masks(pad, None, B, H, Tq, Tk, False)
-    assert list(kv) == [7, 5] and am is None
+    kv, am, c = nn._core_masks(pad, None, B, H, Tq, Tk, False)
+    assert list(kv) == [7, 5] and am is None and c is False
     # a zero-max mask passes through unchanged (no copy)
     z = np.zeros((Tq, Tk))
     z[:, 3] = -1e30
-    kv, am = nn._core_masks(None, z, B, H, Tq, Tk, False)
-    assert kv is None and am is z
+    kv, am, c = nn._core_masks(None, z, B, H, Tq, Tk, True)
+    assert kv is None and am is z and c is True
     # holes + a (B*H, Tq, Tk) mask with a large common offset, causal
     holes = pad.copy()
     holes[0, 2] = 1
     um = r.standard_normal((B * H, Tq, Tk)) - 1e4
     scores = r.standard_normal((B, H, Tq, Tk))
-    kv, am = nn._core_masks(holes, um, B, H, Tq, Tk, True)
-    assert kv is None and am.shape == (B, H, Tq, Tk)
+    kv, am, c = nn._core_masks(holes, um, B, H, Tq, Tk, True)
+    assert kv is None and am.shape == (B, H, Tq, Tk) and c is True
     win = np.arange(Tk)[None, :] <= np.arange(Tq)[:, None]
 
     def softmax(x):
@@ -255,23 +254,85 @@ def test_core_masks_forms():
     assert np.all(inwin == 0.0)
     # suffix padding + a (Tq, Tk) mask: the window max depends on kv_len
     tm = r.standard_normal((Tq, Tk)) * 3
-    kv, am = nn._core_masks(pad, tm, B, H, Tq, Tk, False)
+    kv, am, c = nn._core_masks(pad, tm, B, H, Tq, Tk, False)
     assert list(kv) == [7, 5] and am.shape == (B, Tq, Tk)
     np.testing.assert_array_equal(am[0], tm - tm.max(-1, keepdims=True))
     np.testing.assert_array_equal(am[1], tm - tm[:, :5].max(-1, keepdims=True))
-    # rows with no unblocked key: a fully padded sequence, and a causal row 0
-    # whose only key (key 0) the mask blocks
-    full = pad.copy()
-    full[0] = 1
-    with pytest.raises(ValueError, match="no unblocked key"):
-        nn._core_masks(full, None, B, H, Tq, Tk, False)
     b0 = np.zeros((Tq, Tk))
     b0[0, 0] = -1e30
-    nn._core_masks(None, b0, B, H, Tq, Tk, False)  # non-causal: keys 1.. remain
-    with pytest.raises(ValueError, match="no unblocked key"):
-        nn._core_masks(None, b0, B, H, Tq, Tk, True)
+    kv, am, c = nn._core_masks(None, b0, B, H, Tq, Tk, False)  # non-causal: keys 1.. remain
+    assert am is b0 and c is False
     with pytest.raises(ValueError, match="attn mask shape"):
         nn._core_masks(None, np.zeros((Tq, Tk + 1)), B, H, Tq, Tk, False)
+
+
+def test_core_masks_blocked_rows():
+    """Rows with no unblocked key (nn._core_masks' whole-row form): GoNN adds
+    causalMaskAdd, the attn mask and keyPaddingMaskAdd as fp64 -1e30 terms
+    (nn/attention.go:185-196, :261-272, :321-330), which absorb the scores,
+    so a blocked row is a uniform average over the keys whose summed mask is
+    the row's maximum, future keys included. The whole-row form must give
+    GoNN's probabilities (scores + its masks in fp64, max-subtracted softmax)
+    for every row, in the reference's order of additions; rows it cannot
+    reproduce are refused."""
+    from gonn_amd import nn
+    B, H, Tq, Tk = 2, 2, 6, 6
+    r = np.random.default_rng(4)
+    scores = r.standard_normal((B, H, Tq, Tk)) * 3
+
+    def gonn_probs(causal, attn, keypad):
+        x = scores.copy()
+        if causal:
+            x = x + np.where(np.arange(Tk)[None, :] > np.arange(Tq)[:, None], -1e30, 0.0)
+        if attn is not None:
+            x = x + np.broadcast_to(attn, x.shape) if attn.ndim == 2 else \
+                x + attn.reshape(B, -1, Tq, Tk)
+        if keypad is not None:
+            x = x + np.where(keypad != 0, -1e30, 0.0)[:, None, None, :]
+        e = np.exp(x - x.max(-1, keepdims=True))
+        return e / e.sum(-1, keepdims=True)
+
+    def probs(am):
+        x = scores + (am[:, None] if am.ndim == 3 else am)
+        e = np.exp(x - x.max(-1, keepdims=True))
+        return e / e.sum(-1, keepdims=True)
+
+    cases = []
+    # a fully padded sequence (suffix form with no key left), non-causal
+    full = np.zeros((B, Tk))
+    full[0] = 1
+    full[1, 4:] = 1
+    cases.append((False, None, full))
+    # causal with padded leading keys: rows 0-1 keep none of theirs; their
+    # maximum class holds the padded keys up to the row and the unpadded
+    # future keys (each one -1e30), not the padded future keys (-2e30)
+    lead = np.zeros((B, Tk))
+    lead[:, :2] = 1
+    cases.append((True, None, lead))
+    # causal, an attn mask blocking row 0's only key, plus holes
+    b0 = r.standard_normal((Tq, Tk))
+    b0[0, 0] = -1e30
+    holes = np.zeros((B, Tk))
+    holes[1, 3] = 1
+    cases.append((True, b0, holes))
+    for causal, attn, keypad in cases:
+        kv, am, c = nn._core_masks(keypad, attn, B, H, Tq, Tk, causal)
+        assert kv is None and c is False
+        ref = gonn_probs(causal, attn, keypad)
+        np.testing.assert_allclose(probs(am), ref, rtol=1e-12, atol=1e-300)
+    # the second case's row 0 of batch 0: padded key 0 and unpadded keys 2..5
+    ref = gonn_probs(True, None, lead)[0, 0, 0]
+    np.testing.assert_allclose(ref, [0.2, 0, 0.2, 0.2, 0.2, 0.2], atol=1e-15)
+    # refused: a blocked row whose best value keeps part of the score in fp64
+    mid = np.zeros((Tq, Tk))
+    mid[0] = -1e20
+    with pytest.raises(ValueError, match="between"):
+        nn._core_masks(None, mid, B, H, Tq, Tk, False)
+    # refused: a row of -inf (NaN in the reference)
+    ninf = np.zeros((Tq, Tk))
+    ninf[2] = -np.inf
+    with pytest.raises(ValueError, match="between"):
+        nn._core_masks(None, ninf, B, H, Tq, Tk, False)
 
 
 def test_resident_layer_and_cache_need_a_device():

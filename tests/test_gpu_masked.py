@@ -116,11 +116,34 @@ def test_mha_forward_masked_and_cross_attention(causal):
     got = mha.forward_masked(x, x, x, causal=causal, key_padding_mask=holes)
     ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, key_pad=holes)
     assert_close(got, ref, "fp32", f"forward_masked holes causal={causal}")
-    # a sequence with every key padded: GoNN's uniform average is not defined here
+    # rows with no unblocked key: GoNN's -1e30 terms absorb their scores,
+    # so each is a uniform average over the keys whose summed mask is the
+    # row's maximum (future keys included, with their causal -1e30); the
+    # mirror runs them in the whole-row form. A sequence with every key
+    # padded; padded leading keys (under causal, the first rows keep none of
+    # their own); an attn mask blocking row 0's only key.
     full = pad.copy()
     full[1] = 1
-    with pytest.raises(ValueError, match="no unblocked key"):
-        mha.forward_masked(x, x, x, causal=causal, key_padding_mask=full)
+    got = mha.forward_masked(x, x, x, causal=causal, key_padding_mask=full)
+    ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, key_pad=full)
+    assert_close(got, ref, "fp32", f"forward_masked fully padded causal={causal}")
+    lead = np.zeros((B, Tk))
+    lead[:, :3] = 1
+    lead[2, 60:] = 1
+    got = mha.forward_masked(x, x, x, causal=causal, key_padding_mask=lead)
+    ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, key_pad=lead)
+    assert_close(got, ref, "fp32", f"forward_masked padded leading keys causal={causal}")
+    am = randn((Tk, Tk), 853).astype(np.float64)
+    am[0, 0] = -1e30
+    am[5, :] = -1e30
+    got = mha.forward_masked(x, x, x, causal=causal, attn_mask=am, key_padding_mask=pad)
+    ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, key_pad=pad, attn_mask=am)
+    assert_close(got, ref, "fp32", f"forward_masked blocked rows + attn mask causal={causal}")
+    # refused: a blocked row whose best value keeps part of the score in fp64
+    mid = np.zeros((Tk, Tk))
+    mid[4, :] = -1e20
+    with pytest.raises(ValueError, match="between"):
+        mha.forward_masked(x, x, x, causal=causal, attn_mask=mid)
     with pytest.raises(ValueError):
         mha.forward_masked(x, x, x, dropout=0.1)
     with pytest.raises(ValueError):
@@ -315,6 +338,49 @@ def test_forward_masked_large_offset_mask(mode):
             got = mha.forward_masked(x, x, x, causal=causal, attn_mask=m)
             ref = oracle.mha_fwd(x, x, x, p, H, causal=causal, attn_mask=m)
             assert_close(got, ref, mode, f"large-offset mask causal={causal}")
+    finally:
+        hip.SetAttnMode(prev)
+
+
+@pytest.mark.parametrize("mode", ["fp32", "bf16", "f64"])
+def test_forward_masked_blocked_rows_modes(mode):
+    """forward_masked rows with no unblocked key, in each mode of the f64
+    entries, cross-attention (Tq != Tk) included: GoNN's -1e30 terms absorb
+    such a row's scores (a uniform average over the keys of the row's
+    maximum summed mask, future keys included); the mirror passes them in
+    the whole-row form, where the kernels' fp32 (or fp64) sums absorb the
+    scores the same way. Against the oracle (fp64, GoNN's additions) at the
+    mode's bar (f64: 1e-9, the reference's gate)."""
+    from gonn_amd import hip, nn
+    E, H, B, Tq, Tk = 256, 4, 3, 72, 136
+    p = _params(E, 1500)
+    mha = nn.MultiHeadAttention(E, H, p["Wq"], p["bq"], p["Wk"], p["bk"], p["Wv"], p["bv"],
+                                p["Wo"], p["bo"])
+    x = randn((B, Tk, E), 1501).astype(np.float64)
+    q = randn((B, Tq, E), 1502).astype(np.float64)
+    pad = np.zeros((B, Tk))
+    pad[0, :5] = 1      # padded leading keys
+    pad[1] = 1          # every key padded
+    pad[2, 100:] = 1    # a suffix
+    am = randn((B, Tk, Tk), 1503).astype(np.float64)
+    am[:, 7, :] = -1e30
+    am[2, 0, 0] = -1e30
+    prev = hip.AttnMode()
+    hip.SetAttnMode(mode)
+    try:
+        for causal in (False, True):
+            for (qq, kk, tag) in ((x, x, "self"), (q, x, "cross")):
+                say(f"[masked] blocked rows mode={mode} causal={causal} {tag}")
+                mk = am[:, :qq.shape[1], :kk.shape[1]]
+                got = mha.forward_masked(qq, kk, kk, causal=causal, key_padding_mask=pad,
+                                         attn_mask=np.ascontiguousarray(mk))
+                ref = oracle.mha_fwd(qq, kk, kk, p, H, causal=causal, key_pad=pad, attn_mask=mk)
+                if mode == "f64":
+                    err = float(np.abs(got - ref).max())
+                    say(f"[blocked rows f64] max_abs={err:.3e}")
+                    assert err <= 1e-9, (tag, causal, err)
+                else:
+                    assert_close(got, ref, mode, f"blocked rows {tag} causal={causal}")
     finally:
         hip.SetAttnMode(prev)
 
