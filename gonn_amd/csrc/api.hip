@@ -246,29 +246,72 @@ struct BwdLayout {
 
 // The bf16 backward stores dS (bf16 blocks of 128 keys x 64 queries; for a
 // causal call only the blocks a key block reaches, ds_block_base) and
-// computes dQ from it in one GEMM when that buffer is at most kDsMaxBytes
-// and one slice of it fits the kernels' 32-bit buffer offsets; otherwise (and
-// with GONN_HIP_BWD_DQ=recompute) the dQ kernel forms S and dP again. The
-// choice depends on the shape and the environment. A call reads the
-// variable once and sizes, checks and lays out its workspace for that one
-// choice, so a workspace sized by gonn_hip_attn_workspace_bytes under the
-// same setting fits, and one sized under the other setting is either big
-// enough or refused with GONN_E_WORKSPACE before any work is queued.
+// computes dQ from it in one GEMM. The stored dS of a call is capped by a
+// byte budget: a call whose whole dS exceeds it runs its key blocks in
+// chunks of consecutive blocks whose dS fits, each chunk's dK/dV storing its
+// dS and the dQ kernel adding that chunk's keys to dQ (BwdParams::kb0, nkb,
+// dq_mode), so the workspace stays within the budget. Each further chunk
+// costs a dQ round trip and a shorter dK/dV grid (one workgroup per CU, so
+// its tail idles CUs): measured at B=1 H=16 S=32768 causal, two chunks ran
+// 13.5 ms, five 15.2 ms, and forming S and dP again in the dQ kernel 14.4
+// ms. So by default (budget kDsMaxBytes) a call takes at most kMaxAutoChunks
+// chunks and otherwise the recompute path, whose memory is O(S). A budget
+// given in GONN_HIP_BWD_DS_MB (MB) always takes the chunks: the caller
+// asked for that bound. GONN_HIP_BWD_DQ=recompute takes the recompute path,
+// as does the rare shape where one key block of one slice exceeds the
+// kernels' 32-bit buffer offsets. A call reads the variables once and sizes,
+// checks and lays out its workspace for that one plan, so a workspace sized
+// by gonn_hip_attn_workspace_bytes under the same settings fits, and one
+// sized under others is either big enough or refused with GONN_E_WORKSPACE
+// before any work is queued.
 constexpr double kDsMaxBytes = 16.0 * 1024 * 1024 * 1024;
-double ds_slice_bytes(int S, int Sk, int causal) {
-    const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
-    const int Skp = (int)round_up((size_t)Sk, gonn::kBwdPad);
-    return (double)gonn::ds_slice_blocks(Skp / 128, Sp / 64, causal) * gonn::kDsTileElems * 2;
+constexpr int kMaxAutoChunks = 2;
+struct DqPlan {
+    bool use_ds;
+    double budget;  // bytes of stored dS per call
+};
+// The key-block chunks of a dS-path call: consecutive 128-key blocks, as
+// many per chunk as keep BH x the chunk's blocks within the budget and one
+// slice's part within 32-bit offsets, at least one. f(kb0, nkb, first,
+// last) for each chunk in order; returns the most blocks one slice's part
+// of a chunk holds.
+template <typename F>
+long long ds_chunks(size_t BH, int S, int Sk, int causal, double budget, F f) {
+    const int nkb = (int)(round_up((size_t)Sk, gonn::kBwdPad) / 128);
+    const int nqt = (int)(round_up((size_t)S, gonn::kBwdPad) / 64);
+    const double per = (double)gonn::kDsTileElems * 2;  // bytes per block
+    auto fits = [&](int kb0, int n) {
+        const double b = (double)gonn::ds_chunk_blocks(kb0, n, nqt, causal) * per;
+        return b * (double)BH <= budget && b < 2147483648.0;
+    };
+    long long most = 0;
+    for (int kb0 = 0; kb0 < nkb;) {
+        int n = 1;
+        while (kb0 + n < nkb && fits(kb0, n + 1)) n++;
+        most = std::max(most, gonn::ds_chunk_blocks(kb0, n, nqt, causal));
+        f(kb0, n, kb0 == 0, kb0 + n == nkb);
+        kb0 += n;
+    }
+    return most;
 }
-bool bwd_use_ds(int mode, size_t BH, int S, int Sk, int causal) {
-    if (mode != GONN_ATTN_BF16_MFMA) return false;
+DqPlan bwd_dq_plan(int mode, size_t BH, int S, int Sk, int causal) {
+    DqPlan q{false, kDsMaxBytes};
+    if (mode != GONN_ATTN_BF16_MFMA) return q;
     const char* e = std::getenv("GONN_HIP_BWD_DQ");
-    if (e && std::strcmp(e, "recompute") == 0) return false;
-    const double slice = ds_slice_bytes(S, Sk, causal);
-    return slice < 2147483648.0 && (double)BH * slice <= kDsMaxBytes;
+    if (e && std::strcmp(e, "recompute") == 0) return q;
+    const char* m = std::getenv("GONN_HIP_BWD_DS_MB");
+    const bool given = m && std::atof(m) > 0;
+    if (given) q.budget = std::atof(m) * 1024.0 * 1024.0;
+    // one key block of one slice: every query tile's block
+    const int nqt = (int)(round_up((size_t)S, gonn::kBwdPad) / 64);
+    if ((double)nqt * gonn::kDsTileElems * 2 >= 2147483648.0) return q;
+    int chunks = 0;
+    ds_chunks(BH, S, Sk, causal, q.budget, [&](int, int, bool, bool) { chunks++; });
+    q.use_ds = given || chunks <= kMaxAutoChunks;
+    return q;
 }
 
-BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal, bool use_ds) {
+BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal, const DqPlan& plan) {
     BwdLayout L{};
     const size_t Sp = round_up((size_t)S, gonn::kBwdPad), Skp = round_up((size_t)Sk, gonn::kBwdPad);
     size_t off = 0;
@@ -283,23 +326,25 @@ BwdLayout bwd_layout(int mode, size_t BH, int S, int Sk, int D, int causal, bool
             L.packed[i] = off;
             off = round_up(off + BH * (keyside[i] ? Skp : Sp) * D * 2, 256);
         }
-        if (use_ds) {
+        if (plan.use_ds) {
+            const long long most =
+                ds_chunks(BH, S, Sk, causal, plan.budget, [](int, int, bool, bool) {});
             L.ds = off;
-            off = round_up(off + BH * (size_t)ds_slice_bytes(S, Sk, causal), 256);
+            off = round_up(off + BH * (size_t)most * gonn::kDsTileElems * 2, 256);
         }
     }
     L.total = off;
     return L;
 }
 
-size_t bwd_ws(const gonn_attn_bwd_args* a, bool use_ds) {
+size_t bwd_ws(const gonn_attn_bwd_args* a, const DqPlan& plan) {
     return bwd_layout(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->D, a->causal,
-                      use_ds)
+                      plan)
                .total +
            256;
 }
-bool bwd_use_ds(const gonn_attn_bwd_args* a) {
-    return bwd_use_ds(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->causal);
+DqPlan bwd_dq_plan(const gonn_attn_bwd_args* a) {
+    return bwd_dq_plan(bwd_mode(a), (size_t)a->B * a->H, a->S, bwd_keys_of(a), a->causal);
 }
 
 // ---- helpers for the host shims ----------------------------------------
@@ -747,7 +792,7 @@ size_t gonn_hip_attn_workspace_bytes(int op, const void* args) {
         case GONN_OP_BWD: {
             const auto* a = (const gonn_attn_bwd_args*)args;
             if (a->B <= 0 || a->H <= 0 || a->S <= 0 || !head_dim_ok(a->D)) return 0;
-            return bwd_ws(a, bwd_use_ds(a));
+            return bwd_ws(a, bwd_dq_plan(a));
         }
         case GONN_OP_DECODE: {
             const auto* a = (const gonn_attn_decode_args*)args;
@@ -816,14 +861,15 @@ int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, vo
 
 int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, void* stream) {
     TRY(check_bwd(a));
-    const bool use_ds = bwd_use_ds(a);  // the dQ path of this call, read once
-    const size_t need = bwd_ws(a, use_ds);
+    const DqPlan plan = bwd_dq_plan(a);  // the dQ path of this call, read once
+    const bool use_ds = plan.use_ds;
+    const size_t need = bwd_ws(a, plan);
     if (!ws || ws_bytes < need) return GONN_E_WORKSPACE;
     hipStream_t s = (hipStream_t)stream;
     const int BH = a->B * a->H, S = a->S, D = a->D;
     const int Sp = (int)round_up((size_t)S, gonn::kBwdPad);
     const int mode = bwd_mode(a);
-    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, bwd_keys_of(a), D, a->causal, use_ds);
+    const BwdLayout L = bwd_layout(mode, (size_t)BH, S, bwd_keys_of(a), D, a->causal, plan);
     uint8_t* w = (uint8_t*)round_up((size_t)ws, 256);
     gonn::BwdParams p{};
     if (a->attn_mask.ptr) {
@@ -898,13 +944,36 @@ int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, vo
         p.v = a->v.ptr;
     }
     p.ds = use_ds ? (bf16*)(w + L.ds) : nullptr;
-    {
-        ProfScope ps("bwd_dkdv", s);
-        TRYH(gonn::launch_bwd_dkdv(p, mode, D, a->causal, s));
+    if (!use_ds) {
+        {
+            ProfScope ps("bwd_dkdv", s);
+            TRYH(gonn::launch_bwd_dkdv(p, mode, D, a->causal, s));
+        }
+        ProfScope ps("bwd_dq", s);
+        return herr(gonn::launch_bwd_dq(p, mode, D, a->causal, s));
     }
-    ProfScope ps("bwd_dq", s);
-    if (use_ds) return herr(gonn::launch_bwd_dq_ds(p, D, a->causal, s));
-    return herr(gonn::launch_bwd_dq(p, mode, D, a->causal, s));
+    // dS path: one chunk of every key block, or chunks within the budget.
+    int nchunks = 0;
+    ds_chunks((size_t)BH, S, p.Sk, a->causal, plan.budget,
+              [&](int, int, bool, bool) { nchunks++; });
+    hipError_t err = hipSuccess;
+    ds_chunks((size_t)BH, S, p.Sk, a->causal, plan.budget,
+              [&](int kb0, int nkb, bool first, bool last) {
+                  if (err != hipSuccess) return;
+                  if (nchunks > 1) {
+                      p.kb0 = kb0;
+                      p.nkb = nkb;
+                      p.dq_mode = first ? 1 : (last ? 3 : 2);
+                  }
+                  {
+                      ProfScope ps("bwd_dkdv", s);
+                      err = gonn::launch_bwd_dkdv(p, mode, D, a->causal, s);
+                  }
+                  if (err != hipSuccess) return;
+                  ProfScope ps("bwd_dq", s);
+                  err = gonn::launch_bwd_dq_ds(p, D, a->causal, s);
+              });
+    return herr(err);
 }
 
 int gonn_hip_attn_decode(const gonn_attn_decode_args* a, void* ws, size_t ws_bytes, void* stream) {

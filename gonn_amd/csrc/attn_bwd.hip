@@ -130,8 +130,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     const int g = lane >> 5, ln = lane & 31;
     const int S = p.S, Sp = p.Sp;  // query rows (Q, dO, L, D padded to Sp)
     const int Sk = p.Sk, Skp = p.Skp;  // key rows (K, V padded to Skp)
+    // This launch's key blocks: [kb0, kb0 + nkbc) (a chunk of the dS path, or all).
+    const int nkbc = p.nkb ? p.nkb : Skp / BN;
     int bh, kb;
-    map_block(blockIdx.x, Skp / BN, p.BH, false, bh, kb);
+    map_block(blockIdx.x, nkbc, p.BH, false, bh, kb);
+    kb += p.kb0;
     const int kw = kb * BN + wave * 32;  // first key of this wave
     const int kj = kw + ln;              // this lane's key
     // Keys >= Skv are padded: zero probability for every query, so their dK
@@ -246,9 +249,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     // one of its steps as one contiguous 8 KB. A padded key (kj >= Skv) stores zeros. Without
     // p.ds the resource has no range and every store is dropped.
     const bool store_ds = p.ds != nullptr;
-    // This key block's blocks (query tiles qb0 .. Sp/64 - 1).
-    const size_t ds0 = (size_t)(bh * ds_slice_blocks(Skp / BN, Sp / BM, CAUSAL) +
-                                ds_block_base(kb, Sp / BM, CAUSAL));
+    // This key block's blocks (query tiles qb0 .. Sp/64 - 1) in the chunk's
+    // stored dS.
+    const size_t ds0 = (size_t)(bh * ds_chunk_blocks(p.kb0, nkbc, Sp / BM, CAUSAL) +
+                                ds_block_base(kb, Sp / BM, CAUSAL) -
+                                ds_block_base(p.kb0, Sp / BM, CAUSAL));
     const brsrc dsrs = make_rsrc(store_ds ? p.ds + ds0 * kDsTileElems : p.ds,
                                  store_ds ? (uint32_t)(Sp / BM - qb0) * kDsTileElems * 2 : 0u);
     // Piece (key / 64) * 512 + chunk * 64 + key % 64 of a block, chunk 2e + g
@@ -812,7 +817,12 @@ static void launch_dkdv_bf16(const BwdParams& p, dim3 grid, hipStream_t s) {
 
 hipError_t launch_bwd_dkdv(const BwdParams& p, int mode, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0) return hipErrorInvalidValue;
-    const dim3 grid((p.Skp / 128) * p.BH);
+    // A key-block chunk (bf16 kernels only) lies inside the slice's blocks.
+    const int nkb = p.Skp / 128;
+    if (p.kb0 < 0 || p.nkb < 0 || p.kb0 + p.nkb > nkb || (p.nkb == 0 && p.kb0 != 0) ||
+        (mode != 1 && p.nkb != 0))
+        return hipErrorInvalidValue;
+    const dim3 grid((p.nkb ? p.nkb : nkb) * p.BH);
     if (mode == 1) {
         if (D == 64) {
             if (causal) launch_dkdv_bf16<64, true>(p, grid, s);

@@ -71,7 +71,13 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
     if (q0 >= S) return;  // padding rows only
     int kend = bwd_keys(p, bh);
     if (CAUSAL && q0 + BM < kend) kend = q0 + BM;
-    const int ntiles = (kend + BN - 1) / BN;
+    // Key tiles [t0, t1) of this launch: the chunk's key blocks (two 64-key
+    // tiles each) that hold keys this block attends.
+    const int nkbc = p.nkb ? p.nkb : Skp / 128;
+    const int t0 = 2 * p.kb0;
+    int t1 = (kend + BN - 1) / BN;
+    if (t1 > 2 * (p.kb0 + nkbc)) t1 = 2 * (p.kb0 + nkbc);
+    const int ntiles = t1 > t0 ? t1 - t0 : 0;
 
     // ---- tile loads (direct to LDS): instruction i of thread tid fills the
     // 16-byte position i*NT + tid of a Kt tile (slab_chunk gives its row and
@@ -93,7 +99,8 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
     // query-major order, which makes each workgroup's reads one stream but
     // puts concurrent workgroups 1 MB apart, measured 10% slower).
     const int nqt = Sp / 64, qt0 = q0 / 64;
-    const long long nblk = ds_slice_blocks(Skp / 128, nqt, CAUSAL);
+    const long long nblk = ds_chunk_blocks(p.kb0, nkbc, nqt, CAUSAL);
+    const long long cbase = ds_block_base(p.kb0, nqt, CAUSAL);  // the chunk's first block
     const brsrc srs = make_rsrc((const bf16*)p.ds + (size_t)(bh * nblk) * kDsTileElems,
                                 (uint32_t)(nblk * kDsTileElems * 2));
     const uint32_t kl = lds_addr(sK) + wave * 1024, sl = lds_addr(sS);
@@ -101,9 +108,10 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
     // waves skip this key tile) still issues, so every wave's vmcnt counts
     // match, but against a zero-size buffer: it moves no bytes.
     const brsrc nul = make_rsrc(p.ds, 0u);
-    auto load_tile = [&](int t0, int slot) {
-        const bool real = t0 < ntiles;
-        const int t = real ? t0 : ntiles - 1;
+    // Local tile u of this launch: key tile t0 + u.
+    auto load_tile = [&](int u, int slot) {
+        const bool real = u < ntiles;
+        const int t = t0 + (real ? u : ntiles - 1);
         const brsrc kr = real ? krs : nul;
         for (int i = 0; i < NKI; i++)
             dma16(kr, kl + slot * KTB + i * NT * 16, koff[i], (uint32_t)t * BN * 2);
@@ -113,7 +121,7 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
         // causal, or past Sp) is clamped into it: only a wave that skips this
         // key tile, or dQ rows past S (not written), read that column.
         const int kb = t / 2, f = ds_first_qt(kb, CAUSAL);
-        const long long kbase = ds_block_base(kb, nqt, CAUSAL);
+        const long long kbase = ds_block_base(kb, nqt, CAUSAL) - cbase;
         for (int i = 0; i < NSC / NW; i++) {
             const int c = NW * i + wave;
             int qt = qt0 + c / 8;
@@ -147,8 +155,20 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
         return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(sS3 + byte));
     };
 
+    // Lane (ln, g) holds query column 32 wave + ln of the block (stored
+    // order), i.e. query q0 + 16 (c / 16) + vt_pos(c % 16); dQ^T register r
+    // of d-tile dt is d = 32 dt + 8 (r / 4) + 4 g + r % 4.
+    const int c = 32 * wave + ln;
+    const int qi = q0 + (c & ~15) + vt_pos(c & 15);
+    float* dqr = p.dq + ((size_t)bh * S + (qi < S ? qi : S - 1)) * D;
     f32x16 acc[NDT];
     for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x16{};
+    if (p.dq_mode >= 2)  // continue the partial sum an earlier chunk stored
+        for (int dt = 0; dt < NDT; dt++)
+            for (int rq4 = 0; rq4 < 4; rq4++) {
+                const f32x4 a = *(const f32x4*)(dqr + dt * 32 + rq4 * 8 + g * 4);
+                for (int k = 0; k < 4; k++) acc[dt][rq4 * 4 + k] = a[k];
+            }
     // Tiles past the last are loads of no bytes into a slot no step reads,
     // so every step issues NLD loads and the wait for tile t+1 at the end of
     // step t is always "all but the newest PF-1 tiles".
@@ -156,9 +176,9 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
         for (int j = 0; j < PF; j++) load_tile(j, j);
         GONN_VMCNT((PF - 1) * NLD);
         __syncthreads();
-        for (int t = 0; t < ntiles; t++) {
-            const int cur = t % NSLOT;
-            load_tile(t + PF, (t + PF) % NSLOT);
+        for (int u = 0; u < ntiles; u++) {
+            const int t = t0 + u, cur = u % NSLOT;
+            load_tile(u + PF, (u + PF) % NSLOT);
             const char* kbase = (const char*)sK + cur * KTB;
             const uint32_t sbase = cur * STB + sb;
             // Causal: this wave's 32 queries lie in query tile qt0 + wave/2,
@@ -184,14 +204,9 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
         GONN_VMCNT(0);
     }
 
-    // Lane (ln, g) holds query column 32 wave + ln of the block (stored
-    // order), i.e. query q0 + 16 (c / 16) + vt_pos(c % 16); dQ^T register r
-    // of d-tile dt is d = 32 dt + 8 (r / 4) + 4 g + r % 4.
-    const int c = 32 * wave + ln;
-    const int qi = q0 + (c & ~15) + vt_pos(c & 15);
     if (qi < S) {
-        const float sc = p.dqs;
-        float* dqr = p.dq + ((size_t)bh * S + qi) * D;
+        // dqs on the whole sum (modes 0 and 3); a partial is stored as it is.
+        const float sc = (p.dq_mode == 1 || p.dq_mode == 2) ? 1.f : p.dqs;
         for (int dt = 0; dt < NDT; dt++)
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 f32x4 a;
@@ -203,6 +218,9 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
 
 hipError_t launch_bwd_dq_ds(const BwdParams& p, int D, int causal, hipStream_t s) {
     if (p.Sp % kBwdPad != 0 || p.Skp % kBwdPad != 0 || !p.ds || !p.kt)
+        return hipErrorInvalidValue;
+    if (p.kb0 < 0 || p.nkb < 0 || p.kb0 + p.nkb > p.Skp / 128 || (p.nkb == 0 && p.kb0 != 0) ||
+        p.dq_mode < 0 || p.dq_mode > 3 || (p.nkb == 0 && p.dq_mode != 0))
         return hipErrorInvalidValue;
     constexpr int BM = kDqDsWaves * 32, NT = kDqDsWaves * 64;
     const dim3 grid(((p.Sp + BM - 1) / BM) * p.BH);

@@ -100,6 +100,17 @@ struct BwdParams {
     // Optional additive mask, as in FwdParams.
     const float* mask;
     long long mask_sb, mask_sh;
+    // Key-block chunk of the dS-store path (nkb = 0: every key block, the
+    // whole call). The bf16 dK/dV kernel covers the 128-key blocks
+    // [kb0, kb0 + nkb) and stores their dS, each slice's chunk from block
+    // bh * ds_chunk_blocks(..) on, key block kb's part at ds_block_base(kb)
+    // - ds_block_base(kb0); bwd_dq_ds_kernel adds the chunk's key tiles to
+    // dQ. dq_mode: 0 the whole sum (start from 0, store dqs * sum); 1 a first
+    // partial (start from 0, store the sum); 2 a middle one (start from the
+    // stored partial, store the sum); 3 the last (start from the stored
+    // partial, store dqs * sum). The partials pass through memory as fp32
+    // unchanged, so a chunked call gives the same bits as a whole one.
+    int kb0, nkb, dq_mode;
 };
 
 // Exact fp64 attention (attn_f64.hip): fp64 (BH, rows, d) buffers.
@@ -251,6 +262,10 @@ __host__ __device__ inline long long ds_block_base(int kb, int nqt, int causal) 
 }
 __host__ __device__ inline long long ds_slice_blocks(int nkb, int nqt, int causal) {
     return ds_block_base(nkb, nqt, causal);
+}
+// Stored dS blocks of key blocks [kb0, kb0 + nkb) of one slice.
+__host__ __device__ inline long long ds_chunk_blocks(int kb0, int nkb, int nqt, int causal) {
+    return ds_block_base(kb0 + nkb, nqt, causal) - ds_block_base(kb0, nqt, causal);
 }
 
 // f64 <-> f32/bf16 conversion with optional head-dim padding:

@@ -246,6 +246,54 @@ def test_bwd_workspace_contract():
     assert lib.gonn_hip_attn_bwd(ctypes.byref(a), P, nb32, None) == GONN_E_WORKSPACE
 
 
+def test_bwd_ds_budget_workspace(monkeypatch):
+    """The bf16 backward's stored dS is capped by a byte budget
+    (GONN_HIP_BWD_DS_MB; 16 GiB by default): a call whose whole dS exceeds it
+    runs its 128-key blocks in chunks that fit, at least one block each, and
+    its workspace holds the largest chunk. B=2 H=2 S=4096 causal: key block kb
+    reaches query tiles 2 kb .. 63, 64 - 2 kb blocks of 128 keys x 64 queries
+    (16 KB) per slice, 1056 in all."""
+    lib = _lib.load()
+    B, H, S, D = 2, 2, 4096, 128
+    n = B * H * S * D * 4
+    f = lambda: Buf(P, n, GONN_F32)  # noqa: E731
+    a = BwdArgs(f(), f(), f(), f(), Buf(P, B * H * S * 4, GONN_F32), f(), f(), f(), f(), B, H,
+                S, D, 0.125, 1, 0, 1)
+    a.mode = 1
+    blk = 128 * 64 * 2 * B * H  # one block in every slice
+
+    def ws(mb=None, dq=None):
+        for k, v in (("GONN_HIP_BWD_DS_MB", mb), ("GONN_HIP_BWD_DQ", dq)):
+            if v is None:
+                monkeypatch.delenv(k, raising=False)
+            else:
+                monkeypatch.setenv(k, v)
+        return lib.gonn_hip_attn_workspace_bytes(GONN_OP_BWD, ctypes.byref(a))
+    full, recompute = ws(), ws(dq="recompute")
+    assert full - recompute == 1056 * blk
+    # 1 MB: one key block per chunk; key block 0 is the largest (64 blocks)
+    assert ws("1") - recompute == 64 * blk
+    # 20 MB: at most 320 blocks per slice; the chunks are key blocks 0-4
+    # (64 + ... + 56 = 300), 5-10 (294), 11-19 (42 + ... + 26 = 306), 20-31
+    # (156); the workspace holds the largest, 306
+    assert ws("20") - recompute == 306 * blk
+    assert ws("100") == full
+    # By default (a 16 GiB budget) a call takes at most two chunks, else the
+    # recompute path (O(S) memory): B=1 H=16 S=32768 causal stores 17.2 GB
+    # of dS (two chunks), S=65536 69 GB (five).
+    a.B, a.H, a.S = 1, 16, 32768
+    a.dq = a.dk = a.dv = a.q = a.k = a.v = a.o = a.dO = Buf(P, 16 * 32768 * 128 * 4, GONN_F32)
+    a.lse = Buf(P, 16 * 32768 * 4, GONN_F32)
+    assert ws() > ws(dq="recompute") + 8 * 2**30
+    a.S = 65536
+    a.dq = a.dk = a.dv = a.q = a.k = a.v = a.o = a.dO = Buf(P, 16 * 65536 * 128 * 4, GONN_F32)
+    a.lse = Buf(P, 16 * 65536 * 4, GONN_F32)
+    assert ws() == ws(dq="recompute")
+    assert ws("4096") > ws(dq="recompute")  # a given budget always chunks
+    monkeypatch.delenv("GONN_HIP_BWD_DS_MB", raising=False)
+    monkeypatch.delenv("GONN_HIP_BWD_DQ", raising=False)
+
+
 def test_no_device_fails_loudly():
     """Without a gfx950 device the reference-named entry points raise; there is
     no CPU fallback (like the reference's non-cuda stubs,

@@ -84,8 +84,8 @@ def test_bwd_scale_variants(mode):
 def test_bwd_bf16_dq_paths(D, causal, case, monkeypatch):
     """The bf16 backward's two dQ paths: dQ from the dS the dK/dV kernel
     stores (the default) and dQ with S and dP formed a second time
-    (GONN_HIP_BWD_DQ=recompute; also taken when the dS buffer would exceed
-    its cap). Both are held to the bf16 bar against the oracle, with key
+    (GONN_HIP_BWD_DQ=recompute). Both are held to the bf16 bar against the
+    oracle, with key
     padding and an additive mask; dK and dV come from the same kernel on
     either path and agree bitwise."""
     from gonn_amd import hip
@@ -148,6 +148,53 @@ def test_bwd_bf16_dq_paths_cross(shape, causal, monkeypatch):
             assert_close(x, ref, "bf16", f"{n} path={path}")
     assert np.array_equal(got["ds"][1], got["recompute"][1])
     assert np.array_equal(got["ds"][2], got["recompute"][2])
+
+
+@pytest.mark.parametrize("D", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("case", ["self", "kv_len", "mask", "Sq>Sk", "Sq<Sk"])
+def test_bwd_bf16_ds_chunks_bit_exact(D, causal, case, monkeypatch):
+    """The dS path in key-block chunks (GONN_HIP_BWD_DS_MB below the call's
+    dS): each chunk's dK/dV stores its dS and the dQ kernel adds the chunk's
+    keys to dQ, from the fp32 partial the previous chunk stored, with the
+    scale on the last chunk only. The MFMAs accumulate the same products in
+    the same order, so dQ, dK and dV equal the one-chunk call's bit for bit.
+    Budgets of 3 MB (two 128-key blocks a chunk at 1000 keys) and 0.25 MB
+    (one block a chunk, and causal chunks past every query holding no
+    blocks); the chunked result also against the oracle."""
+    from gonn_amd import hip
+    from tests.test_gpu_masked import _mask_of
+    B, H = 2, 3
+    Sq, Sk = {"Sq>Sk": (900, 400), "Sq<Sk": (400, 900)}.get(case, (1000, 1000))
+    lens = np.array([Sk, 3 * Sk // 5], dtype=np.int32) if case == "kv_len" else None
+    m = _mask_of("BHTqTk4", B, H, Sq, Sk, 78)[0] if case == "mask" else None
+    q, g = (randn((B * H, Sq, D), 4500 + D + i) for i in range(2))
+    k, v = (randn((B * H, Sk, D), 4510 + D + i) for i in range(2))
+    dev = [torch.from_numpy(x).cuda().reshape(B, H, x.shape[1], D) for x in (q, k, v, g)]
+    kl = torch.from_numpy(lens).cuda() if lens is not None else None
+    md = torch.from_numpy(m.astype(np.float32)).cuda() if m is not None else None
+    monkeypatch.delenv("GONN_HIP_BWD_DQ", raising=False)
+    o, l = hip.attn_fwd(*dev[:3], causal=causal, mode="bf16", kv_len=kl, attn_mask=md)
+    got = {}
+    for mb in (None, "3", "0.25"):
+        if mb is None:
+            monkeypatch.delenv("GONN_HIP_BWD_DS_MB", raising=False)
+        else:
+            monkeypatch.setenv("GONN_HIP_BWD_DS_MB", mb)
+        say(f"bwd dS chunks budget={mb} MB D={D} causal={causal} case={case}")
+        dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=causal, mode="bf16",
+                                  kv_len=kl, attn_mask=md)
+        torch.cuda.synchronize()
+        got[mb] = [x.reshape(B * H, -1, D).cpu().numpy() for x in (dq, dk, dv)]
+    monkeypatch.delenv("GONN_HIP_BWD_DS_MB", raising=False)
+    for mb in ("3", "0.25"):
+        for a, b, n in zip(got[mb], got[None], ("dQ", "dK", "dV")):
+            assert np.array_equal(a, b), (n, mb, float(np.abs(a - b).max()))
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal, kv_len=lens, H=H,
+                                          attn_mask=m)
+    live = np.ones(B * H, bool) if lens is None else np.repeat(lens > 0, H)
+    for x, ref, n in zip(got["0.25"], (rq, rk, rv), ("dQ", "dK", "dV")):
+        assert_close(x[live], ref[live], "bf16", f"{n} in chunks")
 
 
 @pytest.mark.parametrize("path", ["ds", "recompute"])
