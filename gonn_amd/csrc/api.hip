@@ -253,9 +253,11 @@ struct BwdLayout {
 // dq_mode), so the workspace stays within the budget. Each further chunk
 // costs a dQ round trip and a shorter dK/dV grid (one workgroup per CU, so
 // its tail idles CUs): measured at B=1 H=16 S=32768 causal, two chunks ran
-// 13.5 ms, five 15.2 ms, and forming S and dP again in the dQ kernel 14.4
-// ms. So by default (budget kDsMaxBytes) a call takes at most kMaxAutoChunks
-// chunks and otherwise the recompute path, whose memory is O(S). A budget
+// 13.2 ms, five 15.0 ms, and forming S and dP again in the dQ kernel 15.1
+// ms; at B=2 H=16 S=8192, three chunks 2.23 ms, the recompute path 2.21 ms.
+// Past two chunks the dS path is no faster than the recompute path, which
+// needs no dS memory, so by default (budget kDsMaxBytes) a call takes at
+// most kMaxAutoChunks chunks and otherwise the recompute path. A budget
 // given in GONN_HIP_BWD_DS_MB (MB) always takes the chunks: the caller
 // asked for that bound. GONN_HIP_BWD_DQ=recompute takes the recompute path,
 // as does the rare shape where one key block of one slice exceeds the

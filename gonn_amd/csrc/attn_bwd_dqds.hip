@@ -163,12 +163,19 @@ __global__ __launch_bounds__(kDqDsWaves * 64, 1) void bwd_dq_ds_kernel(BwdParams
     float* dqr = p.dq + ((size_t)bh * S + (qi < S ? qi : S - 1)) * D;
     f32x16 acc[NDT];
     for (int dt = 0; dt < NDT; dt++) acc[dt] = f32x16{};
-    if (p.dq_mode >= 2)  // continue the partial sum an earlier chunk stored
+    if (p.dq_mode >= 2) {  // continue the partial sum an earlier chunk stored
+#pragma unroll
         for (int dt = 0; dt < NDT; dt++)
+#pragma unroll
             for (int rq4 = 0; rq4 < 4; rq4++) {
                 const f32x4 a = *(const f32x4*)(dqr + dt * 32 + rq4 * 8 + g * 4);
                 for (int k = 0; k < 4; k++) acc[dt][rq4 * 4 + k] = a[k];
             }
+        // Landed here: otherwise the compiler guards the accumulators' first
+        // use inside the step loop with waits that also cover the tile loads
+        // in flight, and every step waits for its own prefetch (+22% at C5).
+        GONN_VMCNT(0);
+    }
     // Tiles past the last are loads of no bytes into a slot no step reads,
     // so every step issues NLD loads and the wait for tile t+1 at the end of
     // step t is always "all but the newest PF-1 tiles".
