@@ -202,7 +202,13 @@ size_t gonn_hip_attn_workspace_bytes(int op, const void* args);
 int gonn_hip_attn_fwd(const gonn_attn_fwd_args* a, void* ws, size_t ws_bytes, void* stream);
 
 /* Flash backward. Replaces gonn_flash_attn_f64_bwd
- * (backend/cuda/gonn_cuda.h:71-74, gonn_cuda.cu:501-529) for device buffers. */
+ * (backend/cuda/gonn_cuda.h:71-74, gonn_cuda.cu:501-529) for device buffers.
+ * ws: gonn_hip_attn_workspace_bytes(GONN_OP_BWD) bytes. In bf16 mode it holds
+ * the dS that dQ is formed from, at most 16 GiB; a call with up to twice that
+ * runs in two key-block chunks (same results), a larger one forms dS again in
+ * the dQ kernel (no dS buffer). Environment, read by each call and by the
+ * workspace query alike: GONN_HIP_BWD_DS_MB=<MB> sets the dS budget and always
+ * chunks within it; GONN_HIP_BWD_DQ=recompute forms dS again.               */
 int gonn_hip_attn_bwd(const gonn_attn_bwd_args* a, void* ws, size_t ws_bytes, void* stream);
 
 /* Split-KV decode plus combine. New: the reference has no KV cache; the
