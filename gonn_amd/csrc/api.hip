@@ -1098,6 +1098,25 @@ int upload_kv_len(DevMem& mem, const int* kv_len, int B, const int** out) {
     return GONN_OK;
 }
 
+// The causal split of the fp64 forward (gonn::f64_fwd_split_plan): device
+// item table and partials from `mem`, set in p. `items` holds the host
+// table until the stream has copied it.
+int f64_fwd_split_setup(DevMem& mem, gonn::F64Params& p, std::vector<int>& items) {
+    gonn::F64FwdSplit sp = gonn::f64_fwd_split_plan(p);
+    if (sp.items.empty()) return GONN_OK;
+    items = std::move(sp.items);
+    void *it = nullptr, *part = nullptr;
+    TRY(mem.alloc(&it, items.size() * sizeof(int)));
+    TRY(mem.alloc(&part, sp.part_bytes));
+    TRYH(hipMemcpyAsync(it, items.data(), items.size() * sizeof(int), hipMemcpyHostToDevice,
+                        mem.s));
+    p.items = (const int*)it;
+    p.nitems = (int)items.size();
+    p.split_q0 = sp.split_q0;
+    p.part = (double*)part;
+    return GONN_OK;
+}
+
 // Forward on host fp64 data: O (and L when non-null) back in host memory.
 int f64_exact_fwd(const double* Q, const double* K, const double* V, double* O, double* L, int B,
                   int H, int Sq, int Sk, int d, double scale, int causal, const int* kv_len,
@@ -1131,6 +1150,8 @@ int f64_exact_fwd(const double* Q, const double* K, const double* V, double* O, 
     p.d = d;
     p.scale = scale;
     p.causal = causal;
+    std::vector<int> items;
+    TRY(f64_fwd_split_setup(mem, p, items));
     {
         ProfScope ps("fwd_f64", hs);
         TRYH(gonn::launch_f64_fwd(p, hs));
@@ -1425,6 +1446,8 @@ static double bench_f64_exact(int BH, int S, int d, int iters, int causal) {
     p.d = d;
     p.scale = 1.0 / std::sqrt((double)d);
     p.causal = causal;
+    std::vector<int> items;
+    if (f64_fwd_split_setup(mem, p, items) != GONN_OK) return -1.0;
     return time_calls([&] { return gonn::launch_f64_fwd(p, nullptr) == hipSuccess; }, iters);
 }
 

@@ -41,6 +41,9 @@
 #include <cmath>
 #include <cstdlib>
 
+#include <algorithm>
+#include <utility>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -171,7 +174,11 @@ __global__ __launch_bounds__(256) void fwd_f64_kernel(F64Params p) {
 // doubles in lane order:
 //   sK[t][s][j][q] = K[16 t + j][4 s + q]               (S^T k-step s)
 //   sV[t][r][dt][q][j] = V[16 t + 4 r + q][16 dt + j]   (PV k-step r, d tile dt)
-// Causal grids put the longest q-blocks first.
+// Causal grids put the longest q-blocks first. From 16 q-blocks on, the later
+// half of a causal grid's q-blocks is split into two key ranges run by two
+// workgroups (F64Params::items), and fwd_f64_combine_kernel merges their
+// partials: a grid that is one round of workgroups then lasts about half the
+// longest q-block instead of all of it.
 typedef double f64x4_t __attribute__((ext_vector_type(4)));
 typedef double f64x2_t __attribute__((ext_vector_type(2)));
 constexpr int kMWaveQ = 16;                   // queries per wave
@@ -212,11 +219,24 @@ __global__ __launch_bounds__(256, 2) void fwd_f64_mfma_kernel(F64Params p) {
     const int nqb = (Sq + kMRows - 1) / kMRows, BH = p.B * p.H;
     const int rank = blockIdx.x / BH;
     const int bh = blockIdx.x - rank * BH;
-    const int qb = p.causal ? nqb - 1 - rank : rank;
+    // Causal grids run the longest work first: whole q-blocks from the last,
+    // or the items of the split plan (halves of the long q-blocks' key
+    // ranges, which even out a grid that is a single round of workgroups).
+    int qb = p.causal ? nqb - 1 - rank : rank, part = -1;
+    if (p.items) {
+        const int c = p.items[rank];
+        qb = c >> 2;
+        part = (c & 3) - 1;
+    }
     const int q0 = qb * kMRows, qw = q0 + wave * kMWaveQ, qi = qw + col;
     const int kend_b = keys_of(p, bh);
-    int kend = kend_b;
+    int kend = kend_b, kbeg = 0;
     if (p.causal && q0 + kMRows < kend) kend = q0 + kMRows;
+    if (part >= 0) {  // keys [0, mid) or [mid, kend), mid on a stage boundary
+        const int mid = (kend / 2) / kMStage * kMStage;
+        if (part == 0) kend = mid;
+        else kbeg = mid;
+    }
 
     // Q^T fragment: qf[s] = Q[qi][4 s + quad].
     double qf[NS];
@@ -266,8 +286,8 @@ __global__ __launch_bounds__(256, 2) void fwd_f64_mfma_kernel(F64Params p) {
         }
     };
 
-    if (kend > 0) load_stage(0);
-    for (int j0 = 0; j0 < kend; j0 += kMStage) {
+    if (kend > kbeg) load_stage(kbeg);
+    for (int j0 = kbeg; j0 < kend; j0 += kMStage) {
         __syncthreads();  // the previous stage is consumed
         store_stage();
         __syncthreads();
@@ -317,6 +337,19 @@ __global__ __launch_bounds__(256, 2) void fwd_f64_mfma_kernel(F64Params p) {
         }
     }
     const double lt = quad_sum(l);
+    if (part >= 0) {
+        // A half's partial, per row of the q-block: O unnormalised (DP
+        // columns), then m and l; fwd_f64_combine_kernel merges the halves.
+        const int si = bh * (nqb - p.split_q0) + (qb - p.split_q0);
+        double* row = p.part + (((size_t)si * 2 + part) * kMRows + wave * kMWaveQ + col) * (DP + 2);
+        for (int dt = 0; dt < NDT; dt++)
+            for (int r = 0; r < 4; r++) row[16 * dt + 4 * r + quad] = oacc[dt][r];
+        if (quad == 0) {
+            row[DP] = m;
+            row[DP + 1] = lt;
+        }
+        return;
+    }
     if (qi < Sq) {
         double* orow = p.out_o + ((size_t)bh * Sq + qi) * d;
         const double inv = lt > 0.0 ? 1.0 / lt : 0.0;
@@ -328,6 +361,30 @@ __global__ __launch_bounds__(256, 2) void fwd_f64_mfma_kernel(F64Params p) {
         if (p.out_lse && quad == 0)
             p.out_lse[(size_t)bh * Sq + qi] = lt > 0.0 ? m + log(lt) : -INFINITY;
     }
+}
+
+// The two halves of each split q-block (fwd_f64_mfma_kernel): one thread per
+// (row, column) of a split q-block, O = (o0 a0 + o1 a1) / (l0 a0 + l1 a1)
+// with a = exp(m - max(m0, m1)), LSE = max(m0, m1) + log(l); a row no key
+// reaches gets O = 0 and LSE = -inf, as in the whole kernel.
+template <int DP>
+__global__ __launch_bounds__(256) void fwd_f64_combine_kernel(F64Params p) {
+    const int nqb = (p.Sq + kMRows - 1) / kMRows, ns = nqb - p.split_q0;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t per = (size_t)kMRows * DP;  // threads per split q-block
+    if (i >= (size_t)p.B * p.H * ns * per) return;
+    const int si = (int)(i / per), rc = (int)(i % per), r = rc / DP, c = rc % DP;
+    const int bh = si / ns, qb = p.split_q0 + si % ns, qi = qb * kMRows + r;
+    if (qi >= p.Sq || c >= p.d) return;
+    const double* h0 = p.part + (((size_t)si * 2 + 0) * kMRows + r) * (DP + 2);
+    const double* h1 = h0 + (size_t)kMRows * (DP + 2);
+    const double m0 = h0[DP], l0 = h0[DP + 1], m1 = h1[DP], l1 = h1[DP + 1];
+    const double mm = fmax(m0, m1);
+    const double a0 = m0 == -INFINITY ? 0.0 : exp(m0 - mm);
+    const double a1 = m1 == -INFINITY ? 0.0 : exp(m1 - mm);
+    const double l = l0 * a0 + l1 * a1;
+    p.out_o[((size_t)bh * p.Sq + qi) * p.d + c] = l > 0.0 ? (h0[c] * a0 + h1[c] * a1) / l : 0.0;
+    if (p.out_lse && c == 0) p.out_lse[(size_t)bh * p.Sq + qi] = l > 0.0 ? mm + log(l) : -INFINITY;
 }
 
 // Backward on v_mfma_f64_16x16x4f64, the forward's layout applied to the
@@ -697,15 +754,66 @@ bool f64_args_ok(const F64Params& p) {
 
 }  // namespace
 
+F64FwdSplit f64_fwd_split_plan(const F64Params& p) {
+    F64FwdSplit r;
+    // From 16 q-blocks on: at 8 (GoNN's BH 64, S 512 shape) the combine launch
+    // and the extra workgroups cost more than the balance gains (22.97
+    // against 23.98 TFLOP/s; at S 1024 27.06 against 25.23, at S 2048 28.70
+    // against 25.84).
+    const int nqb = (p.Sq + kMRows - 1) / kMRows;
+    if (!p.causal || nqb < 16) return r;
+    const int stage = mstage(dp_of(p.d) <= 64 ? 64 : 128);
+    // Keys of q-block qb (top-left causal, at most Sk); the later half of
+    // the q-blocks is split into two key ranges at a stage boundary.
+    auto keys = [&](int qb) { return std::min(p.Sk, (qb + 1) * kMRows); };
+    r.split_q0 = nqb / 2;
+    std::vector<std::pair<int, int>> it;  // (keys, code)
+    for (int qb = 0; qb < nqb; qb++) {
+        const int k = keys(qb);
+        if (qb < r.split_q0) {
+            it.push_back({k, 4 * qb});
+        } else {
+            const int mid = (k / 2) / stage * stage;
+            it.push_back({mid, 4 * qb + 1});
+            it.push_back({k - mid, 4 * qb + 2});
+        }
+    }
+    std::stable_sort(it.begin(), it.end(), [](const std::pair<int, int>& a,
+                                              const std::pair<int, int>& b) {
+        return a.first > b.first || (a.first == b.first && a.second > b.second);
+    });
+    for (const auto& x : it) r.items.push_back(x.second);
+    const int dp = dp_of(p.d) <= 64 ? 64 : 128;
+    const size_t bh = (size_t)p.B * p.H;
+    r.part_bytes = bh * (size_t)(nqb - r.split_q0) * 2 * kMRows * (dp + 2) * sizeof(double);
+    return r;
+}
+
 hipError_t launch_f64_fwd(const F64Params& p, hipStream_t s) {
     if (!f64_args_ok(p) || !p.out_o) return hipErrorInvalidValue;
+    if (p.items && (!p.causal || !p.part || p.nitems <= 0 || p.split_q0 < 0 ||
+                    p.split_q0 >= (p.Sq + kMRows - 1) / kMRows))
+        return hipErrorInvalidValue;
     const char* e = std::getenv("GONN_HIP_F64_FWD");
     if (!(e && e[0] == 'v')) {  // "valu": the team kernel (kept for comparison)
-        const dim3 grid(((p.Sq + kMRows - 1) / kMRows) * p.B * p.H);
+        const int nqb = (p.Sq + kMRows - 1) / kMRows;
+        const int ranks = p.items ? p.nitems : nqb;
+        const dim3 grid(ranks * p.B * p.H);
+        // the split q-blocks' halves, then their combine
+        const size_t nc = p.items ? (size_t)p.B * p.H * (nqb - p.split_q0) * kMRows *
+                                        (dp_of(p.d) <= 64 ? 64 : 128)
+                                  : 0;
+        const dim3 gc((unsigned)((nc + 255) / 256));
         switch (dp_of(p.d)) {
         case 32:
-        case 64: fwd_f64_mfma_kernel<64><<<grid, 256, 0, s>>>(p); break;
-        default: fwd_f64_mfma_kernel<128><<<grid, 256, 0, s>>>(p); break;
+        case 64:
+            fwd_f64_mfma_kernel<64><<<grid, 256, 0, s>>>(p);
+            if (nc) fwd_f64_combine_kernel<64><<<gc, 256, 0, s>>>(p);
+            break;
+        default:
+            fwd_f64_mfma_kernel<128><<<grid, 256, 0, s>>>(p);
+            if (nc) fwd_f64_combine_kernel<128><<<gc, 256, 0, s>>>(p);
+            break;
         }
         return hipGetLastError();
     }

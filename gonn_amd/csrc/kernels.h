@@ -1,5 +1,6 @@
 // kernels.h -- launch interface between the C ABI (api.hip) and the kernels.
 #pragma once
+#include <vector>
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
@@ -133,7 +134,25 @@ struct F64Params {
     int B, H, Sq, Sk, d;  // d <= 128
     double scale;
     int causal;           // top-left: key j > query i is masked
+    // Causal forward split (fwd_f64_mfma_kernel; null items: none): rank r of
+    // the grid (blockIdx / BH) runs item items[r] = 4 qb + part + 1, q-block
+    // qb whole (part -1) or one half of its key range (part 0, 1). Q-blocks
+    // from split_q0 on are split; each half writes its partial (per row: O
+    // unnormalised, m, l) to `part`, and fwd_f64_combine_kernel, launched
+    // after it, writes their O and LSE.
+    const int* items;
+    int nitems, split_q0;
+    double* part;
 };
+// The causal split plan of the fp64 MFMA forward for these parameters: the
+// item table (empty: no split), its first split q-block, and the bytes of
+// the partials it needs.
+struct F64FwdSplit {
+    std::vector<int> items;
+    int split_q0 = 0;
+    size_t part_bytes = 0;
+};
+F64FwdSplit f64_fwd_split_plan(const F64Params& p);
 hipError_t launch_f64_fwd(const F64Params& p, hipStream_t s);
 hipError_t launch_f64_bwd(const F64Params& p, hipStream_t s);
 

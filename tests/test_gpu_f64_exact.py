@@ -189,6 +189,59 @@ def test_many_blocks_both_kernel_families(f64_mode, monkeypatch, kernels, d, cau
             _close(np.reshape(got, ref.shape), ref, x)
 
 
+@pytest.mark.parametrize("shape", [(64, 512), (32, 1024), (16, 2048)],
+                         ids=lambda s: f"BH{s[0]}xS{s[1]}")
+def test_causal_split_published_shapes(f64_mode, monkeypatch, shape):
+    """GoNN's published causal shapes (benchmark/results/gonn_flash.json,
+    d = 64). From 16 q-blocks of 64 rows on (S >= 961), the MFMA forward
+    splits the key range of the later half of the q-blocks over two
+    workgroups, whose partials (m, l, O) a combine kernel merges; it
+    must equal the team kernel (GONN_HIP_F64_FWD=valu, no split, its own
+    summation order) at the fp64 bar on every row, and the oracle on
+    sampled rows."""
+    hip = f64_mode
+    BH, S = shape
+    d = 64
+    rng = np.random.default_rng(990 + S)
+    q, k, v = (rng.standard_normal((BH, S, d)) for _ in range(3))
+    scale = 1.0 / math.sqrt(d)
+    say(f"f64 causal split BH={BH} S={S}")
+    O, L = hip.FlashAttnF64Ex(q, k, v, BH, 1, S, S, d, scale, True, lse=True)
+    monkeypatch.setenv("GONN_HIP_F64_FWD", "valu")
+    Ov, Lv = hip.FlashAttnF64Ex(q, k, v, BH, 1, S, S, d, scale, True, lse=True)
+    monkeypatch.delenv("GONN_HIP_F64_FWD")
+    _close(O, Ov, "O split vs team kernel")
+    _close(L, Lv, "LSE split vs team kernel")
+    rows = np.array(sorted({0, 1, 63, 64, S // 2 - 1, S // 2, S - 65, S - 64, S - 1}),
+                    dtype=np.int32)
+    ro, rl = oracle.attn_fwd(q, k, v, scale, True, rows=rows)
+    O = O.reshape(BH, S, d)
+    _close(O[:, rows], ro[:, rows], "O sampled rows")
+    _close(L.reshape(BH, S)[:, rows], rl[:, rows], "LSE sampled rows")
+
+
+def test_causal_split_mask_kv_len(f64_mode):
+    """The split causal forward (16 q-blocks at S = 1000) with key padding
+    (one sequence ending inside a split q-block's first half) and an
+    additive mask with blocked keys, against the oracle on every row."""
+    hip = f64_mode
+    from tests.test_gpu_masked import _mask_of
+    B, H, S, d = 2, 2, 1000, 64
+    lens = np.array([S, 545], dtype=np.int32)
+    m, _ = _mask_of("BHTqTk4", B, H, S, S, 995)
+    rng = np.random.default_rng(996)
+    q, k, v = (rng.standard_normal((B * H, S, d)) for _ in range(3))
+    scale = 1.0 / math.sqrt(d)
+    say("f64 causal split, mask + kv_len")
+    O, L = hip.FlashAttnF64Ex(q, k, v, B, H, S, S, d, scale, True, kv_len=lens, lse=True,
+                              attn_mask=m)
+    ro, rl = oracle.attn_fwd(q, k, v, scale, True, kv_len=lens, H=H, attn_mask=m)
+    _close(O.reshape(ro.shape), ro, "O")
+    live = np.isfinite(rl)
+    assert np.array_equal(np.isfinite(L.reshape(rl.shape)), live)
+    _close(L.reshape(rl.shape)[live], rl[live], "LSE")
+
+
 def test_mha_fused_protocol(f64_mode):
     """benchmark/mha: ForwardFused against the unfused Forward at <= 1e-9
     (the oracle's op sequence stands in for GoNN's CPU Forward)."""
