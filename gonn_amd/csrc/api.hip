@@ -1117,6 +1117,39 @@ int f64_fwd_split_setup(DevMem& mem, gonn::F64Params& p, std::vector<int>& items
     return GONN_OK;
 }
 
+// The causal split of the fp64 backward (gonn::f64_bwd_split_plan): device
+// item tables and partials from `mem`, set in p; `items` and `items_k` hold
+// the host tables until the stream has copied them.
+int f64_bwd_split_setup(DevMem& mem, gonn::F64Params& p, std::vector<int>& items,
+                        std::vector<int>& items_k) {
+    gonn::F64BwdSplit sp = gonn::f64_bwd_split_plan(p);
+    items = std::move(sp.items);
+    items_k = std::move(sp.items_k);
+    if (!items.empty()) {
+        void *it = nullptr, *part = nullptr;
+        TRY(mem.alloc(&it, items.size() * sizeof(int)));
+        TRY(mem.alloc(&part, sp.part_bytes));
+        TRYH(hipMemcpyAsync(it, items.data(), items.size() * sizeof(int), hipMemcpyHostToDevice,
+                            mem.s));
+        p.items = (const int*)it;
+        p.nitems = (int)items.size();
+        p.split_q0 = sp.split_q0;
+        p.part = (double*)part;
+    }
+    if (!items_k.empty()) {
+        void *it = nullptr, *part = nullptr;
+        TRY(mem.alloc(&it, items_k.size() * sizeof(int)));
+        TRY(mem.alloc(&part, sp.part_k_bytes));
+        TRYH(hipMemcpyAsync(it, items_k.data(), items_k.size() * sizeof(int),
+                            hipMemcpyHostToDevice, mem.s));
+        p.items_k = (const int*)it;
+        p.nitems_k = (int)items_k.size();
+        p.split_k1 = sp.split_k1;
+        p.part_k = (double*)part;
+    }
+    return GONN_OK;
+}
+
 // Forward on host fp64 data: O (and L when non-null) back in host memory.
 int f64_exact_fwd(const double* Q, const double* K, const double* V, double* O, double* L, int B,
                   int H, int Sq, int Sk, int d, double scale, int causal, const int* kv_len,
@@ -1203,6 +1236,8 @@ int f64_exact_bwd(const double* Q, const double* K, const double* V, const doubl
     p.d = d;
     p.scale = scale;
     p.causal = causal;
+    std::vector<int> items, items_k;
+    TRY(f64_bwd_split_setup(mem, p, items, items_k));
     {
         ProfScope ps("bwd_f64", hs);
         TRYH(gonn::launch_f64_bwd(p, hs));
@@ -1484,6 +1519,8 @@ static double bench_f64_exact_bwd(int BH, int S, int d, int iters, int causal) {
     p.d = d;
     p.scale = 1.0 / std::sqrt((double)d);
     p.causal = causal;
+    std::vector<int> items, items_k;
+    if (f64_bwd_split_setup(mem, p, items, items_k) != GONN_OK) return -1.0;
     return time_calls([&] { return gonn::launch_f64_bwd(p, nullptr) == hipSuccess; }, iters);
 }
 

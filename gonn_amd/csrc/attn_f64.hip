@@ -461,11 +461,21 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dq_f64_mfma_kernel(F64Param
     const int Sq = p.Sq, Sk = p.Sk, d = p.d;
     const int nqb = (Sq + kMRows - 1) / kMRows, BH = p.B * p.H;
     const int rank = blockIdx.x / BH, bh = blockIdx.x - rank * BH;
-    const int qb = p.causal ? nqb - 1 - rank : rank;
+    int qb = p.causal ? nqb - 1 - rank : rank, part = -1;
+    if (p.items) {  // the causal split (F64Params::items)
+        const int c = p.items[rank];
+        qb = c >> 2;
+        part = (c & 3) - 1;
+    }
     const int q0 = qb * kMRows, qw = q0 + wave * kMWaveQ, qi = qw + col;
     const int kend_b = keys_of(p, bh);
-    int kend = kend_b;
+    int kend = kend_b, kbeg = 0;
     if (p.causal && q0 + kMRows < kend) kend = q0 + kMRows;
+    if (part >= 0) {  // keys [0, mid) or [mid, kend), mid on a stage boundary
+        const int mid = (kend / 2) / STG * STG;
+        if (part == 0) kend = mid;
+        else kbeg = mid;
+    }
     const int ic = qi < Sq ? qi : 0;
     const size_t row = ((size_t)bh * Sq + ic) * d;
     double qf[NS], gf[NS];
@@ -482,8 +492,8 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dq_f64_mfma_kernel(F64Param
     const double* kg = p.k + (size_t)bh * Sk * d;
     const double* vg = p.v + (size_t)bh * Sk * d;
     F64Stage<DP, STG> st;
-    if (kend > 0) st.load(kg, vg, 0, Sk, d);
-    for (int j0 = 0; j0 < kend; j0 += STG) {
+    if (kend > kbeg) st.load(kg, vg, kbeg, Sk, d);
+    for (int j0 = kbeg; j0 < kend; j0 += STG) {
         __syncthreads();
         st.store(sK, sV, sKt, nullptr);
         __syncthreads();
@@ -507,6 +517,13 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dq_f64_mfma_kernel(F64Param
                                          dqacc[dt]);
             }
         }
+    }
+    if (part == 1) {  // the second half's partial, all DP columns of its rows
+        const int si = bh * (nqb - p.split_q0) + (qb - p.split_q0);
+        double* pr = p.part + ((size_t)si * kMRows + wave * kMWaveQ + col) * DP;
+        for (int dt = 0; dt < NDT; dt++)
+            for (int r = 0; r < 4; r++) pr[16 * dt + 4 * r + quad] = dqacc[dt][r];
+        return;
     }
     if (qi < Sq) {
         double* dqr = p.dq + row;
@@ -535,7 +552,12 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dkdv_f64_mfma_kernel(F64Par
     const int rank = blockIdx.x / BH, bh = blockIdx.x - rank * BH;
     // Causal key blocks see queries from their first key on: the first
     // blocks are the longest.
-    const int kb = rank;
+    int kb = rank, part = -1;
+    if (p.items_k) {  // the causal split (F64Params::items_k)
+        const int c = p.items_k[rank];
+        kb = c >> 2;
+        part = (c & 3) - 1;
+    }
     const int k0 = kb * kMRows, kw = k0 + wave * kMWaveQ, kj = kw + col;
     const int kend_b = keys_of(p, bh);
     const int jc = kj < Sk ? kj : 0;
@@ -549,12 +571,17 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dkdv_f64_mfma_kernel(F64Par
     const bool klive = kj < kend_b;
     f64x4_t dkacc[NDT], dvacc[NDT];
     for (int t = 0; t < NDT; t++) dkacc[t] = dvacc[t] = f64x4_t{0.0, 0.0, 0.0, 0.0};
-    const int i_start = (p.causal ? k0 : 0) / STG * STG;
+    int i_start = (p.causal ? k0 : 0) / STG * STG, i_end = Sq;
+    if (part >= 0) {  // queries [i_start, mid) or [mid, Sq), mid on a stage boundary
+        const int mid = i_start + (Sq > i_start ? (Sq - i_start) / 2 / STG * STG : 0);
+        if (part == 0) i_end = mid;
+        else i_start = mid;
+    }
     const double* qg = p.q + (size_t)bh * Sq * d;
     const double* gg = p.dO + (size_t)bh * Sq * d;
     F64Stage<DP, STG> st;
-    if (k0 < kend_b && i_start < Sq) st.load(qg, gg, i_start, Sq, d);
-    for (int i0 = i_start; k0 < kend_b && i0 < Sq; i0 += STG) {
+    if (k0 < kend_b && i_start < i_end) st.load(qg, gg, i_start, Sq, d);
+    for (int i0 = i_start; k0 < kend_b && i0 < i_end; i0 += STG) {
         __syncthreads();
         st.store(sQ, sG, sQt, sGt);
         if (tid < STG) {
@@ -563,7 +590,7 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dkdv_f64_mfma_kernel(F64Par
             sD[tid] = ii < Sq ? p.delta[(size_t)bh * Sq + ii] : 0.0;
         }
         __syncthreads();
-        if (i0 + STG < Sq) st.load(qg, gg, i0 + STG, Sq, d);
+        if (i0 + STG < i_end) st.load(qg, gg, i0 + STG, Sq, d);
         for (int t = 0; t < NT16; t++) {
             const int it0 = i0 + 16 * t;
             if (it0 >= Sq || (p.causal && it0 + 15 < kw)) continue;  // wave-uniform
@@ -588,6 +615,16 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dkdv_f64_mfma_kernel(F64Par
             }
         }
     }
+    if (part == 1) {  // the second half's partials, all DP columns of its keys
+        const int sk = bh * p.split_k1 + kb;
+        double* pr = p.part_k + ((size_t)sk * kMRows + wave * kMWaveQ + col) * 2 * DP;
+        for (int dt = 0; dt < NDT; dt++)
+            for (int r = 0; r < 4; r++) {
+                pr[16 * dt + 4 * r + quad] = dkacc[dt][r];
+                pr[DP + 16 * dt + 4 * r + quad] = dvacc[dt][r];
+            }
+        return;
+    }
     if (kj < Sk) {
         double* dkr = p.dk + row;
         double* dvr = p.dv + row;
@@ -600,6 +637,33 @@ __global__ __launch_bounds__(256, mb_waves(DP)) void dkdv_f64_mfma_kernel(F64Par
                 }
             }
     }
+}
+
+// Adds the second halves' partials of the causal backward split: dQ rows of
+// the split q-blocks, then dK and dV rows of the split key blocks; one thread
+// per (row, column).
+template <int DP>
+__global__ __launch_bounds__(256) void bwd_f64_combine_kernel(F64Params p) {
+    const int nqb = (p.Sq + kMRows - 1) / kMRows, nsq = nqb - p.split_q0;
+    const size_t per = (size_t)kMRows * DP, BH = (size_t)p.B * p.H;
+    const size_t nq = p.items ? BH * nsq * per : 0, nk = p.items_k ? BH * p.split_k1 * per : 0;
+    size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < nq) {
+        const int si = (int)(i / per), rc = (int)(i % per), r = rc / DP, c = rc % DP;
+        const int bh = si / nsq, qi = (p.split_q0 + si % nsq) * kMRows + r;
+        if (qi < p.Sq && c < p.d)
+            p.dq[((size_t)bh * p.Sq + qi) * p.d + c] += p.part[((size_t)si * kMRows + r) * DP + c];
+        return;
+    }
+    i -= nq;
+    if (i >= nk) return;
+    const int sk = (int)(i / per), rc = (int)(i % per), r = rc / DP, c = rc % DP;
+    const int bh = sk / p.split_k1, kj = (sk % p.split_k1) * kMRows + r;
+    if (kj >= p.Sk || c >= p.d) return;
+    const double* pr = p.part_k + ((size_t)sk * kMRows + r) * 2 * DP;
+    const size_t o = ((size_t)bh * p.Sk + kj) * p.d + c;
+    p.dk[o] += pr[c];
+    p.dv[o] += pr[DP + c];
 }
 
 // D_i = dO_i . O_i, one team per row.
@@ -826,22 +890,83 @@ hipError_t launch_f64_fwd(const F64Params& p, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Items (4 b + part + 1) of a split grid, longest first: blocks whose
+// range is keys(b) long, the blocks `split(b)` halved at a stage boundary
+// (mid = lo(b) + (n / 2) / stage * stage for n = keys(b) - lo(b)).
+template <typename K, typename L, typename P>
+static std::vector<int> f64_split_items(int nb, int stage, K keys, L lo, P split) {
+    std::vector<std::pair<int, int>> it;  // (length, code)
+    for (int b = 0; b < nb; b++) {
+        const int n = keys(b) - lo(b);
+        if (!split(b)) {
+            it.push_back({n, 4 * b});
+        } else {
+            const int mid = (n / 2) / stage * stage;
+            it.push_back({mid, 4 * b + 1});
+            it.push_back({n - mid, 4 * b + 2});
+        }
+    }
+    std::stable_sort(it.begin(), it.end(), [](const std::pair<int, int>& a,
+                                              const std::pair<int, int>& b) {
+        return a.first > b.first || (a.first == b.first && a.second > b.second);
+    });
+    std::vector<int> r;
+    for (const auto& x : it) r.push_back(x.second);
+    return r;
+}
+
+F64BwdSplit f64_bwd_split_plan(const F64Params& p) {
+    F64BwdSplit r;
+    const int nqb = (p.Sq + kMRows - 1) / kMRows, nkb = (p.Sk + kMRows - 1) / kMRows;
+    if (!p.causal) return r;
+    const int dp = dp_of(p.d) <= 64 ? 64 : 128, stage = mstage(dp);
+    const size_t bh = (size_t)p.B * p.H;
+    if (nqb >= 16) {  // dQ: the later q-blocks' key ranges (top-left causal)
+        r.split_q0 = nqb / 2;
+        r.items = f64_split_items(
+            nqb, stage, [&](int qb) { return std::min(p.Sk, (qb + 1) * kMRows); },
+            [](int) { return 0; }, [&](int qb) { return qb >= r.split_q0; });
+        r.part_bytes = bh * (size_t)(nqb - r.split_q0) * kMRows * dp * sizeof(double);
+    }
+    if (nkb >= 16) {  // dK/dV: the first key blocks' query ranges
+        r.split_k1 = nkb / 2;
+        r.items_k = f64_split_items(
+            nkb, stage, [&](int) { return p.Sq; },
+            [&](int kb) { return std::min(p.Sq, kb * kMRows / stage * stage); },
+            [&](int kb) { return kb < r.split_k1; });
+        r.part_k_bytes = bh * (size_t)r.split_k1 * kMRows * 2 * dp * sizeof(double);
+    }
+    return r;
+}
+
 hipError_t launch_f64_bwd(const F64Params& p, hipStream_t s) {
     if (!f64_args_ok(p) || !p.o || !p.dO || !p.lse || !p.delta || !p.dq || !p.dk || !p.dv)
+        return hipErrorInvalidValue;
+    const int nqb = (p.Sq + kMRows - 1) / kMRows, nkb = (p.Sk + kMRows - 1) / kMRows;
+    if (p.items && (!p.causal || !p.part || p.nitems <= 0 || p.split_q0 < 0 || p.split_q0 >= nqb))
+        return hipErrorInvalidValue;
+    if (p.items_k &&
+        (!p.causal || !p.part_k || p.nitems_k <= 0 || p.split_k1 <= 0 || p.split_k1 > nkb))
         return hipErrorInvalidValue;
     const char* e = std::getenv("GONN_HIP_F64_BWD");
     if (!(e && e[0] == 'v')) {  // "valu": the team kernels (kept for comparison)
         const dim3 gp((p.Sq + kRowsWG - 1) / kRowsWG, p.B * p.H);
-        const dim3 gq(((p.Sq + kMRows - 1) / kMRows) * p.B * p.H);
-        const dim3 gk(((p.Sk + kMRows - 1) / kMRows) * p.B * p.H);
-        if (dp_of(p.d) <= 64) {
+        const dim3 gq((p.items ? p.nitems : nqb) * p.B * p.H);
+        const dim3 gk((p.items_k ? p.nitems_k : nkb) * p.B * p.H);
+        const size_t dp = dp_of(p.d) <= 64 ? 64 : 128, bh = (size_t)p.B * p.H;
+        const size_t nc = (p.items ? bh * (nqb - p.split_q0) * kMRows * dp : 0) +
+                          (p.items_k ? bh * p.split_k1 * kMRows * dp : 0);
+        const dim3 gc((unsigned)((nc + 255) / 256));
+        if (dp == 64) {
             prep_f64_kernel<64><<<gp, 256, 0, s>>>(p);
             dq_f64_mfma_kernel<64><<<gq, 256, 0, s>>>(p);
             dkdv_f64_mfma_kernel<64><<<gk, 256, 0, s>>>(p);
+            if (nc) bwd_f64_combine_kernel<64><<<gc, 256, 0, s>>>(p);
         } else {
             prep_f64_kernel<128><<<gp, 256, 0, s>>>(p);
             dq_f64_mfma_kernel<128><<<gq, 256, 0, s>>>(p);
             dkdv_f64_mfma_kernel<128><<<gk, 256, 0, s>>>(p);
+            if (nc) bwd_f64_combine_kernel<128><<<gc, 256, 0, s>>>(p);
         }
         return hipGetLastError();
     }

@@ -143,6 +143,15 @@ struct F64Params {
     const int* items;
     int nitems, split_q0;
     double* part;
+    // Causal backward split, the same scheme in both kernels: the dQ kernel
+    // halves the later q-blocks' key ranges (items, split_q0), the dK/dV
+    // kernel the first key blocks' query ranges (items_k = 4 kb + part + 1,
+    // key blocks before split_k1; those are the longest). Half 0 writes dQ
+    // (dK, dV) itself and half 1 its partial to part (part_k), which
+    // bwd_f64_combine_kernel, launched after both, adds in.
+    const int* items_k;
+    int nitems_k, split_k1;
+    double* part_k;
 };
 // The causal split plan of the fp64 MFMA forward for these parameters: the
 // item table (empty: no split), its first split q-block, and the bytes of
@@ -153,6 +162,13 @@ struct F64FwdSplit {
     size_t part_bytes = 0;
 };
 F64FwdSplit f64_fwd_split_plan(const F64Params& p);
+// The causal split plan of the fp64 MFMA backward (empty tables: none).
+struct F64BwdSplit {
+    std::vector<int> items, items_k;
+    int split_q0 = 0, split_k1 = 0;
+    size_t part_bytes = 0, part_k_bytes = 0;
+};
+F64BwdSplit f64_bwd_split_plan(const F64Params& p);
 hipError_t launch_f64_fwd(const F64Params& p, hipStream_t s);
 hipError_t launch_f64_bwd(const F64Params& p, hipStream_t s);
 

@@ -215,15 +215,24 @@ def test_causal_split_published_shapes(f64_mode, monkeypatch, shape):
     rows = np.array(sorted({0, 1, 63, 64, S // 2 - 1, S // 2, S - 65, S - 64, S - 1}),
                     dtype=np.int32)
     ro, rl = oracle.attn_fwd(q, k, v, scale, True, rows=rows)
-    O = O.reshape(BH, S, d)
-    _close(O[:, rows], ro[:, rows], "O sampled rows")
+    _close(O.reshape(BH, S, d)[:, rows], ro[:, rows], "O sampled rows")
     _close(L.reshape(BH, S)[:, rows], rl[:, rows], "LSE sampled rows")
+    # the backward's split (dQ: the later q-blocks' key ranges; dK/dV: the
+    # first key blocks' query ranges) against the team kernels
+    g = rng.standard_normal((BH, S, d))
+    got = hip.FlashAttnF64BwdEx(q, k, v, O, L, g, BH, 1, S, d, scale, True)
+    monkeypatch.setenv("GONN_HIP_F64_BWD", "valu")
+    ref = hip.FlashAttnF64BwdEx(q, k, v, O, L, g, BH, 1, S, d, scale, True)
+    monkeypatch.delenv("GONN_HIP_F64_BWD")
+    for x, a, b in zip(("dQ", "dK", "dV"), got, ref):
+        _close(a, b, f"{x} split vs team kernels")
 
 
 def test_causal_split_mask_kv_len(f64_mode):
-    """The split causal forward (16 q-blocks at S = 1000) with key padding
-    (one sequence ending inside a split q-block's first half) and an
-    additive mask with blocked keys, against the oracle on every row."""
+    """The split causal forward and backward (16 q-blocks and key blocks at
+    S = 1000) with key padding (one sequence ending inside a split q-block's
+    first half) and an additive mask with blocked keys, against the oracle
+    on every row."""
     hip = f64_mode
     from tests.test_gpu_masked import _mask_of
     B, H, S, d = 2, 2, 1000, 64
@@ -240,6 +249,13 @@ def test_causal_split_mask_kv_len(f64_mode):
     live = np.isfinite(rl)
     assert np.array_equal(np.isfinite(L.reshape(rl.shape)), live)
     _close(L.reshape(rl.shape)[live], rl[live], "LSE")
+    g = rng.standard_normal((B * H, S, d))
+    dQ, dK, dV = hip.FlashAttnF64BwdEx(q, k, v, O, L, g, B, H, S, d, scale, True, kv_len=lens,
+                                       attn_mask=m)
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, scale=scale, causal=True, kv_len=lens,
+                                          H=H, attn_mask=m)
+    for x, got, ref in (("dQ", dQ, rq), ("dK", dK, rk), ("dV", dV, rv)):
+        _close(np.reshape(got, ref.shape), ref, x)
 
 
 def test_mha_fused_protocol(f64_mode):
