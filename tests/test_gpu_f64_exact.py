@@ -258,6 +258,31 @@ def test_causal_split_mask_kv_len(f64_mode):
         _close(np.reshape(got, ref.shape), ref, x)
 
 
+@pytest.mark.parametrize("d,Sq,Sk", [(128, 1030, 1030), (40, 1100, 1040), (100, 1000, 1500)],
+                         ids=lambda x: str(x))
+def test_causal_split_head_dims_and_cross(f64_mode, d, Sq, Sk):
+    """The causal splits at other head widths (d = 40 runs the 64-wide
+    kernels, 100 and 128 the 128-wide ones, with their own LDS stage) and
+    with Sq != Sk (top-left causal: with Sq > Sk the later q-blocks all see
+    every key; with Sq < Sk the last key blocks see no query). Every
+    q-block count and key-block count here is at least 16, so the forward
+    and both backward kernels run split; every row against the oracle."""
+    hip = f64_mode
+    B, H = 1, 2
+    rng = np.random.default_rng(997 + d + Sq + Sk)
+    q, k, v, g = (rng.standard_normal((B * H, n, d)) for n in (Sq, Sk, Sk, Sq))
+    scale = 1.0 / math.sqrt(d)
+    say(f"f64 causal split d={d} Sq={Sq} Sk={Sk}")
+    O, L = hip.FlashAttnF64Ex(q, k, v, B, H, Sq, Sk, d, scale, True, lse=True)
+    ro, rl = oracle.attn_fwd(q, k, v, scale, True)
+    _close(O.reshape(ro.shape), ro, "O")
+    _close(L.reshape(rl.shape), rl, "LSE")
+    dQ, dK, dV = hip.FlashAttnF64BwdEx(q, k, v, O, L, g, B, H, Sq, d, scale, True, Sk=Sk)
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, scale=scale, causal=True)
+    for x, got, ref in (("dQ", dQ, rq), ("dK", dK, rk), ("dV", dV, rv)):
+        _close(np.reshape(got, ref.shape), ref, x)
+
+
 def test_mha_fused_protocol(f64_mode):
     """benchmark/mha: ForwardFused against the unfused Forward at <= 1e-9
     (the oracle's op sequence stands in for GoNN's CPU Forward)."""
