@@ -108,6 +108,28 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(const float* __restrict__
 constexpr int kDkdvLookahead = 3;
 constexpr int kDkdvDmaSpan = 16;  // slots over which a step's tile loads are spread (0: all)
 
+// S / dP products of the bf16 dK/dV kernel with VGPR accumulators and the
+// K / V fragment (B operand) in AGPRs, so the softmax VALU reads S and dP
+// where the MFMA leaves them. Left to the compiler, at one wave per SIMD
+// every MFMA of the kernel gets an AGPR accumulator and S / dP were copied
+// out with 64 v_accvgpr_read per step (same results bit for bit without
+// them; C5 dK/dV 1.287-1.291 -> 1.251-1.259 ms, cross 0.392-0.393 ->
+// 0.379-0.383 ms, same box, three interleaved rounds). The compiler does not
+// track MFMA hazards through inline asm, so the kernel provides the wait
+// states, each in an asm statement that the registers pass through (so the
+// compiler cannot schedule an access of them ahead of it): the fragments go
+// into AGPRs through an s_nop 4 each, then an s_nop 7 precedes the first of
+// these MFMAs; three s_nop 7 (24 wait states, above the result latency of
+// this 32-cycle MFMA) separate each step's last S / dP MFMA from any VALU
+// access of its accumulators. Chained MFMAs on one accumulator and A
+// operands loaded from LDS (the compiler's waitcnt covers them) need none.
+GONN_DEV void mfma_vacc0(f32x16& d, bf16x8 a, bf16x8 b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, 0" : "=&v"(d) : "v"(a), "a"(b));
+}
+GONN_DEV void mfma_vacc(f32x16& d, bf16x8 a, bf16x8 b) {
+    asm volatile("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+v"(d) : "v"(a), "a"(b));
+}
+
 template <int D, bool CAUSAL, bool MASK>
 __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     constexpr int BN = 128;      // keys per workgroup
@@ -121,6 +143,10 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     constexpr int NRI = RTILE / 8 / 256;
     static_assert(NRI * 256 * 8 == RTILE, "whole load instructions per tile");
     constexpr int NSLOT = 4;
+    // S / dP accumulators in VGPRs (mfma_vacc), except with the additive
+    // mask: its registers leave no room (at D = 64 the compiler then moves
+    // values between VGPRs and AGPRs, and D = 128 already spills).
+    constexpr bool VACC = !MASK;
     __shared__ __attribute__((aligned(16))) bf16 sQ[NSLOT * RTILE];
     __shared__ __attribute__((aligned(16))) bf16 sdO[NSLOT * RTILE];
     __shared__ __attribute__((aligned(16))) float sLD[2][2 * BM];  // L*log2e, then D
@@ -158,6 +184,13 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             kf[ks] = *(const bf16x8*)(kr + ks * 16);
             vf[ks] = *(const bf16x8*)(vr + ks * 16);
         }
+    }
+    if constexpr (VACC) {  // fragments into AGPRs, then wait states (mfma_vacc)
+        for (int ks = 0; ks < NKS; ks++) {
+            asm volatile("s_nop 4" : "+a"(kf[ks]));
+            asm volatile("s_nop 4" : "+a"(vf[ks]));
+        }
+        asm volatile("s_nop 7");
     }
     const bf16* Qg = (const bf16*)p.q + (size_t)bh * Sp * D;
     const bf16* dOg = (const bf16*)p.dO + (size_t)bh * Sp * D;
@@ -324,10 +357,11 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
                     dkacc[t] = mfma_bf16(opr[e % NO], __builtin_bit_cast(bf16x8, pd[ks]), dkacc[t]);
             } else {
                 constexpr int u = w - HCn, kk = ks * (NKS / 4) + u / 4, mt = u & 1;
-                if constexpr (u & 2)
-                    dA[mt] = mfma_bf16(opr[e % NO], vf[kk], kk == 0 ? f32x16{} : dA[mt]);
-                else
-                    sA[mt] = mfma_bf16(opr[e % NO], kf[kk], kk == 0 ? f32x16{} : sA[mt]);
+                f32x16& acc = (u & 2) ? dA[mt] : sA[mt];
+                const bf16x8& b = (u & 2) ? vf[kk] : kf[kk];
+                if constexpr (!VACC) acc = mfma_bf16(opr[e % NO], b, kk == 0 ? f32x16{} : acc);
+                else if constexpr (kk == 0) mfma_vacc0(acc, opr[e % NO], b);
+                else mfma_vacc(acc, opr[e % NO], b);
             }
         };
         // VALU of tile i in 8 groups k = mt*4 + j4 (registers 4 j4 .. +3 of
@@ -415,6 +449,12 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
             if constexpr (NM == 0 || 1 + d * DS >= NM) dma_row(qb + 2, nsl, d, dr);
         });
         uops_at(std::integral_constant<int, NM>{});
+        // Wait states between this step's last S / dP MFMA and VALU access.
+        // The accumulators pass through the statement, so no access of them
+        // is scheduled before it.
+        if constexpr (VACC && HA)
+            asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                         : "+v"(sA[0]), "+v"(sA[1]), "+v"(dA[0]), "+v"(dA[1]));
         GONN_VMCNT(0);
         __syncthreads();
         if constexpr (MASK && HA) MaskRow::add(mreg, sA);
@@ -432,9 +472,22 @@ __global__ __launch_bounds__(256, 1) void bwd_dkdv_bf16_kernel(BwdParams p) {
     for (int mt = 0; mt < 2; mt++) sX[mt] = dX[mt] = f32x16{};
     for (int kk = 0; kk < NKS; kk++)
         for (int mt = 0; mt < 2; mt++) {
-            sX[mt] = mfma_bf16(*(const bf16x8*)(cQ + rowa(kk, mt)), kf[kk], sX[mt]);
-            dX[mt] = mfma_bf16(*(const bf16x8*)(cdO + rowa(kk, mt)), vf[kk], dX[mt]);
+            const bf16x8 aq = *(const bf16x8*)(cQ + rowa(kk, mt));
+            const bf16x8 ad = *(const bf16x8*)(cdO + rowa(kk, mt));
+            if constexpr (!VACC) {
+                sX[mt] = mfma_bf16(aq, kf[kk], sX[mt]);
+                dX[mt] = mfma_bf16(ad, vf[kk], dX[mt]);
+            } else if (kk == 0) {
+                mfma_vacc0(sX[mt], aq, kf[kk]);
+                mfma_vacc0(dX[mt], ad, vf[kk]);
+            } else {
+                mfma_vacc(sX[mt], aq, kf[kk]);
+                mfma_vacc(dX[mt], ad, vf[kk]);
+            }
         }
+    if constexpr (VACC)
+        asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                     : "+v"(sX[0]), "+v"(sX[1]), "+v"(dX[0]), "+v"(dX[1]));
     if constexpr (MASK) {
         mcol.load(qb0, g, mreg);
         MaskRow::add(mreg, sX);
