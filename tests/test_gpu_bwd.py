@@ -222,6 +222,25 @@ def test_bwd_bf16_full_rows_many_key_blocks(path, monkeypatch):
     assert_close(dv.cpu().numpy(), rv, "bf16", f"dV path={path}")
 
 
+@pytest.mark.parametrize("D,causal", [(128, True), (64, False), (64, True)])
+def test_bwd_fp32_full_rows_many_blocks(D, causal):
+    """fp32-MFMA mode, B=1 H=2 S=1536: every row of dQ, dK and dV against
+    the oracle's autograd chain at the fp32 bar (1e-4). 1536 rows span 12
+    key blocks and 12 query blocks of the fp32 kernels, causal and not."""
+    from gonn_amd import hip
+    B, H, S = 1, 2, 1536
+    q, k, v, g = (randn((B * H, S, D), 4500 + D + int(causal) + i) for i in range(4))
+    dev = [torch.from_numpy(x).cuda() for x in (q, k, v, g)]
+    say(f"bwd fp32 full rows S={S} D={D} causal={causal}")
+    o, l = hip.attn_fwd(*dev[:3], causal=causal, mode="fp32")
+    dq, dk, dv = hip.attn_bwd(*dev[:3], o, l, dev[3], causal=causal, mode="fp32")
+    torch.cuda.synchronize()
+    rq, rk, rv = oracle.attn_bwd_autograd(q, k, v, g, causal=causal)
+    assert_close(dq.cpu().numpy(), rq, "fp32", "dQ")
+    assert_close(dk.cpu().numpy(), rk, "fp32", "dK")
+    assert_close(dv.cpu().numpy(), rv, "fp32", "dV")
+
+
 @pytest.mark.parametrize("D", [64, 128])
 @pytest.mark.parametrize("shape", [(592, 3, True), (1200, 8, False), (2400, 3, True)],
                          ids=lambda s: f"{s[0]}x{s[1]}{'c' if s[2] else ''}")
