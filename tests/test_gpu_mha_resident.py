@@ -136,6 +136,44 @@ def test_resident_device_buffers_reuse_workspace(mode_guard):
             dev.dev.forward_dev(xd, xd, xd, ws=ws[:16])
 
 
+@pytest.mark.parametrize("mode", ["fp32", "bf16"])
+def test_resident_forward_dev_graph_replay(mode_guard, mode):
+    """The device-resident forward allocates nothing and only launches
+    kernels on the caller's stream, so a caller can capture it in a HIP
+    graph (here torch's CUDAGraph) and replay it. C1's shape (both
+    projections on the skinny fp64 GEMM kernel): three replays, each after
+    new inputs are copied into the captured buffer and with eager calls and
+    synchronisations in between, each bit-identical to an eager call on the
+    same inputs; the eager result is checked against the oracle."""
+    hip = mode_guard
+    hip.SetAttnMode(mode)
+    B, S, E, H = 2, 128, 256, 4
+    mha, p = _layer(E, H, E, E, 1500)
+    with mha.to_device() as dev:
+        ws = torch.empty(dev.dev.workspace_bytes(B, S, S), dtype=torch.uint8, device="cuda")
+        ws2 = torch.empty_like(ws)
+        xs = [randn((B, S, E), 1501 + i).astype(np.float64) / math.sqrt(E) for i in range(3)]
+        xd = torch.from_numpy(xs[0]).cuda()
+        out = torch.empty_like(xd)
+        dev.dev.forward_dev(xd, xd, xd, out=out, causal=True, ws=ws)  # eager first call
+        torch.cuda.synchronize()
+        say(f"[mha resident] graph capture mode={mode}")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            dev.dev.forward_dev(xd, xd, xd, out=out, causal=True, ws=ws)
+        for i, x in enumerate(xs):
+            xe = torch.from_numpy(x).cuda()
+            xd.copy_(xe)
+            g.replay()
+            torch.cuda.synchronize()
+            got = out.clone()
+            ref = dev.dev.forward_dev(xe, xe, xe, causal=True, ws=ws2)
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref), f"replay {i}"
+            assert_close(ref.cpu().numpy(), oracle.mha_fwd(x, x, x, p, H, causal=True), mode,
+                         f"graph replay {i}")
+
+
 def test_resident_layer_in_the_f64_entries_mode(mode_guard):
     """With the f64 entries' fp64 mode set, the resident layer still runs
     (its core on fp32-MFMA over its fp32 intermediates)."""
