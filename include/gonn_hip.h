@@ -347,7 +347,11 @@ int gonn_hip_mha_forward_f64(gonn_mha* m, const double* q, const double* k, cons
                              double* out, int B, int Tq, int Tk, int causal, const int* kv_len);
 /* The same on GONN_F64 device buffers (kv_len: GONN_I32 device buffer or
  * null) with a caller workspace of gonn_hip_mha_workspace_bytes bytes, on
- * `stream`; allocates nothing. Calls that share a workspace must not overlap. */
+ * `stream`; allocates nothing. Calls that share a workspace must not overlap.
+ * Where both projections take the library's skinny fp64 GEMM (B*Tq <= 256
+ * rows, E a multiple of 128, as at C1), the call only launches kernels and
+ * can be captured in a HIP graph once an eager call has run on the device
+ * (it creates the GEMM handle); replays are bit-identical to eager calls.   */
 size_t gonn_hip_mha_workspace_bytes(const gonn_mha* m, int B, int Tq, int Tk);
 int gonn_hip_mha_forward_dev(gonn_mha* m, const gonn_buf* q, const gonn_buf* k, const gonn_buf* v,
                              gonn_buf* out, int B, int Tq, int Tk, int causal,
