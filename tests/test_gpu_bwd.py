@@ -197,6 +197,42 @@ def test_bwd_bf16_ds_chunks_bit_exact(D, causal, case, monkeypatch):
         assert_close(x[live], ref[live], "bf16", f"{n} in chunks")
 
 
+@pytest.mark.parametrize("i", range(24))
+def test_bwd_bf16_ds_chunks_random(i, monkeypatch):
+    """The random sweep's shapes and options (tests/test_gpu_random.py: ragged
+    Sq and Sk, cross-attention, causal, key padding with empty sequences,
+    every mask shape), bf16 mode: the dS path cut into one-key-block chunks
+    by a 0.03 MB budget gives dQ, dK and dV bit-identical to one pass."""
+    from gonn_amd import hip
+    import tests.test_gpu_random as R
+    c = R._case(i)
+    B, H, D, Sq, Sk = c["B"], c["H"], c["D"], c["Sq"], c["Sk"]
+    r = np.random.default_rng(c["seed"])
+    q, g = (r.standard_normal((B * H, Sq, D)) for _ in range(2))
+    k, v = (r.standard_normal((B * H, Sk, D)) for _ in range(2))
+    m = R._mask(c["mkind"], B, H, Sq, Sk, r) if c["mkind"] else None
+    dev = lambda x, S: torch.from_numpy(x.astype(np.float32)).cuda().reshape(B, H, S, D)  # noqa: E731
+    dq_, dk_, dv_, dg_ = dev(q, Sq), dev(k, Sk), dev(v, Sk), dev(g, Sq)
+    kl = torch.from_numpy(c["kv"]).cuda() if c["kv"] is not None else None
+    md = torch.from_numpy(m.astype(np.float32)).cuda() if m is not None else None
+    say(f"[chunks random {i}] B={B} H={H} D={D} Sq={Sq} Sk={Sk} causal={c['causal']} "
+        f"kv={None if c['kv'] is None else list(c['kv'])} mask={c['mkind']}")
+    o, l = hip.attn_fwd(dq_, dk_, dv_, causal=c["causal"], mode="bf16", kv_len=kl, attn_mask=md)
+    got = []
+    for budget in (None, "0.03"):
+        monkeypatch.delenv("GONN_HIP_BWD_DQ", raising=False)
+        if budget is None:
+            monkeypatch.delenv("GONN_HIP_BWD_DS_MB", raising=False)
+        else:
+            monkeypatch.setenv("GONN_HIP_BWD_DS_MB", budget)
+        gr = hip.attn_bwd(dq_, dk_, dv_, o, l, dg_, causal=c["causal"], mode="bf16", kv_len=kl,
+                          attn_mask=md)
+        torch.cuda.synchronize()
+        got.append([t.cpu() for t in gr])
+    for n, a, b in zip(("dQ", "dK", "dV"), *got):
+        assert torch.equal(a, b), n
+
+
 @pytest.mark.parametrize("path", ["ds", "recompute"])
 def test_bwd_bf16_full_rows_many_key_blocks(path, monkeypatch):
     """B=1 H=2 S=4096 D=128 causal, bf16 MFMA: every row of dQ, dK and dV
